@@ -1,0 +1,719 @@
+// cx_api.hip — the C ABI (include/cosxamix_hip.h): kernel contract,
+// operators, and the Qwen2 model with its cache and captured decode step.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <math.h>
+
+#include <string>
+#include <vector>
+
+#include "cx_ops.h"
+
+// =================================================================== errors
+static thread_local char g_err[512];
+void cx_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+extern "C" const char* cx_last_error(void) { return g_err; }
+
+// ==================================================== library-wide state
+static thread_local int g_device = 0;
+static cx_lib g_libs[64];
+static bool g_lib_ready[64];
+
+cx_lib* cx_lib_get() {
+  int dev = g_device;
+  if (dev < 0 || dev >= 64) return nullptr;
+  if (!g_lib_ready[dev]) {
+    if (hipSetDevice(dev) != hipSuccess) return nullptr;
+    cx_lib& L = g_libs[dev];
+    L.device = dev;
+    if (hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    L.scratch = nullptr;
+    L.scratch_bytes = 0;
+    g_lib_ready[dev] = true;
+  }
+  return &g_libs[g_device];
+}
+
+int cx_scratch_reserve(size_t bytes, void** out) {
+  cx_lib* L = cx_lib_get();
+  if (!L) {
+    cx_set_error("no HIP device %d", g_device);
+    return CX_EHIP;
+  }
+  if (L->scratch_bytes < bytes) {
+    CX_HIP(hipStreamSynchronize(L->stream));
+    if (L->scratch) CX_HIP(hipFree(L->scratch));
+    L->scratch = nullptr;
+    L->scratch_bytes = 0;
+    CX_HIP(hipMalloc(&L->scratch, bytes));
+    L->scratch_bytes = bytes;
+  }
+  *out = L->scratch;
+  return CX_OK;
+}
+
+extern "C" int cx_init(int device) {
+  int n = 0;
+  CX_HIP(hipGetDeviceCount(&n));
+  CX_REQUIRE(device >= 0 && device < n && device < 64, "cx_init: device %d of %d", device, n);
+  g_device = device;
+  CX_HIP(hipSetDevice(device));
+  return cx_lib_get() ? CX_OK : CX_EHIP;
+}
+
+extern "C" size_t cx_row_bytes(int type, size_t k) {
+  const int vpb = cx_vpb(type);
+  if (!vpb || k % (size_t)vpb) return 0;
+  return k / vpb * cx_bpb(type);
+}
+extern "C" int cx_sub_block(int type) { return cx_sub(type); }
+
+// ================================================== 1. kernel contract
+static float dot_host(int type, const uint8_t* b, const int8_t* xq, const float* xe,
+                      const float* xs, size_t nb) {
+  if (!b || !xq || !xe || !xs || !nb) {
+    cx_set_error("dot: null pointer or zero blocks");
+    return NAN;
+  }
+  cx_lib* L = cx_lib_get();
+  if (!L) {
+    cx_set_error("no HIP device");
+    return NAN;
+  }
+  const size_t k = nb * 256, nsub = k / cx_sub(type), rb = nb * cx_bpb(type);
+  const size_t o_x = (rb + 255) / 256 * 256, o_e = o_x + k, o_s = o_e + nsub * 4,
+               o_y = o_s + nsub * 4, total = o_y + 256;
+  void* sp = nullptr;
+  if (cx_scratch_reserve(total, &sp)) return NAN;
+  uint8_t* d = (uint8_t*)sp;
+  hipStream_t s = L->stream;
+  if (hipMemcpyAsync(d, b, rb, hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipMemcpyAsync(d + o_x, xq, k, hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipMemcpyAsync(d + o_e, xe, nsub * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipMemcpyAsync(d + o_s, xs, nsub * 4, hipMemcpyHostToDevice, s) != hipSuccess) {
+    cx_set_error("dot: copy to device failed");
+    return NAN;
+  }
+  cx_seg seg{d, (float*)(d + o_y), nullptr, 1};
+  cx_act act{};
+  act.src = CX_ACT_QUANTIZED;
+  act.xq = (const int8_t*)(d + o_x);
+  act.xe = (const float*)(d + o_e);
+  act.xs = (const float*)(d + o_s);
+  if (cx_launch_gemv(type, &seg, 1, (uint32_t)k, act, CX_EPI_STORE, nullptr, s)) return NAN;
+  float y = NAN;
+  if (hipMemcpyAsync(&y, d + o_y, 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess) {
+    cx_set_error("dot: copy back failed");
+    return NAN;
+  }
+  return y;
+}
+extern "C" float cx_dot_q2k_i8(const uint8_t* b, const int8_t* q, const float* e, const float* s, size_t n) {
+  return dot_host(CX_Q2_K, b, q, e, s, n);
+}
+extern "C" float cx_dot_q3k_i8(const uint8_t* b, const int8_t* q, const float* e, const float* s, size_t n) {
+  return dot_host(CX_Q3_K, b, q, e, s, n);
+}
+extern "C" float cx_dot_q4k_i8(const uint8_t* b, const int8_t* q, const float* e, const float* s, size_t n) {
+  return dot_host(CX_Q4_K, b, q, e, s, n);
+}
+extern "C" float cx_dot_q5k_i8(const uint8_t* b, const int8_t* q, const float* e, const float* s, size_t n) {
+  return dot_host(CX_Q5_K, b, q, e, s, n);
+}
+extern "C" float cx_dot_q6k_i8(const uint8_t* b, const int8_t* q, const float* e, const float* s, size_t n) {
+  return dot_host(CX_Q6_K, b, q, e, s, n);
+}
+
+// ============================================================ 2. operators
+#define STREAM(s) ((hipStream_t)(s))
+
+extern "C" int cx_quantize_act(const float* x, size_t rows, size_t k, int sub, int8_t* xq,
+                               float* xe, float* xs, void* stream) {
+  return cx_launch_quantize(x, rows, k, sub, xq, xe, xs, STREAM(stream));
+}
+
+static int gemv_quantized(int type, const uint8_t* w, size_t n, size_t k, const int8_t* xq,
+                          const float* xe, const float* xs, float* y, int32_t* dbg,
+                          hipStream_t s) {
+  CX_REQUIRE(n < (1u << 31) && k < (1u << 31), "gemv: shape too large");
+  cx_seg seg{w, y, nullptr, (uint32_t)n};
+  cx_act act{};
+  act.src = CX_ACT_QUANTIZED;
+  act.xq = xq;
+  act.xe = xe;
+  act.xs = xs;
+  if (dbg) {  // the debug path writes sums only; point y at a throwaway row
+    CX_REQUIRE(y, "gemv: null output");
+  }
+  return cx_launch_gemv(type, &seg, 1, (uint32_t)k, act, CX_EPI_STORE, dbg, s);
+}
+
+extern "C" int cx_gemv(int type, const uint8_t* w, size_t n, size_t k, const int8_t* xq,
+                       const float* xe, const float* xs, float* y, void* stream) {
+  return gemv_quantized(type, w, n, k, xq, xe, xs, y, nullptr, STREAM(stream));
+}
+
+extern "C" int cx_gemv_subsums(int type, const uint8_t* w, size_t n, size_t k, const int8_t* xq,
+                               const float* xe, const float* xs, int32_t* out, void* stream) {
+  void* sp = nullptr;
+  int rc = cx_scratch_reserve(n * sizeof(float) + 256, &sp);
+  if (rc) return rc;
+  return gemv_quantized(type, w, n, k, xq, xe, xs, (float*)sp, out, STREAM(stream));
+}
+
+extern "C" int cx_quantize_blocks(int type, const float* x, size_t n, uint8_t* out, void* stream) {
+  CX_REQUIRE(x && out, "quantize_blocks: null pointer");
+  return cx_quantize_blocks_dev(type, x, n, out, STREAM(stream));
+}
+
+extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, const uint8_t* w,
+                              int type, float* dst, void* stream) {
+  CX_REQUIRE(cx_is_kquant(type), "matmul_auto: type %d has no k-quant path here", type);
+  CX_REQUIRE(k % 256 == 0, "matmul_auto: a row of %zu is not a multiple of the block of 256", k);
+  CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
+  CX_REQUIRE(n < (1u << 31) && k < (1u << 31), "matmul_auto: shape too large");
+  // Each output row is the fused GEMV of its own input row, with the
+  // activation quantized inside the kernel (ops.rs:469-483 per row). Row by
+  // row is exactly the reference's "one row equals a batch" (ops.rs:1364-1393).
+  for (size_t f = 0; f < m; f++) {
+    cx_seg seg{w, dst + f * n, nullptr, (uint32_t)n};
+    cx_act act{};
+    act.src = CX_ACT_PLAIN;
+    act.x = lhs + f * k;
+    int rc = cx_launch_gemv(type, &seg, 1, (uint32_t)k, act, CX_EPI_STORE, nullptr, STREAM(stream));
+    if (rc) return rc;
+  }
+  return CX_OK;
+}
+
+extern "C" int cx_matmul_multi_1row(const float* x, size_t k, size_t count,
+                                    const uint8_t* const* w, const int* types, const size_t* ns,
+                                    float* const* dsts, void* stream) {
+  CX_REQUIRE(x && w && types && ns && dsts, "multi: null pointer");
+  CX_REQUIRE(k % 256 == 0, "multi: a row of %zu is not a multiple of 256", k);
+  std::vector<bool> done(count, false);
+  for (size_t i = 0; i < count; i++) {
+    if (done[i]) continue;
+    CX_REQUIRE(cx_is_kquant(types[i]), "multi: type %d has no k-quant path here", types[i]);
+    cx_seg segs[4];
+    int nseg = 0;
+    for (size_t j = i; j < count && nseg < 4; j++) {
+      if (done[j] || types[j] != types[i]) continue;
+      segs[nseg++] = cx_seg{w[j], dsts[j], nullptr, (uint32_t)ns[j]};
+      done[j] = true;
+    }
+    cx_act act{};
+    act.src = CX_ACT_PLAIN;
+    act.x = x;
+    int rc = cx_launch_gemv(types[i], segs, nseg, (uint32_t)k, act, CX_EPI_STORE, nullptr,
+                            STREAM(stream));
+    if (rc) return rc;
+  }
+  return CX_OK;
+}
+
+extern "C" int cx_rmsnorm(float* out, const float* in, const float* w, size_t rows, size_t n,
+                          float eps, void* stream) {
+  return cx_launch_rmsnorm(out, in, w, rows, n, eps, STREAM(stream));
+}
+extern "C" int cx_silu(float* out, const float* in, size_t n, void* stream) {
+  CX_REQUIRE(out && in, "silu: null pointer");
+  return cx_launch_silu(out, in, n, STREAM(stream));
+}
+
+// src/ops.rs:1108-1129: f32 powf frequency, f64 angle, f64 cos/sin, f32 store
+extern "C" int cx_rope_tables(size_t hd, float base, size_t ctx, float* c, float* s) {
+  CX_REQUIRE(hd % 2 == 0 && c && s, "rope_tables: head_dim %zu must be even", hd);
+  const size_t half = hd / 2;
+  for (size_t j = 0; j < half; j++) {
+    const float freq = 1.0f / powf(base, 2.0f * (float)j / (float)hd);
+    for (size_t p = 0; p < ctx; p++) {
+      const double ang = (double)p * (double)freq;
+      c[p * half + j] = (float)cos(ang);
+      s[p * half + j] = (float)sin(ang);
+    }
+  }
+  return CX_OK;
+}
+
+extern "C" int cx_rope(float* x, size_t tokens, size_t heads, size_t hd, const float* cos_t,
+                       const float* sin_t, size_t ctx, size_t pos, void* stream) {
+  CX_REQUIRE(hd % 2 == 0, "rope: head_dim %zu must be even", hd);
+  CX_REQUIRE(pos + tokens <= ctx, "rope: positions %zu..%zu past the table of %zu", pos,
+             pos + tokens, ctx);
+  CX_REQUIRE(x && cos_t && sin_t, "rope: null pointer");
+  return cx_launch_rope(x, tokens, heads, hd, cos_t, sin_t, pos, STREAM(stream));
+}
+
+extern "C" int cx_softmax(float* x, size_t len, size_t width, void* stream) {
+  CX_REQUIRE(x, "softmax: null pointer");
+  return cx_launch_softmax(x, len, width, STREAM(stream));
+}
+
+extern "C" int cx_attention(const float* q, const float* k, const float* v, size_t tokens,
+                            size_t total, size_t heads, size_t kv_heads, size_t hd, float* out,
+                            void* stream) {
+  CX_REQUIRE(q && k && v && out, "attention: null pointer");
+  return cx_launch_attention(q, k, v, tokens, total, heads, kv_heads, hd, out, STREAM(stream));
+}
+
+extern "C" int cx_argmax(const float* v, size_t n, uint32_t* out, void* stream) {
+  return cx_launch_argmax_one(v, n, out, STREAM(stream));
+}
+
+// ================================================================ 3. model
+namespace {
+struct Tensor {
+  std::string name;
+  int type;
+  uint64_t dims[2];  // width, rows
+  size_t bytes;
+  size_t offset;
+};
+struct Layer {
+  const float *attn_norm, *q_bias, *k_bias, *v_bias, *ffn_norm;
+  const uint8_t *q, *k, *v, *o, *gate, *up, *down;
+};
+}  // namespace
+
+struct cx_model {
+  cx_config cfg;
+  int device;
+  int t_lin, t_down, t_out;
+  hipStream_t stream;
+  uint8_t* pool;
+  size_t pool_bytes;
+  std::vector<Tensor> tensors;
+  std::vector<Layer> layers;
+  const float* embd;
+  const float* out_norm;
+  const uint8_t* out;
+  float *cos_t, *sin_t;
+  // per-step activations
+  float *x, *q, *k, *v, *att, *g, *u, *logits, *apv;
+  uint32_t* api;
+  uint32_t* amax_out;
+};
+
+struct cx_cache {
+  cx_model* m;
+  size_t cap, len;
+  float* kv;        // [layers][2][cap][kvd]
+  uint32_t* hist;   // tokens by position, cap + 1
+  cx_dstate* st;
+  float *pm, *pl, *po;
+  hipGraphExec_t exec;
+  bool have_graph;
+};
+
+static void* pool_at(cx_model* m, size_t off) { return m->pool + off; }
+
+extern "C" void cx_model_free(cx_model* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->device);
+  (void)hipStreamSynchronize(m->stream);
+  float* bufs[] = {m->x, m->q, m->k, m->v, m->att, m->g, m->u, m->logits, m->apv, m->cos_t, m->sin_t};
+  for (float* b : bufs)
+    if (b) (void)hipFree(b);
+  if (m->api) (void)hipFree(m->api);
+  if (m->amax_out) (void)hipFree(m->amax_out);
+  if (m->pool) (void)hipFree(m->pool);
+  (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+// src/daiss.rs:396-407 (inicio_de)
+static float init_sigma(const std::string& n, uint32_t layers, int* kind) {
+  auto ends = [&](const char* s) {
+    size_t l = strlen(s);
+    return n.size() >= l && n.compare(n.size() - l, l, s) == 0;
+  };
+  if (ends(".bias")) { *kind = 0; return 0.0f; }
+  if (ends("_norm.weight")) { *kind = 1; return 1.0f; }
+  *kind = 2;
+  if (ends("attn_output.weight") || ends("ffn_down.weight"))
+    return 0.02f / sqrtf(2.0f * (float)layers);
+  return 0.02f;
+}
+
+extern "C" int cx_model_create_daiss(const cx_config* cfg, int t_lin, int t_down, int t_out,
+                                     uint64_t seed, cx_model** out) {
+  CX_REQUIRE(cfg && out, "model: null argument");
+  const cx_config c = *cfg;
+  CX_REQUIRE(c.layers && c.dim && c.heads && c.kv_heads && c.ffn && c.vocab && c.ctx,
+             "model: zero-sized config");
+  CX_REQUIRE(c.dim % c.heads == 0 && c.heads % c.kv_heads == 0, "model: heads do not divide");
+  CX_REQUIRE(c.dim % 256 == 0 && c.ffn % 256 == 0, "model: dim and ffn must be multiples of 256");
+  CX_REQUIRE((c.dim / c.heads) % 2 == 0, "model: odd head_dim");
+  CX_REQUIRE(cx_is_kquant(t_lin) && cx_is_kquant(t_down) && cx_is_kquant(t_out) &&
+                 t_lin != CX_Q6_K && t_down != CX_Q6_K && t_out != CX_Q6_K,
+             "model: weights must be Q2_K..Q5_K (the quantizers the reference has)");
+  CX_HIP(hipSetDevice(g_device));
+  cx_model* m = new cx_model();
+  m->cfg = c;
+  m->device = g_device;
+  m->t_lin = t_lin;
+  m->t_down = t_down;
+  m->t_out = t_out;
+  if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
+    delete m;
+    cx_set_error("model: stream");
+    return CX_EHIP;
+  }
+  const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn, V = c.vocab;
+  // tensor table in the order of src/daiss.rs:236-303
+  auto add = [&](const std::string& n, int t, uint64_t w, uint64_t r) {
+    Tensor T{n, t, {w, r}, (size_t)(w / cx_vpb(t) * cx_bpb(t) * r), 0};
+    m->tensors.push_back(T);
+  };
+  add("token_embd.weight", CX_F32, D, V);
+  for (uint32_t i = 0; i < c.layers; i++) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    add(p + "attn_norm.weight", CX_F32, D, 1);
+    add(p + "attn_q.weight", t_lin, D, D);
+    add(p + "attn_q.bias", CX_F32, D, 1);
+    add(p + "attn_k.weight", t_lin, D, kvd);
+    add(p + "attn_k.bias", CX_F32, kvd, 1);
+    add(p + "attn_v.weight", t_lin, D, kvd);
+    add(p + "attn_v.bias", CX_F32, kvd, 1);
+    add(p + "attn_output.weight", t_lin, D, D);
+    add(p + "ffn_norm.weight", CX_F32, D, 1);
+    add(p + "ffn_gate.weight", t_lin, D, I);
+    add(p + "ffn_up.weight", t_lin, D, I);
+    add(p + "ffn_down.weight", t_down, I, D);
+  }
+  add("output_norm.weight", CX_F32, D, 1);
+  add("output.weight", t_out, D, V);
+  size_t off = 0, biggest = 0;
+  for (Tensor& T : m->tensors) {
+    T.offset = off;
+    off += (T.bytes + 255) / 256 * 256;
+    const size_t elems = T.dims[0] * T.dims[1];
+    if (T.type != CX_F32 && elems > biggest) biggest = elems;
+  }
+  m->pool_bytes = off;
+  int rc = CX_OK;
+  float* tmp = nullptr;
+  auto fail = [&](int code) {
+    if (tmp) (void)hipFree(tmp);
+    cx_model_free(m);
+    return code;
+  };
+  if (hipMalloc(&m->pool, m->pool_bytes) != hipSuccess) {
+    cx_set_error("model: cannot allocate %zu bytes of weights", m->pool_bytes);
+    return fail(CX_ENOMEM);
+  }
+  if (hipMalloc(&tmp, biggest * sizeof(float)) != hipSuccess) {
+    cx_set_error("model: cannot allocate the generation buffer");
+    return fail(CX_ENOMEM);
+  }
+  for (const Tensor& T : m->tensors) {
+    int kind;
+    const float sigma = init_sigma(T.name, c.layers, &kind);
+    const size_t elems = T.dims[0] * T.dims[1];
+    float* dstf = T.type == CX_F32 ? (float*)pool_at(m, T.offset) : tmp;
+    if (kind == 2)
+      rc = cx_gen_rows_f32(dstf, cx_fnv_name(T.name.c_str()), seed, (uint32_t)T.dims[1],
+                           (uint32_t)T.dims[0], sigma, m->stream);
+    else
+      rc = cx_gen_fill(dstf, elems, sigma, m->stream);
+    if (!rc && T.type != CX_F32)
+      rc = cx_quantize_blocks_dev(T.type, tmp, elems, (uint8_t*)pool_at(m, T.offset), m->stream);
+    if (rc) return fail(rc);
+  }
+  if (hipStreamSynchronize(m->stream) != hipSuccess) {
+    cx_set_error("model: generation failed: %s", hipGetErrorString(hipGetLastError()));
+    return fail(CX_EHIP);
+  }
+  (void)hipFree(tmp);
+  tmp = nullptr;
+  // named views
+  size_t ti = 0;
+  auto nextp = [&]() { return pool_at(m, m->tensors[ti++].offset); };
+  m->embd = (const float*)nextp();
+  for (uint32_t i = 0; i < c.layers; i++) {
+    Layer L;
+    L.attn_norm = (const float*)nextp();
+    L.q = (const uint8_t*)nextp();
+    L.q_bias = (const float*)nextp();
+    L.k = (const uint8_t*)nextp();
+    L.k_bias = (const float*)nextp();
+    L.v = (const uint8_t*)nextp();
+    L.v_bias = (const float*)nextp();
+    L.o = (const uint8_t*)nextp();
+    L.ffn_norm = (const float*)nextp();
+    L.gate = (const uint8_t*)nextp();
+    L.up = (const uint8_t*)nextp();
+    L.down = (const uint8_t*)nextp();
+    m->layers.push_back(L);
+  }
+  m->out_norm = (const float*)nextp();
+  m->out = (const uint8_t*)nextp();
+  // rope tables on the host, exactly as src/ops.rs:1108-1129, then uploaded
+  {
+    const size_t n = (size_t)c.ctx * (hd / 2);
+    std::vector<float> hc(n), hs(n);
+    cx_rope_tables(hd, c.rope_base, c.ctx, hc.data(), hs.data());
+    if (hipMalloc(&m->cos_t, n * 4) != hipSuccess || hipMalloc(&m->sin_t, n * 4) != hipSuccess ||
+        hipMemcpy(m->cos_t, hc.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->sin_t, hs.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+      cx_set_error("model: rope tables");
+      return fail(CX_ENOMEM);
+    }
+  }
+  const size_t parts = cx_argmax_parts(V);
+  if (hipMalloc(&m->x, D * 4) || hipMalloc(&m->q, D * 4) || hipMalloc(&m->k, kvd * 4) ||
+      hipMalloc(&m->v, kvd * 4) || hipMalloc(&m->att, D * 4) || hipMalloc(&m->g, I * 4) ||
+      hipMalloc(&m->u, I * 4) || hipMalloc(&m->logits, (size_t)V * 4) ||
+      hipMalloc(&m->apv, parts * 4) || hipMalloc(&m->api, parts * 4) ||
+      hipMalloc(&m->amax_out, 4)) {
+    cx_set_error("model: activation buffers");
+    return fail(CX_ENOMEM);
+  }
+  *out = m;
+  return CX_OK;
+}
+
+extern "C" int cx_model_config(const cx_model* m, cx_config* out) {
+  CX_REQUIRE(m && out, "null");
+  *out = m->cfg;
+  return CX_OK;
+}
+extern "C" int cx_model_tensor_count(const cx_model* m) { return m ? (int)m->tensors.size() : 0; }
+extern "C" int cx_model_tensor_info(const cx_model* m, int idx, char* name, size_t cap, int* type,
+                                    uint64_t dims[2], size_t* bytes) {
+  CX_REQUIRE(m && idx >= 0 && idx < (int)m->tensors.size(), "tensor index %d", idx);
+  const Tensor& T = m->tensors[idx];
+  if (name && cap) snprintf(name, cap, "%s", T.name.c_str());
+  if (type) *type = T.type;
+  if (dims) { dims[0] = T.dims[0]; dims[1] = T.dims[1]; }
+  if (bytes) *bytes = T.bytes;
+  return CX_OK;
+}
+extern "C" int cx_model_tensor_copy(const cx_model* m, int idx, void* host, size_t bytes) {
+  CX_REQUIRE(m && idx >= 0 && idx < (int)m->tensors.size() && host, "tensor copy: index %d", idx);
+  const Tensor& T = m->tensors[idx];
+  CX_REQUIRE(bytes >= T.bytes, "tensor copy: %zu bytes for a tensor of %zu", bytes, T.bytes);
+  CX_HIP(hipSetDevice(m->device));
+  CX_HIP(hipMemcpy(host, m->pool + T.offset, T.bytes, hipMemcpyDeviceToHost));
+  return CX_OK;
+}
+extern "C" const void* cx_model_tensor_data(const cx_model* m, int idx) {
+  if (!m || idx < 0 || idx >= (int)m->tensors.size()) {
+    cx_set_error("tensor index %d", idx);
+    return nullptr;
+  }
+  return m->pool + m->tensors[idx].offset;
+}
+extern "C" size_t cx_model_weight_bytes(const cx_model* m) {
+  if (!m) return 0;
+  size_t b = 0;
+  for (const Tensor& T : m->tensors)
+    if (T.name != "token_embd.weight") b += T.bytes;
+  return b + (size_t)m->cfg.dim * 4;  // one embedding row
+}
+
+// ------------------------------------------------------------------ cache
+extern "C" int cx_cache_new(cx_model* m, size_t cap, cx_cache** out) {
+  CX_REQUIRE(m && out && cap > 0, "cache: bad arguments");
+  CX_REQUIRE(cap <= m->cfg.ctx, "cache: %zu tokens past the context of %u", cap, m->cfg.ctx);
+  CX_HIP(hipSetDevice(m->device));
+  const cx_config& c = m->cfg;
+  const size_t kvd = (size_t)c.kv_heads * (c.dim / c.heads);
+  cx_cache* C = new cx_cache();
+  C->m = m;
+  C->cap = cap;
+  C->len = 0;
+  const size_t ns = cx_attn_splits(cap);
+  if (hipMalloc(&C->kv, (size_t)c.layers * 2 * cap * kvd * 4) || hipMalloc(&C->hist, (cap + 1) * 4) ||
+      hipMalloc(&C->st, sizeof(cx_dstate)) || hipMalloc(&C->pm, ns * c.heads * 4) ||
+      hipMalloc(&C->pl, ns * c.heads * 4) || hipMalloc(&C->po, ns * c.heads * (c.dim / c.heads) * 4)) {
+    cx_cache_free(C);
+    cx_set_error("cache: cannot allocate %zu tokens", cap);
+    return CX_ENOMEM;
+  }
+  *out = C;
+  return CX_OK;
+}
+extern "C" size_t cx_cache_len(const cx_cache* c) { return c ? c->len : 0; }
+// src/forward.rs:98-110
+extern "C" int cx_cache_truncate(cx_cache* c, size_t n) {
+  CX_REQUIRE(c, "null cache");
+  if (n < c->len) c->len = n;
+  return CX_OK;
+}
+extern "C" void cx_cache_clear(cx_cache* c) {
+  if (c) c->len = 0;
+}
+extern "C" void cx_cache_free(cx_cache* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->m->device);
+  (void)hipStreamSynchronize(c->m->stream);
+  if (c->have_graph) (void)hipGraphExecDestroy(c->exec);
+  void* bufs[] = {c->kv, c->hist, c->st, c->pm, c->pl, c->po};
+  for (void* b : bufs)
+    if (b) (void)hipFree(b);
+  delete c;
+}
+
+// ------------------------------------------------------- one decode step
+// src/forward.rs:420-501 for one token at position st->pos, then argmax and
+// the position advance. Every kernel reads the position from the device
+// state, so the sequence is captured once per cache and replayed.
+static int enqueue_step(cx_cache* C) {
+  cx_model* m = C->m;
+  const cx_config& c = m->cfg;
+  hipStream_t s = m->stream;
+  const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn;
+  int rc = cx_launch_embed(m->embd, D, C->st, C->hist, m->x, s);
+  if (rc) return rc;
+  for (uint32_t li = 0; li < c.layers; li++) {
+    const Layer& L = m->layers[li];
+    float* kc = C->kv + (size_t)li * 2 * C->cap * kvd;
+    float* vc = kc + C->cap * kvd;
+    cx_act norm{};
+    norm.src = CX_ACT_NORM;
+    norm.x = m->x;
+    norm.norm_w = L.attn_norm;
+    norm.eps = c.eps;
+    cx_seg qkv[3] = {{L.q, m->q, L.q_bias, D}, {L.k, m->k, L.k_bias, kvd}, {L.v, m->v, L.v_bias, kvd}};
+    if ((rc = cx_launch_gemv(m->t_lin, qkv, 3, D, norm, CX_EPI_STORE, nullptr, s))) return rc;
+    if ((rc = cx_launch_rope_kv(m->q, m->k, m->v, kc, vc, m->cos_t, m->sin_t, c.heads, c.kv_heads,
+                                hd, C->st, s)))
+      return rc;
+    if ((rc = cx_launch_attn_decode(m->q, kc, vc, c.heads, c.kv_heads, hd, C->st, (uint32_t)C->cap,
+                                    C->pm, C->pl, C->po, m->att, s)))
+      return rc;
+    cx_act plain{};
+    plain.src = CX_ACT_PLAIN;
+    plain.x = m->att;
+    cx_seg o{L.o, m->x, nullptr, D};
+    if ((rc = cx_launch_gemv(m->t_lin, &o, 1, D, plain, CX_EPI_ACCUM, nullptr, s))) return rc;
+    norm.norm_w = L.ffn_norm;
+    cx_seg gu[2] = {{L.gate, m->g, nullptr, I}, {L.up, m->u, nullptr, I}};
+    if ((rc = cx_launch_gemv(m->t_lin, gu, 2, D, norm, CX_EPI_STORE, nullptr, s))) return rc;
+    cx_act sw{};
+    sw.src = CX_ACT_SWIGLU;
+    sw.x = m->g;
+    sw.x2 = m->u;
+    cx_seg dn{L.down, m->x, nullptr, D};
+    if ((rc = cx_launch_gemv(m->t_down, &dn, 1, I, sw, CX_EPI_ACCUM, nullptr, s))) return rc;
+  }
+  cx_act fin{};
+  fin.src = CX_ACT_NORM;
+  fin.x = m->x;
+  fin.norm_w = m->out_norm;
+  fin.eps = c.eps;
+  cx_seg lm{m->out, m->logits, nullptr, c.vocab};
+  if ((rc = cx_launch_gemv(m->t_out, &lm, 1, D, fin, CX_EPI_STORE, nullptr, s))) return rc;
+  return cx_launch_argmax(m->logits, c.vocab, m->apv, m->api, m->amax_out, C->st, C->hist, s);
+}
+
+static int ensure_graph(cx_cache* C) {
+  if (C->have_graph) return CX_OK;
+  cx_model* m = C->m;
+  hipGraph_t g;
+  CX_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+  int rc = enqueue_step(C);
+  hipError_t e = hipStreamEndCapture(m->stream, &g);
+  if (rc) {
+    if (e == hipSuccess) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  CX_HIP(e);
+  hipError_t ie = hipGraphInstantiate(&C->exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  CX_HIP(ie);
+  C->have_graph = true;
+  return CX_OK;
+}
+
+// Runs `steps` decode steps starting at position C->len, with positions
+// [C->len, prompt_end) fed from `toks` (already in hist).
+static int run_steps(cx_cache* C, size_t prompt_end, size_t steps, float* step_ms) {
+  cx_model* m = C->m;
+  cx_dstate st{(uint32_t)C->len, (uint32_t)prompt_end, (uint32_t)C->cap, 0};
+  CX_HIP(hipMemcpyAsync(C->st, &st, sizeof st, hipMemcpyHostToDevice, m->stream));
+  int rc = ensure_graph(C);
+  if (rc) return rc;
+  std::vector<hipEvent_t> ev;
+  if (step_ms) {
+    ev.resize(steps + 1);
+    for (auto& e : ev) CX_HIP(hipEventCreate(&e));
+    CX_HIP(hipEventRecord(ev[0], m->stream));
+  }
+  for (size_t i = 0; i < steps; i++) {
+    CX_HIP(hipGraphLaunch(C->exec, m->stream));
+    if (step_ms) CX_HIP(hipEventRecord(ev[i + 1], m->stream));
+  }
+  CX_HIP(hipStreamSynchronize(m->stream));
+  if (step_ms) {
+    for (size_t i = 0; i < steps; i++) CX_HIP(hipEventElapsedTime(&step_ms[i], ev[i], ev[i + 1]));
+    for (auto& e : ev) (void)hipEventDestroy(e);
+  }
+  C->len += steps;
+  return CX_OK;
+}
+
+extern "C" int cx_forward(cx_model* m, cx_cache* C, const uint32_t* toks, size_t t,
+                          float* logits_host, uint32_t* argmax_out) {
+  CX_REQUIRE(m && C && C->m == m, "forward: model/cache mismatch");
+  CX_REQUIRE(toks && t > 0, "forward: no tokens to process");
+  CX_REQUIRE(C->len + t <= C->cap, "forward: %zu tokens past the cache of %zu", C->len + t, C->cap);
+  for (size_t i = 0; i < t; i++)
+    CX_REQUIRE(toks[i] < m->cfg.vocab, "forward: token %u is not in a vocabulary of %u", toks[i],
+               m->cfg.vocab);
+  CX_HIP(hipSetDevice(m->device));
+  CX_HIP(hipMemcpyAsync(C->hist + C->len, toks, t * 4, hipMemcpyHostToDevice, m->stream));
+  int rc = run_steps(C, C->len + t, t, nullptr);
+  if (rc) return rc;
+  if (logits_host)
+    CX_HIP(hipMemcpy(logits_host, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
+  if (argmax_out) CX_HIP(hipMemcpy(argmax_out, m->amax_out, 4, hipMemcpyDeviceToHost));
+  return CX_OK;
+}
+
+extern "C" int cx_generate(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n,
+                           size_t max_new, uint32_t eos, uint32_t* out, size_t* n_out,
+                           float* step_ms) {
+  CX_REQUIRE(m && C && C->m == m && n_out, "generate: bad arguments");
+  CX_REQUIRE(prompt && n > 0, "generate: empty prompt");
+  *n_out = 0;
+  const size_t start = C->len;
+  // forward(prompt) + one forward per generated token, the last included
+  // (src/forward.rs:544-557), bounded by the context.
+  size_t steps = n + max_new;
+  if (start + steps > m->cfg.ctx) steps = m->cfg.ctx - start;
+  CX_REQUIRE(start + steps <= C->cap, "generate: %zu tokens past the cache of %zu", start + steps,
+             C->cap);
+  CX_REQUIRE(steps >= n, "generate: the prompt does not fit the context");
+  for (size_t i = 0; i < n; i++)
+    CX_REQUIRE(prompt[i] < m->cfg.vocab, "generate: token %u is not in the vocabulary", prompt[i]);
+  CX_HIP(hipSetDevice(m->device));
+  CX_HIP(hipMemcpyAsync(C->hist + start, prompt, n * 4, hipMemcpyHostToDevice, m->stream));
+  int rc = run_steps(C, start + n, n, nullptr);
+  if (rc) return rc;
+  rc = run_steps(C, start + n, steps - n, step_ms);
+  if (rc) return rc;
+  // generated token i sits at position start+n+i
+  const size_t made = steps - n + 1 > max_new ? max_new : steps - n + 1;
+  std::vector<uint32_t> toks(made);
+  CX_HIP(hipMemcpy(toks.data(), C->hist + start + n, made * 4, hipMemcpyDeviceToHost));
+  size_t k = 0;
+  for (; k < made; k++) {
+    if (toks[k] == eos) break;
+    if (out) out[k] = toks[k];
+  }
+  *n_out = k;
+  // Modelo::generar forwards every pushed token, and stops at EOS without
+  // forwarding it: the cache holds the prompt plus the pushed tokens.
+  if (k < made) C->len = start + n + k;
+  return CX_OK;
+}

@@ -1,0 +1,122 @@
+// cx_common.h — shared device/host helpers for the gfx950 decode path.
+//
+// Everything in this library is compiled with -ffp-contract=off: an f32
+// expression rounds exactly where it is written, the way the reference's Rust
+// does. Where a fused multiply-add is wanted it is spelled out (fmaf).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/cosxamix_hip.h"
+
+#define CX_WAVE 64
+
+// ------------------------------------------------------------------ errors
+void cx_set_error(const char* fmt, ...);
+#define CX_HIP(call)                                                          \
+  do {                                                                        \
+    hipError_t e_ = (call);                                                   \
+    if (e_ != hipSuccess) {                                                   \
+      cx_set_error("%s:%d: %s: %s", __FILE__, __LINE__, #call,                \
+                   hipGetErrorString(e_));                                    \
+      return CX_EHIP;                                                         \
+    }                                                                         \
+  } while (0)
+#define CX_REQUIRE(cond, ...)                                                 \
+  do {                                                                        \
+    if (!(cond)) {                                                            \
+      cx_set_error(__VA_ARGS__);                                              \
+      return CX_EINVAL;                                                       \
+    }                                                                         \
+  } while (0)
+
+// ------------------------------------------------------- format geometry
+// src/gguf.rs:83-111 and src/quant.rs:213-219
+__host__ __device__ inline int cx_bpb(int t) {
+  switch (t) {
+    case CX_F32: return 4;
+    case CX_F16: return 2;
+    case CX_Q8_0: return 34;
+    case CX_Q5_0: return 22;
+    case CX_Q2_K: return 84;
+    case CX_Q3_K: return 110;
+    case CX_Q4_K: return 144;
+    case CX_Q5_K: return 176;
+    case CX_Q6_K: return 210;
+    default: return 0;
+  }
+}
+__host__ __device__ inline int cx_vpb(int t) {
+  switch (t) {
+    case CX_F32: case CX_F16: return 1;
+    case CX_Q8_0: case CX_Q5_0: return 32;
+    case CX_Q2_K: case CX_Q3_K: case CX_Q4_K: case CX_Q5_K: case CX_Q6_K: return 256;
+    default: return 0;
+  }
+}
+__host__ __device__ inline int cx_sub(int t) {
+  switch (t) {
+    case CX_Q8_0: case CX_Q5_0: case CX_Q4_K: case CX_Q5_K: return 32;
+    case CX_Q2_K: case CX_Q3_K: case CX_Q6_K: return 16;
+    default: return 0;
+  }
+}
+inline bool cx_is_kquant(int t) {
+  return t == CX_Q2_K || t == CX_Q3_K || t == CX_Q4_K || t == CX_Q5_K || t == CX_Q6_K;
+}
+
+// ------------------------------------------------------ device helpers
+__device__ inline float cx_h2f(uint32_t h16) {
+  // v_cvt_f32_f16: exact for every finite half, subnormals included (f16
+  // denormals are not flushed in this build). Matches quant.rs:38-60.
+  _Float16 h;
+  uint16_t b = (uint16_t)h16;
+  __builtin_memcpy(&h, &b, 2);
+  return (float)h;
+}
+
+// lane i <- lane i^1, inside a quad (DPP quad_perm [1,0,3,2])
+__device__ inline int cx_xor1(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+}
+
+// Deterministic wave64 sum: butterfly, every lane ends with the same value.
+__device__ inline float cx_wave_sum(float v) {
+  v += __shfl_xor(v, 1, CX_WAVE);
+  v += __shfl_xor(v, 2, CX_WAVE);
+  v += __shfl_xor(v, 4, CX_WAVE);
+  v += __shfl_xor(v, 8, CX_WAVE);
+  v += __shfl_xor(v, 16, CX_WAVE);
+  v += __shfl_xor(v, 32, CX_WAVE);
+  return v;
+}
+__device__ inline double cx_wave_sum_d(double v) {
+  for (int o = 1; o < CX_WAVE; o <<= 1) v += __shfl_xor(v, o, CX_WAVE);
+  return v;
+}
+__device__ inline float cx_wave_max(float v) {
+  for (int o = 1; o < CX_WAVE; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, CX_WAVE));
+  return v;
+}
+
+// Rust `f32 as i32` (saturating, NaN -> 0) then `as i8` (low 8 bits).
+__device__ inline int8_t cx_rust_i8(float r) {
+  int32_t v;
+  if (r != r) v = 0;
+  else if (r >= 2147483648.0f) v = 2147483647;
+  else if (r <= -2147483648.0f) v = (int32_t)0x80000000u;
+  else v = (int32_t)r;
+  return (int8_t)(uint8_t)(uint32_t)v;
+}
+
+// ------------------------------------------------- library-wide state
+struct cx_lib {
+  int device;
+  hipStream_t stream;   // library stream for host-pointer entry points
+  void* scratch;        // device scratch for host-pointer entry points
+  size_t scratch_bytes;
+};
+cx_lib* cx_lib_get();   // initialises lazily on device 0
+int cx_scratch_reserve(size_t bytes, void** out);

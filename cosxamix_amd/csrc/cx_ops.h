@@ -1,0 +1,44 @@
+// cx_ops.h — launchers of the per-token ops (cx_ops.hip).
+#pragma once
+
+#include "cx_internal.h"
+
+// Device-side state of one cache's token loop. Kernels of a captured decode
+// step read the position from here, so one graph serves every position.
+struct cx_dstate {
+  uint32_t pos;         // tokens already in the cache = position of this step
+  uint32_t prompt_end;  // positions below this come from the prompt
+  uint32_t cap;         // cache capacity (tokens)
+  uint32_t pad;
+};
+
+#define CX_ATT_MAX_TOTAL 16000  // general attention keeps scores in LDS
+
+int cx_launch_embed(const float* embd, uint32_t dim, const cx_dstate* st, const uint32_t* hist,
+                    float* x, hipStream_t s);
+int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc,
+                      const float* cos_t, const float* sin_t, uint32_t heads, uint32_t kvh,
+                      uint32_t hd, const cx_dstate* st, hipStream_t s);
+size_t cx_attn_splits(size_t cap);
+int cx_launch_attn_decode(const float* q, const float* kc, const float* vc, uint32_t heads,
+                          uint32_t kvh, uint32_t hd, const cx_dstate* st, uint32_t cap,
+                          float* pm, float* pl, float* po, float* out, hipStream_t s);
+int cx_launch_attention(const float* q, const float* k, const float* v, size_t tokens,
+                        size_t total, size_t heads, size_t kvh, size_t hd, float* out,
+                        hipStream_t s);
+int cx_launch_softmax(float* x, size_t len, size_t width, hipStream_t s);
+int cx_launch_silu(float* out, const float* in, size_t n, hipStream_t s);
+size_t cx_argmax_parts(size_t n);
+int cx_launch_argmax(const float* v, size_t n, float* pv, uint32_t* pi, uint32_t* out,
+                     cx_dstate* st, uint32_t* hist, hipStream_t s);
+
+int cx_launch_argmax_one(const float* v, size_t n, uint32_t* out, hipStream_t s);
+int cx_launch_rope(float* x, size_t tokens, size_t heads, size_t hd, const float* cos_t,
+                   const float* sin_t, size_t pos, hipStream_t s);
+
+// cx_gen.hip: daiss-style seeded weights generated in HBM
+int cx_gen_rows_f32(float* out, uint64_t name_hash, uint64_t seed, uint32_t rows, uint32_t width,
+                    float sigma, hipStream_t s);
+int cx_gen_fill(float* out, size_t n, float value, hipStream_t s);
+int cx_quantize_blocks_dev(int type, const float* x, size_t n, uint8_t* out, hipStream_t s);
+uint64_t cx_fnv_name(const char* name);

@@ -1,0 +1,426 @@
+// cx_ops.hip — the per-token ops around the GEMV, for gfx950.
+//
+//   embedding row copy           src/forward.rs:391-405
+//   RoPE (split halves) + KV     src/ops.rs:1150-1193, src/forward.rs:440-456
+//   decode attention (split-K)   src/ops.rs:1258-1325 at tokens = 1
+//   causal GQA attention         src/ops.rs:1258-1325
+//   softmax                      src/ops.rs:1206-1230
+//   silu                         src/kernels/scalar.rs:63-67
+//   argmax + token loop state    src/sampler.rs:129-137, src/forward.rs:544-557
+#include "cx_ops.h"
+
+namespace {
+
+// ---------------------------------------------------------- embedding
+__global__ __launch_bounds__(256) void k_embed(const float* embd, uint32_t dim,
+                                               const cx_dstate* st, const uint32_t* hist,
+                                               float* x) {
+  const uint32_t tok = hist[st->pos];
+  const float* row = embd + (size_t)tok * dim;
+  for (uint32_t i = threadIdx.x; i < dim; i += 256) x[i] = row[i];
+}
+
+// ------------------------------------------------------ rope + KV append
+// One token at position st->pos: q (H heads) rotated in place, k (Hkv heads)
+// rotated and written to K[pos], v copied to V[pos]. Rotation as
+// src/ops.rs:1185-1188: a' = a*c - b*s, b' = a*s + b*c (no FMA).
+__global__ __launch_bounds__(256) void k_rope_kv(float* q, const float* k, const float* v,
+                                                 float* kc, float* vc, const float* cos_t,
+                                                 const float* sin_t, uint32_t heads,
+                                                 uint32_t kvh, uint32_t hd,
+                                                 const cx_dstate* st) {
+  const uint32_t pos = st->pos, half = hd / 2, kvd = kvh * hd;
+  const float* c = cos_t + (size_t)pos * half;
+  const float* s = sin_t + (size_t)pos * half;
+  float* kd = kc + (size_t)pos * kvd;
+  float* vd = vc + (size_t)pos * kvd;
+  for (uint32_t i = threadIdx.x; i < heads * half; i += 256) {
+    const uint32_t h = i / half, j = i % half;
+    float* lo = q + h * hd + j;
+    const float x0 = lo[0], x1 = lo[half];
+    lo[0] = x0 * c[j] - x1 * s[j];
+    lo[half] = x0 * s[j] + x1 * c[j];
+  }
+  for (uint32_t i = threadIdx.x; i < kvh * half; i += 256) {
+    const uint32_t h = i / half, j = i % half;
+    const float x0 = k[h * hd + j], x1 = k[h * hd + j + half];
+    kd[h * hd + j] = x0 * c[j] - x1 * s[j];
+    kd[h * hd + j + half] = x0 * s[j] + x1 * c[j];
+  }
+  for (uint32_t i = threadIdx.x; i < kvd; i += 256) vd[i] = v[i];
+}
+
+// ------------------------------------------------- decode attention
+// Split-K over cached positions ("flash decoding"). Workgroup (split, g)
+// handles positions [split*P, +P) for all H/Hkv query heads of KV group g:
+// K and V rows of the split are staged in LDS once and shared by the group's
+// heads. Scores use the reference's sequential dot order
+// (src/kernels/scalar.rs:16-23) times 1/sqrt(hd); each split keeps its own
+// max m, sum l = sum exp(s - m) and unnormalised output o = sum e * v.
+constexpr int ATT_P = 64;     // positions per split
+constexpr int ATT_MAXG = 16;  // query heads per KV group supported
+
+__global__ __launch_bounds__(256) void k_attn_split(const float* q, const float* kc,
+                                                    const float* vc, uint32_t heads,
+                                                    uint32_t kvh, uint32_t hd,
+                                                    const cx_dstate* st, float scale,
+                                                    float* pm, float* pl, float* po,
+                                                    uint32_t max_splits) {
+  extern __shared__ __align__(16) float sh[];
+  const uint32_t total = st->pos + 1;
+  const uint32_t split = blockIdx.x, g = blockIdx.y, per = heads / kvh;
+  const uint32_t p0 = split * ATT_P;
+  if (p0 >= total) return;
+  const uint32_t np = min((uint32_t)ATT_P, total - p0);
+  const uint32_t kvd = kvh * hd, ld = hd + 1;
+  float* sq = sh;                       // per x hd
+  float* skv = sq + per * hd;           // ATT_P x (hd+1)
+  float* ssc = skv + ATT_P * ld;        // per x ATT_P
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  for (uint32_t i = tid; i < per * hd; i += 256) sq[i] = q[(g * per) * hd + i];
+  for (uint32_t i = tid; i < np * hd; i += 256) {
+    const uint32_t p = i / hd, d = i % hd;
+    skv[p * ld + d] = kc[(size_t)(p0 + p) * kvd + g * hd + d];
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < per * np; i += 256) {
+    const uint32_t h = i / np, p = i % np;
+    const float* a = sq + h * hd;
+    const float* b = skv + p * ld;
+    float s = 0.0f;
+    for (uint32_t d = 0; d < hd; d++) s += a[d] * b[d];
+    ssc[h * ATT_P + p] = s * scale;
+  }
+  __syncthreads();
+  for (uint32_t h = wave; h < per; h += 4) {
+    const float s = lane < (int)np ? ssc[h * ATT_P + lane] : -INFINITY;
+    const float m = cx_wave_max(s);
+    const float e = lane < (int)np ? expf(s - m) : 0.0f;
+    const float l = cx_wave_sum(e);
+    if (lane < (int)np) ssc[h * ATT_P + lane] = e;
+    if (lane == 0) {
+      const size_t o = ((size_t)split * heads + g * per + h);
+      pm[o] = m;
+      pl[o] = l;
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < np * hd; i += 256) {
+    const uint32_t p = i / hd, d = i % hd;
+    skv[p * ld + d] = vc[(size_t)(p0 + p) * kvd + g * hd + d];
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < per * hd; i += 256) {
+    const uint32_t h = i / hd, d = i % hd;
+    float o = 0.0f;
+    for (uint32_t p = 0; p < np; p++) o += ssc[h * ATT_P + p] * skv[p * ld + d];
+    po[((size_t)split * heads + g * per + h) * hd + d] = o;
+  }
+}
+
+// Merge the splits of every head: M = max m_s, w_s = exp(m_s - M),
+// out = (sum w_s o_s) * (1 / sum w_s l_s).
+__global__ void k_attn_combine(const float* pm, const float* pl, const float* po,
+                               uint32_t heads, uint32_t hd, const cx_dstate* st,
+                               float* out) {
+  const uint32_t total = st->pos + 1, ns = (total + ATT_P - 1) / ATT_P;
+  const uint32_t h = blockIdx.x;
+  float M = -INFINITY;
+  for (uint32_t s = 0; s < ns; s++) M = fmaxf(M, pm[(size_t)s * heads + h]);
+  float L = 0.0f;
+  for (uint32_t s = 0; s < ns; s++) L += pl[(size_t)s * heads + h] * expf(pm[(size_t)s * heads + h] - M);
+  const float inv = 1.0f / L;
+  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+    float o = 0.0f;
+    for (uint32_t s = 0; s < ns; s++)
+      o += po[((size_t)s * heads + h) * hd + d] * expf(pm[(size_t)s * heads + h] - M);
+    out[h * hd + d] = o * inv;
+  }
+}
+
+// ---------------------------------------------- general causal attention
+// One workgroup per (head, token). Scores in the reference's order (sequential
+// dot, times 1/sqrt(hd)), softmax over the visible positions (max, exp, sum,
+// times 1/sum), output accumulated position by position like
+// src/ops.rs:1316-1321. Scores live in LDS (total <= CX_ATT_MAX_TOTAL).
+__global__ __launch_bounds__(256) void k_attention(const float* q, const float* k,
+                                                   const float* v, uint32_t tokens,
+                                                   uint32_t total, uint32_t heads,
+                                                   uint32_t kvh, uint32_t hd, float scale,
+                                                   float* out) {
+  extern __shared__ __align__(16) float sc[];
+  __shared__ float red[4];
+  const uint32_t h = blockIdx.x, t = blockIdx.y;
+  const uint32_t vis = total - tokens + t + 1, per = heads / kvh, g = h / per;
+  const uint32_t wq = heads * hd, wkv = kvh * hd;
+  const float* qh = q + (size_t)t * wq + h * hd;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float mx = -INFINITY;
+  for (uint32_t p = tid; p < vis; p += 256) {
+    const float* kp = k + (size_t)p * wkv + g * hd;
+    float s = 0.0f;
+    for (uint32_t d = 0; d < hd; d++) s += qh[d] * kp[d];
+    s = s * scale;
+    sc[p] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = cx_wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float tot = 0.0f;
+  for (uint32_t p = tid; p < vis; p += 256) {
+    const float e = expf(sc[p] - mx);
+    sc[p] = e;
+    tot += e;
+  }
+  tot = cx_wave_sum(tot);
+  if (lane == 0) red[wave] = tot;
+  __syncthreads();
+  tot = ((red[0] + red[1]) + red[2]) + red[3];
+  const float inv = 1.0f / tot;
+  for (uint32_t p = tid; p < vis; p += 256) sc[p] = sc[p] * inv;
+  __syncthreads();
+  for (uint32_t d = tid; d < hd; d += 256) {
+    float o = 0.0f;
+    for (uint32_t p = 0; p < vis; p++) o += sc[p] * v[(size_t)p * wkv + g * hd + d];
+    out[(size_t)t * wq + h * hd + d] = o;
+  }
+}
+
+// -------------------------------------------------------------- softmax
+__global__ __launch_bounds__(256) void k_softmax(float* x, uint32_t width) {
+  __shared__ float red[4];
+  float* row = x + (size_t)blockIdx.x * width;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float mx = -INFINITY;
+  for (uint32_t i = tid; i < width; i += 256) mx = fmaxf(mx, row[i]);
+  mx = cx_wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  if (!isfinite(mx)) {  // all -inf, or a NaN: uniform (src/ops.rs:1214-1219)
+    const float p = 1.0f / (float)width;
+    for (uint32_t i = tid; i < width; i += 256) row[i] = p;
+    return;
+  }
+  float tot = 0.0f;
+  for (uint32_t i = tid; i < width; i += 256) {
+    const float e = expf(row[i] - mx);
+    row[i] = e;
+    tot += e;
+  }
+  tot = cx_wave_sum(tot);
+  if (lane == 0) red[wave] = tot;
+  __syncthreads();
+  tot = ((red[0] + red[1]) + red[2]) + red[3];
+  const float inv = 1.0f / tot;
+  for (uint32_t i = tid; i < width; i += 256) row[i] = row[i] * inv;
+}
+
+__global__ void k_silu(float* out, const float* in, size_t n) {
+  for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const float x = in[i];
+    out[i] = x / (1.0f + expf(-x));
+  }
+}
+
+// -------------------------------------------------------------- argmax
+// (value, index) pairs; a beats b if larger, or equal with a lower index.
+// NaN entries never win; index 0 wins when v[0] is NaN (strict '>' scan of
+// src/sampler.rs:129-137 never leaves index 0 then).
+struct VI { float v; uint32_t i; };
+__device__ inline VI vi_best(VI a, VI b) {
+  return (a.v > b.v || (a.v == b.v && a.i < b.i)) ? a : b;
+}
+__device__ inline VI vi_wave(VI a) {
+  for (int o = 1; o < 64; o <<= 1) {
+    VI b{__shfl_xor(a.v, o, 64), (uint32_t)__shfl_xor((int)a.i, o, 64)};
+    a = vi_best(a, b);
+  }
+  return a;
+}
+constexpr uint32_t ARG_CHUNK = 4096;
+
+__global__ __launch_bounds__(256) void k_argmax_part(const float* v, uint32_t n, float* pv,
+                                                     uint32_t* pi) {
+  __shared__ VI red[4];
+  const uint32_t b0 = blockIdx.x * ARG_CHUNK, b1 = min(n, b0 + ARG_CHUNK);
+  VI best{-INFINITY, 0xFFFFFFFFu};
+  for (uint32_t i = b0 + threadIdx.x; i < b1; i += 256) {
+    const float x = v[i];
+    if (!(x != x)) best = vi_best(best, VI{x, i});
+  }
+  best = vi_wave(best);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    VI r = vi_best(vi_best(red[0], red[1]), vi_best(red[2], red[3]));
+    pv[blockIdx.x] = r.v;
+    pi[blockIdx.x] = r.i;
+  }
+}
+
+// Final reduction. With `st` (the model's token loop), also advances the
+// loop: hist[pos+1] = argmax when position pos+1 is past the prompt, then
+// pos += 1.
+__global__ __launch_bounds__(256) void k_argmax_final(const float* v, const float* pv,
+                                                      const uint32_t* pi, uint32_t nparts,
+                                                      uint32_t* out, cx_dstate* st,
+                                                      uint32_t* hist) {
+  __shared__ VI red[4];
+  VI best{-INFINITY, 0xFFFFFFFFu};
+  for (uint32_t i = threadIdx.x; i < nparts; i += 256) best = vi_best(best, VI{pv[i], pi[i]});
+  best = vi_wave(best);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    VI r = vi_best(vi_best(red[0], red[1]), vi_best(red[2], red[3]));
+    uint32_t tok = r.i;
+    const float v0 = v[0];
+    if (v0 != v0 || tok == 0xFFFFFFFFu) tok = 0;
+    if (out) *out = tok;
+    if (st) {
+      const uint32_t nxt = st->pos + 1;
+      if (nxt >= st->prompt_end && nxt <= st->cap) hist[nxt] = tok;  // hist has cap+1 slots
+      st->pos = nxt;
+    }
+  }
+}
+
+// single-workgroup argmax for the operator entry point (no partial buffers)
+__global__ __launch_bounds__(1024) void k_argmax_one(const float* v, uint32_t n, uint32_t* out) {
+  __shared__ VI red[16];
+  VI best{-INFINITY, 0xFFFFFFFFu};
+  for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+    const float x = v[i];
+    if (!(x != x)) best = vi_best(best, VI{x, i});
+  }
+  best = vi_wave(best);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    VI r = red[0];
+    for (int w = 1; w < 16; w++) r = vi_best(r, red[w]);
+    const float v0 = v[0];
+    *out = (v0 != v0 || r.i == 0xFFFFFFFFu) ? 0u : r.i;
+  }
+}
+
+// General RoPE for the operator entry point: tokens at positions pos.. .
+__global__ __launch_bounds__(256) void k_rope(float* x, uint32_t tokens, uint32_t heads,
+                                              uint32_t hd, const float* cos_t,
+                                              const float* sin_t, uint32_t pos) {
+  const uint32_t half = hd / 2, per_tok = heads * half;
+  const size_t total = (size_t)tokens * per_tok;
+  for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+    const uint32_t t = (uint32_t)(i / per_tok), r = (uint32_t)(i % per_tok);
+    const uint32_t h = r / half, j = r % half;
+    const float c = cos_t[(size_t)(pos + t) * half + j], s = sin_t[(size_t)(pos + t) * half + j];
+    float* lo = x + (size_t)t * heads * hd + h * hd + j;
+    const float x0 = lo[0], x1 = lo[half];
+    lo[0] = x0 * c - x1 * s;
+    lo[half] = x0 * s + x1 * c;
+  }
+}
+
+}  // namespace
+
+// ================================================================ launchers
+int cx_launch_argmax_one(const float* v, size_t n, uint32_t* out, hipStream_t s) {
+  CX_REQUIRE(v && out && n > 0 && n < 0xFFFFFFFFull, "argmax: bad arguments (n=%zu)", n);
+  hipLaunchKernelGGL(k_argmax_one, dim3(1), dim3(1024), 0, s, v, (uint32_t)n, out);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_rope(float* x, size_t tokens, size_t heads, size_t hd, const float* cos_t,
+                   const float* sin_t, size_t pos, hipStream_t s) {
+  const size_t total = tokens * heads * (hd / 2);
+  if (!total) return CX_OK;
+  const unsigned grid = (unsigned)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+  hipLaunchKernelGGL(k_rope, dim3(grid), dim3(256), 0, s, x, (uint32_t)tokens, (uint32_t)heads,
+                     (uint32_t)hd, cos_t, sin_t, (uint32_t)pos);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+int cx_launch_embed(const float* embd, uint32_t dim, const cx_dstate* st, const uint32_t* hist,
+                    float* x, hipStream_t s) {
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, dim, st, hist, x);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc,
+                      const float* cos_t, const float* sin_t, uint32_t heads, uint32_t kvh,
+                      uint32_t hd, const cx_dstate* st, hipStream_t s) {
+  hipLaunchKernelGGL(k_rope_kv, dim3(1), dim3(256), 0, s, q, k, v, kc, vc, cos_t, sin_t, heads,
+                     kvh, hd, st);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+size_t cx_attn_splits(size_t cap) { return (cap + ATT_P - 1) / ATT_P; }
+
+int cx_launch_attn_decode(const float* q, const float* kc, const float* vc, uint32_t heads,
+                          uint32_t kvh, uint32_t hd, const cx_dstate* st, uint32_t cap,
+                          float* pm, float* pl, float* po, float* out, hipStream_t s) {
+  CX_REQUIRE(kvh && heads % kvh == 0 && heads / kvh <= ATT_MAXG, "attention: %u heads / %u groups",
+             heads, kvh);
+  const uint32_t ns = (uint32_t)cx_attn_splits(cap), per = heads / kvh;
+  const size_t lds = sizeof(float) * (per * hd + ATT_P * (hd + 1) + per * ATT_P);
+  const float scale = 1.0f / sqrtf((float)hd);
+  hipLaunchKernelGGL(k_attn_split, dim3(ns, kvh), dim3(256), lds, s, q, kc, vc, heads, kvh, hd,
+                     st, scale, pm, pl, po, ns);
+  CX_HIP(hipGetLastError());
+  hipLaunchKernelGGL(k_attn_combine, dim3(heads), dim3(128), 0, s, pm, pl, po, heads, hd, st, out);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_attention(const float* q, const float* k, const float* v, size_t tokens,
+                        size_t total, size_t heads, size_t kvh, size_t hd, float* out,
+                        hipStream_t s) {
+  CX_REQUIRE(kvh && heads % kvh == 0, "attention: %zu heads do not split in %zu groups", heads, kvh);
+  CX_REQUIRE(tokens <= total, "attention: %zu new tokens and only %zu in total", tokens, total);
+  CX_REQUIRE(total <= CX_ATT_MAX_TOTAL, "attention: total %zu above %d", total, CX_ATT_MAX_TOTAL);
+  if (!tokens) return CX_OK;
+  const float scale = 1.0f / sqrtf((float)hd);
+  hipLaunchKernelGGL(k_attention, dim3((unsigned)heads, (unsigned)tokens), dim3(256),
+                     total * sizeof(float), s, q, k, v, (uint32_t)tokens, (uint32_t)total,
+                     (uint32_t)heads, (uint32_t)kvh, (uint32_t)hd, scale, out);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_softmax(float* x, size_t len, size_t width, hipStream_t s) {
+  CX_REQUIRE(width && len % width == 0, "softmax: %zu values are not rows of %zu", len, width);
+  if (!len) return CX_OK;
+  hipLaunchKernelGGL(k_softmax, dim3((unsigned)(len / width)), dim3(256), 0, s, x, (uint32_t)width);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_silu(float* out, const float* in, size_t n, hipStream_t s) {
+  if (!n) return CX_OK;
+  const unsigned grid = (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  hipLaunchKernelGGL(k_silu, dim3(grid), dim3(256), 0, s, out, in, n);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+size_t cx_argmax_parts(size_t n) { return (n + ARG_CHUNK - 1) / ARG_CHUNK; }
+
+int cx_launch_argmax(const float* v, size_t n, float* pv, uint32_t* pi, uint32_t* out,
+                     cx_dstate* st, uint32_t* hist, hipStream_t s) {
+  CX_REQUIRE(n > 0 && n < 0xFFFFFFFFull, "argmax: length %zu", n);
+  const uint32_t parts = (uint32_t)cx_argmax_parts(n);
+  hipLaunchKernelGGL(k_argmax_part, dim3(parts), dim3(256), 0, s, v, (uint32_t)n, pv, pi);
+  CX_HIP(hipGetLastError());
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, v, pv, pi, parts, out, st, hist);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}

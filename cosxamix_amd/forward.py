@@ -1,0 +1,162 @@
+"""The model level of the boundary: ``forward::{Config, Cache, Modelo}``
+(src/forward.rs:36-137, 375-559) over the C ABI.
+
+A ``Modelo`` owns its weights in HBM; a ``Cache`` owns the f32 KV cache and
+the captured decode step. ``forward`` appends tokens and returns the logits
+of the last one; ``generar`` is the greedy token loop of Modelo::generar.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib as L
+
+_lib = L.load()
+
+
+@dataclass(frozen=True)
+class Config:
+    """forward::Config (src/forward.rs:36-55) plus the daiss family shapes
+    (src/daiss.rs:77-139)."""
+    capas: int
+    dim: int
+    cabezas: int
+    cabezas_kv: int
+    ffn: int
+    vocab: int
+    contexto: int
+    eps: float = 1e-6
+    rope: float = 1_000_000.0
+
+    def dim_cabeza(self) -> int:
+        return self.dim // self.cabezas
+
+    def dim_kv(self) -> int:
+        return self.cabezas_kv * self.dim_cabeza()
+
+    def c(self) -> L.CxConfig:
+        return L.CxConfig(self.capas, self.dim, self.cabezas, self.cabezas_kv, self.ffn, self.vocab,
+                          self.contexto, self.eps, self.rope)
+
+
+# daiss-3b (src/daiss.rs:103-114) = the Qwen2.5-3B shape of the benchmark
+DAISS_3B = Config(36, 2048, 16, 2, 11008, 151936, 32768, 1e-6, 1_000_000.0)
+# Llama-3-8B shape written as a qwen2-architecture model (zero biases)
+LLAMA3_8B = Config(32, 4096, 32, 8, 14336, 128256, 8448 + 256, 1e-5, 500_000.0)
+
+
+def bytes_de_cache_por_token(cfg: Config) -> int:
+    """forward::bytes_de_cache_por_token (src/forward.rs:563-565)."""
+    return 2 * cfg.capas * cfg.dim_kv() * 4
+
+
+class Modelo:
+    """A Qwen2 model resident in HBM with daiss-style seeded weights."""
+
+    def __init__(self, cfg: Config, tipo=L.Q4_K, semilla: int = 42, tipo_down=None,
+                 tipo_salida=None):
+        self.cfg = cfg
+        h = C.c_void_p()
+        L.check(_lib.cx_model_create_daiss(C.byref(cfg.c()), tipo, tipo_down or tipo,
+                                           tipo_salida or tipo, semilla, C.byref(h)),
+                "Modelo")
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.cx_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def bytes_por_token(self) -> int:
+        """Weight bytes streamed per decode token (matrices + one embedding row)."""
+        return int(_lib.cx_model_weight_bytes(self._h))
+
+    def tensores(self):
+        """[(name, type, (width, rows), bytes)] in GGUF declaration order."""
+        out = []
+        for i in range(_lib.cx_model_tensor_count(self._h)):
+            name = C.create_string_buffer(128)
+            t = C.c_int()
+            dims = (C.c_uint64 * 2)()
+            nb = C.c_size_t()
+            L.check(_lib.cx_model_tensor_info(self._h, i, name, 128, C.byref(t), dims, C.byref(nb)),
+                    "tensor_info")
+            out.append((name.value.decode(), t.value, (dims[0], dims[1]), nb.value))
+        return out
+
+    def tensor(self, idx: int) -> np.ndarray:
+        name, t, dims, nb = self.tensores()[idx]
+        buf = np.empty(nb, dtype=np.uint8)
+        L.check(_lib.cx_model_tensor_copy(self._h, idx, buf.ctypes.data_as(C.c_void_p), nb),
+                "tensor_copy")
+        if t == L.F32:
+            return buf.view(np.float32)
+        return buf.reshape(dims[1], -1)
+
+    def tensor_ptr(self, idx: int) -> int:
+        """Device address of tensor `idx` (a view owned by the model)."""
+        p = _lib.cx_model_tensor_data(self._h, idx)
+        if not p:
+            raise L.CxError(L.last_error())
+        return p
+
+    def nueva_cache(self, capacidad: int) -> "Cache":
+        return Cache(self, capacidad)
+
+    def forward(self, tokens, cache: "Cache", logits: bool = True):
+        """Modelo::forward: logits (f32[vocab]) of the last token, and its argmax."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        lg = np.empty(self.cfg.vocab, np.float32) if logits else None
+        am = C.c_uint32()
+        L.check(_lib.cx_forward(self._h, cache._h, t.ctypes.data_as(L._u32p), t.size,
+                                lg.ctypes.data_as(L._f32p) if logits else None, C.byref(am)),
+                "forward")
+        return lg, am.value
+
+    def generar(self, prompt, max_nuevos: int, cache: "Cache", fin: int | None = None,
+                tiempos: bool = False):
+        """Modelo::generar with the greedy sampler. Returns the tokens, and the
+        per-token decode times in ms if `tiempos`."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(max_nuevos, 1), np.uint32)
+        n = C.c_size_t()
+        ms = np.zeros(max(max_nuevos, 1), np.float32) if tiempos else None
+        L.check(_lib.cx_generate(self._h, cache._h, p.ctypes.data_as(L._u32p), p.size, max_nuevos,
+                                 0xFFFFFFFF if fin is None else fin, out.ctypes.data_as(L._u32p),
+                                 C.byref(n), ms.ctypes.data_as(L._f32p) if tiempos else None),
+                "generar")
+        toks = out[: n.value].copy()
+        return (toks, ms) if tiempos else toks
+
+
+class Cache:
+    """forward::Cache (src/forward.rs:62-137) with room for `capacidad` tokens."""
+
+    def __init__(self, modelo: Modelo, capacidad: int):
+        self.modelo = modelo
+        h = C.c_void_p()
+        L.check(_lib.cx_cache_new(modelo._h, capacidad, C.byref(h)), "Cache")
+        self._h = h
+
+    def largo(self) -> int:
+        return int(_lib.cx_cache_len(self._h))
+
+    def truncar(self, n: int) -> None:
+        L.check(_lib.cx_cache_truncate(self._h, n), "truncar")
+
+    def limpiar(self) -> None:
+        _lib.cx_cache_clear(self._h)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.cx_cache_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()

@@ -1,0 +1,222 @@
+/*
+ * cosxamix_hip.h — C ABI of the MI355X (gfx950) decode path.
+ *
+ * Drop-in boundary for the reference crate Brashkie/Cosxamix's batch-1 decode
+ * token loop. Three levels, mirroring the reference's own nesting:
+ *
+ *   1. kernel contract   — the reference's `type Kernel` FFI
+ *                          (src/kernels/q2k.rs:153, src/kernels/q5k.rs:35);
+ *   2. operators         — ops::matmul_auto / matmul_varias_una_fila /
+ *                          cuantizar_i8_en / rope / atencion / softmax,
+ *                          kernels::rmsnorm / silu, sampler::argmax;
+ *   3. model             — forward::Modelo::{forward, generar} and
+ *                          forward::Cache.
+ *
+ * Conventions
+ *   - Return value: CX_OK (0) or a negative CX_E* code; cx_last_error()
+ *     gives the message (replaces the reference's Result<_, String>).
+ *     Level-1 functions return the f32 like the reference and report an
+ *     error as NaN plus cx_last_error().
+ *   - Level-1 pointers are HOST pointers (same as the reference contract).
+ *     Level-2 pointers are DEVICE pointers (hipMalloc'd or torch tensors);
+ *     `stream` is a hipStream_t (NULL = the HIP null stream) and the call is
+ *     asynchronous on it. Level-3 objects own their device memory.
+ *   - Types are GGML type ids (src/gguf.rs:39-54).
+ *   - A cx_model / cx_cache is not thread-safe; the reference serialises
+ *     generation behind a Mutex (src/engine_own.rs:62,185).
+ */
+#ifndef COSXAMIX_HIP_H
+#define COSXAMIX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids — src/gguf.rs:39-54 */
+enum {
+  CX_F32 = 0, CX_F16 = 1, CX_Q5_0 = 6, CX_Q8_0 = 8,
+  CX_Q2_K = 10, CX_Q3_K = 11, CX_Q4_K = 12, CX_Q5_K = 13, CX_Q6_K = 14
+};
+
+/* status codes */
+enum { CX_OK = 0, CX_EINVAL = -1, CX_EHIP = -2, CX_ENOMEM = -3, CX_ENOTSUP = -4 };
+
+/* Last error message of the calling thread ("" if none). */
+const char *cx_last_error(void);
+
+/* Select the device used by host-pointer entry points and by models created
+ * afterwards on this thread. Optional: device 0 is used by default. */
+int cx_init(int device);
+
+/* Bytes of one row of `k` values of `type` (src/ops.rs:462:
+ * k / valores_por_bloque * bytes_por_bloque). 0 if the type is unknown or k
+ * is not a multiple of the block. */
+size_t cx_row_bytes(int type, size_t k);
+/* Sub-block the activation is quantized with for `type`
+ * (src/quant.rs:213-219); 0 = none. */
+int cx_sub_block(int type);
+
+/* ===================================================== 1. kernel contract
+ * float kernel(const u8 *bloques, const i8 *xq, const f32 *xe, const f32 *xs,
+ *              size_t n_bloques)
+ * One row of n_bloques super-blocks against an i8 activation with one f32
+ * scale xe and one f32 sum xs per sub-block. HOST pointers; runs the same
+ * GEMV kernel as cx_gemv on one row. Replace, one for one:
+ *   cx_dot_q2k_i8 <- cosxamix_q2k_{asm,c,zig} / q2k::dot (src/kernels/q2k.rs:153-185,262-292)
+ *   cx_dot_q3k_i8 <- cosxamix_q3k_{c,completo} / kernels::dot_q3k_i8 (src/kernels/mod.rs:416-446)
+ *   cx_dot_q4k_i8 <- kernels::dot_q4k_i8 (src/kernels/mod.rs:347-400); the asm
+ *                    cosxamix_q4k_completo contract with acc[16] is
+ *                    subsumed: this returns the reduced f32.
+ *   cx_dot_q5k_i8 <- cosxamix_q5k_{asm,c,zig} / kernels::dot_q5k_i8 (src/kernels/q5k.rs:35, mod.rs:480-493)
+ *   cx_dot_q6k_i8 <- kernels::dot_q6k_i8 (src/kernels/mod.rs:453-473)
+ */
+float cx_dot_q2k_i8(const uint8_t *bloques, const int8_t *xq, const float *xe,
+                    const float *xs, size_t n_bloques);
+float cx_dot_q3k_i8(const uint8_t *bloques, const int8_t *xq, const float *xe,
+                    const float *xs, size_t n_bloques);
+float cx_dot_q4k_i8(const uint8_t *bloques, const int8_t *xq, const float *xe,
+                    const float *xs, size_t n_bloques);
+float cx_dot_q5k_i8(const uint8_t *bloques, const int8_t *xq, const float *xe,
+                    const float *xs, size_t n_bloques);
+float cx_dot_q6k_i8(const uint8_t *bloques, const int8_t *xq, const float *xe,
+                    const float *xs, size_t n_bloques);
+
+/* ============================================================ 2. operators
+ * All pointers are DEVICE pointers. */
+
+/* ops::cuantizar_i8_en + the per-sub-block sums (src/ops.rs:178-198,
+ * 472-483), applied to `rows` rows of `k` values: xq[rows*k],
+ * xe/xs[rows*k/sub]. Bit-exact with the reference. */
+int cx_quantize_act(const float *x, size_t rows, size_t k, int sub,
+                    int8_t *xq, float *xe, float *xs, void *stream);
+
+/* y[r] = row r of W (n rows, GGUF raw bytes) . activation, for r < n.
+ * The per-row fused dot of ops::matmul_i8_fusionado with m = 1
+ * (src/ops.rs:435-522). Q2_K, Q3_K, Q4_K, Q5_K, Q6_K. */
+int cx_gemv(int type, const uint8_t *w, size_t n, size_t k, const int8_t *xq,
+            const float *xe, const float *xs, float *y, void *stream);
+
+/* Test hook on the GEMV kernel: writes the integer per-sub-block sums that
+ * the kernel's lanes form (out[n][k/sub]) — the E_j of
+ * src/kernels/scalar.rs:147-166 (Q3_K: the +4-biased sum, scalar.rs:262-270;
+ * Q6_K: unsigned 0..63). No counterpart in the reference. */
+int cx_gemv_subsums(int type, const uint8_t *w, size_t n, size_t k,
+                    const int8_t *xq, const float *xe, const float *xs,
+                    int32_t *out, void *stream);
+
+/* quant::cuantizar_bloques for the k-quants (src/quant.rs:744-805 ->
+ * src/quant_kquants.rs:160-399): n f32 values (n % 256 == 0) -> GGUF blocks,
+ * one GPU thread per 256-value block. Q2_K, Q3_K, Q4_K, Q5_K. The same bytes
+ * as the reference's quantizers for the same input. */
+int cx_quantize_blocks(int type, const float *x, size_t n, uint8_t *out,
+                       void *stream);
+
+/* ops::matmul_auto (src/ops.rs:1056-1093): dst[m,n] = lhs[m,k] . W[n,k]^T,
+ * lhs/dst f32 row-major, W GGUF raw rows. Quantizes lhs internally. */
+int cx_matmul_auto(size_t m, size_t k, size_t n, const float *lhs,
+                   const uint8_t *w, int type, float *dst, void *stream);
+
+/* ops::matmul_varias_una_fila (src/ops.rs:895-1009): dsts[i] = x . W_i^T for
+ * `count` matrices sharing one activation vector of length k; one
+ * quantization per sub size and one launch per type. Bit-identical to
+ * `count` separate cx_matmul_auto(1, ...) calls (src/ops.rs:1614-1670).
+ * The arrays are host arrays of device pointers. */
+int cx_matmul_multi_1row(const float *x, size_t k, size_t count,
+                         const uint8_t *const *w, const int *types,
+                         const size_t *ns, float *const *dsts, void *stream);
+
+/* kernels::rmsnorm (src/kernels/mod.rs:511-536; spec scalar.rs:36-54, f64
+ * accumulation), over `rows` rows of n. */
+int cx_rmsnorm(float *out, const float *in, const float *w, size_t rows,
+               size_t n, float eps, void *stream);
+
+/* kernels::silu (src/kernels/mod.rs:495-509): out = x / (1 + exp(-x)). */
+int cx_silu(float *out, const float *in, size_t n, void *stream);
+
+/* ops::frecuencias_rope (src/ops.rs:1108-1129) — HOST arrays of ctx*hd/2. */
+int cx_rope_tables(size_t head_dim, float base, size_t ctx, float *cos_host,
+                   float *sin_host);
+
+/* ops::rope (src/ops.rs:1150-1193), split-half rotation in place.
+ * x[tokens][heads*head_dim]; cos_t/sin_t device tables of ctx*head_dim/2. */
+int cx_rope(float *x, size_t tokens, size_t heads, size_t head_dim,
+            const float *cos_t, const float *sin_t, size_t ctx, size_t pos,
+            void *stream);
+
+/* ops::softmax (src/ops.rs:1206-1230), rows of `width` in place. */
+int cx_softmax(float *x, size_t len, size_t width, void *stream);
+
+/* ops::atencion (src/ops.rs:1258-1325): causal GQA. q[tokens][H*hd],
+ * k/v[total][Hkv*hd], out[tokens][H*hd]. */
+int cx_attention(const float *q, const float *k, const float *v, size_t tokens,
+                 size_t total, size_t heads, size_t kv_heads, size_t head_dim,
+                 float *out, void *stream);
+
+/* sampler::argmax (src/sampler.rs:129-137): first index of the max;
+ * *out is a DEVICE uint32. */
+int cx_argmax(const float *v, size_t n, uint32_t *out, void *stream);
+
+/* ================================================================ 3. model */
+
+/* forward::Config (src/forward.rs:36-55) */
+typedef struct {
+  uint32_t layers, dim, heads, kv_heads, ffn, vocab, ctx;
+  float eps, rope_base;
+} cx_config;
+
+typedef struct cx_model cx_model;
+typedef struct cx_cache cx_cache;
+
+/* A Qwen2-architecture model with daiss-style seeded random weights
+ * (src/daiss.rs:236-303 tensors, 317-379 RNG, 396-407 init, 494-586 write),
+ * generated directly in HBM. Linear weights in `linear_type`, ffn_down in
+ * `down_type`, output.weight in `out_type`; token_embd, norms and q/k/v
+ * biases F32. The reference writes a GGUF and opens it with Modelo::abrir
+ * (src/forward.rs:187-266); here the tensors are made where they are used. */
+int cx_model_create_daiss(const cx_config *cfg, int linear_type, int down_type,
+                          int out_type, uint64_t seed, cx_model **out);
+void cx_model_free(cx_model *m);
+int cx_model_config(const cx_model *m, cx_config *out);
+
+/* Tensor table, for mirroring the model on the host: names as in GGUF
+ * (src/daiss.rs:236-303), dims[0] = row width, dims[1] = rows. */
+int cx_model_tensor_count(const cx_model *m);
+int cx_model_tensor_info(const cx_model *m, int idx, char *name,
+                         size_t name_cap, int *type, uint64_t dims[2],
+                         size_t *bytes);
+int cx_model_tensor_copy(const cx_model *m, int idx, void *host, size_t bytes);
+/* Device address of a tensor's bytes (read-only view, owned by the model). */
+const void *cx_model_tensor_data(const cx_model *m, int idx);
+/* Bytes of weights streamed per decode token (all matrices + one embedding
+ * row); the algorithmic traffic of one token without the KV reads. */
+size_t cx_model_weight_bytes(const cx_model *m);
+
+/* forward::Cache (src/forward.rs:62-137), with room for `cap` tokens. */
+int cx_cache_new(cx_model *m, size_t cap, cx_cache **out);
+size_t cx_cache_len(const cx_cache *c);
+int cx_cache_truncate(cx_cache *c, size_t n);
+void cx_cache_clear(cx_cache *c);
+void cx_cache_free(cx_cache *c);
+
+/* Modelo::forward (src/forward.rs:375-505): appends `t` tokens to the cache
+ * and gives the logits of the last one (HOST buffer of vocab floats, may be
+ * NULL) and its argmax (may be NULL). */
+int cx_forward(cx_model *m, cx_cache *c, const uint32_t *toks, size_t t,
+               float *logits_host, uint32_t *argmax_out);
+
+/* Modelo::generar (src/forward.rs:533-559) with a greedy sampler
+ * (src/sampler.rs:65-66): prefill `prompt`, then up to max_new tokens.
+ * `eos` stops generation like Modelo::fin (pass UINT32_MAX for none).
+ * out[] gets the tokens, *n_out how many. If step_ms is not NULL it gets
+ * max_new per-token decode times (ms, measured with HIP events). */
+int cx_generate(cx_model *m, cx_cache *c, const uint32_t *prompt, size_t n,
+                size_t max_new, uint32_t eos, uint32_t *out, size_t *n_out,
+                float *step_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
