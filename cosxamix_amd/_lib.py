@@ -58,6 +58,7 @@ SIGNATURES = {
     "cx_rope": (C.c_int, [_vp, _sz, _sz, _sz, _vp, _vp, _sz, _sz, _vp]),
     "cx_softmax": (C.c_int, [_vp, _sz, _sz, _vp]),
     "cx_attention": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp]),
+    "cx_attention_decode": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, C.c_int, _vp, _vp]),
     "cx_argmax": (C.c_int, [_vp, _sz, _vp, _vp]),
     "cx_model_create_daiss": (C.c_int, [C.POINTER(CxConfig), C.c_int, C.c_int, C.c_int,
                                         C.c_uint64, C.POINTER(_vp)]),
@@ -95,6 +96,16 @@ def load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} is missing: build it with `python cosxamix_amd/build.py` "
                           "or __graft_entry__.build(); there is no CPU fallback")
+    # One process can hold only one ROCm runtime instance. PyTorch's wheel
+    # bundles its own libamdhip64 (SONAME libamdhip64.so.7, the same as
+    # /opt/rocm's); loading torch first makes this library bind to that copy,
+    # so torch tensors, streams and graphs share the runtime with our kernels.
+    # Loaded the other way round, torch would bring a second copy that can no
+    # longer acquire the GPU.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

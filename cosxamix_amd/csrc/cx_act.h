@@ -40,9 +40,16 @@ __device__ inline void cx_quant_sub(const float (&v)[SUB], int8_t* q, float* xe,
   *xs = (float)s;
 }
 
-// kernels::silu (src/kernels/scalar.rs:63-67) times up (src/forward.rs:483-487)
+#include "cx_expf.h"
+
+// kernels::silu (src/kernels/scalar.rs:63-67) with the reference's exp
+// (glibc expf, reproduced bit for bit by cx_expf): SiLU feeds an i8
+// quantization whose rounding a one-ulp difference can flip.
+__device__ inline float cx_silu1(float x) { return x / (1.0f + cx_expf(-x)); }
+
+// silu(gate) * up (src/forward.rs:483-487)
 __device__ inline float cx_swiglu(float g, float u) {
-  float a = g / (1.0f + expf(-g));
+  float a = cx_silu1(g);
   return a * u;
 }
 

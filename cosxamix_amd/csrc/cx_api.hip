@@ -264,6 +264,40 @@ extern "C" int cx_attention(const float* q, const float* k, const float* v, size
   return cx_launch_attention(q, k, v, tokens, total, heads, kv_heads, hd, out, STREAM(stream));
 }
 
+extern "C" int cx_attention_decode(const float* q, const float* k, const float* v, size_t total,
+                                   size_t heads, size_t kvh, size_t hd, int mode, float* out,
+                                   void* stream) {
+  CX_REQUIRE(q && k && v && out && total > 0, "attention_decode: bad arguments");
+  CX_REQUIRE(mode >= 0 && mode <= 2, "attention_decode: mode %d", mode);
+  CX_REQUIRE(mode != 1 || total <= CX_ATT_EXACT_MAX, "attention_decode: exact mode up to %d",
+             CX_ATT_EXACT_MAX);
+  // the decode kernels pick their path from the cache capacity they were
+  // sized for: the exact path for <= CX_ATT_EXACT_MAX, split-K above
+  size_t cap = total;
+  if (mode == 2 && cap <= CX_ATT_EXACT_MAX) cap = CX_ATT_EXACT_MAX + 1;
+  if (mode == 1) cap = total;
+  const size_t ns = cx_attn_splits(cap);
+  const size_t bytes = 256 + ns * heads * 8 + ns * heads * hd * 4 + heads * cap * 4;
+  void* sp = nullptr;
+  int rc = cx_scratch_reserve(bytes, &sp);
+  if (rc) return rc;
+  uint8_t* b = (uint8_t*)sp;
+  cx_dstate* st = (cx_dstate*)b;
+  float* pm = (float*)(b + 256);
+  float* pl = pm + ns * heads;
+  float* po = pl + ns * heads;
+  float* sc = po + ns * heads * hd;
+  hipStream_t s = STREAM(stream);
+  // the kernels read the position from device state: pos = total - 1
+  cx_dstate h{(uint32_t)(total - 1), 0u, (uint32_t)cap, 0u};
+  CX_HIP(hipMemcpyAsync(st, &h, sizeof h, hipMemcpyHostToDevice, s));
+  rc = cx_launch_attn_decode(q, k, v, (uint32_t)heads, (uint32_t)kvh, (uint32_t)hd, st,
+                             (uint32_t)cap, pm, pl, po, sc, out, s);
+  if (rc) return rc;
+  CX_HIP(hipStreamSynchronize(s));  // the state lives in shared scratch
+  return CX_OK;
+}
+
 extern "C" int cx_argmax(const float* v, size_t n, uint32_t* out, void* stream) {
   return cx_launch_argmax_one(v, n, out, STREAM(stream));
 }
@@ -308,7 +342,8 @@ struct cx_cache {
   float* kv;        // [layers][2][cap][kvd]
   uint32_t* hist;   // tokens by position, cap + 1
   cx_dstate* st;
-  float *pm, *pl, *po;
+  float *pm, *pl, *po;  // split-K partials
+  float* sc;            // scores of the order-exact attention, heads x cap
   hipGraphExec_t exec;
   bool have_graph;
 };
@@ -534,7 +569,8 @@ extern "C" int cx_cache_new(cx_model* m, size_t cap, cx_cache** out) {
   const size_t ns = cx_attn_splits(cap);
   if (hipMalloc(&C->kv, (size_t)c.layers * 2 * cap * kvd * 4) || hipMalloc(&C->hist, (cap + 1) * 4) ||
       hipMalloc(&C->st, sizeof(cx_dstate)) || hipMalloc(&C->pm, ns * c.heads * 4) ||
-      hipMalloc(&C->pl, ns * c.heads * 4) || hipMalloc(&C->po, ns * c.heads * (c.dim / c.heads) * 4)) {
+      hipMalloc(&C->pl, ns * c.heads * 4) || hipMalloc(&C->po, ns * c.heads * (c.dim / c.heads) * 4) ||
+      hipMalloc(&C->sc, (size_t)c.heads * cap * 4)) {
     cx_cache_free(C);
     cx_set_error("cache: cannot allocate %zu tokens", cap);
     return CX_ENOMEM;
@@ -557,7 +593,7 @@ extern "C" void cx_cache_free(cx_cache* c) {
   (void)hipSetDevice(c->m->device);
   (void)hipStreamSynchronize(c->m->stream);
   if (c->have_graph) (void)hipGraphExecDestroy(c->exec);
-  void* bufs[] = {c->kv, c->hist, c->st, c->pm, c->pl, c->po};
+  void* bufs[] = {c->kv, c->hist, c->st, c->pm, c->pl, c->po, c->sc};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   delete c;
@@ -589,7 +625,7 @@ static int enqueue_step(cx_cache* C) {
                                 hd, C->st, s)))
       return rc;
     if ((rc = cx_launch_attn_decode(m->q, kc, vc, c.heads, c.kv_heads, hd, C->st, (uint32_t)C->cap,
-                                    C->pm, C->pl, C->po, m->att, s)))
+                                    C->pm, C->pl, C->po, C->sc, m->att, s)))
       return rc;
     cx_act plain{};
     plain.src = CX_ACT_PLAIN;

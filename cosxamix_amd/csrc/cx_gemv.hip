@@ -55,8 +55,8 @@ template <> struct KQ<CX_Q4_K> {
     r[0] = h.x; r[1] = h.y; r[2] = h.z; r[3] = h.w;
     r[4] = q.x; r[5] = q.y; r[6] = q.z; r[7] = q.w;
   }
-  __device__ static float term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg) {
+  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
+                               const float* xe, const float* xs, int32_t* dbg, float* to) {
     const int p = l >> 1, h = l & 1;
     const int4 xa = *reinterpret_cast<const int4*>(xb + 64 * p + 16 * h);
     const int4 xc = *reinterpret_cast<const int4*>(xb + 64 * p + 32 + 16 * h);
@@ -68,12 +68,12 @@ template <> struct KQ<CX_Q4_K> {
     e1 = dot4((r[5] >> 4) & M4, xc.y, e1);
     e1 = dot4((r[6] >> 4) & M4, xc.z, e1);
     e1 = dot4((r[7] >> 4) & M4, xc.w, e1);
-    return finish(r, h ? e0 : e1, h ? e1 : e0, 2 * p + h, xe, xs, dbg);
+    finish(r, h ? e0 : e1, h ? e1 : e0, 2 * p + h, xe, xs, dbg, to);
   }
   // shared with Q5_K: exchange, 6-bit scale unpack, the f32 term
   template <int N>
-  __device__ static float finish(const uint32_t (&r)[N], int send, int mine, int j,
-                                 const float* xe, const float* xs, int32_t* dbg) {
+  __device__ static void finish(const uint32_t (&r)[N], int send, int mine, int j,
+                                 const float* xe, const float* xs, int32_t* dbg, float* to) {
     const int e = mine + cx_xor1(send);
     // branch-free 6-bit unpack, the word form of src/kernels/x86.rs:437-447;
     // equal to quant::escala_y_minimo (src/quant.rs:108-117)
@@ -89,7 +89,7 @@ template <> struct KQ<CX_Q4_K> {
     }
     const float d = cx_h2f(r[0] & 0xFFFF), dm = cx_h2f(r[0] >> 16);
     if (dbg) dbg[j] = e;
-    return xe[j] * (d * (float)sc * (float)e - dm * (float)mn * xs[j]);
+    if (to) to[j] = xe[j] * (d * (float)sc * (float)e - dm * (float)mn * xs[j]);
   }
 };
 
@@ -107,8 +107,8 @@ template <> struct KQ<CX_Q5_K> {
     r[4] = q.x; r[5] = q.y; r[6] = q.z; r[7] = q.w;
     r[8] = qh.x; r[9] = qh.y; r[10] = qh.z; r[11] = qh.w;
   }
-  __device__ static float term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg) {
+  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
+                               const float* xe, const float* xs, int32_t* dbg, float* to) {
     const int p = l >> 1, h = l & 1;
     const int4 xa = *reinterpret_cast<const int4*>(xb + 64 * p + 16 * h);
     const int4 xc = *reinterpret_cast<const int4*>(xb + 64 * p + 32 + 16 * h);
@@ -124,7 +124,7 @@ template <> struct KQ<CX_Q5_K> {
       e0 = dot4(lo, xav[w], e0);
       e1 = dot4(hi, xcv[w], e1);
     }
-    return KQ<CX_Q4_K>::finish(r, h ? e0 : e1, h ? e1 : e0, 2 * p + h, xe, xs, dbg);
+    KQ<CX_Q4_K>::finish(r, h ? e0 : e1, h ? e1 : e0, 2 * p + h, xe, xs, dbg, to);
   }
 };
 
@@ -163,8 +163,8 @@ template <> struct KQ<CX_Q2_K> {
     r[2] = s[0]; r[3] = s[1]; r[4] = s[2]; r[5] = s[3];
     r[6] = *reinterpret_cast<const uint32_t*>(b + 80);
   }
-  __device__ static float term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg) {
+  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
+                               const float* xe, const float* xs, int32_t* dbg, float* to) {
     const int half = l >> 2, c = l & 3;
     int E[4];
 #pragma unroll
@@ -183,7 +183,10 @@ template <> struct KQ<CX_Q2_K> {
                             dm * (float)(sc0 >> 4) * xs[sw.s0]);
     float t1 = xe[sw.s1] * (d * (float)(sc1 & 0xF) * (float)sw.own1 -
                             dm * (float)(sc1 >> 4) * xs[sw.s1]);
-    return t0 + t1;
+    if (to) {
+      to[sw.s0] = t0;
+      to[sw.s1] = t1;
+    }
   }
 };
 
@@ -203,8 +206,8 @@ template <> struct KQ<CX_Q3_K> {
     r[6] = ld32u(b + 104);
     r[7] = (uint32_t)b[108] | ((uint32_t)b[109] << 8);
   }
-  __device__ static float term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg) {
+  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
+                               const float* xe, const float* xs, int32_t* dbg, float* to) {
     const int half = l >> 2, c = l & 3;
     int E[4];
 #pragma unroll
@@ -230,7 +233,10 @@ template <> struct KQ<CX_Q3_K> {
     const float sc0 = d * ((float)esc0 - 32.0f), sc1 = d * ((float)esc1 - 32.0f);
     float t0 = xe[sw.s0] * sc0 * ((float)sw.own0 - 4.0f * xs[sw.s0]);
     float t1 = xe[sw.s1] * sc1 * ((float)sw.own1 - 4.0f * xs[sw.s1]);
-    return t0 + t1;
+    if (to) {
+      to[sw.s0] = t0;
+      to[sw.s1] = t1;
+    }
   }
 };
 
@@ -249,8 +255,8 @@ template <> struct KQ<CX_Q6_K> {
     r[6] = ld32u(b + 192); r[7] = ld32u(b + 196); r[8] = ld32u(b + 200); r[9] = ld32u(b + 204);
     r[10] = (uint32_t)b[208] | ((uint32_t)b[209] << 8);
   }
-  __device__ static float term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg) {
+  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
+                               const float* xe, const float* xs, int32_t* dbg, float* to) {
     const int half = l >> 2, c = l & 3;
     int E[4];
 #pragma unroll
@@ -274,7 +280,10 @@ template <> struct KQ<CX_Q6_K> {
     const float sc0 = d * (float)e0, sc1 = d * (float)e1;
     float t0 = xe[sw.s0] * sc0 * ((float)sw.own0 - 32.0f * xs[sw.s0]);
     float t1 = xe[sw.s1] * sc1 * ((float)sw.own1 - 32.0f * xs[sw.s1]);
-    return t0 + t1;
+    if (to) {
+      to[sw.s0] = t0;
+      to[sw.s1] = t1;
+    }
   }
 };
 
@@ -302,7 +311,6 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
   using Q = KQ<T>;
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ double red[4];
-  __shared__ float partial[4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t row_in_wg = wave / P.waves_per_row, part = wave % P.waves_per_row;
@@ -352,30 +360,26 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
   }
   __syncthreads();
 
-  // 3. integer dots + the reference's per-sub-block f32 terms
-  float acc = 0.0f;
+  // 3. integer dots + the reference's per-sub-block f32 terms, staged in LDS
+  //    by sub-block index (every sub-block of the row is owned by one lane)
+  float* terms = ss + P.nsub + row_in_wg * P.nsub;
   constexpr int SPB = 256 / Q::SUB;  // sub-blocks per super-block
 #pragma unroll
   for (int it = 0; it < MAXIT; it++) {
     const uint32_t slot = s_begin + it * 64 + lane;
     const uint32_t blk = valid[it] ? (slot >> 3) : 0;
     int32_t* dbg = (P.dbg && valid[it]) ? P.dbg + (size_t)grow * P.nsub + blk * SPB : nullptr;
-    const float t = Q::term(regs[it], lane & 7, sq + blk * 256, se + blk * SPB, ss + blk * SPB, dbg);
-    acc += valid[it] ? t : 0.0f;
+    float* to = valid[it] ? terms + blk * SPB : nullptr;
+    Q::term(regs[it], lane & 7, sq + blk * 256, se + blk * SPB, ss + blk * SPB, dbg, to);
   }
-  acc = cx_wave_sum(acc);
+  __syncthreads();
 
-  // 4. waves of one row, summed in a fixed order
-  if (P.waves_per_row > 1) {
-    if (lane == 0) partial[wave] = acc;
-    __syncthreads();
-    if (part == 0) {
-      float s = partial[wave];
-      for (uint32_t p = 1; p < P.waves_per_row; p++) s += partial[wave + p];
-      acc = s;
-    }
-  }
+  // 4. the row's sum in the scalar spec's order: total = 0; total += term_s
+  //    for s = 0, 1, ... (src/kernels/scalar.rs:141-167), so a row's result
+  //    is bit-identical to the reference's scalar kernel.
   if (part == 0 && lane == 0 && row_ok) {
+    float acc = 0.0f;
+    for (uint32_t s = 0; s < P.nsub; s++) acc += terms[s];
     const cx_seg& S = P.seg[sg];
     if (P.epi == CX_EPI_ACCUM) {
       S.y[row] += acc;
@@ -404,7 +408,8 @@ int launch_t(GemvParams& P, uint32_t total_rows, hipStream_t s) {
   CX_REQUIRE(maxit, "gemv: row of %u values is too long", P.k);
   P.rows_per_wg = 4 / P.waves_per_row;
   const uint32_t grid = (total_rows + P.rows_per_wg - 1) / P.rows_per_wg;
-  const size_t lds = P.k + 8 * (size_t)P.nsub;
+  // activation (k + 8 * nsub) + one row of f32 terms per row of the workgroup
+  const size_t lds = P.k + 8 * (size_t)P.nsub + 4 * (size_t)P.nsub * P.rows_per_wg;
   switch (maxit) {
     case 1: hipLaunchKernelGGL((k_gemv<T, 1>), dim3(grid), dim3(256), lds, s, P); break;
     case 2: hipLaunchKernelGGL((k_gemv<T, 2>), dim3(grid), dim3(256), lds, s, P); break;

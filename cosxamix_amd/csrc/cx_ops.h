@@ -13,6 +13,10 @@ struct cx_dstate {
 };
 
 #define CX_ATT_MAX_TOTAL 16000  // general attention keeps scores in LDS
+// Decode attention runs in the reference's exact order (bit-identical) for
+// caches up to this many tokens, and as split-K ("flash decoding") above it,
+// where the sequential sums would dominate the step.
+#define CX_ATT_EXACT_MAX 4096
 
 int cx_launch_embed(const float* embd, uint32_t dim, const cx_dstate* st, const uint32_t* hist,
                     float* x, hipStream_t s);
@@ -22,7 +26,8 @@ int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float
 size_t cx_attn_splits(size_t cap);
 int cx_launch_attn_decode(const float* q, const float* kc, const float* vc, uint32_t heads,
                           uint32_t kvh, uint32_t hd, const cx_dstate* st, uint32_t cap,
-                          float* pm, float* pl, float* po, float* out, hipStream_t s);
+                          float* pm, float* pl, float* po, float* sc, float* out,
+                          hipStream_t s);
 int cx_launch_attention(const float* q, const float* k, const float* v, size_t tokens,
                         size_t total, size_t heads, size_t kvh, size_t hd, float* out,
                         hipStream_t s);

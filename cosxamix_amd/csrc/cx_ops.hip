@@ -8,6 +8,7 @@
 //   silu                         src/kernels/scalar.rs:63-67
 //   argmax + token loop state    src/sampler.rs:129-137, src/forward.rs:544-557
 #include "cx_ops.h"
+#include "cx_act.h"
 
 namespace {
 
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* q, const float*
   for (uint32_t h = wave; h < per; h += 4) {
     const float s = lane < (int)np ? ssc[h * ATT_P + lane] : -INFINITY;
     const float m = cx_wave_max(s);
-    const float e = lane < (int)np ? expf(s - m) : 0.0f;
+    const float e = lane < (int)np ? cx_expf(s - m) : 0.0f;
     const float l = cx_wave_sum(e);
     if (lane < (int)np) ssc[h * ATT_P + lane] = e;
     if (lane == 0) {
@@ -129,14 +130,39 @@ __global__ void k_attn_combine(const float* pm, const float* pl, const float* po
   float M = -INFINITY;
   for (uint32_t s = 0; s < ns; s++) M = fmaxf(M, pm[(size_t)s * heads + h]);
   float L = 0.0f;
-  for (uint32_t s = 0; s < ns; s++) L += pl[(size_t)s * heads + h] * expf(pm[(size_t)s * heads + h] - M);
+  for (uint32_t s = 0; s < ns; s++) L += pl[(size_t)s * heads + h] * cx_expf(pm[(size_t)s * heads + h] - M);
   const float inv = 1.0f / L;
   for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
     float o = 0.0f;
     for (uint32_t s = 0; s < ns; s++)
-      o += po[((size_t)s * heads + h) * hd + d] * expf(pm[(size_t)s * heads + h] - M);
+      o += po[((size_t)s * heads + h) * hd + d] * cx_expf(pm[(size_t)s * heads + h] - M);
     out[h * hd + d] = o * inv;
   }
+}
+
+// softmax of one row x[0..n) whose max is mx, in place, in the reference's
+// order (src/ops.rs:1211-1229): non-finite max -> uniform; e = exp(x - max);
+// the sum accumulated sequentially from 0; x = e * (1 / sum). 256 threads.
+__device__ void seq_softmax_inplace(float* x, uint32_t n, float mx, float* red) {
+  const int tid = threadIdx.x;
+  if (!isfinite(mx)) {
+    const float pr = 1.0f / (float)n;
+    for (uint32_t p = tid; p < n; p += 256) x[p] = pr;
+    __syncthreads();
+    return;
+  }
+  for (uint32_t p = tid; p < n; p += 256) x[p] = cx_expf(x[p] - mx);
+  __syncthreads();
+  if (tid == 0) {
+    float tot = 0.0f;
+#pragma unroll 8
+    for (uint32_t p = 0; p < n; p++) tot += x[p];
+    red[0] = 1.0f / tot;
+  }
+  __syncthreads();
+  const float inv = red[0];
+  for (uint32_t p = tid; p < n; p += 256) x[p] = x[p] * inv;
+  __syncthreads();
 }
 
 // ---------------------------------------------- general causal attention
@@ -170,23 +196,79 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   __syncthreads();
-  float tot = 0.0f;
-  for (uint32_t p = tid; p < vis; p += 256) {
-    const float e = expf(sc[p] - mx);
-    sc[p] = e;
-    tot += e;
-  }
-  tot = cx_wave_sum(tot);
-  if (lane == 0) red[wave] = tot;
-  __syncthreads();
-  tot = ((red[0] + red[1]) + red[2]) + red[3];
-  const float inv = 1.0f / tot;
-  for (uint32_t p = tid; p < vis; p += 256) sc[p] = sc[p] * inv;
-  __syncthreads();
+  seq_softmax_inplace(sc, vis, mx, red);
   for (uint32_t d = tid; d < hd; d += 256) {
     float o = 0.0f;
     for (uint32_t p = 0; p < vis; p++) o += sc[p] * v[(size_t)p * wkv + g * hd + d];
     out[(size_t)t * wq + h * hd + d] = o;
+  }
+}
+
+// ------------------------------------------- order-exact decode attention
+// The decode step's attention in the reference's own order, for contexts up
+// to CX_ATT_EXACT_MAX. Scores: one thread per (head, position), the
+// sequential dot of src/kernels/scalar.rs:16-23 times 1/sqrt(hd), written to
+// sc[head][pos]. Then one workgroup per head: exact max, e = exp(s - max)
+// (glibc's expf), the sequential sum, p = e * (1/sum) (src/ops.rs:1218-1229),
+// and out[d] = sum over p of prob_p * v_p[d] in position order
+// (src/ops.rs:1316-1321). Bit-identical to the scalar reference.
+__global__ __launch_bounds__(256) void k_attn_scores(const float* q, const float* kc,
+                                                     uint32_t heads, uint32_t kvh, uint32_t hd,
+                                                     const cx_dstate* st, float scale,
+                                                     float* sc, uint32_t cap) {
+  const uint32_t total = st->pos + 1;
+  const uint32_t p = blockIdx.x * 256 + threadIdx.x, h = blockIdx.y;
+  if (p >= total) return;
+  const uint32_t g = h / (heads / kvh);
+  const float4* qh = reinterpret_cast<const float4*>(q + h * hd);
+  const float4* kp = reinterpret_cast<const float4*>(kc + (size_t)p * kvh * hd + g * hd);
+  float s = 0.0f;
+  for (uint32_t d = 0; d < hd / 4; d++) {
+    const float4 a = qh[d], b = kp[d];
+    s += a.x * b.x;
+    s += a.y * b.y;
+    s += a.z * b.z;
+    s += a.w * b.w;
+  }
+  sc[(size_t)h * cap + p] = s * scale;
+}
+
+__global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
+                                                  uint32_t heads, uint32_t kvh, uint32_t hd,
+                                                  const cx_dstate* st, uint32_t cap,
+                                                  float* out) {
+  extern __shared__ __align__(16) float e[];
+  __shared__ float red[4];
+  const uint32_t total = st->pos + 1, h = blockIdx.x, g = h / (heads / kvh);
+  const float* sc = sc_all + (size_t)h * cap;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float mx = -INFINITY;
+  for (uint32_t p = tid; p < total; p += 256) {
+    const float s = sc[p];
+    e[p] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = cx_wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  seq_softmax_inplace(e, total, mx, red);
+  const size_t kvd = (size_t)kvh * hd;
+  for (uint32_t d = tid; d < hd; d += 256) {
+    const float* vp = vc + g * hd + d;
+    float o = 0.0f;
+    uint32_t p = 0;
+    for (; p + 4 <= total; p += 4) {  // loads hoisted, adds in position order
+      const float v0 = vp[p * kvd], v1 = vp[(p + 1) * kvd], v2 = vp[(p + 2) * kvd],
+                  v3 = vp[(p + 3) * kvd];
+      o += e[p] * v0;
+      o += e[p + 1] * v1;
+      o += e[p + 2] * v2;
+      o += e[p + 3] * v3;
+    }
+    for (; p < total; p++) o += e[p] * vp[p * kvd];
+    out[h * hd + d] = o;
   }
 }
 
@@ -209,7 +291,7 @@ __global__ __launch_bounds__(256) void k_softmax(float* x, uint32_t width) {
   }
   float tot = 0.0f;
   for (uint32_t i = tid; i < width; i += 256) {
-    const float e = expf(row[i] - mx);
+    const float e = cx_expf(row[i] - mx);
     row[i] = e;
     tot += e;
   }
@@ -224,7 +306,7 @@ __global__ __launch_bounds__(256) void k_softmax(float* x, uint32_t width) {
 __global__ void k_silu(float* out, const float* in, size_t n) {
   for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
     const float x = in[i];
-    out[i] = x / (1.0f + expf(-x));
+    out[i] = cx_silu1(x);
   }
 }
 
@@ -367,12 +449,23 @@ size_t cx_attn_splits(size_t cap) { return (cap + ATT_P - 1) / ATT_P; }
 
 int cx_launch_attn_decode(const float* q, const float* kc, const float* vc, uint32_t heads,
                           uint32_t kvh, uint32_t hd, const cx_dstate* st, uint32_t cap,
-                          float* pm, float* pl, float* po, float* out, hipStream_t s) {
+                          float* pm, float* pl, float* po, float* sc, float* out,
+                          hipStream_t s) {
   CX_REQUIRE(kvh && heads % kvh == 0 && heads / kvh <= ATT_MAXG, "attention: %u heads / %u groups",
              heads, kvh);
+  CX_REQUIRE(hd % 4 == 0, "attention: head_dim %u must be a multiple of 4", hd);
+  const float scale = 1.0f / sqrtf((float)hd);
+  if (cap <= CX_ATT_EXACT_MAX) {
+    hipLaunchKernelGGL(k_attn_scores, dim3((cap + 255) / 256, heads), dim3(256), 0, s, q, kc,
+                       heads, kvh, hd, st, scale, sc, cap);
+    CX_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_attn_seq, dim3(heads), dim3(256), cap * sizeof(float), s, vc, sc, heads,
+                       kvh, hd, st, cap, out);
+    CX_HIP(hipGetLastError());
+    return CX_OK;
+  }
   const uint32_t ns = (uint32_t)cx_attn_splits(cap), per = heads / kvh;
   const size_t lds = sizeof(float) * (per * hd + ATT_P * (hd + 1) + per * ATT_P);
-  const float scale = 1.0f / sqrtf((float)hd);
   hipLaunchKernelGGL(k_attn_split, dim3(ns, kvh), dim3(256), lds, s, q, kc, vc, heads, kvh, hd,
                      st, scale, pm, pl, po, ns);
   CX_HIP(hipGetLastError());

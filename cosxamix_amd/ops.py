@@ -171,6 +171,15 @@ def atencion(q, k, v, forma, salida) -> None:
           dim_cabeza, _ptr(salida), _stream(), what="atencion")
 
 
+def atencion_decode(q, k, v, forma, salida, modo: int = 0) -> None:
+    """ops::atencion at tokens = 1 with the model's decode kernels.
+    forma = (total, cabezas, cabezas_kv, dim_cabeza); modo 0 auto, 1 order-
+    exact, 2 split-K."""
+    total, cabezas, cabezas_kv, dim_cabeza = forma
+    _call(_lib.cx_attention_decode, _ptr(q), _ptr(k), _ptr(v), total, cabezas, cabezas_kv,
+          dim_cabeza, modo, _ptr(salida), _stream(), what="atencion_decode")
+
+
 def argmax(v: torch.Tensor) -> int:
     """sampler::argmax (src/sampler.rs:129-137)."""
     out = torch.empty(1, dtype=torch.int32, device=v.device)

@@ -250,6 +250,29 @@ def test_softmax_silu_argmax(cx, dev):
     assert ops.argmax(T(big, dev)) == 100
 
 
+@pytest.mark.parametrize("heads,kvh", [(16, 2), (32, 8), (4, 2)])
+def test_decode_attention_paths(cx, dev, heads, kvh):
+    """The model's decode attention: order-exact mode bit-identical to the
+    oracle (src/ops.rs:1258-1325); split-K mode within f32 rounding."""
+    ops, _ = cx
+    hd = 128
+    for total in (1, 2, 37, 63, 64, 65, 100, 150, 640, 1000):
+        rng = np.random.default_rng(total + heads)
+        q = rng.normal(0, 1, heads * hd).astype(np.float32)
+        k = rng.normal(0, 1, total * kvh * hd).astype(np.float32)
+        v = rng.normal(0, 1, total * kvh * hd).astype(np.float32)
+        want = O.attention(q, k, v, 1, total, heads, kvh, hd)
+        for mode in (1, 2):
+            out = torch.empty(heads * hd, dtype=torch.float32, device=dev)
+            ops.atencion_decode(T(q, dev), T(k, dev), T(v, dev), (total, heads, kvh, hd), out, mode)
+            got = out.cpu().numpy()
+            if mode == 1:
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (total, mode)
+            else:
+                assert np.allclose(got, want, rtol=1e-5, atol=1e-6), (
+                    total, float(np.max(np.abs(got - want))))
+
+
 def test_attention_matches_oracle_and_properties(cx, dev):
     ops, _ = cx
     heads, kvh, hd = 16, 2, 128
