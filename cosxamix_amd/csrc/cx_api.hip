@@ -47,7 +47,8 @@ int cx_scratch_reserve(size_t bytes, void** out) {
     return CX_EHIP;
   }
   if (L->scratch_bytes < bytes) {
-    CX_HIP(hipStreamSynchronize(L->stream));
+    // the old buffer may still be read by work on any stream of the device
+    CX_HIP(hipDeviceSynchronize());
     if (L->scratch) CX_HIP(hipFree(L->scratch));
     L->scratch = nullptr;
     L->scratch_bytes = 0;
@@ -101,11 +102,7 @@ static float dot_host(int type, const uint8_t* b, const int8_t* xq, const float*
     return NAN;
   }
   cx_seg seg{d, (float*)(d + o_y), nullptr, 1};
-  cx_act act{};
-  act.src = CX_ACT_QUANTIZED;
-  act.xq = (const int8_t*)(d + o_x);
-  act.xe = (const float*)(d + o_e);
-  act.xs = (const float*)(d + o_s);
+  cx_qact act{(const int8_t*)(d + o_x), (const float*)(d + o_e), (const float*)(d + o_s)};
   if (cx_launch_gemv(type, &seg, 1, (uint32_t)k, act, CX_EPI_STORE, nullptr, s)) return NAN;
   float y = NAN;
   if (hipMemcpyAsync(&y, d + o_y, 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
@@ -144,14 +141,7 @@ static int gemv_quantized(int type, const uint8_t* w, size_t n, size_t k, const 
                           hipStream_t s) {
   CX_REQUIRE(n < (1u << 31) && k < (1u << 31), "gemv: shape too large");
   cx_seg seg{w, y, nullptr, (uint32_t)n};
-  cx_act act{};
-  act.src = CX_ACT_QUANTIZED;
-  act.xq = xq;
-  act.xe = xe;
-  act.xs = xs;
-  if (dbg) {  // the debug path writes sums only; point y at a throwaway row
-    CX_REQUIRE(y, "gemv: null output");
-  }
+  cx_qact act{xq, xe, xs};
   return cx_launch_gemv(type, &seg, 1, (uint32_t)k, act, CX_EPI_STORE, dbg, s);
 }
 
@@ -173,21 +163,61 @@ extern "C" int cx_quantize_blocks(int type, const float* x, size_t n, uint8_t* o
   return cx_quantize_blocks_dev(type, x, n, out, STREAM(stream));
 }
 
+// The i8 activation of `rows` rows of k values in the library's scratch:
+// xq (rows*k bytes), xe and xs (rows*k/sub floats each), for each sub-block
+// size asked for. The scratch is shared by every call on the device, so
+// these operators are stream-ordered with each other only on one stream.
+namespace {
+struct QuantScratch {
+  int8_t* xq = nullptr;
+  float* xe = nullptr;
+  float* xs = nullptr;
+  cx_qact row(size_t f, size_t k, int sub) const {
+    const size_t ns = k / sub;
+    return cx_qact{xq + f * k, xe + f * ns, xs + f * ns};
+  }
+};
+}  // namespace
+
+static int quant_scratch(size_t rows, size_t k, QuantScratch* q16, QuantScratch* q32) {
+  auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t xq_b = up(rows * k);
+  auto part = [&](int sub) { return xq_b + 2 * up(rows * (k / sub) * 4); };
+  void* sp = nullptr;
+  int rc = cx_scratch_reserve((q16 ? part(16) : 0) + (q32 ? part(32) : 0), &sp);
+  if (rc) return rc;
+  uint8_t* p = (uint8_t*)sp;
+  auto carve = [&](QuantScratch* q, int sub) {
+    const size_t eb = up(rows * (k / sub) * 4);
+    q->xq = (int8_t*)p;
+    q->xe = (float*)(p + xq_b);
+    q->xs = (float*)(p + xq_b + eb);
+    p += part(sub);
+  };
+  if (q16) carve(q16, 16);
+  if (q32) carve(q32, 32);
+  return CX_OK;
+}
+
 extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, const uint8_t* w,
                               int type, float* dst, void* stream) {
   CX_REQUIRE(cx_is_kquant(type), "matmul_auto: type %d has no k-quant path here", type);
   CX_REQUIRE(k % 256 == 0, "matmul_auto: a row of %zu is not a multiple of the block of 256", k);
   CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
   CX_REQUIRE(n < (1u << 31) && k < (1u << 31), "matmul_auto: shape too large");
-  // Each output row is the fused GEMV of its own input row, with the
-  // activation quantized inside the kernel (ops.rs:469-483 per row). Row by
-  // row is exactly the reference's "one row equals a batch" (ops.rs:1364-1393).
+  if (!m || !n) return CX_OK;
+  // Every input row is quantized once (ops.rs:469-483), then each output row
+  // is the fused GEMV of its own input row: row by row is exactly the
+  // reference's "one row equals a batch" (ops.rs:1364-1393).
+  QuantScratch q;
+  const int sub = cx_sub(type);
+  int rc = quant_scratch(m, k, sub == 16 ? &q : nullptr, sub == 32 ? &q : nullptr);
+  if (!rc) rc = cx_launch_quantize(lhs, m, k, sub, q.xq, q.xe, q.xs, STREAM(stream));
+  if (rc) return rc;
   for (size_t f = 0; f < m; f++) {
     cx_seg seg{w, dst + f * n, nullptr, (uint32_t)n};
-    cx_act act{};
-    act.src = CX_ACT_PLAIN;
-    act.x = lhs + f * k;
-    int rc = cx_launch_gemv(type, &seg, 1, (uint32_t)k, act, CX_EPI_STORE, nullptr, STREAM(stream));
+    rc = cx_launch_gemv(type, &seg, 1, (uint32_t)k, q.row(f, k, cx_sub(type)), CX_EPI_STORE,
+                        nullptr, STREAM(stream));
     if (rc) return rc;
   }
   return CX_OK;
@@ -198,10 +228,22 @@ extern "C" int cx_matmul_multi_1row(const float* x, size_t k, size_t count,
                                     float* const* dsts, void* stream) {
   CX_REQUIRE(x && w && types && ns && dsts, "multi: null pointer");
   CX_REQUIRE(k % 256 == 0, "multi: a row of %zu is not a multiple of 256", k);
+  // the row quantized once per sub-block size in use (16 and/or 32)
+  bool need16 = false, need32 = false;
+  for (size_t i = 0; i < count; i++) {
+    CX_REQUIRE(cx_is_kquant(types[i]), "multi: type %d has no k-quant path here", types[i]);
+    (cx_sub(types[i]) == 16 ? need16 : need32) = true;
+  }
+  QuantScratch q16, q32;
+  int rc = quant_scratch(1, k, need16 ? &q16 : nullptr, need32 ? &q32 : nullptr);
+  if (rc) return rc;
+  if (need16 && (rc = cx_launch_quantize(x, 1, k, 16, q16.xq, q16.xe, q16.xs, STREAM(stream))))
+    return rc;
+  if (need32 && (rc = cx_launch_quantize(x, 1, k, 32, q32.xq, q32.xe, q32.xs, STREAM(stream))))
+    return rc;
   std::vector<bool> done(count, false);
   for (size_t i = 0; i < count; i++) {
     if (done[i]) continue;
-    CX_REQUIRE(cx_is_kquant(types[i]), "multi: type %d has no k-quant path here", types[i]);
     cx_seg segs[4];
     int nseg = 0;
     for (size_t j = i; j < count && nseg < 4; j++) {
@@ -209,11 +251,9 @@ extern "C" int cx_matmul_multi_1row(const float* x, size_t k, size_t count,
       segs[nseg++] = cx_seg{w[j], dsts[j], nullptr, (uint32_t)ns[j]};
       done[j] = true;
     }
-    cx_act act{};
-    act.src = CX_ACT_PLAIN;
-    act.x = x;
-    int rc = cx_launch_gemv(types[i], segs, nseg, (uint32_t)k, act, CX_EPI_STORE, nullptr,
-                            STREAM(stream));
+    const QuantScratch& q = cx_sub(types[i]) == 16 ? q16 : q32;
+    rc = cx_launch_gemv(types[i], segs, nseg, (uint32_t)k, q.row(0, k, cx_sub(types[i])),
+                        CX_EPI_STORE, nullptr, STREAM(stream));
     if (rc) return rc;
   }
   return CX_OK;
@@ -334,6 +374,9 @@ struct cx_model {
   float *x, *q, *k, *v, *att, *g, *u, *logits, *apv;
   uint32_t* api;
   uint32_t* amax_out;
+  // the i8 activation of the next GEMV: max(dim, ffn) values, sub >= 16
+  int8_t* xq;
+  float *xe, *xs;
 };
 
 struct cx_cache {
@@ -354,9 +397,11 @@ extern "C" void cx_model_free(cx_model* m) {
   if (!m) return;
   (void)hipSetDevice(m->device);
   (void)hipStreamSynchronize(m->stream);
-  float* bufs[] = {m->x, m->q, m->k, m->v, m->att, m->g, m->u, m->logits, m->apv, m->cos_t, m->sin_t};
+  float* bufs[] = {m->x,      m->q,   m->k,     m->v,     m->att, m->g, m->u,
+                   m->logits, m->apv, m->cos_t, m->sin_t, m->xe,  m->xs};
   for (float* b : bufs)
     if (b) (void)hipFree(b);
+  if (m->xq) (void)hipFree(m->xq);
   if (m->api) (void)hipFree(m->api);
   if (m->amax_out) (void)hipFree(m->amax_out);
   if (m->pool) (void)hipFree(m->pool);
@@ -508,7 +553,8 @@ extern "C" int cx_model_create_daiss(const cx_config* cfg, int t_lin, int t_down
       hipMalloc(&m->v, kvd * 4) || hipMalloc(&m->att, D * 4) || hipMalloc(&m->g, I * 4) ||
       hipMalloc(&m->u, I * 4) || hipMalloc(&m->logits, (size_t)V * 4) ||
       hipMalloc(&m->apv, parts * 4) || hipMalloc(&m->api, parts * 4) ||
-      hipMalloc(&m->amax_out, 4)) {
+      hipMalloc(&m->amax_out, 4) || hipMalloc(&m->xq, (D > I ? D : I)) ||
+      hipMalloc(&m->xe, (D > I ? D : I) / 16 * 4) || hipMalloc(&m->xs, (D > I ? D : I) / 16 * 4)) {
     cx_set_error("model: activation buffers");
     return fail(CX_ENOMEM);
   }
@@ -608,47 +654,43 @@ static int enqueue_step(cx_cache* C) {
   const cx_config& c = m->cfg;
   hipStream_t s = m->stream;
   const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn;
+  const int sl = cx_sub(m->t_lin), sd = cx_sub(m->t_down), so = cx_sub(m->t_out);
+  const cx_qact act{m->xq, m->xe, m->xs};
   int rc = cx_launch_embed(m->embd, D, C->st, C->hist, m->x, s);
   if (rc) return rc;
   for (uint32_t li = 0; li < c.layers; li++) {
     const Layer& L = m->layers[li];
     float* kc = C->kv + (size_t)li * 2 * C->cap * kvd;
     float* vc = kc + C->cap * kvd;
-    cx_act norm{};
-    norm.src = CX_ACT_NORM;
-    norm.x = m->x;
-    norm.norm_w = L.attn_norm;
-    norm.eps = c.eps;
+    // src/forward.rs:422-464: rmsnorm, q/k/v with bias, rope, attention
+    if ((rc = cx_launch_norm_quant(m->x, L.attn_norm, D, c.eps, sl, m->xq, m->xe, m->xs, s)))
+      return rc;
     cx_seg qkv[3] = {{L.q, m->q, L.q_bias, D}, {L.k, m->k, L.k_bias, kvd}, {L.v, m->v, L.v_bias, kvd}};
-    if ((rc = cx_launch_gemv(m->t_lin, qkv, 3, D, norm, CX_EPI_STORE, nullptr, s))) return rc;
+    if ((rc = cx_launch_gemv(m->t_lin, qkv, 3, D, act, CX_EPI_STORE, nullptr, s))) return rc;
     if ((rc = cx_launch_rope_kv(m->q, m->k, m->v, kc, vc, m->cos_t, m->sin_t, c.heads, c.kv_heads,
                                 hd, C->st, s)))
       return rc;
     if ((rc = cx_launch_attn_decode(m->q, kc, vc, c.heads, c.kv_heads, hd, C->st, (uint32_t)C->cap,
                                     C->pm, C->pl, C->po, C->sc, m->att, s)))
       return rc;
-    cx_act plain{};
-    plain.src = CX_ACT_PLAIN;
-    plain.x = m->att;
+    // src/forward.rs:466-469: output projection added to the residual
+    if ((rc = cx_launch_quantize(m->att, 1, D, sl, m->xq, m->xe, m->xs, s))) return rc;
     cx_seg o{L.o, m->x, nullptr, D};
-    if ((rc = cx_launch_gemv(m->t_lin, &o, 1, D, plain, CX_EPI_ACCUM, nullptr, s))) return rc;
-    norm.norm_w = L.ffn_norm;
+    if ((rc = cx_launch_gemv(m->t_lin, &o, 1, D, act, CX_EPI_ACCUM, nullptr, s))) return rc;
+    // src/forward.rs:472-491: rmsnorm, gate/up, SwiGLU, down added to the residual
+    if ((rc = cx_launch_norm_quant(m->x, L.ffn_norm, D, c.eps, sl, m->xq, m->xe, m->xs, s)))
+      return rc;
     cx_seg gu[2] = {{L.gate, m->g, nullptr, I}, {L.up, m->u, nullptr, I}};
-    if ((rc = cx_launch_gemv(m->t_lin, gu, 2, D, norm, CX_EPI_STORE, nullptr, s))) return rc;
-    cx_act sw{};
-    sw.src = CX_ACT_SWIGLU;
-    sw.x = m->g;
-    sw.x2 = m->u;
+    if ((rc = cx_launch_gemv(m->t_lin, gu, 2, D, act, CX_EPI_STORE, nullptr, s))) return rc;
+    if ((rc = cx_launch_swiglu_quant(m->g, m->u, I, sd, m->xq, m->xe, m->xs, s))) return rc;
     cx_seg dn{L.down, m->x, nullptr, D};
-    if ((rc = cx_launch_gemv(m->t_down, &dn, 1, I, sw, CX_EPI_ACCUM, nullptr, s))) return rc;
+    if ((rc = cx_launch_gemv(m->t_down, &dn, 1, I, act, CX_EPI_ACCUM, nullptr, s))) return rc;
   }
-  cx_act fin{};
-  fin.src = CX_ACT_NORM;
-  fin.x = m->x;
-  fin.norm_w = m->out_norm;
-  fin.eps = c.eps;
+  // src/forward.rs:495-501: final rmsnorm and the output projection
+  if ((rc = cx_launch_norm_quant(m->x, m->out_norm, D, c.eps, so, m->xq, m->xe, m->xs, s)))
+    return rc;
   cx_seg lm{m->out, m->logits, nullptr, c.vocab};
-  if ((rc = cx_launch_gemv(m->t_out, &lm, 1, D, fin, CX_EPI_STORE, nullptr, s))) return rc;
+  if ((rc = cx_launch_gemv(m->t_out, &lm, 1, D, act, CX_EPI_STORE, nullptr, s))) return rc;
   return cx_launch_argmax(m->logits, c.vocab, m->apv, m->api, m->amax_out, C->st, C->hist, s);
 }
 

@@ -1,29 +1,32 @@
 // cx_gemv.hip — batch-1 k-quant GEMV for gfx950 (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K).
 //
 // y[r] = sum over super-blocks of row r of the reference's fused dot
-// (src/kernels/scalar.rs:132-324, src/kernels/q2k.rs:41-69).
+// (src/kernels/scalar.rs:132-324, src/kernels/q2k.rs:41-69) against an i8
+// activation quantized beforehand (xq, xe, xs).
 //
-// Work split. A super-block (256 values) is handled by 8 consecutive lanes,
-// one "slot" each; a wave covers 8 super-blocks per step. A lane loads its
-// slice of the block straight from HBM into registers (16-byte loads for
-// Q4_K/Q5_K, whose 144/176-byte blocks keep rows 16-byte aligned; dword
-// loads for Q2_K; 2-byte-aligned dword loads for Q3_K/Q6_K), unpacks the
-// quants and the 6-bit scales in registers, and forms integer partial sums
-// with v_dot4c_i32_i8 against the i8 activation held in LDS. The two lanes
-// that share a sub-block swap partial sums with one DPP move, so every
-// sub-block integer sum E_j is formed exactly. The lane that owns sub-block j
-// then computes the reference's f32 term with the reference's rounding:
+// Data movement. A workgroup owns a tile of R consecutive rows, i.e. one
+// contiguous byte range of the matrix. Its four waves copy that range into
+// LDS with global_load_lds_dwordx4 (gfx950's 16-byte direct-to-LDS load):
+// every lane moves 16 consecutive bytes, so a wave reads 1 KiB of contiguous
+// HBM per instruction, no VGPRs hold weight data, and the whole tile is in
+// flight at once. The activation (k bytes + 2*k/sub floats) follows into LDS
+// the same way. R is chosen per launch so that there are >= 2 tiles per CU
+// and a tile fits in 64 KiB of LDS; with several workgroups resident per CU
+// the whole matrix is in flight within one wave of workgroups.
+//
+// Arithmetic. A super-block (256 values) is handled by 8 consecutive lanes,
+// one "slot" each. A lane reads its slice of the block from LDS, unpacks the
+// quants and the 6-bit scales in registers and forms integer partial sums
+// with v_dot4c_i32_i8. The two lanes that share a sub-block swap partial
+// sums with one DPP move, so every sub-block integer sum E_j is formed
+// exactly. The lane that owns sub-block j then computes the reference's f32
+// term with the reference's rounding:
 //   Q4_K/Q5_K/Q2_K : xe[j] * ((d*sc_j)*E_j - (dmin*mn_j)*xs[j])
 //   Q3_K           : (xe[j] * (d*(esc_j-32))) * (E'_j - 4*xs[j])
 //   Q6_K           : (xe[j] * (d*esc_j)) * (E'_j - 32*xs[j])
-// Only the order in which the per-sub-block terms are summed differs from
-// the scalar loop (per lane, then a fixed butterfly, then a fixed cross-wave
-// order), so results are deterministic run to run.
-//
-// Rows: one row is handled by 1, 2 or 4 waves of a 256-thread workgroup
-// (more waves per row for long rows, so that every wave issues all of its
-// loads up front). All loads of a wave are issued before the activation is
-// built in LDS, so weight traffic overlaps the prologue.
+// and stores it in LDS at its sub-block index. Finally one lane per row adds
+// the row's terms in sub-block order starting from 0.0, as the scalar kernel
+// does, so every row is bit-identical to the reference's scalar dot.
 
 #include "cx_internal.h"
 #include "cx_act.h"
@@ -31,14 +34,18 @@
 namespace {
 
 constexpr uint32_t M4 = 0x0F0F0F0Fu;
+constexpr uint32_t TILE_LDS_MAX = 64 * 1024;
 
-__device__ inline uint32_t ld32u(const uint8_t* p) {
-  uint32_t v;
-  __builtin_memcpy(&v, p, 4);
-  return v;
-}
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
 __device__ inline int dot4(uint32_t a, int b, int c) {
   return __builtin_amdgcn_sdot4((int)a, b, c, false);
+}
+// a dword at any byte offset of LDS: two aligned reads and v_alignbyte_b32.
+// May read up to 3 bytes past off+4 (the tile region is padded for it).
+__device__ inline uint32_t lds32(const uint8_t* lds, uint32_t off) {
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(lds + (off & ~3u));
+  return __builtin_amdgcn_alignbyte(q[1], q[0], off & 3u);
 }
 
 template <int T> struct KQ;
@@ -47,11 +54,13 @@ template <int T> struct KQ;
 // 144 B: d(2) dmin(2) scales(12) qs(128). Slot l: pair p = l/2, half h = l%2,
 // qs bytes [16+32p+16h, +16): low nibbles -> sub-block 2p positions
 // 16h..16h+15, high nibbles -> sub-block 2p+1 same positions.
+// Blocks are read as 16-byte words: the tile must start 16-byte aligned.
 template <> struct KQ<CX_Q4_K> {
   static constexpr int BPB = 144, SUB = 32, NW = 8;
-  __device__ static void load(const uint8_t* b, int l, uint32_t (&r)[NW]) {
-    uint4 h = *reinterpret_cast<const uint4*>(b);
-    uint4 q = *reinterpret_cast<const uint4*>(b + 16 + 16 * l);
+  static constexpr bool ALIGNED = true;
+  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
+    uint4 h = *reinterpret_cast<const uint4*>(lds + off);
+    uint4 q = *reinterpret_cast<const uint4*>(lds + off + 16 + 16 * l);
     r[0] = h.x; r[1] = h.y; r[2] = h.z; r[3] = h.w;
     r[4] = q.x; r[5] = q.y; r[6] = q.z; r[7] = q.w;
   }
@@ -89,7 +98,7 @@ template <> struct KQ<CX_Q4_K> {
     }
     const float d = cx_h2f(r[0] & 0xFFFF), dm = cx_h2f(r[0] >> 16);
     if (dbg) dbg[j] = e;
-    if (to) to[j] = xe[j] * (d * (float)sc * (float)e - dm * (float)mn * xs[j]);
+    to[j] = xe[j] * (d * (float)sc * (float)e - dm * (float)mn * xs[j]);
   }
 };
 
@@ -98,11 +107,12 @@ template <> struct KQ<CX_Q4_K> {
 // position i of sub-block j = bit j of qh[i] (src/kernels/scalar.rs:205-210).
 template <> struct KQ<CX_Q5_K> {
   static constexpr int BPB = 176, SUB = 32, NW = 12;
-  __device__ static void load(const uint8_t* b, int l, uint32_t (&r)[NW]) {
+  static constexpr bool ALIGNED = true;
+  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
     const int p = l >> 1, h = l & 1;
-    uint4 hd = *reinterpret_cast<const uint4*>(b);
-    uint4 qh = *reinterpret_cast<const uint4*>(b + 16 + 16 * h);
-    uint4 q = *reinterpret_cast<const uint4*>(b + 48 + 32 * p + 16 * h);
+    uint4 hd = *reinterpret_cast<const uint4*>(lds + off);
+    uint4 qh = *reinterpret_cast<const uint4*>(lds + off + 16 + 16 * h);
+    uint4 q = *reinterpret_cast<const uint4*>(lds + off + 48 + 32 * p + 16 * h);
     r[0] = hd.x; r[1] = hd.y; r[2] = hd.z; r[3] = hd.w;
     r[4] = q.x; r[5] = q.y; r[6] = q.z; r[7] = q.w;
     r[8] = qh.x; r[9] = qh.y; r[10] = qh.z; r[11] = qh.w;
@@ -155,13 +165,14 @@ __device__ inline uint32_t sel4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t 
 // 84 B: scales(16) qs(64) d dmin. value = (qs >> 2(g%4)) & 3.
 template <> struct KQ<CX_Q2_K> {
   static constexpr int BPB = 84, SUB = 16, NW = 7;
-  __device__ static void load(const uint8_t* b, int l, uint32_t (&r)[NW]) {
+  static constexpr bool ALIGNED = false;
+  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
     const int half = l >> 2, c = l & 3;
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(b + 16 + 32 * half + 8 * c);
-    const uint32_t* s = reinterpret_cast<const uint32_t*>(b);
-    r[0] = q[0]; r[1] = q[1];
-    r[2] = s[0]; r[3] = s[1]; r[4] = s[2]; r[5] = s[3];
-    r[6] = *reinterpret_cast<const uint32_t*>(b + 80);
+    const uint32_t q = off + 16 + 32 * half + 8 * c;
+    r[0] = lds32(lds, q); r[1] = lds32(lds, q + 4);
+    r[2] = lds32(lds, off); r[3] = lds32(lds, off + 4);
+    r[4] = lds32(lds, off + 8); r[5] = lds32(lds, off + 12);
+    r[6] = lds32(lds, off + 80);
   }
   __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
                                const float* xe, const float* xs, int32_t* dbg, float* to) {
@@ -179,14 +190,10 @@ template <> struct KQ<CX_Q2_K> {
     const uint32_t sc0 = (word >> (8 * m)) & 0xFF, sc1 = (word >> (8 * (m + 2))) & 0xFF;
     const float d = cx_h2f(r[6] & 0xFFFF), dm = cx_h2f(r[6] >> 16);
     if (dbg) { dbg[sw.s0] = sw.own0; dbg[sw.s1] = sw.own1; }
-    float t0 = xe[sw.s0] * (d * (float)(sc0 & 0xF) * (float)sw.own0 -
-                            dm * (float)(sc0 >> 4) * xs[sw.s0]);
-    float t1 = xe[sw.s1] * (d * (float)(sc1 & 0xF) * (float)sw.own1 -
-                            dm * (float)(sc1 >> 4) * xs[sw.s1]);
-    if (to) {
-      to[sw.s0] = t0;
-      to[sw.s1] = t1;
-    }
+    to[sw.s0] = xe[sw.s0] * (d * (float)(sc0 & 0xF) * (float)sw.own0 -
+                             dm * (float)(sc0 >> 4) * xs[sw.s0]);
+    to[sw.s1] = xe[sw.s1] * (d * (float)(sc1 & 0xF) * (float)sw.own1 -
+                             dm * (float)(sc1 >> 4) * xs[sw.s1]);
   }
 };
 
@@ -195,16 +202,17 @@ template <> struct KQ<CX_Q2_K> {
 // ((qs >> 2(g%4)) & 3) | ((hmask >> g) & 1) << 2   (src/kernels/scalar.rs:262-268)
 template <> struct KQ<CX_Q3_K> {
   static constexpr int BPB = 110, SUB = 16, NW = 8;
-  __device__ static void load(const uint8_t* b, int l, uint32_t (&r)[NW]) {
+  static constexpr bool ALIGNED = false;
+  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
     const int half = l >> 2, c = l & 3;
-    r[0] = ld32u(b + 8 * c);
-    r[1] = ld32u(b + 8 * c + 4);
-    r[2] = ld32u(b + 32 + 32 * half + 8 * c);
-    r[3] = ld32u(b + 32 + 32 * half + 8 * c + 4);
-    r[4] = ld32u(b + 96);
-    r[5] = ld32u(b + 100);
-    r[6] = ld32u(b + 104);
-    r[7] = (uint32_t)b[108] | ((uint32_t)b[109] << 8);
+    r[0] = lds32(lds, off + 8 * c);
+    r[1] = lds32(lds, off + 8 * c + 4);
+    r[2] = lds32(lds, off + 32 + 32 * half + 8 * c);
+    r[3] = lds32(lds, off + 32 + 32 * half + 8 * c + 4);
+    r[4] = lds32(lds, off + 96);
+    r[5] = lds32(lds, off + 100);
+    r[6] = lds32(lds, off + 104);
+    r[7] = lds32(lds, off + 108) & 0xFFFFu;
   }
   __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
                                const float* xe, const float* xs, int32_t* dbg, float* to) {
@@ -231,12 +239,8 @@ template <> struct KQ<CX_Q3_K> {
     const float d = cx_h2f(r[7]);
     if (dbg) { dbg[sw.s0] = sw.own0; dbg[sw.s1] = sw.own1; }
     const float sc0 = d * ((float)esc0 - 32.0f), sc1 = d * ((float)esc1 - 32.0f);
-    float t0 = xe[sw.s0] * sc0 * ((float)sw.own0 - 4.0f * xs[sw.s0]);
-    float t1 = xe[sw.s1] * sc1 * ((float)sw.own1 - 4.0f * xs[sw.s1]);
-    if (to) {
-      to[sw.s0] = t0;
-      to[sw.s1] = t1;
-    }
+    to[sw.s0] = xe[sw.s0] * sc0 * ((float)sw.own0 - 4.0f * xs[sw.s0]);
+    to[sw.s1] = xe[sw.s1] * sc1 * ((float)sw.own1 - 4.0f * xs[sw.s1]);
   }
 };
 
@@ -245,15 +249,17 @@ template <> struct KQ<CX_Q3_K> {
 // nib | ((qh >> 2gi) & 3) << 4   (src/kernels/scalar.rs:305-320)
 template <> struct KQ<CX_Q6_K> {
   static constexpr int BPB = 210, SUB = 16, NW = 11;
-  __device__ static void load(const uint8_t* b, int l, uint32_t (&r)[NW]) {
+  static constexpr bool ALIGNED = false;
+  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
     const int half = l >> 2, c = l & 3;
-    const uint8_t* qa = b + 64 * half + 8 * c;
-    r[0] = ld32u(qa); r[1] = ld32u(qa + 4);
-    r[2] = ld32u(qa + 32); r[3] = ld32u(qa + 36);
-    r[4] = ld32u(b + 128 + 32 * half + 8 * c);
-    r[5] = ld32u(b + 128 + 32 * half + 8 * c + 4);
-    r[6] = ld32u(b + 192); r[7] = ld32u(b + 196); r[8] = ld32u(b + 200); r[9] = ld32u(b + 204);
-    r[10] = (uint32_t)b[208] | ((uint32_t)b[209] << 8);
+    const uint32_t qa = off + 64 * half + 8 * c;
+    r[0] = lds32(lds, qa); r[1] = lds32(lds, qa + 4);
+    r[2] = lds32(lds, qa + 32); r[3] = lds32(lds, qa + 36);
+    r[4] = lds32(lds, off + 128 + 32 * half + 8 * c);
+    r[5] = lds32(lds, off + 128 + 32 * half + 8 * c + 4);
+    r[6] = lds32(lds, off + 192); r[7] = lds32(lds, off + 196);
+    r[8] = lds32(lds, off + 200); r[9] = lds32(lds, off + 204);
+    r[10] = lds32(lds, off + 208) & 0xFFFFu;
   }
   __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
                                const float* xe, const float* xs, int32_t* dbg, float* to) {
@@ -278,205 +284,228 @@ template <> struct KQ<CX_Q6_K> {
     const float d = cx_h2f(r[10]);
     if (dbg) { dbg[sw.s0] = sw.own0; dbg[sw.s1] = sw.own1; }
     const float sc0 = d * (float)e0, sc1 = d * (float)e1;
-    float t0 = xe[sw.s0] * sc0 * ((float)sw.own0 - 32.0f * xs[sw.s0]);
-    float t1 = xe[sw.s1] * sc1 * ((float)sw.own1 - 32.0f * xs[sw.s1]);
-    if (to) {
-      to[sw.s0] = t0;
-      to[sw.s1] = t1;
-    }
+    to[sw.s0] = xe[sw.s0] * sc0 * ((float)sw.own0 - 32.0f * xs[sw.s0]);
+    to[sw.s1] = xe[sw.s1] * sc1 * ((float)sw.own1 - 32.0f * xs[sw.s1]);
   }
 };
 
 // -------------------------------------------------------------- kernel
 struct GemvParams {
   cx_seg seg[4];
-  uint32_t seg_end[4];  // cumulative rows
+  uint32_t tile_end[4];  // cumulative tile counts
   int nseg;
   uint32_t k, nb, nsub;
-  uint32_t waves_per_row, rows_per_wg, slots_per_wave;
-  int src;
-  const int8_t* xq;
-  const float* xe;
-  const float* xs;
-  const float* x;
-  const float* x2;
-  const float* nw;
-  float eps;
+  uint32_t R;            // rows per tile
+  uint32_t row_bytes;
+  uint32_t tstride;      // floats between two rows' terms (nsub + 4)
+  uint32_t lds_act;      // byte offsets in LDS: activation, xe/xs, terms
+  uint32_t lds_scale;
+  uint32_t lds_terms;
+  cx_qact act;
   int epi;
   int32_t* dbg;
 };
 
-template <int T, int MAXIT>
-__global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
-  using Q = KQ<T>;
-  extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ double red[4];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t row_in_wg = wave / P.waves_per_row, part = wave % P.waves_per_row;
-  const uint32_t grow = blockIdx.x * P.rows_per_wg + row_in_wg;
-  const bool row_ok = grow < P.seg_end[P.nseg - 1];
-  int sg = 0;
-  uint32_t rbase = 0;
-  if (row_ok) {
-    while (grow >= P.seg_end[sg]) sg++;
-    rbase = sg ? P.seg_end[sg - 1] : 0;
-  }
-  const uint32_t row = grow - rbase;
-  const size_t row_bytes = (size_t)P.nb * Q::BPB;
-  const uint8_t* wrow = row_ok ? P.seg[sg].w + (size_t)row * row_bytes : nullptr;
-  const uint32_t nslots = P.nb * 8, s_begin = part * P.slots_per_wave;
-
-  // 1. every weight load of this wave, issued up front
-  uint32_t regs[MAXIT][Q::NW];
-  bool valid[MAXIT];
-#pragma unroll
-  for (int it = 0; it < MAXIT; it++) {
-    const uint32_t off = it * 64 + lane, slot = s_begin + off;
-    valid[it] = row_ok && off < P.slots_per_wave && slot < nslots;
-    if (valid[it]) {
-      Q::load(wrow + (size_t)(slot >> 3) * Q::BPB, slot & 7, regs[it]);
-    } else {
-#pragma unroll
-      for (int w = 0; w < Q::NW; w++) regs[it][w] = 0;
-    }
-  }
-
-  // 2. the i8 activation of this launch, built in LDS by every workgroup
-  int8_t* sq = reinterpret_cast<int8_t*>(lds);
-  float* se = reinterpret_cast<float*>(lds + P.k);
-  float* ss = se + P.nsub;
-  if (P.src == CX_ACT_QUANTIZED) {
-    const uint4* gq = reinterpret_cast<const uint4*>(P.xq);
-    for (uint32_t i = tid; i < P.k / 16; i += 256) reinterpret_cast<uint4*>(sq)[i] = gq[i];
-    for (uint32_t i = tid; i < P.nsub; i += 256) {
-      se[i] = P.xe[i];
-      ss[i] = P.xs[i];
-    }
-  } else {
-    double scale = 1.0;
-    if (P.src == CX_ACT_NORM) scale = cx_rms_scale(P.x, P.k, P.eps, red);
-    cx_build_act_rows<Q::SUB>(P.src, P.x, P.x2, P.nw, scale, P.k, sq, se, ss, tid, 256);
-  }
-  __syncthreads();
-
-  // 3. integer dots + the reference's per-sub-block f32 terms, staged in LDS
-  //    by sub-block index (every sub-block of the row is owned by one lane)
-  float* terms = ss + P.nsub + row_in_wg * P.nsub;
-  constexpr int SPB = 256 / Q::SUB;  // sub-blocks per super-block
-#pragma unroll
-  for (int it = 0; it < MAXIT; it++) {
-    const uint32_t slot = s_begin + it * 64 + lane;
-    const uint32_t blk = valid[it] ? (slot >> 3) : 0;
-    int32_t* dbg = (P.dbg && valid[it]) ? P.dbg + (size_t)grow * P.nsub + blk * SPB : nullptr;
-    float* to = valid[it] ? terms + blk * SPB : nullptr;
-    Q::term(regs[it], lane & 7, sq + blk * 256, se + blk * SPB, ss + blk * SPB, dbg, to);
-  }
-  __syncthreads();
-
-  // 4. the row's sum in the scalar spec's order: total = 0; total += term_s
-  //    for s = 0, 1, ... (src/kernels/scalar.rs:141-167), so a row's result
-  //    is bit-identical to the reference's scalar kernel.
-  if (part == 0 && lane == 0 && row_ok) {
-    float acc = 0.0f;
-    for (uint32_t s = 0; s < P.nsub; s++) acc += terms[s];
-    const cx_seg& S = P.seg[sg];
-    if (P.epi == CX_EPI_ACCUM) {
-      S.y[row] += acc;
-    } else {
-      S.y[row] = S.bias ? acc + S.bias[row] : acc;
-    }
+// 16-byte chunks [0, n) of `g` into LDS at `l`, 1 KiB per wave instruction.
+// global_load_lds writes lane i's 16 bytes at (wave-uniform LDS address) +
+// 16*i; lanes past the end are masked off.
+__device__ inline void copy_to_lds(const uint8_t* g, uint8_t* l, uint32_t n, int wave, int lane,
+                                   int nwaves) {
+  for (uint32_t c0 = 64u * wave; c0 < n; c0 += 64u * nwaves) {
+    if (c0 + lane < n)
+      __builtin_amdgcn_global_load_lds(g + 16 * (size_t)(c0 + lane), (lds_ptr_t)(l + 16 * c0), 16,
+                                       0, 0);
   }
 }
 
 template <int T>
-int launch_t(GemvParams& P, uint32_t total_rows, hipStream_t s) {
-  const uint32_t nslots = P.nb * 8;
-  int maxit = 0;
-  for (int m : {1, 2, 4, 8}) {
-    for (uint32_t S : {1u, 2u, 4u}) {
-      uint32_t spw = ((nslots + S - 1) / S + 7) / 8 * 8;
-      if (spw <= 64u * m) {
-        P.waves_per_row = S;
-        P.slots_per_wave = spw;
-        maxit = m;
-        break;
-      }
+__global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
+  using Q = KQ<T>;
+  constexpr int SPB = 256 / Q::SUB;  // sub-blocks per super-block
+  extern __shared__ __align__(16) uint8_t lds[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t tile = blockIdx.x;
+  int sg = 0;
+  while (tile >= P.tile_end[sg]) sg++;
+  if (sg) tile -= P.tile_end[sg - 1];
+  const cx_seg S = P.seg[sg];
+  const uint32_t row0 = tile * P.R;
+  const uint32_t rows = min(P.R, S.rows - row0);
+
+  // 1. the tile (rows * row_bytes contiguous bytes) and the activation into
+  //    LDS; the tile starts `skew` bytes into LDS when the rows are not
+  //    16-byte aligned (Q2_K/Q3_K/Q6_K rows of some widths)
+  const uint8_t* src = S.w + (size_t)row0 * P.row_bytes;
+  const uint32_t skew = (uint32_t)((uintptr_t)src & 15u);
+  copy_to_lds(src - skew, lds, (skew + rows * P.row_bytes + 15) >> 4, wave, lane, 4);
+  int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
+  copy_to_lds(reinterpret_cast<const uint8_t*>(P.act.xq), reinterpret_cast<uint8_t*>(sq),
+              P.k >> 4, wave, lane, 4);
+  float* se = reinterpret_cast<float*>(lds + P.lds_scale);
+  float* ss = se + P.nsub;
+  for (uint32_t i = tid; i < P.nsub; i += 256) {
+    se[i] = P.act.xe[i];
+    ss[i] = P.act.xs[i];
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the direct-to-LDS loads have landed
+  __syncthreads();
+
+  // 2. integer dots + the reference's per-sub-block f32 terms, staged in LDS
+  //    by (row, sub-block); every sub-block of a row is owned by one lane
+  float* terms = reinterpret_cast<float*>(lds + P.lds_terms);
+  const uint32_t nb8 = P.nb * 8, total = rows * nb8;
+  for (uint32_t slot = tid; slot < total; slot += 256) {
+    const uint32_t r = slot / nb8, w = slot - r * nb8, blk = w >> 3;
+    const int l = (int)(w & 7);
+    uint32_t regs[Q::NW];
+    Q::load(lds, skew + r * P.row_bytes + blk * Q::BPB, l, regs);
+    int32_t* dbg = P.dbg ? P.dbg + (size_t)(row0 + r) * P.nsub + blk * SPB : nullptr;
+    Q::term(regs, l, sq + blk * 256, se + blk * SPB, ss + blk * SPB, dbg,
+            terms + r * P.tstride + blk * SPB);
+  }
+  __syncthreads();
+
+  // 3. the row's sum in the scalar spec's order: total = 0; total += term_s
+  //    for s = 0, 1, ... (src/kernels/scalar.rs:141-167)
+  if ((uint32_t)tid < rows) {
+    const float4* t = reinterpret_cast<const float4*>(terms + tid * P.tstride);
+    float acc = 0.0f;
+    for (uint32_t s = 0; s < P.nsub / 4; s++) {
+      const float4 v = t[s];
+      acc += v.x;
+      acc += v.y;
+      acc += v.z;
+      acc += v.w;
     }
-    if (maxit) break;
+    const uint32_t row = row0 + tid;
+    if (P.epi == CX_EPI_ACCUM)
+      S.y[row] += acc;
+    else
+      S.y[row] = S.bias ? acc + S.bias[row] : acc;
   }
-  CX_REQUIRE(maxit, "gemv: row of %u values is too long", P.k);
-  P.rows_per_wg = 4 / P.waves_per_row;
-  const uint32_t grid = (total_rows + P.rows_per_wg - 1) / P.rows_per_wg;
-  // activation (k + 8 * nsub) + one row of f32 terms per row of the workgroup
-  const size_t lds = P.k + 8 * (size_t)P.nsub + 4 * (size_t)P.nsub * P.rows_per_wg;
-  switch (maxit) {
-    case 1: hipLaunchKernelGGL((k_gemv<T, 1>), dim3(grid), dim3(256), lds, s, P); break;
-    case 2: hipLaunchKernelGGL((k_gemv<T, 2>), dim3(grid), dim3(256), lds, s, P); break;
-    case 4: hipLaunchKernelGGL((k_gemv<T, 4>), dim3(grid), dim3(256), lds, s, P); break;
-    default: hipLaunchKernelGGL((k_gemv<T, 8>), dim3(grid), dim3(256), lds, s, P); break;
+}
+
+struct TilePlan {
+  uint32_t R, tiles, lds, lds_act, lds_scale, lds_terms;
+};
+
+// LDS layout of a tile of R rows: [16 skew + R*row_bytes + 16 pad] [xq k]
+// [xe, xs] [terms R x (nsub+4)]
+TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
+                   const uint32_t* rows, int nseg) {
+  TilePlan t{};
+  t.R = R;
+  for (int i = 0; i < nseg; i++) t.tiles += (rows[i] + R - 1) / R;
+  t.lds_act = (16 + R * row_bytes + 16 + 15) / 16 * 16;
+  t.lds_scale = t.lds_act + k;
+  t.lds_terms = t.lds_scale + (8 * nsub + 15) / 16 * 16;
+  t.lds = t.lds_terms + 4 * R * (nsub + 4);
+  return t;
+}
+
+template <int T>
+int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
+  using Q = KQ<T>;
+  if (Q::ALIGNED) {
+    for (int i = 0; i < P.nseg; i++)
+      CX_REQUIRE(((uintptr_t)P.seg[i].w & 15u) == 0,
+                 "gemv: %s weights must start 16-byte aligned", T == CX_Q4_K ? "Q4_K" : "Q5_K");
   }
+  // largest tile (<= 64 rows) that fits the LDS budget and leaves >= 2
+  // tiles per CU; small matrices fall back to the smallest tiles
+  TilePlan best{};
+  for (uint32_t R = 64; R >= 1; R >>= 1) {
+    TilePlan t = plan_tile(R, P.row_bytes, P.k, P.nsub, rows, P.nseg);
+    if (t.lds > TILE_LDS_MAX) continue;
+    best = t;
+    if (t.tiles >= 512) break;
+  }
+  CX_REQUIRE(best.R, "gemv: a row of %u values does not fit in LDS", P.k);
+  P.R = best.R;
+  P.lds_act = best.lds_act;
+  P.lds_scale = best.lds_scale;
+  P.lds_terms = best.lds_terms;
+  uint32_t acc = 0;
+  for (int i = 0; i < P.nseg; i++) {
+    acc += (rows[i] + best.R - 1) / best.R;
+    P.tile_end[i] = acc;
+  }
+  hipLaunchKernelGGL((k_gemv<T>), dim3(best.tiles), dim3(256), best.lds, s, P);
   CX_HIP(hipGetLastError());
   return CX_OK;
 }
 
 }  // namespace
 
-int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k, const cx_act& act,
+int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k, const cx_qact& act,
                    int epi, int32_t* dbg, hipStream_t s) {
   CX_REQUIRE(nseg >= 1 && nseg <= 4, "gemv: 1..4 matrices per launch");
   CX_REQUIRE(cx_is_kquant(type), "gemv: type %d has no fused GEMV", type);
   CX_REQUIRE(k > 0 && k % 256 == 0, "gemv: k=%u is not a multiple of 256", k);
+  CX_REQUIRE(act.xq && act.xe && act.xs, "gemv: missing quantized activation");
+  CX_REQUIRE(((uintptr_t)act.xq & 15u) == 0, "gemv: xq must be 16-byte aligned");
+  CX_REQUIRE(!dbg || nseg == 1, "gemv: sub-block sums need a single matrix");
   GemvParams P{};
-  uint32_t total = 0;
+  uint32_t rows[4], total = 0;
   for (int i = 0; i < nseg; i++) {
     CX_REQUIRE(segs[i].w && segs[i].y, "gemv: null matrix or output");
     P.seg[i] = segs[i];
+    rows[i] = segs[i].rows;
     total += segs[i].rows;
-    P.seg_end[i] = total;
   }
   if (total == 0) return CX_OK;
-  P.nseg = nseg;
+  // empty segments would own no tile; keep them out of the tile table
+  int n = 0;
+  for (int i = 0; i < nseg; i++)
+    if (rows[i]) {
+      P.seg[n] = segs[i];
+      rows[n++] = segs[i].rows;
+    }
+  P.nseg = n;
   P.k = k;
   P.nb = k / 256;
   P.nsub = k / cx_sub(type);
-  P.src = act.src;
-  P.xq = act.xq; P.xe = act.xe; P.xs = act.xs;
-  P.x = act.x; P.x2 = act.x2; P.nw = act.norm_w; P.eps = act.eps;
+  P.row_bytes = P.nb * cx_bpb(type);
+  P.tstride = P.nsub + 4;
+  P.act = act;
   P.epi = epi;
   P.dbg = dbg;
-  if (act.src == CX_ACT_QUANTIZED)
-    CX_REQUIRE(act.xq && act.xe && act.xs, "gemv: missing quantized activation");
-  else
-    CX_REQUIRE(act.x && (act.src != CX_ACT_NORM || act.norm_w) &&
-                   (act.src != CX_ACT_SWIGLU || act.x2),
-               "gemv: missing activation");
   switch (type) {
-    case CX_Q2_K: return launch_t<CX_Q2_K>(P, total, s);
-    case CX_Q3_K: return launch_t<CX_Q3_K>(P, total, s);
-    case CX_Q4_K: return launch_t<CX_Q4_K>(P, total, s);
-    case CX_Q5_K: return launch_t<CX_Q5_K>(P, total, s);
-    default: return launch_t<CX_Q6_K>(P, total, s);
+    case CX_Q2_K: return launch_t<CX_Q2_K>(P, rows, s);
+    case CX_Q3_K: return launch_t<CX_Q3_K>(P, rows, s);
+    case CX_Q4_K: return launch_t<CX_Q4_K>(P, rows, s);
+    case CX_Q5_K: return launch_t<CX_Q5_K>(P, rows, s);
+    default: return launch_t<CX_Q6_K>(P, rows, s);
   }
 }
 
 // ------------------------------------------------- activation kernels
 namespace {
+// x: rows*k values; a sub-block never straddles two rows (k % SUB == 0)
 template <int SUB>
-__global__ __launch_bounds__(256) void k_quantize(const float* x, size_t rows, uint32_t k,
-                                                  int8_t* xq, float* xe, float* xs) {
-  const uint32_t nsub = k / SUB;
-  const size_t total = rows * nsub;
-  for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
-    float v[SUB];
-    const float4* px = reinterpret_cast<const float4*>(x + i * SUB);
-#pragma unroll
-    for (int j = 0; j < SUB / 4; j++) {
-      float4 f = px[j];
-      v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
-    }
-    cx_quant_sub<SUB>(v, xq + i * SUB, xe + i, xs + i);
-  }
+__global__ __launch_bounds__(256) void k_quantize(const float* x, size_t n, int8_t* xq,
+                                                  float* xe, float* xs) {
+  const size_t i = blockIdx.x * 256ull + threadIdx.x;
+  if (i < n) cx_quant_lane<SUB>(x[i], i, xq, xe, xs);  // n % SUB == 0: whole groups
+}
+
+template <int SUB>
+__global__ __launch_bounds__(256) void k_swiglu_quant(const float* g, const float* u, uint32_t n,
+                                                      int8_t* xq, float* xe, float* xs) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i < n) cx_quant_lane<SUB>(cx_swiglu(g[i], u[i]), i, xq, xe, xs);
+}
+
+// rmsnorm (src/kernels/scalar.rs:40-53) of one row, then its quantization:
+// (x as f64 * scale) as f32 * w
+template <int SUB>
+__global__ __launch_bounds__(256) void k_norm_quant(const float* x, const float* w, uint32_t n,
+                                                    float eps, int8_t* xq, float* xe, float* xs) {
+  __shared__ double red[4];
+  const double scale = cx_rms_scale(x, n, eps, red);
+  for (uint32_t i = threadIdx.x; i < n; i += 256)  // n % 256 == 0: whole groups
+    cx_quant_lane<SUB>((float)((double)x[i] * scale) * w[i], i, xq, xe, xs);
 }
 
 __global__ __launch_bounds__(256) void k_rmsnorm(float* out, const float* in, const float* w,
@@ -492,15 +521,41 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float* out, const float* in, co
 int cx_launch_quantize(const float* x, size_t rows, size_t k, int sub, int8_t* xq, float* xe,
                        float* xs, hipStream_t s) {
   CX_REQUIRE(sub == 16 || sub == 32, "quantize: sub must be 16 or 32, got %d", sub);
-  CX_REQUIRE(k % (size_t)sub == 0 && k % 4 == 0, "quantize: k=%zu not a multiple of %d", k, sub);
+  CX_REQUIRE(k % (size_t)sub == 0, "quantize: k=%zu not a multiple of %d", k, sub);
   CX_REQUIRE(x && xq && xe && xs, "quantize: null pointer");
-  const size_t total = rows * (k / sub);
-  if (!total) return CX_OK;
-  const unsigned grid = (unsigned)((total + 255) / 256 < 65535 ? (total + 255) / 256 : 65535);
+  const size_t n = rows * k;
+  if (!n) return CX_OK;
+  const size_t grid = (n + 255) / 256;
+  CX_REQUIRE(grid < (1ull << 31), "quantize: %zu values is too many", n);
   if (sub == 16)
-    hipLaunchKernelGGL(k_quantize<16>, dim3(grid), dim3(256), 0, s, x, rows, (uint32_t)k, xq, xe, xs);
+    hipLaunchKernelGGL(k_quantize<16>, dim3((unsigned)grid), dim3(256), 0, s, x, n, xq, xe, xs);
   else
-    hipLaunchKernelGGL(k_quantize<32>, dim3(grid), dim3(256), 0, s, x, rows, (uint32_t)k, xq, xe, xs);
+    hipLaunchKernelGGL(k_quantize<32>, dim3((unsigned)grid), dim3(256), 0, s, x, n, xq, xe, xs);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_swiglu_quant(const float* g, const float* u, size_t n, int sub, int8_t* xq,
+                           float* xe, float* xs, hipStream_t s) {
+  CX_REQUIRE(sub == 16 || sub == 32, "swiglu: sub must be 16 or 32, got %d", sub);
+  CX_REQUIRE(n % (size_t)sub == 0 && n < (1u << 31), "swiglu: bad width %zu", n);
+  const unsigned grid = (unsigned)((n + 255) / 256);
+  if (sub == 16)
+    hipLaunchKernelGGL(k_swiglu_quant<16>, dim3(grid), dim3(256), 0, s, g, u, (uint32_t)n, xq, xe, xs);
+  else
+    hipLaunchKernelGGL(k_swiglu_quant<32>, dim3(grid), dim3(256), 0, s, g, u, (uint32_t)n, xq, xe, xs);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_norm_quant(const float* x, const float* w, size_t n, float eps, int sub,
+                         int8_t* xq, float* xe, float* xs, hipStream_t s) {
+  CX_REQUIRE(sub == 16 || sub == 32, "norm: sub must be 16 or 32, got %d", sub);
+  CX_REQUIRE(n % 256 == 0 && n < (1u << 31), "norm: width %zu must be a multiple of 256", n);
+  if (sub == 16)
+    hipLaunchKernelGGL(k_norm_quant<16>, dim3(1), dim3(256), 0, s, x, w, (uint32_t)n, eps, xq, xe, xs);
+  else
+    hipLaunchKernelGGL(k_norm_quant<32>, dim3(1), dim3(256), 0, s, x, w, (uint32_t)n, eps, xq, xe, xs);
   CX_HIP(hipGetLastError());
   return CX_OK;
 }

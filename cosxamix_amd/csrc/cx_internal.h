@@ -12,35 +12,31 @@ struct cx_seg {
   uint32_t rows;
 };
 
-// Where the GEMV's activation comes from. Every workgroup builds the same
-// i8 activation (xq, xe, xs) in LDS from it, with the same arithmetic as
-// cx_quantize_act, so the result is bit-identical across workgroups.
-enum cx_act_src {
-  CX_ACT_QUANTIZED = 0,  // xq/xe/xs given in device memory
-  CX_ACT_NORM = 1,       // rmsnorm(x, w, eps) then quantize   (kernels/mod.rs:511 + ops.rs:178)
-  CX_ACT_PLAIN = 2,      // quantize x                           (ops.rs:178)
-  CX_ACT_SWIGLU = 3,     // quantize silu(x) * x2               (forward.rs:483-487)
-};
-
-struct cx_act {
-  int src;
+// The i8 activation of a GEMV (ops::cuantizar_i8_en, src/ops.rs:178-198,
+// with the per-sub-block sums of src/ops.rs:472-483): xq[k] (16-byte
+// aligned), xe[k/sub], xs[k/sub] in device memory.
+struct cx_qact {
   const int8_t* xq;
   const float* xe;
   const float* xs;
-  const float* x;
-  const float* x2;
-  const float* norm_w;
-  float eps;
 };
 
 enum cx_epi { CX_EPI_STORE = 0, CX_EPI_ACCUM = 1 };
 
 // GEMV over `nseg` segments: seg[i].y[r] (=|+=) row r of seg[i].w . act.
-int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k,
-                   const cx_act& act, int epi, int32_t* dbg, hipStream_t s);
+// `dbg` (single segment only) receives the integer sub-block sums.
+int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k, const cx_qact& act,
+                   int epi, int32_t* dbg, hipStream_t s);
 
-// Activation quantization for `rows` rows (bit-exact, ops.rs:178-198).
-int cx_launch_quantize(const float* x, size_t rows, size_t k, int sub,
-                       int8_t* xq, float* xe, float* xs, hipStream_t s);
-int cx_launch_rmsnorm(float* out, const float* in, const float* w,
-                      size_t rows, size_t n, float eps, hipStream_t s);
+// Producers of the i8 activation, one value per lane:
+//   quantize   : rows x k values of x                           (ops.rs:178)
+//   swiglu     : silu(g) * u, n values                          (forward.rs:483-487)
+//   norm       : rmsnorm(x, w, eps) of one row of n values     (kernels/mod.rs:511)
+int cx_launch_quantize(const float* x, size_t rows, size_t k, int sub, int8_t* xq, float* xe,
+                       float* xs, hipStream_t s);
+int cx_launch_swiglu_quant(const float* g, const float* u, size_t n, int sub, int8_t* xq,
+                           float* xe, float* xs, hipStream_t s);
+int cx_launch_norm_quant(const float* x, const float* w, size_t n, float eps, int sub,
+                         int8_t* xq, float* xe, float* xs, hipStream_t s);
+int cx_launch_rmsnorm(float* out, const float* in, const float* w, size_t rows, size_t n,
+                      float eps, hipStream_t s);
