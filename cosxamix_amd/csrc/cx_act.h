@@ -16,27 +16,49 @@
 
 #include "cx_common.h"
 
-// Every lane of the SUB-lane group holding value `v` at position `i` of the
-// activation (i % SUB == lane % SUB) must call this together.
+// Each lane holds 8 consecutive values v[0..8) at position i (i % 8 == 0);
+// the SUB/8 lanes of one sub-block are consecutive lanes of one quad and
+// must call this together. Writes 8 bytes of xq and, from the sub-block's
+// first lane, its xe and xs.
 template <int SUB>
-__device__ inline void cx_quant_lane(float v, size_t i, int8_t* xq, float* xe, float* xs) {
-  float amax = fabsf(v);
+__device__ inline void cx_quant8(const float (&v)[8], size_t i, int8_t* xq, float* xe,
+                                 float* xs) {
+  static_assert(SUB == 16 || SUB == 32, "sub-blocks of 16 or 32");
+  float amax = 0.0f;
 #pragma unroll
-  for (int o = 1; o < SUB; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, CX_WAVE));
+  for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[j]));
+  amax = fmaxf(amax, cx_xor1f(amax));
+  if (SUB == 32) amax = fmaxf(amax, cx_xor2f(amax));
   float d = 0.0f, inv = 0.0f;
   if (amax > 0.0f) {
     d = amax / 127.0f;
     inv = 127.0f / amax;
   }
-  const int8_t q = cx_rust_i8(roundf(v * inv));
-  int32_t s = q;
+  int32_t s = 0;
+  uint32_t lo = 0, hi = 0;
 #pragma unroll
-  for (int o = 1; o < SUB; o <<= 1) s += __shfl_xor(s, o, CX_WAVE);
-  xq[i] = q;
+  for (int j = 0; j < 8; j++) {
+    const int8_t q = cx_rust_i8(roundf(v[j] * inv));
+    s += q;
+    if (j < 4)
+      lo |= (uint32_t)(uint8_t)q << (8 * j);
+    else
+      hi |= (uint32_t)(uint8_t)q << (8 * (j - 4));
+  }
+  s += cx_xor1(s);
+  if (SUB == 32) s += cx_xor2(s);
+  *reinterpret_cast<uint2*>(xq + i) = make_uint2(lo, hi);
   if ((i & (SUB - 1)) == 0) {
     xe[i / SUB] = d;
     xs[i / SUB] = (float)s;
   }
+}
+
+__device__ inline void cx_load8(const float* p, float (&v)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
 #include "cx_expf.h"

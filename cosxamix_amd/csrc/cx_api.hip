@@ -311,11 +311,7 @@ extern "C" int cx_attention_decode(const float* q, const float* k, const float* 
   CX_REQUIRE(mode >= 0 && mode <= 2, "attention_decode: mode %d", mode);
   CX_REQUIRE(mode != 1 || total <= CX_ATT_EXACT_MAX, "attention_decode: exact mode up to %d",
              CX_ATT_EXACT_MAX);
-  // the decode kernels pick their path from the cache capacity they were
-  // sized for: the exact path for <= CX_ATT_EXACT_MAX, split-K above
-  size_t cap = total;
-  if (mode == 2 && cap <= CX_ATT_EXACT_MAX) cap = CX_ATT_EXACT_MAX + 1;
-  if (mode == 1) cap = total;
+  const size_t cap = total;
   const size_t ns = cx_attn_splits(cap);
   const size_t bytes = 256 + ns * heads * 8 + ns * heads * hd * 4 + heads * cap * 4;
   void* sp = nullptr;
@@ -331,8 +327,22 @@ extern "C" int cx_attention_decode(const float* q, const float* k, const float* 
   // the kernels read the position from device state: pos = total - 1
   cx_dstate h{(uint32_t)(total - 1), 0u, (uint32_t)cap, 0u};
   CX_HIP(hipMemcpyAsync(st, &h, sizeof h, hipMemcpyHostToDevice, s));
-  rc = cx_launch_attn_decode(q, k, v, (uint32_t)heads, (uint32_t)kvh, (uint32_t)hd, st,
-                             (uint32_t)cap, pm, pl, po, sc, out, s);
+  cx_attn_args a{};
+  a.q = (float*)q;  // not written: no rope tables
+  a.kc = (float*)k;
+  a.vc = (float*)v;
+  a.heads = (uint32_t)heads;
+  a.kvh = (uint32_t)kvh;
+  a.hd = (uint32_t)hd;
+  a.cap = (uint32_t)cap;
+  a.st = st;
+  a.pm = pm;
+  a.pl = pl;
+  a.po = po;
+  a.sc = sc;
+  a.out = out;
+  a.mode = mode;
+  rc = cx_launch_attn_decode(a, s);
   if (rc) return rc;
   CX_HIP(hipStreamSynchronize(s));  // the state lives in shared scratch
   return CX_OK;
@@ -431,7 +441,8 @@ extern "C" int cx_model_create_daiss(const cx_config* cfg, int t_lin, int t_down
              "model: zero-sized config");
   CX_REQUIRE(c.dim % c.heads == 0 && c.heads % c.kv_heads == 0, "model: heads do not divide");
   CX_REQUIRE(c.dim % 256 == 0 && c.ffn % 256 == 0, "model: dim and ffn must be multiples of 256");
-  CX_REQUIRE((c.dim / c.heads) % 2 == 0, "model: odd head_dim");
+  CX_REQUIRE(c.dim / c.heads == 64 || c.dim / c.heads == 128,
+             "model: head_dim %u (the decode attention supports 64 and 128)", c.dim / c.heads);
   CX_REQUIRE(cx_is_kquant(t_lin) && cx_is_kquant(t_down) && cx_is_kquant(t_out) &&
                  t_lin != CX_Q6_K && t_down != CX_Q6_K && t_out != CX_Q6_K,
              "model: weights must be Q2_K..Q5_K (the quantizers the reference has)");
@@ -667,14 +678,30 @@ static int enqueue_step(cx_cache* C) {
       return rc;
     cx_seg qkv[3] = {{L.q, m->q, L.q_bias, D}, {L.k, m->k, L.k_bias, kvd}, {L.v, m->v, L.v_bias, kvd}};
     if ((rc = cx_launch_gemv(m->t_lin, qkv, 3, D, act, CX_EPI_STORE, nullptr, s))) return rc;
-    if ((rc = cx_launch_rope_kv(m->q, m->k, m->v, kc, vc, m->cos_t, m->sin_t, c.heads, c.kv_heads,
-                                hd, C->st, s)))
-      return rc;
-    if ((rc = cx_launch_attn_decode(m->q, kc, vc, c.heads, c.kv_heads, hd, C->st, (uint32_t)C->cap,
-                                    C->pm, C->pl, C->po, C->sc, m->att, s)))
-      return rc;
+    cx_attn_args a{};
+    a.q = m->q;
+    a.knew = m->k;
+    a.vnew = m->v;
+    a.kc = kc;
+    a.vc = vc;
+    a.cos_t = m->cos_t;
+    a.sin_t = m->sin_t;
+    a.heads = c.heads;
+    a.kvh = c.kv_heads;
+    a.hd = hd;
+    a.cap = (uint32_t)C->cap;
+    a.st = C->st;
+    a.pm = C->pm;
+    a.pl = C->pl;
+    a.po = C->po;
+    a.sc = C->sc;
+    a.out = m->att;
+    a.xq = m->xq;  // the output projection's activation
+    a.xe = m->xe;
+    a.xs = m->xs;
+    a.sub = sl;
+    if ((rc = cx_launch_attn_decode(a, s))) return rc;
     // src/forward.rs:466-469: output projection added to the residual
-    if ((rc = cx_launch_quantize(m->att, 1, D, sl, m->xq, m->xe, m->xs, s))) return rc;
     cx_seg o{L.o, m->x, nullptr, D};
     if ((rc = cx_launch_gemv(m->t_lin, &o, 1, D, act, CX_EPI_ACCUM, nullptr, s))) return rc;
     // src/forward.rs:472-491: rmsnorm, gate/up, SwiGLU, down added to the residual

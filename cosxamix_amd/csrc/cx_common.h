@@ -81,6 +81,16 @@ __device__ inline float cx_h2f(uint32_t h16) {
 __device__ inline int cx_xor1(int v) {
   return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
 }
+// lane i <- lane i^2, inside a quad (DPP quad_perm [2,3,0,1])
+__device__ inline int cx_xor2(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+}
+__device__ inline float cx_xor1f(float v) {
+  return __int_as_float(cx_xor1(__float_as_int(v)));
+}
+__device__ inline float cx_xor2f(float v) {
+  return __int_as_float(cx_xor2(__float_as_int(v)));
+}
 
 // Deterministic wave64 sum: butterfly, every lane ends with the same value.
 __device__ inline float cx_wave_sum(float v) {

@@ -482,19 +482,30 @@ int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k, const cx_
 
 // ------------------------------------------------- activation kernels
 namespace {
-// x: rows*k values; a sub-block never straddles two rows (k % SUB == 0)
+// 8 values per lane; n % SUB == 0, so a lane group is either wholly inside
+// [0, n) or wholly past it. x: rows*k values; a sub-block never straddles
+// two rows (k % SUB == 0).
 template <int SUB>
 __global__ __launch_bounds__(256) void k_quantize(const float* x, size_t n, int8_t* xq,
                                                   float* xe, float* xs) {
-  const size_t i = blockIdx.x * 256ull + threadIdx.x;
-  if (i < n) cx_quant_lane<SUB>(x[i], i, xq, xe, xs);  // n % SUB == 0: whole groups
+  const size_t i = 8 * (blockIdx.x * 256ull + threadIdx.x);
+  if (i >= n) return;
+  float v[8];
+  cx_load8(x + i, v);
+  cx_quant8<SUB>(v, i, xq, xe, xs);
 }
 
 template <int SUB>
 __global__ __launch_bounds__(256) void k_swiglu_quant(const float* g, const float* u, uint32_t n,
                                                       int8_t* xq, float* xe, float* xs) {
-  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-  if (i < n) cx_quant_lane<SUB>(cx_swiglu(g[i], u[i]), i, xq, xe, xs);
+  const uint32_t i = 8 * (blockIdx.x * 256u + threadIdx.x);
+  if (i >= n) return;
+  float v[8], w[8];
+  cx_load8(g + i, v);
+  cx_load8(u + i, w);
+#pragma unroll
+  for (int j = 0; j < 8; j++) v[j] = cx_swiglu(v[j], w[j]);
+  cx_quant8<SUB>(v, i, xq, xe, xs);
 }
 
 // rmsnorm (src/kernels/scalar.rs:40-53) of one row, then its quantization:
@@ -504,8 +515,14 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float* x, const float*
                                                     float eps, int8_t* xq, float* xe, float* xs) {
   __shared__ double red[4];
   const double scale = cx_rms_scale(x, n, eps, red);
-  for (uint32_t i = threadIdx.x; i < n; i += 256)  // n % 256 == 0: whole groups
-    cx_quant_lane<SUB>((float)((double)x[i] * scale) * w[i], i, xq, xe, xs);
+  for (uint32_t i = 8 * threadIdx.x; i < n; i += 8 * 256) {  // n % SUB == 0: whole groups
+    float v[8], nw[8];
+    cx_load8(x + i, v);
+    cx_load8(w + i, nw);
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = (float)((double)v[j] * scale) * nw[j];
+    cx_quant8<SUB>(v, i, xq, xe, xs);
+  }
 }
 
 __global__ __launch_bounds__(256) void k_rmsnorm(float* out, const float* in, const float* w,
@@ -523,9 +540,11 @@ int cx_launch_quantize(const float* x, size_t rows, size_t k, int sub, int8_t* x
   CX_REQUIRE(sub == 16 || sub == 32, "quantize: sub must be 16 or 32, got %d", sub);
   CX_REQUIRE(k % (size_t)sub == 0, "quantize: k=%zu not a multiple of %d", k, sub);
   CX_REQUIRE(x && xq && xe && xs, "quantize: null pointer");
+  CX_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)xq & 7) == 0,
+             "quantize: x must be 16-byte and xq 8-byte aligned");
   const size_t n = rows * k;
   if (!n) return CX_OK;
-  const size_t grid = (n + 255) / 256;
+  const size_t grid = (n / 8 + 255) / 256;
   CX_REQUIRE(grid < (1ull << 31), "quantize: %zu values is too many", n);
   if (sub == 16)
     hipLaunchKernelGGL(k_quantize<16>, dim3((unsigned)grid), dim3(256), 0, s, x, n, xq, xe, xs);
@@ -539,7 +558,7 @@ int cx_launch_swiglu_quant(const float* g, const float* u, size_t n, int sub, in
                            float* xe, float* xs, hipStream_t s) {
   CX_REQUIRE(sub == 16 || sub == 32, "swiglu: sub must be 16 or 32, got %d", sub);
   CX_REQUIRE(n % (size_t)sub == 0 && n < (1u << 31), "swiglu: bad width %zu", n);
-  const unsigned grid = (unsigned)((n + 255) / 256);
+  const unsigned grid = (unsigned)((n / 8 + 255) / 256);
   if (sub == 16)
     hipLaunchKernelGGL(k_swiglu_quant<16>, dim3(grid), dim3(256), 0, s, g, u, (uint32_t)n, xq, xe, xs);
   else

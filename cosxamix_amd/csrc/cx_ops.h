@@ -24,10 +24,26 @@ int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float
                       const float* cos_t, const float* sin_t, uint32_t heads, uint32_t kvh,
                       uint32_t hd, const cx_dstate* st, hipStream_t s);
 size_t cx_attn_splits(size_t cap);
-int cx_launch_attn_decode(const float* q, const float* kc, const float* vc, uint32_t heads,
-                          uint32_t kvh, uint32_t hd, const cx_dstate* st, uint32_t cap,
-                          float* pm, float* pl, float* po, float* sc, float* out,
-                          hipStream_t s);
+
+// One decode step's attention (src/ops.rs:1258-1325 at tokens = 1).
+struct cx_attn_args {
+  float* q;                    // heads*hd; rotated in place by the split-K path
+  const float* knew;           // this step's k and v (kvh*hd), used with rope
+  const float* vnew;
+  float* kc;                   // caches [cap][kvh*hd]
+  float* vc;
+  const float* cos_t;          // rope tables; null: q is final and the caches
+  const float* sin_t;          //   already hold position st->pos
+  uint32_t heads, kvh, hd, cap;
+  const cx_dstate* st;
+  float *pm, *pl, *po, *sc;    // split-K partials, exact-path scores
+  float* out;                  // heads*hd
+  int8_t* xq;                  // optional: out quantized for the next GEMV
+  float *xe, *xs;
+  int sub;
+  int mode;                    // 0: by cap, 1: order-exact, 2: split-K
+};
+int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s);
 int cx_launch_attention(const float* q, const float* k, const float* v, size_t tokens,
                         size_t total, size_t heads, size_t kvh, size_t hd, float* out,
                         hipStream_t s);

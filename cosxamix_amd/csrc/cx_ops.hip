@@ -206,39 +206,106 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 
 // ------------------------------------------- order-exact decode attention
 // The decode step's attention in the reference's own order, for contexts up
-// to CX_ATT_EXACT_MAX. Scores: one thread per (head, position), the
-// sequential dot of src/kernels/scalar.rs:16-23 times 1/sqrt(hd), written to
-// sc[head][pos]. Then one workgroup per head: exact max, e = exp(s - max)
-// (glibc's expf), the sequential sum, p = e * (1/sum) (src/ops.rs:1218-1229),
-// and out[d] = sum over p of prob_p * v_p[d] in position order
-// (src/ops.rs:1316-1321). Bit-identical to the scalar reference.
-__global__ __launch_bounds__(256) void k_attn_scores(const float* q, const float* kc,
-                                                     uint32_t heads, uint32_t kvh, uint32_t hd,
-                                                     const cx_dstate* st, float scale,
-                                                     float* sc, uint32_t cap) {
-  const uint32_t total = st->pos + 1;
-  const uint32_t p = blockIdx.x * 256 + threadIdx.x, h = blockIdx.y;
-  if (p >= total) return;
-  const uint32_t g = h / (heads / kvh);
-  const float4* qh = reinterpret_cast<const float4*>(q + h * hd);
-  const float4* kp = reinterpret_cast<const float4*>(kc + (size_t)p * kvh * hd + g * hd);
+// to CX_ATT_EXACT_MAX, in two kernels.
+//
+// k_attn_scores, workgroup (split, head h): positions [64*split, +64), one
+// lane each: the sequential dot of src/kernels/scalar.rs:16-23 times
+// 1/sqrt(hd), written to sc[h][p]. With rope tables it first rotates q and
+// this step's key (src/ops.rs:1185-1188: a' = a*c - b*s, b' = a*s + b*c,
+// no FMA); the first head of each KV group appends the rotated key and the
+// value to the cache at st->pos (src/forward.rs:454-455). The score at st->pos
+// uses the rotated key from LDS, so no workgroup reads a cache row written in
+// the same launch.
+//
+// k_attn_seq, one workgroup per head: exact max, e = exp(s - max) (glibc's
+// expf), the sequential sum, p = e * (1/sum) (src/ops.rs:1218-1229), and
+// out[d] = sum over p of prob_p * v_p[d] in position order
+// (src/ops.rs:1316-1321), with V prefetched 32 positions ahead. The head's
+// output is then quantized for the output projection (its head_dim values
+// are whole sub-blocks). Bit-identical to the scalar reference.
+constexpr uint32_t SC_P = 64;  // positions per scores workgroup
+
+template <int HD>
+__device__ inline float seq_dot(const float* a_lds, const float* b) {
+  float4 r[HD / 4];
+#pragma unroll
+  for (int i = 0; i < HD / 4; i++) r[i] = reinterpret_cast<const float4*>(b)[i];
   float s = 0.0f;
-  for (uint32_t d = 0; d < hd / 4; d++) {
-    const float4 a = qh[d], b = kp[d];
-    s += a.x * b.x;
-    s += a.y * b.y;
-    s += a.z * b.z;
-    s += a.w * b.w;
+#pragma unroll
+  for (int i = 0; i < HD / 4; i++) {
+    const float4 a = reinterpret_cast<const float4*>(a_lds)[i];
+    s += a.x * r[i].x;
+    s += a.y * r[i].y;
+    s += a.z * r[i].z;
+    s += a.w * r[i].w;
+  }
+  return s;
+}
+
+template <int HD>
+__global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float* knew,
+                                                    const float* vnew, float* kc, float* vc,
+                                                    const float* cos_t, const float* sin_t,
+                                                    uint32_t heads, uint32_t kvh,
+                                                    const cx_dstate* st, float scale,
+                                                    float* sc, uint32_t cap) {
+  __shared__ __align__(16) float qr[HD];
+  __shared__ __align__(16) float kr[HD];
+  constexpr uint32_t half = HD / 2;
+  const uint32_t pos = st->pos, total = pos + 1;
+  const uint32_t p0 = blockIdx.x * SC_P, h = blockIdx.y, per = heads / kvh, g = h / per;
+  if (p0 >= total) return;
+  const uint32_t kvd = kvh * HD;
+  const int t = threadIdx.x;
+  const bool rot = cos_t != nullptr, has_new = rot && pos < p0 + SC_P;
+  if (rot) {
+    const float* c = cos_t + (size_t)pos * half;
+    const float* s = sin_t + (size_t)pos * half;
+    for (uint32_t j = t; j < half; j += 64) {
+      const float x0 = q[h * HD + j], x1 = q[h * HD + j + half];
+      qr[j] = x0 * c[j] - x1 * s[j];
+      qr[j + half] = x0 * s[j] + x1 * c[j];
+      if (has_new) {
+        const float k0 = knew[g * HD + j], k1 = knew[g * HD + j + half];
+        const float a = k0 * c[j] - k1 * s[j], b = k0 * s[j] + k1 * c[j];
+        kr[j] = a;
+        kr[j + half] = b;
+        if (h % per == 0) {
+          float* kd = kc + (size_t)pos * kvd + g * HD;
+          float* vd = vc + (size_t)pos * kvd + g * HD;
+          kd[j] = a;
+          kd[j + half] = b;
+          vd[j] = vnew[g * HD + j];
+          vd[j + half] = vnew[g * HD + j + half];
+        }
+      }
+    }
+  } else {
+    for (uint32_t j = t; j < HD; j += 64) qr[j] = q[h * HD + j];
+  }
+  __syncthreads();
+  const uint32_t p = p0 + t;
+  if (p >= total) return;
+  float s;
+  if (has_new && p == pos) {
+    s = 0.0f;
+    for (int d = 0; d < HD; d++) s += qr[d] * kr[d];
+  } else {
+    s = seq_dot<HD>(qr, kc + (size_t)p * kvd + g * HD);
   }
   sc[(size_t)h * cap + p] = s * scale;
 }
 
+constexpr int PV_CHUNK = 32;
+
+template <int HD, int SUB>
 __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
-                                                  uint32_t heads, uint32_t kvh, uint32_t hd,
-                                                  const cx_dstate* st, uint32_t cap,
-                                                  float* out) {
+                                                  uint32_t heads, uint32_t kvh,
+                                                  const cx_dstate* st, uint32_t cap, float* out,
+                                                  int8_t* xq, float* xe, float* xs) {
   extern __shared__ __align__(16) float e[];
   __shared__ float red[4];
+  __shared__ __align__(16) float os[HD];
   const uint32_t total = st->pos + 1, h = blockIdx.x, g = h / (heads / kvh);
   const float* sc = sc_all + (size_t)h * cap;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -254,21 +321,38 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   __syncthreads();
   seq_softmax_inplace(e, total, mx, red);
-  const size_t kvd = (size_t)kvh * hd;
-  for (uint32_t d = tid; d < hd; d += 256) {
-    const float* vp = vc + g * hd + d;
+  if (tid < HD) {
+    const size_t kvd = (size_t)kvh * HD;
+    const float* vp = vc + g * HD + tid;
+    float cur[PV_CHUNK], nxt[PV_CHUNK];
+#pragma unroll
+    for (int j = 0; j < PV_CHUNK; j++) cur[j] = (uint32_t)j < total ? vp[j * kvd] : 0.0f;
     float o = 0.0f;
-    uint32_t p = 0;
-    for (; p + 4 <= total; p += 4) {  // loads hoisted, adds in position order
-      const float v0 = vp[p * kvd], v1 = vp[(p + 1) * kvd], v2 = vp[(p + 2) * kvd],
-                  v3 = vp[(p + 3) * kvd];
-      o += e[p] * v0;
-      o += e[p + 1] * v1;
-      o += e[p + 2] * v2;
-      o += e[p + 3] * v3;
+    for (uint32_t p0 = 0; p0 < total; p0 += PV_CHUNK) {
+      const uint32_t pn = p0 + PV_CHUNK;
+#pragma unroll
+      for (int j = 0; j < PV_CHUNK; j++) nxt[j] = pn + j < total ? vp[(pn + j) * kvd] : 0.0f;
+      if (p0 + PV_CHUNK <= total) {
+#pragma unroll
+        for (int j = 0; j < PV_CHUNK; j++) o += e[p0 + j] * cur[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < PV_CHUNK; j++)
+          if (p0 + j < total) o += e[p0 + j] * cur[j];
+      }
+#pragma unroll
+      for (int j = 0; j < PV_CHUNK; j++) cur[j] = nxt[j];
     }
-    for (; p < total; p++) o += e[p] * vp[p * kvd];
-    out[h * hd + d] = o;
+    out[h * HD + tid] = o;
+    os[tid] = o;
+  }
+  if (!xq) return;
+  __syncthreads();
+  if (tid < HD / 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = os[8 * tid + j];
+    cx_quant8<SUB>(v, (size_t)h * HD + 8 * tid, xq, xe, xs);
   }
 }
 
@@ -447,30 +531,52 @@ int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float
 
 size_t cx_attn_splits(size_t cap) { return (cap + ATT_P - 1) / ATT_P; }
 
-int cx_launch_attn_decode(const float* q, const float* kc, const float* vc, uint32_t heads,
-                          uint32_t kvh, uint32_t hd, const cx_dstate* st, uint32_t cap,
-                          float* pm, float* pl, float* po, float* sc, float* out,
-                          hipStream_t s) {
+namespace {
+template <int HD>
+int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
+  hipLaunchKernelGGL(k_attn_scores<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads), dim3(64), 0, s,
+                     a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads, a.kvh, a.st,
+                     scale, a.sc, a.cap);
+  CX_HIP(hipGetLastError());
+  const size_t lds = a.cap * sizeof(float);
+  if (a.sub == 16)
+    hipLaunchKernelGGL((k_attn_seq<HD, 16>), dim3(a.heads), dim3(256), lds, s, a.vc, a.sc, a.heads,
+                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+  else
+    hipLaunchKernelGGL((k_attn_seq<HD, 32>), dim3(a.heads), dim3(256), lds, s, a.vc, a.sc, a.heads,
+                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+}  // namespace
+
+int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s) {
+  const uint32_t heads = a.heads, kvh = a.kvh, hd = a.hd;
   CX_REQUIRE(kvh && heads % kvh == 0 && heads / kvh <= ATT_MAXG, "attention: %u heads / %u groups",
              heads, kvh);
-  CX_REQUIRE(hd % 4 == 0, "attention: head_dim %u must be a multiple of 4", hd);
+  CX_REQUIRE(hd == 64 || hd == 128, "attention: head_dim %u (64 or 128 supported)", hd);
+  CX_REQUIRE(!a.xq || ((a.sub == 16 || a.sub == 32) && a.xe && a.xs),
+             "attention: quantized output needs sub 16 or 32");
+  CX_REQUIRE(!a.cos_t || (a.knew && a.vnew && a.sin_t), "attention: rope needs the new k/v");
   const float scale = 1.0f / sqrtf((float)hd);
-  if (cap <= CX_ATT_EXACT_MAX) {
-    hipLaunchKernelGGL(k_attn_scores, dim3((cap + 255) / 256, heads), dim3(256), 0, s, q, kc,
-                       heads, kvh, hd, st, scale, sc, cap);
-    CX_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_attn_seq, dim3(heads), dim3(256), cap * sizeof(float), s, vc, sc, heads,
-                       kvh, hd, st, cap, out);
-    CX_HIP(hipGetLastError());
-    return CX_OK;
+  const bool exact = a.mode == 1 || (a.mode == 0 && a.cap <= CX_ATT_EXACT_MAX);
+  if (exact) {
+    CX_REQUIRE(a.cap <= CX_ATT_EXACT_MAX, "attention: exact path up to %d tokens", CX_ATT_EXACT_MAX);
+    return hd == 64 ? launch_exact<64>(a, scale, s) : launch_exact<128>(a, scale, s);
   }
-  const uint32_t ns = (uint32_t)cx_attn_splits(cap), per = heads / kvh;
+  int rc;
+  if (a.cos_t && (rc = cx_launch_rope_kv(a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, heads,
+                                         kvh, hd, a.st, s)))
+    return rc;
+  const uint32_t ns = (uint32_t)cx_attn_splits(a.cap), per = heads / kvh;
   const size_t lds = sizeof(float) * (per * hd + ATT_P * (hd + 1) + per * ATT_P);
-  hipLaunchKernelGGL(k_attn_split, dim3(ns, kvh), dim3(256), lds, s, q, kc, vc, heads, kvh, hd,
-                     st, scale, pm, pl, po, ns);
+  hipLaunchKernelGGL(k_attn_split, dim3(ns, kvh), dim3(256), lds, s, a.q, a.kc, a.vc, heads, kvh,
+                     hd, a.st, scale, a.pm, a.pl, a.po, ns);
   CX_HIP(hipGetLastError());
-  hipLaunchKernelGGL(k_attn_combine, dim3(heads), dim3(128), 0, s, pm, pl, po, heads, hd, st, out);
+  hipLaunchKernelGGL(k_attn_combine, dim3(heads), dim3(128), 0, s, a.pm, a.pl, a.po, heads, hd,
+                     a.st, a.out);
   CX_HIP(hipGetLastError());
+  if (a.xq) return cx_launch_quantize(a.out, 1, (size_t)heads * hd, a.sub, a.xq, a.xe, a.xs, s);
   return CX_OK;
 }
 
