@@ -313,16 +313,19 @@ extern "C" int cx_attention_decode(const float* q, const float* k, const float* 
              CX_ATT_EXACT_MAX);
   const size_t cap = total;
   const size_t ns = cx_attn_splits(cap);
-  const size_t bytes = 256 + ns * heads * 8 + ns * heads * hd * 4 + heads * cap * 4;
+  auto up = [](size_t n) { return (n + 255) / 256 * 256; };
+  const size_t o_pm = 256, o_pl = o_pm + up(ns * heads * 4), o_po = o_pl + up(ns * heads * 4),
+               o_sc = o_po + up(ns * heads * hd * 4),
+               bytes = o_sc + up(cx_attn_score_floats(heads, cap) * 4);
   void* sp = nullptr;
   int rc = cx_scratch_reserve(bytes, &sp);
   if (rc) return rc;
   uint8_t* b = (uint8_t*)sp;
   cx_dstate* st = (cx_dstate*)b;
-  float* pm = (float*)(b + 256);
-  float* pl = pm + ns * heads;
-  float* po = pl + ns * heads;
-  float* sc = po + ns * heads * hd;
+  float* pm = (float*)(b + o_pm);
+  float* pl = (float*)(b + o_pl);
+  float* po = (float*)(b + o_po);
+  float* sc = (float*)(b + o_sc);
   hipStream_t s = STREAM(stream);
   // the kernels read the position from device state: pos = total - 1
   cx_dstate h{(uint32_t)(total - 1), 0u, (uint32_t)cap, 0u};
@@ -627,7 +630,7 @@ extern "C" int cx_cache_new(cx_model* m, size_t cap, cx_cache** out) {
   if (hipMalloc(&C->kv, (size_t)c.layers * 2 * cap * kvd * 4) || hipMalloc(&C->hist, (cap + 1) * 4) ||
       hipMalloc(&C->st, sizeof(cx_dstate)) || hipMalloc(&C->pm, ns * c.heads * 4) ||
       hipMalloc(&C->pl, ns * c.heads * 4) || hipMalloc(&C->po, ns * c.heads * (c.dim / c.heads) * 4) ||
-      hipMalloc(&C->sc, (size_t)c.heads * cap * 4)) {
+      hipMalloc(&C->sc, cx_attn_score_floats(c.heads, cap) * 4)) {
     cx_cache_free(C);
     cx_set_error("cache: cannot allocate %zu tokens", cap);
     return CX_ENOMEM;
@@ -674,10 +677,9 @@ static int enqueue_step(cx_cache* C) {
     float* kc = C->kv + (size_t)li * 2 * C->cap * kvd;
     float* vc = kc + C->cap * kvd;
     // src/forward.rs:422-464: rmsnorm, q/k/v with bias, rope, attention
-    if ((rc = cx_launch_norm_quant(m->x, L.attn_norm, D, c.eps, sl, m->xq, m->xe, m->xs, s)))
-      return rc;
     cx_seg qkv[3] = {{L.q, m->q, L.q_bias, D}, {L.k, m->k, L.k_bias, kvd}, {L.v, m->v, L.v_bias, kvd}};
-    if ((rc = cx_launch_gemv(m->t_lin, qkv, 3, D, act, CX_EPI_STORE, nullptr, s))) return rc;
+    if ((rc = cx_launch_gemv_norm(m->t_lin, qkv, 3, D, m->x, L.attn_norm, c.eps, CX_EPI_STORE, s)))
+      return rc;
     cx_attn_args a{};
     a.q = m->q;
     a.knew = m->k;
@@ -705,10 +707,9 @@ static int enqueue_step(cx_cache* C) {
     cx_seg o{L.o, m->x, nullptr, D};
     if ((rc = cx_launch_gemv(m->t_lin, &o, 1, D, act, CX_EPI_ACCUM, nullptr, s))) return rc;
     // src/forward.rs:472-491: rmsnorm, gate/up, SwiGLU, down added to the residual
-    if ((rc = cx_launch_norm_quant(m->x, L.ffn_norm, D, c.eps, sl, m->xq, m->xe, m->xs, s)))
-      return rc;
     cx_seg gu[2] = {{L.gate, m->g, nullptr, I}, {L.up, m->u, nullptr, I}};
-    if ((rc = cx_launch_gemv(m->t_lin, gu, 2, D, act, CX_EPI_STORE, nullptr, s))) return rc;
+    if ((rc = cx_launch_gemv_norm(m->t_lin, gu, 2, D, m->x, L.ffn_norm, c.eps, CX_EPI_STORE, s)))
+      return rc;
     if ((rc = cx_launch_swiglu_quant(m->g, m->u, I, sd, m->xq, m->xe, m->xs, s))) return rc;
     cx_seg dn{L.down, m->x, nullptr, D};
     if ((rc = cx_launch_gemv(m->t_down, &dn, 1, I, act, CX_EPI_ACCUM, nullptr, s))) return rc;

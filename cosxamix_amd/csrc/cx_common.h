@@ -111,6 +111,40 @@ __device__ inline float cx_wave_max(float v) {
   return v;
 }
 
+// Pipelines of direct-to-LDS loads (global_load_lds) need partial waits:
+// __syncthreads() carries a workgroup fence after which the compiler waits
+// for every outstanding vector load (vmcnt(0)), draining the pipeline. These
+// wait exactly as asked; their "memory" clobbers keep the compiler from
+// moving memory accesses across them.
+typedef __attribute__((address_space(3))) void* cx_lds_ptr;
+template <int N>
+__device__ inline void cx_wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ inline void cx_wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+__device__ inline void cx_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// 16 bytes from global `g` into LDS at (wave-uniform) `l` + 16 * lane
+__device__ inline void cx_dma16(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds(g, (cx_lds_ptr)l, 16, 0, 0);
+}
+// The same load hidden from the compiler: it then inserts no wait of its own
+// before later LDS reads (it would wait for every load, since it cannot tell
+// which LDS bytes are in flight). The caller orders the data with
+// cx_wait_vm<N>() — loads complete in issue order — and must not leave the
+// kernel with such a load outstanding.
+// `l` must be the same for every lane of the wave; M0 (the LDS address of
+// the load) is saved and restored around it.
+__device__ inline void cx_dma16_async(const void* g, void* l) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(cx_lds_ptr)l);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\ts_nop 0\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(la), "v"(g)
+      : "memory");
+}
+
 // Rust `f32 as i32` (saturating, NaN -> 0) then `as i8` (low 8 bits).
 __device__ inline int8_t cx_rust_i8(float r) {
   int32_t v;

@@ -36,12 +36,9 @@
    0x3fef3720dcef9069ull, 0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full,        \
    0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull}
 
-CX_HD static inline uint64_t cx_exp2_tab(uint32_t i) {
-  const uint64_t t[32] = CX_EXP2_TAB;
-  return t[i & 31];
-}
-
-CX_HD static inline float cx_expf(float x) {
+// `tab` holds CX_EXP2_TAB (a device kernel may keep a copy in LDS, so that
+// exp issues no global loads)
+CX_HD static inline float cx_expf_tab(float x, const uint64_t* tab) {
   uint32_t ux;
   memcpy(&ux, &x, 4);
   const uint32_t abstop = (ux >> 20) & 0x7ff;
@@ -61,7 +58,7 @@ CX_HD static inline float cx_expf(float x) {
   memcpy(&ki, &kd, 8);
   kd -= shift;
   const double r = fma(inv_ln2_n, xd, -kd);
-  uint64_t t = cx_exp2_tab((uint32_t)(ki % 32));
+  uint64_t t = tab[ki % 32];
   t += ki << (52 - 5);
   double s;
   memcpy(&s, &t, 8);
@@ -71,4 +68,9 @@ CX_HD static inline float cx_expf(float x) {
   y = fma(z, r2, y);
   y = y * s;
   return (float)y;
+}
+
+CX_HD static inline float cx_expf(float x) {
+  const uint64_t t[32] = CX_EXP2_TAB;
+  return cx_expf_tab(x, t);
 }

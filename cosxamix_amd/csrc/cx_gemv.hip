@@ -14,13 +14,13 @@
 // and a tile fits in 64 KiB of LDS; with several workgroups resident per CU
 // the whole matrix is in flight within one wave of workgroups.
 //
-// Arithmetic. A super-block (256 values) is handled by 8 consecutive lanes,
-// one "slot" each. A lane reads its slice of the block from LDS, unpacks the
-// quants and the 6-bit scales in registers and forms integer partial sums
-// with v_dot4c_i32_i8. The two lanes that share a sub-block swap partial
-// sums with one DPP move, so every sub-block integer sum E_j is formed
-// exactly. The lane that owns sub-block j then computes the reference's f32
-// term with the reference's rounding:
+// Arithmetic. One lane handles one super-block (256 values) of one row: it
+// reads the block from LDS, unpacks the quants and the 6-bit scales in
+// registers (the sub-block index is a compile-time constant, so every shift
+// is an immediate) and forms each sub-block's integer sum E_j exactly with
+// v_dot4c_i32_i8 against the i8 activation in LDS (lanes of different rows
+// read the same activation bytes: LDS broadcast). It then computes each
+// sub-block's f32 term with the reference's rounding:
 //   Q4_K/Q5_K/Q2_K : xe[j] * ((d*sc_j)*E_j - (dmin*mn_j)*xs[j])
 //   Q3_K           : (xe[j] * (d*(esc_j-32))) * (E'_j - 4*xs[j])
 //   Q6_K           : (xe[j] * (d*esc_j)) * (E'_j - 32*xs[j])
@@ -33,259 +33,251 @@
 
 namespace {
 
-constexpr uint32_t M4 = 0x0F0F0F0Fu;
+constexpr uint32_t M4 = 0x0F0F0F0Fu, M2 = 0x03030303u, M1 = 0x01010101u;
 constexpr uint32_t TILE_LDS_MAX = 64 * 1024;
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 __device__ inline int dot4(uint32_t a, int b, int c) {
   return __builtin_amdgcn_sdot4((int)a, b, c, false);
 }
-// a dword at any byte offset of LDS: two aligned reads and v_alignbyte_b32.
-// May read up to 3 bytes past off+4 (the tile region is padded for it).
-__device__ inline uint32_t lds32(const uint8_t* lds, uint32_t off) {
+// N dwords starting at any byte offset of LDS: N+1 aligned reads and
+// v_alignbyte_b32. May read up to 7 bytes past off + 4N (the tile region is
+// padded for it).
+template <int N>
+__device__ inline void lds_words(const uint8_t* lds, uint32_t off, uint32_t (&w)[N]) {
   const uint32_t* q = reinterpret_cast<const uint32_t*>(lds + (off & ~3u));
-  return __builtin_amdgcn_alignbyte(q[1], q[0], off & 3u);
+  const uint32_t sh = off & 3u;
+  uint32_t a[N + 1];
+#pragma unroll
+  for (int i = 0; i <= N; i++) a[i] = q[i];
+#pragma unroll
+  for (int i = 0; i < N; i++) w[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], sh);
+}
+// 8 activation words (32 bytes) of one 32-value group
+__device__ inline void act8(const int8_t* x, int (&v)[8]) {
+  const int4 a = reinterpret_cast<const int4*>(x)[0], b = reinterpret_cast<const int4*>(x)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// Two lanes per super-block: lane half h = 0, 1 computes the terms of
+// sub-blocks [SPB/2 h, SPB/2 (h+1)) — the integer sums E_j with
+// v_dot4c_i32_i8 (exact), then the reference's f32 term with the reference's
+// rounding, written to to[j]; dbg (if set) receives E_j. xb points at the
+// block's 256 activation bytes.
 template <int T> struct KQ;
 
 // ------------------------------------------------------------------ Q4_K
-// 144 B: d(2) dmin(2) scales(12) qs(128). Slot l: pair p = l/2, half h = l%2,
-// qs bytes [16+32p+16h, +16): low nibbles -> sub-block 2p positions
-// 16h..16h+15, high nibbles -> sub-block 2p+1 same positions.
-// Blocks are read as 16-byte words: the tile must start 16-byte aligned.
+// 144 B: d(2) dmin(2) scales(12) qs(128). Pair p = 0..3: qs bytes
+// [32p, 32p+32) hold sub-block 2p (low nibbles) and 2p+1 (high nibbles),
+// positions 0..31 (src/kernels/scalar.rs:132-170). Half h owns pairs 2h and
+// 2h+1. Blocks are read as 16-byte words: the tile must start 16-byte
+// aligned.
 template <> struct KQ<CX_Q4_K> {
-  static constexpr int BPB = 144, SUB = 32, NW = 8;
+  static constexpr int BPB = 144, SUB = 32;
   static constexpr bool ALIGNED = true;
-  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
-    uint4 h = *reinterpret_cast<const uint4*>(lds + off);
-    uint4 q = *reinterpret_cast<const uint4*>(lds + off + 16 + 16 * l);
-    r[0] = h.x; r[1] = h.y; r[2] = h.z; r[3] = h.w;
-    r[4] = q.x; r[5] = q.y; r[6] = q.z; r[7] = q.w;
-  }
-  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg, float* to) {
-    const int p = l >> 1, h = l & 1;
-    const int4 xa = *reinterpret_cast<const int4*>(xb + 64 * p + 16 * h);
-    const int4 xc = *reinterpret_cast<const int4*>(xb + 64 * p + 32 + 16 * h);
-    int e0 = dot4(r[4] & M4, xa.x, 0);
-    e0 = dot4(r[5] & M4, xa.y, e0);
-    e0 = dot4(r[6] & M4, xa.z, e0);
-    e0 = dot4(r[7] & M4, xa.w, e0);
-    int e1 = dot4((r[4] >> 4) & M4, xc.x, 0);
-    e1 = dot4((r[5] >> 4) & M4, xc.y, e1);
-    e1 = dot4((r[6] >> 4) & M4, xc.z, e1);
-    e1 = dot4((r[7] >> 4) & M4, xc.w, e1);
-    finish(r, h ? e0 : e1, h ? e1 : e0, 2 * p + h, xe, xs, dbg, to);
-  }
-  // shared with Q5_K: exchange, 6-bit scale unpack, the f32 term
-  template <int N>
-  __device__ static void finish(const uint32_t (&r)[N], int send, int mine, int j,
-                                 const float* xe, const float* xs, int32_t* dbg, float* to) {
-    const int e = mine + cx_xor1(send);
-    // branch-free 6-bit unpack, the word form of src/kernels/x86.rs:437-447;
-    // equal to quant::escala_y_minimo (src/quant.rs:108-117)
-    const uint32_t a = r[1], b = r[2], c = r[3];
-    const int sh = 8 * (j & 3);
-    uint32_t sc, mn;
-    if (j < 4) {
-      sc = (a >> sh) & 63;
-      mn = (b >> sh) & 63;
+  // quant::escala_y_minimo (src/quant.rs:108-117) for sub-blocks 4h..4h+3,
+  // four at a time, one per byte: h = 0 takes the low 6 bits of bytes 0..3
+  // (a: scales, b: mins); h = 1 the nibbles of c plus the top 2 bits of a/b
+  __device__ static void scales_mins(int h, uint32_t a, uint32_t b, uint32_t c, uint32_t& sc,
+                                     uint32_t& mn) {
+    const uint32_t lo6 = 0x3F3F3F3Fu, top = M2;
+    if (h == 0) {
+      sc = a & lo6;
+      mn = b & lo6;
     } else {
-      sc = ((c >> sh) & 0xF) | (((a >> sh) >> 6 & 3) << 4);
-      mn = ((c >> sh) >> 4 & 0xF) | (((b >> sh) >> 6 & 3) << 4);
+      sc = (c & M4) | (((a >> 6) & top) << 4);
+      mn = ((c >> 4) & M4) | (((b >> 6) & top) << 4);
     }
-    const float d = cx_h2f(r[0] & 0xFFFF), dm = cx_h2f(r[0] >> 16);
+  }
+  __device__ static void term(int j, int jj, int e, float d, float dm, uint32_t sc4, uint32_t mn4,
+                              const float* xe, const float* xs, int32_t* dbg, float* to) {
+    const uint32_t sc = (sc4 >> (8 * jj)) & 0xFF, mn = (mn4 >> (8 * jj)) & 0xFF;
     if (dbg) dbg[j] = e;
     to[j] = xe[j] * (d * (float)sc * (float)e - dm * (float)mn * xs[j]);
+  }
+  __device__ static void half(const uint8_t* lds, uint32_t off, int h, const int8_t* xb,
+                              const float* xe, const float* xs, int32_t* dbg, float* to) {
+    const uint4* bw = reinterpret_cast<const uint4*>(lds + off);
+    const uint4 hd = bw[0];
+    const float d = cx_h2f(hd.x & 0xFFFF), dm = cx_h2f(hd.x >> 16);
+    uint32_t sc4, mn4;
+    scales_mins(h, hd.y, hd.z, hd.w, sc4, mn4);
+#pragma unroll
+    for (int pp = 0; pp < 2; pp++) {
+      const int p = 2 * h + pp;
+      const uint4 u0 = bw[1 + 2 * p], u1 = bw[2 + 2 * p];
+      const uint32_t q[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+      int xa[8], xc[8];
+      act8(xb + 64 * p, xa);
+      act8(xb + 64 * p + 32, xc);
+      int e0 = 0, e1 = 0;
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        e0 = dot4(q[w] & M4, xa[w], e0);
+        e1 = dot4((q[w] >> 4) & M4, xc[w], e1);
+      }
+      term(2 * p, 2 * pp, e0, d, dm, sc4, mn4, xe, xs, dbg, to);
+      term(2 * p + 1, 2 * pp + 1, e1, d, dm, sc4, mn4, xe, xs, dbg, to);
+    }
   }
 };
 
 // ------------------------------------------------------------------ Q5_K
 // 176 B: d dmin scales(12) qh(32) qs(128). As Q4_K plus the fifth bit of
-// position i of sub-block j = bit j of qh[i] (src/kernels/scalar.rs:205-210).
+// position i of sub-block j = bit j of qh[i] (src/kernels/scalar.rs:179-217).
 template <> struct KQ<CX_Q5_K> {
-  static constexpr int BPB = 176, SUB = 32, NW = 12;
+  static constexpr int BPB = 176, SUB = 32;
   static constexpr bool ALIGNED = true;
-  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
-    const int p = l >> 1, h = l & 1;
-    uint4 hd = *reinterpret_cast<const uint4*>(lds + off);
-    uint4 qh = *reinterpret_cast<const uint4*>(lds + off + 16 + 16 * h);
-    uint4 q = *reinterpret_cast<const uint4*>(lds + off + 48 + 32 * p + 16 * h);
-    r[0] = hd.x; r[1] = hd.y; r[2] = hd.z; r[3] = hd.w;
-    r[4] = q.x; r[5] = q.y; r[6] = q.z; r[7] = q.w;
-    r[8] = qh.x; r[9] = qh.y; r[10] = qh.z; r[11] = qh.w;
-  }
-  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg, float* to) {
-    const int p = l >> 1, h = l & 1;
-    const int4 xa = *reinterpret_cast<const int4*>(xb + 64 * p + 16 * h);
-    const int4 xc = *reinterpret_cast<const int4*>(xb + 64 * p + 32 + 16 * h);
-    const int s0 = 2 * p, s1 = 2 * p + 1;
-    int e0 = 0, e1 = 0;
-    const int xav[4] = {xa.x, xa.y, xa.z, xa.w};
-    const int xcv[4] = {xc.x, xc.y, xc.z, xc.w};
+  __device__ static void half(const uint8_t* lds, uint32_t off, int h, const int8_t* xb,
+                              const float* xe, const float* xs, int32_t* dbg, float* to) {
+    const uint4* bw = reinterpret_cast<const uint4*>(lds + off);
+    const uint4 hd = bw[0], h0 = bw[1], h1 = bw[2];
+    const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    const float d = cx_h2f(hd.x & 0xFFFF), dm = cx_h2f(hd.x >> 16);
+    uint32_t sc4, mn4;
+    KQ<CX_Q4_K>::scales_mins(h, hd.y, hd.z, hd.w, sc4, mn4);
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-      uint32_t qs = r[4 + w], qh = r[8 + w];
-      uint32_t lo = (qs & M4) | (((qh >> s0) & 0x01010101u) << 4);
-      uint32_t hi = ((qs >> 4) & M4) | (((qh >> s1) & 0x01010101u) << 4);
-      e0 = dot4(lo, xav[w], e0);
-      e1 = dot4(hi, xcv[w], e1);
+    for (int pp = 0; pp < 2; pp++) {
+      const int p = 2 * h + pp;
+      const uint4 u0 = bw[3 + 2 * p], u1 = bw[4 + 2 * p];
+      const uint32_t q[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+      int xa[8], xc[8];
+      act8(xb + 64 * p, xa);
+      act8(xb + 64 * p + 32, xc);
+      int e0 = 0, e1 = 0;
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        const uint32_t lo = (q[w] & M4) | (((qh[w] >> (2 * p)) & M1) << 4);
+        const uint32_t hi = ((q[w] >> 4) & M4) | (((qh[w] >> (2 * p + 1)) & M1) << 4);
+        e0 = dot4(lo, xa[w], e0);
+        e1 = dot4(hi, xc[w], e1);
+      }
+      KQ<CX_Q4_K>::term(2 * p, 2 * pp, e0, d, dm, sc4, mn4, xe, xs, dbg, to);
+      KQ<CX_Q4_K>::term(2 * p + 1, 2 * pp + 1, e1, d, dm, sc4, mn4, xe, xs, dbg, to);
     }
-    KQ<CX_Q4_K>::finish(r, h ? e0 : e1, h ? e1 : e0, 2 * p + h, xe, xs, dbg, to);
   }
 };
 
-// Shared shape of Q2_K / Q3_K / Q6_K: 16-value sub-blocks, 8 groups of 32.
-// Slot l: half = l/4, c = l%4 -> positions 8c..8c+7 of each of the four
-// groups g = 4*half + r (r = 0..3); sub-block of (g, c) = 2g + c/2. Lanes c
-// and c^1 hold the two halves of the same 16-value sub-blocks; after the
-// swap the even lane owns r = 0,1 and the odd lane r = 2,3.
-struct Swap16 {
-  int own0, own1, s0, s1;
-  __device__ Swap16(const int (&E)[4], int l) {
-    const int half = l >> 2, c = l & 3, odd = c & 1;
-    const int r0 = 2 * odd;
-    own0 = (odd ? E[2] : E[0]) + cx_xor1(odd ? E[0] : E[2]);
-    own1 = (odd ? E[3] : E[1]) + cx_xor1(odd ? E[1] : E[3]);
-    s0 = 2 * (4 * half + r0) + (c >> 1);
-    s1 = s0 + 2;
-  }
-};
-// The scale bytes of the two owned sub-blocks live in one 32-bit word,
-// index 2*half+odd, at byte m and 2+m (m = c/2).
-__device__ inline uint32_t sel4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
-                                int i) {
-  return i == 0 ? w0 : (i == 1 ? w1 : (i == 2 ? w2 : w3));
-}
+// Shared shape of Q2_K / Q3_K / Q6_K: 16-value sub-blocks. Group g = 0..7
+// holds 32 values, positions 0..15 in sub-block 2g and 16..31 in 2g+1. Half
+// h owns groups 4h..4h+3, whose 2-bit fields (Q2_K, Q3_K) or nibbles (Q6_K)
+// live in the h-th half of the quant bytes.
 
 // ------------------------------------------------------------------ Q2_K
-// 84 B: scales(16) qs(64) d dmin. value = (qs >> 2(g%4)) & 3.
+// 84 B: scales(16: low nibble scale, high nibble min) qs(64) d dmin.
+// value = (qs[32(g/4) + i] >> 2(g%4)) & 3   (src/kernels/q2k.rs:41-69)
 template <> struct KQ<CX_Q2_K> {
-  static constexpr int BPB = 84, SUB = 16, NW = 7;
+  static constexpr int BPB = 84, SUB = 16;
   static constexpr bool ALIGNED = false;
-  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
-    const int half = l >> 2, c = l & 3;
-    const uint32_t q = off + 16 + 32 * half + 8 * c;
-    r[0] = lds32(lds, q); r[1] = lds32(lds, q + 4);
-    r[2] = lds32(lds, off); r[3] = lds32(lds, off + 4);
-    r[4] = lds32(lds, off + 8); r[5] = lds32(lds, off + 12);
-    r[6] = lds32(lds, off + 80);
-  }
-  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg, float* to) {
-    const int half = l >> 2, c = l & 3;
-    int E[4];
+  __device__ static void half(const uint8_t* lds, uint32_t off, int h, const int8_t* xb,
+                              const float* xe, const float* xs, int32_t* dbg, float* to) {
+    uint32_t sw[2], qw[8], dw[1];
+    lds_words<2>(lds, off + 8 * h, sw);  // scales of sub-blocks 8h..8h+7
+    lds_words<8>(lds, off + 16 + 32 * h, qw);
+    lds_words<1>(lds, off + 80, dw);
+    const float d = cx_h2f(dw[0] & 0xFFFF), dm = cx_h2f(dw[0] >> 16);
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) {
-      const int2 x = *reinterpret_cast<const int2*>(xb + 32 * (4 * half + rr) + 8 * c);
-      E[rr] = dot4((r[1] >> (2 * rr)) & 0x03030303u, x.y,
-                   dot4((r[0] >> (2 * rr)) & 0x03030303u, x.x, 0));
+    for (int gi = 0; gi < 4; gi++) {
+      const int g = 4 * h + gi, sh = 2 * gi;
+      int x[8];
+      act8(xb + 32 * g, x);
+      int e0 = 0, e1 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        e0 = dot4((qw[i] >> sh) & M2, x[i], e0);
+        e1 = dot4((qw[4 + i] >> sh) & M2, x[4 + i], e1);
+      }
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++) {
+        const int s8 = 2 * gi + hf, sb = 8 * h + s8, e = hf ? e1 : e0;
+        const uint32_t sc = (sw[s8 / 4] >> (8 * (s8 % 4))) & 0xFF;
+        if (dbg) dbg[sb] = e;
+        to[sb] = xe[sb] * (d * (float)(sc & 0xF) * (float)e - dm * (float)(sc >> 4) * xs[sb]);
+      }
     }
-    Swap16 sw(E, l);
-    const uint32_t word = sel4(r[2], r[3], r[4], r[5], 2 * half + (c & 1));
-    const int m = c >> 1;
-    const uint32_t sc0 = (word >> (8 * m)) & 0xFF, sc1 = (word >> (8 * (m + 2))) & 0xFF;
-    const float d = cx_h2f(r[6] & 0xFFFF), dm = cx_h2f(r[6] >> 16);
-    if (dbg) { dbg[sw.s0] = sw.own0; dbg[sw.s1] = sw.own1; }
-    to[sw.s0] = xe[sw.s0] * (d * (float)(sc0 & 0xF) * (float)sw.own0 -
-                             dm * (float)(sc0 >> 4) * xs[sw.s0]);
-    to[sw.s1] = xe[sw.s1] * (d * (float)(sc1 & 0xF) * (float)sw.own1 -
-                             dm * (float)(sc1 >> 4) * xs[sw.s1]);
   }
 };
 
 // ------------------------------------------------------------------ Q3_K
 // 110 B: hmask(32) qs(64) scales(12) d. Biased value (q+4) in 0..7 =
-// ((qs >> 2(g%4)) & 3) | ((hmask >> g) & 1) << 2   (src/kernels/scalar.rs:262-268)
+// ((qs[32(g/4) + i] >> 2(g%4)) & 3) | ((hmask[i] >> g) & 1) << 2
+// (src/kernels/scalar.rs:236-275); scales as quant::escalas_q3k
+// (src/quant.rs:87-106): aux words 2h, 2h+1 hold sub-blocks 8h..8h+7
 template <> struct KQ<CX_Q3_K> {
-  static constexpr int BPB = 110, SUB = 16, NW = 8;
+  static constexpr int BPB = 110, SUB = 16;
   static constexpr bool ALIGNED = false;
-  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
-    const int half = l >> 2, c = l & 3;
-    r[0] = lds32(lds, off + 8 * c);
-    r[1] = lds32(lds, off + 8 * c + 4);
-    r[2] = lds32(lds, off + 32 + 32 * half + 8 * c);
-    r[3] = lds32(lds, off + 32 + 32 * half + 8 * c + 4);
-    r[4] = lds32(lds, off + 96);
-    r[5] = lds32(lds, off + 100);
-    r[6] = lds32(lds, off + 104);
-    r[7] = lds32(lds, off + 108) & 0xFFFFu;
-  }
-  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg, float* to) {
-    const int half = l >> 2, c = l & 3;
-    int E[4];
+  __device__ static void half(const uint8_t* lds, uint32_t off, int h, const int8_t* xb,
+                              const float* xe, const float* xs, int32_t* dbg, float* to) {
+    uint32_t hm[8], qw[8], tw[4];
+    lds_words<8>(lds, off, hm);
+    lds_words<8>(lds, off + 32 + 32 * h, qw);
+    lds_words<4>(lds, off + 96, tw);  // scales(12) d(2)
+    const float d = cx_h2f(tw[3] & 0xFFFF);
+    const uint32_t A = tw[0], B = tw[1], T = tw[2];
+    // aux[2h] and aux[2h+1] of escalas_q3k
+    const uint32_t X = h ? (A >> 4) : A, Y = h ? (B >> 4) : B, Ts = h ? (T >> 4) : T;
+    const uint32_t aux[2] = {(X & M4) | ((Ts & M2) << 4), (Y & M4) | (((Ts >> 2) & M2) << 4)};
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) {
-      const int g = 4 * half + rr;
-      const int2 x = *reinterpret_cast<const int2*>(xb + 32 * g + 8 * c);
-      uint32_t v0 = ((r[2] >> (2 * rr)) & 0x03030303u) | (((r[0] >> g) & 0x01010101u) << 2);
-      uint32_t v1 = ((r[3] >> (2 * rr)) & 0x03030303u) | (((r[1] >> g) & 0x01010101u) << 2);
-      E[rr] = dot4(v1, x.y, dot4(v0, x.x, 0));
+    for (int gi = 0; gi < 4; gi++) {
+      const int g = 4 * h + gi, sh = 2 * gi;
+      int x[8];
+      act8(xb + 32 * g, x);
+      int e0 = 0, e1 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t v0 = ((qw[i] >> sh) & M2) | (((hm[i] >> g) & M1) << 2);
+        const uint32_t v1 = ((qw[4 + i] >> sh) & M2) | (((hm[4 + i] >> g) & M1) << 2);
+        e0 = dot4(v0, x[i], e0);
+        e1 = dot4(v1, x[4 + i], e1);
+      }
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++) {
+        const int s8 = 2 * gi + hf, sb = 8 * h + s8, e = hf ? e1 : e0;
+        const float esc = (float)(int8_t)(uint8_t)(aux[s8 / 4] >> (8 * (s8 % 4)));
+        const float scale = d * (esc - 32.0f);
+        if (dbg) dbg[sb] = e;
+        to[sb] = xe[sb] * scale * ((float)e - 4.0f * xs[sb]);
+      }
     }
-    Swap16 sw(E, l);
-    // escalas_q3k (src/quant.rs:87-106): scale j = low nibble of byte j%4 of
-    // (A or B by (j/4)&1) shifted 4*(j/8), plus 2 bits of T at 8*(j%4)+2*(j/4)
-    const uint32_t A = r[4], B = r[5], T = r[6];
-    const int w = 2 * half + (c & 1), m = c >> 1;
-    const uint32_t src = (w & 1) ? B : A;
-    const int lsh = 4 * (w >> 1);
-    const uint32_t esc0 = ((src >> (8 * m + lsh)) & 0xF) | (((T >> (8 * m + 2 * w)) & 3) << 4);
-    const uint32_t esc1 =
-        ((src >> (8 * (m + 2) + lsh)) & 0xF) | (((T >> (8 * (m + 2) + 2 * w)) & 3) << 4);
-    const float d = cx_h2f(r[7]);
-    if (dbg) { dbg[sw.s0] = sw.own0; dbg[sw.s1] = sw.own1; }
-    const float sc0 = d * ((float)esc0 - 32.0f), sc1 = d * ((float)esc1 - 32.0f);
-    to[sw.s0] = xe[sw.s0] * sc0 * ((float)sw.own0 - 4.0f * xs[sw.s0]);
-    to[sw.s1] = xe[sw.s1] * sc1 * ((float)sw.own1 - 4.0f * xs[sw.s1]);
   }
 };
 
 // ------------------------------------------------------------------ Q6_K
-// 210 B: ql(128) qh(64) scales(16, i8) d. Unsigned value 0..63 =
-// nib | ((qh >> 2gi) & 3) << 4   (src/kernels/scalar.rs:305-320)
+// 210 B: ql(128) qh(64) scales(16, i8) d. Group g: half = g/4, gi = g%4;
+// value 0..63 = nib | ((qh[32 half + i] >> 2gi) & 3) << 4, nib = low (gi < 2)
+// or high nibble of ql[64 half + 32 (gi%2) + i]   (src/kernels/scalar.rs:294-324)
 template <> struct KQ<CX_Q6_K> {
-  static constexpr int BPB = 210, SUB = 16, NW = 11;
+  static constexpr int BPB = 210, SUB = 16;
   static constexpr bool ALIGNED = false;
-  __device__ static void load(const uint8_t* lds, uint32_t off, int l, uint32_t (&r)[NW]) {
-    const int half = l >> 2, c = l & 3;
-    const uint32_t qa = off + 64 * half + 8 * c;
-    r[0] = lds32(lds, qa); r[1] = lds32(lds, qa + 4);
-    r[2] = lds32(lds, qa + 32); r[3] = lds32(lds, qa + 36);
-    r[4] = lds32(lds, off + 128 + 32 * half + 8 * c);
-    r[5] = lds32(lds, off + 128 + 32 * half + 8 * c + 4);
-    r[6] = lds32(lds, off + 192); r[7] = lds32(lds, off + 196);
-    r[8] = lds32(lds, off + 200); r[9] = lds32(lds, off + 204);
-    r[10] = lds32(lds, off + 208) & 0xFFFFu;
-  }
-  __device__ static void term(const uint32_t (&r)[NW], int l, const int8_t* xb,
-                               const float* xe, const float* xs, int32_t* dbg, float* to) {
-    const int half = l >> 2, c = l & 3;
-    int E[4];
+  __device__ static void half(const uint8_t* lds, uint32_t off, int h, const int8_t* xb,
+                              const float* xe, const float* xs, int32_t* dbg, float* to) {
+    uint32_t ql[16], qh[8], sw[2], dw[1];
+    lds_words<16>(lds, off + 64 * h, ql);
+    lds_words<8>(lds, off + 128 + 32 * h, qh);
+    lds_words<2>(lds, off + 192 + 8 * h, sw);  // scales of sub-blocks 8h..8h+7
+    lds_words<1>(lds, off + 208, dw);
+    const float d = cx_h2f(dw[0] & 0xFFFF);
 #pragma unroll
     for (int gi = 0; gi < 4; gi++) {
-      const int g = 4 * half + gi;
-      const int2 x = *reinterpret_cast<const int2*>(xb + 32 * g + 8 * c);
-      const uint32_t s0 = (gi & 1) ? r[2] : r[0], s1 = (gi & 1) ? r[3] : r[1];
-      uint32_t n0 = gi < 2 ? (s0 & M4) : ((s0 >> 4) & M4);
-      uint32_t n1 = gi < 2 ? (s1 & M4) : ((s1 >> 4) & M4);
-      uint32_t v0 = n0 | (((r[4] >> (2 * gi)) & 0x03030303u) << 4);
-      uint32_t v1 = n1 | (((r[5] >> (2 * gi)) & 0x03030303u) << 4);
-      E[gi] = dot4(v1, x.y, dot4(v0, x.x, 0));
+      const int g = 4 * h + gi, lw = 8 * (gi % 2);
+      int x[8];
+      act8(xb + 32 * g, x);
+      int e0 = 0, e1 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t n0 = gi < 2 ? (ql[lw + i] & M4) : ((ql[lw + i] >> 4) & M4);
+        const uint32_t n1 = gi < 2 ? (ql[lw + 4 + i] & M4) : ((ql[lw + 4 + i] >> 4) & M4);
+        e0 = dot4(n0 | (((qh[i] >> (2 * gi)) & M2) << 4), x[i], e0);
+        e1 = dot4(n1 | (((qh[4 + i] >> (2 * gi)) & M2) << 4), x[4 + i], e1);
+      }
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++) {
+        const int s8 = 2 * gi + hf, sb = 8 * h + s8, e = hf ? e1 : e0;
+        const float scale = d * (float)(int8_t)(uint8_t)(sw[s8 / 4] >> (8 * (s8 % 4)));
+        if (dbg) dbg[sb] = e;
+        to[sb] = xe[sb] * scale * ((float)e - 32.0f * xs[sb]);
+      }
     }
-    Swap16 sw(E, l);
-    const uint32_t word = sel4(r[6], r[7], r[8], r[9], 2 * half + (c & 1));
-    const int m = c >> 1;
-    const int8_t e0 = (int8_t)((word >> (8 * m)) & 0xFF);
-    const int8_t e1 = (int8_t)((word >> (8 * (m + 2))) & 0xFF);
-    const float d = cx_h2f(r[10]);
-    if (dbg) { dbg[sw.s0] = sw.own0; dbg[sw.s1] = sw.own1; }
-    const float sc0 = d * (float)e0, sc1 = d * (float)e1;
-    to[sw.s0] = xe[sw.s0] * sc0 * ((float)sw.own0 - 32.0f * xs[sw.s0]);
-    to[sw.s1] = xe[sw.s1] * sc1 * ((float)sw.own1 - 32.0f * xs[sw.s1]);
   }
 };
 
@@ -298,31 +290,73 @@ struct GemvParams {
   uint32_t R;            // rows per tile
   uint32_t row_bytes;
   uint32_t tstride;      // floats between two rows' terms (nsub + 4)
-  uint32_t lds_act;      // byte offsets in LDS: activation, xe/xs, terms
+  uint32_t lds_act;      // byte offsets in LDS: activation, xe/xs, terms, norm input
   uint32_t lds_scale;
   uint32_t lds_terms;
-  cx_qact act;
+  uint32_t lds_norm;
+  cx_qact act;           // the quantized activation, or
+  const float* nx;       // the rmsnorm input and weight it is made from here
+  const float* nw;
+  float eps;
   int epi;
   int32_t* dbg;
 };
 
-// 16-byte chunks [0, n) of `g` into LDS at `l`, 1 KiB per wave instruction.
-// global_load_lds writes lane i's 16 bytes at (wave-uniform LDS address) +
-// 16*i; lanes past the end are masked off.
-__device__ inline void copy_to_lds(const uint8_t* g, uint8_t* l, uint32_t n, int wave, int lane,
-                                   int nwaves) {
-  for (uint32_t c0 = 64u * wave; c0 < n; c0 += 64u * nwaves) {
+// 16-byte chunks [0, n) of global `g` into LDS at `l`, 1 KiB per wave load
+// (wave w moves chunks 64*(w + 4j) + lane). Returns the loads this wave
+// issued; they are untracked by the compiler (see cx_dma16_async).
+__device__ inline uint32_t copy_to_lds(const void* g, void* l, uint32_t n, int wave, int lane) {
+  uint32_t issued = 0;
+  for (uint32_t c0 = 64u * wave; c0 < n; c0 += 256) {
     if (c0 + lane < n)
-      __builtin_amdgcn_global_load_lds(g + 16 * (size_t)(c0 + lane), (lds_ptr_t)(l + 16 * c0), 16,
-                                       0, 0);
+      cx_dma16_async(static_cast<const uint8_t*>(g) + 16 * (size_t)(c0 + lane),
+                     static_cast<uint8_t*>(l) + 16 * c0);
+    issued++;
   }
+  return issued;
 }
 
-template <int T>
+// The activation's 256-byte blocks sit ACT_LDS_BLOCK bytes apart in LDS: the
+// lanes of one wave read up to 8 different blocks at once, and a 272-byte
+// stride puts them on different LDS banks (a 256-byte stride would put all
+// eight on the same ones). The direct loads write 16 bytes per lane at
+// consecutive LDS addresses, so the 17th chunk of each block loads a dummy.
+constexpr uint32_t ACT_LDS_BLOCK = 272;
+__device__ inline void copy_act_padded(const int8_t* xq, int8_t* l, uint32_t nb, int wave,
+                                       int lane) {
+  const uint32_t n = nb * (ACT_LDS_BLOCK / 16);
+  for (uint32_t c0 = 64u * wave; c0 < n; c0 += 256) {
+    const uint32_t c = c0 + lane, b = c / 17, r = c % 17;
+    if (c < n)
+      cx_dma16_async(xq + (r < 16 ? 256 * (size_t)b + 16 * r : 0), l + 16 * c0);
+  }
+}
+// cx_quant8 into the padded LDS layout (8 values never straddle a block)
+template <int SUB>
+__device__ inline void cx_quant8_padded(const float (&v)[8], uint32_t i, int8_t* sq, float* se,
+                                        float* ss) {
+  int8_t* blk = sq + (i / 256) * ACT_LDS_BLOCK - (i / 256) * 256;
+  cx_quant8<SUB>(v, i, blk, se, ss);
+}
+
+// Waits until at most n (wave-uniform) of this wave's loads are outstanding,
+// or fewer: a smaller count only waits longer.
+__device__ inline void wait_all_but(uint32_t n) {
+  if (n >= 48) cx_wait_vm<48>();
+  else if (n >= 32) cx_wait_vm<32>();
+  else if (n >= 16) cx_wait_vm<16>();
+  else if (n >= 8) cx_wait_vm<8>();
+  else if (n >= 4) cx_wait_vm<4>();
+  else if (n >= 2) cx_wait_vm<2>();
+  else cx_wait_vm<0>();
+}
+
+template <int T, bool NORM>
 __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
   using Q = KQ<T>;
   constexpr int SPB = 256 / Q::SUB;  // sub-blocks per super-block
   extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ double red[4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t tile = blockIdx.x;
@@ -332,37 +366,67 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
   const cx_seg S = P.seg[sg];
   const uint32_t row0 = tile * P.R;
   const uint32_t rows = min(P.R, S.rows - row0);
-
-  // 1. the tile (rows * row_bytes contiguous bytes) and the activation into
-  //    LDS; the tile starts `skew` bytes into LDS when the rows are not
-  //    16-byte aligned (Q2_K/Q3_K/Q6_K rows of some widths)
-  const uint8_t* src = S.w + (size_t)row0 * P.row_bytes;
-  const uint32_t skew = (uint32_t)((uintptr_t)src & 15u);
-  copy_to_lds(src - skew, lds, (skew + rows * P.row_bytes + 15) >> 4, wave, lane, 4);
   int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
-  copy_to_lds(reinterpret_cast<const uint8_t*>(P.act.xq), reinterpret_cast<uint8_t*>(sq),
-              P.k >> 4, wave, lane, 4);
   float* se = reinterpret_cast<float*>(lds + P.lds_scale);
   float* ss = se + P.nsub;
-  for (uint32_t i = tid; i < P.nsub; i += 256) {
-    se[i] = P.act.xe[i];
-    ss[i] = P.act.xs[i];
+  float* sx = reinterpret_cast<float*>(lds + P.lds_norm);
+
+  // 1. every input into LDS with direct loads: the rmsnorm input first (so
+  //    the prologue can start before the weights land), then the tile (rows *
+  //    row_bytes contiguous bytes, `skew` bytes into LDS when the rows are not
+  //    16-byte aligned: Q2_K/Q3_K/Q6_K rows of some widths), then the
+  //    quantized activation when it comes ready-made
+  if (NORM) {
+    copy_to_lds(P.nx, sx, P.k / 4, wave, lane);
+    copy_to_lds(P.nw, sx + P.k, P.k / 4, wave, lane);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // the direct-to-LDS loads have landed
+  const uint8_t* src = S.w + (size_t)row0 * P.row_bytes;
+  const uint32_t skew = (uint32_t)((uintptr_t)src & 15u);
+  const uint32_t ntile =
+      copy_to_lds(src - skew, lds, (skew + rows * P.row_bytes + 15) >> 4, wave, lane);
+  if (!NORM) {
+    copy_act_padded(P.act.xq, sq, P.nb, wave, lane);
+    copy_to_lds(P.act.xe, se, P.nsub / 4, wave, lane);
+    copy_to_lds(P.act.xs, ss, P.nsub / 4, wave, lane);
+  } else {
+    // rmsnorm (src/kernels/scalar.rs:40-53) and quantization of the
+    // activation while the weights stream in: f64 sum of squares (8
+    // consecutive values a lane, fixed tree), scale = 1/sqrt(sum/k + eps),
+    // v = (x as f64 * scale) as f32 * w, then ops::cuantizar_i8_en
+    wait_all_but(ntile);
+    cx_barrier();  // every wave's share of x and w has landed
+    const float* sw = sx + P.k;
+    double sum = 0.0;
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048)
+#pragma unroll
+      for (int j = 0; j < 8; j++) sum += (double)sx[i + j] * (double)sx[i + j];
+    sum = cx_wave_sum_d(sum);
+    if (lane == 0) red[wave] = sum;
+    cx_wait_lds();
+    cx_barrier();
+    const double tot = ((red[0] + red[1]) + red[2]) + red[3];
+    const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = (float)((double)sx[i + j] * scale) * sw[i + j];
+      cx_quant8_padded<Q::SUB>(v, i, sq, se, ss);
+    }
+  }
+  cx_wait_vm<0>();  // every direct load has landed
+  cx_wait_lds();
   __syncthreads();
 
   // 2. integer dots + the reference's per-sub-block f32 terms, staged in LDS
-  //    by (row, sub-block); every sub-block of a row is owned by one lane
+  //    by (row, sub-block): two lanes per (row, super-block)
   float* terms = reinterpret_cast<float*>(lds + P.lds_terms);
-  const uint32_t nb8 = P.nb * 8, total = rows * nb8;
-  for (uint32_t slot = tid; slot < total; slot += 256) {
-    const uint32_t r = slot / nb8, w = slot - r * nb8, blk = w >> 3;
-    const int l = (int)(w & 7);
-    uint32_t regs[Q::NW];
-    Q::load(lds, skew + r * P.row_bytes + blk * Q::BPB, l, regs);
+  const uint32_t items = 2 * rows * P.nb;
+  for (uint32_t it = tid; it < items; it += 256) {
+    const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
+    const int h = (int)(it & 1);
     int32_t* dbg = P.dbg ? P.dbg + (size_t)(row0 + r) * P.nsub + blk * SPB : nullptr;
-    Q::term(regs, l, sq + blk * 256, se + blk * SPB, ss + blk * SPB, dbg,
-            terms + r * P.tstride + blk * SPB);
+    Q::half(lds, skew + r * P.row_bytes + blk * Q::BPB, h, sq + blk * ACT_LDS_BLOCK,
+            se + blk * SPB, ss + blk * SPB, dbg, terms + r * P.tstride + blk * SPB);
   }
   __syncthreads();
 
@@ -387,24 +451,25 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
 }
 
 struct TilePlan {
-  uint32_t R, tiles, lds, lds_act, lds_scale, lds_terms;
+  uint32_t R, tiles, lds, lds_act, lds_scale, lds_terms, lds_norm;
 };
 
 // LDS layout of a tile of R rows: [16 skew + R*row_bytes + 16 pad] [xq k]
-// [xe, xs] [terms R x (nsub+4)]
+// [xe, xs] [terms R x (nsub+4)] [norm input x, w: 2k floats]
 TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
-                   const uint32_t* rows, int nseg) {
+                   const uint32_t* rows, int nseg, bool norm) {
   TilePlan t{};
   t.R = R;
   for (int i = 0; i < nseg; i++) t.tiles += (rows[i] + R - 1) / R;
   t.lds_act = (16 + R * row_bytes + 16 + 15) / 16 * 16;
-  t.lds_scale = t.lds_act + k;
+  t.lds_scale = t.lds_act + (k / 256) * ACT_LDS_BLOCK;
   t.lds_terms = t.lds_scale + (8 * nsub + 15) / 16 * 16;
-  t.lds = t.lds_terms + 4 * R * (nsub + 4);
+  t.lds_norm = t.lds_terms + 4 * R * (nsub + 4);
+  t.lds = t.lds_norm + (norm ? 8 * k : 0);
   return t;
 }
 
-template <int T>
+template <int T, bool NORM>
 int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   using Q = KQ<T>;
   if (Q::ALIGNED) {
@@ -416,7 +481,7 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   // tiles per CU; small matrices fall back to the smallest tiles
   TilePlan best{};
   for (uint32_t R = 64; R >= 1; R >>= 1) {
-    TilePlan t = plan_tile(R, P.row_bytes, P.k, P.nsub, rows, P.nseg);
+    TilePlan t = plan_tile(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM);
     if (t.lds > TILE_LDS_MAX) continue;
     best = t;
     if (t.tiles >= 512) break;
@@ -426,13 +491,54 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   P.lds_act = best.lds_act;
   P.lds_scale = best.lds_scale;
   P.lds_terms = best.lds_terms;
+  P.lds_norm = best.lds_norm;
   uint32_t acc = 0;
   for (int i = 0; i < P.nseg; i++) {
     acc += (rows[i] + best.R - 1) / best.R;
     P.tile_end[i] = acc;
   }
-  hipLaunchKernelGGL((k_gemv<T>), dim3(best.tiles), dim3(256), best.lds, s, P);
+  hipLaunchKernelGGL((k_gemv<T, NORM>), dim3(best.tiles), dim3(256), best.lds, s, P);
   CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+template <bool NORM>
+int launch_type(int type, GemvParams& P, const uint32_t* rows, hipStream_t s) {
+  switch (type) {
+    case CX_Q2_K: return launch_t<CX_Q2_K, NORM>(P, rows, s);
+    case CX_Q3_K: return launch_t<CX_Q3_K, NORM>(P, rows, s);
+    case CX_Q4_K: return launch_t<CX_Q4_K, NORM>(P, rows, s);
+    case CX_Q5_K: return launch_t<CX_Q5_K, NORM>(P, rows, s);
+    default: return launch_t<CX_Q6_K, NORM>(P, rows, s);
+  }
+}
+
+// Shared checks and the segment table. Returns CX_OK with *total == 0 when
+// there is nothing to do.
+int gemv_setup(int type, const cx_seg* segs, int nseg, uint32_t k, int epi, int32_t* dbg,
+               GemvParams& P, uint32_t* rows, uint32_t* total) {
+  CX_REQUIRE(nseg >= 1 && nseg <= 4, "gemv: 1..4 matrices per launch");
+  CX_REQUIRE(cx_is_kquant(type), "gemv: type %d has no fused GEMV", type);
+  CX_REQUIRE(k > 0 && k % 256 == 0, "gemv: k=%u is not a multiple of 256", k);
+  CX_REQUIRE(!dbg || nseg == 1, "gemv: sub-block sums need a single matrix");
+  *total = 0;
+  int n = 0;
+  for (int i = 0; i < nseg; i++) {
+    CX_REQUIRE(segs[i].w && segs[i].y, "gemv: null matrix or output");
+    *total += segs[i].rows;
+    if (segs[i].rows) {  // empty segments own no tile
+      P.seg[n] = segs[i];
+      rows[n++] = segs[i].rows;
+    }
+  }
+  P.nseg = n;
+  P.k = k;
+  P.nb = k / 256;
+  P.nsub = k / cx_sub(type);
+  P.row_bytes = P.nb * cx_bpb(type);
+  P.tstride = P.nsub + 4;
+  P.epi = epi;
+  P.dbg = dbg;
   return CX_OK;
 }
 
@@ -440,44 +546,31 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
 
 int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k, const cx_qact& act,
                    int epi, int32_t* dbg, hipStream_t s) {
-  CX_REQUIRE(nseg >= 1 && nseg <= 4, "gemv: 1..4 matrices per launch");
-  CX_REQUIRE(cx_is_kquant(type), "gemv: type %d has no fused GEMV", type);
-  CX_REQUIRE(k > 0 && k % 256 == 0, "gemv: k=%u is not a multiple of 256", k);
   CX_REQUIRE(act.xq && act.xe && act.xs, "gemv: missing quantized activation");
-  CX_REQUIRE(((uintptr_t)act.xq & 15u) == 0, "gemv: xq must be 16-byte aligned");
-  CX_REQUIRE(!dbg || nseg == 1, "gemv: sub-block sums need a single matrix");
+  CX_REQUIRE(((uintptr_t)act.xq & 15u) == 0 && ((uintptr_t)act.xe & 15u) == 0 &&
+                 ((uintptr_t)act.xs & 15u) == 0,
+             "gemv: xq, xe and xs must be 16-byte aligned");
   GemvParams P{};
-  uint32_t rows[4], total = 0;
-  for (int i = 0; i < nseg; i++) {
-    CX_REQUIRE(segs[i].w && segs[i].y, "gemv: null matrix or output");
-    P.seg[i] = segs[i];
-    rows[i] = segs[i].rows;
-    total += segs[i].rows;
-  }
-  if (total == 0) return CX_OK;
-  // empty segments would own no tile; keep them out of the tile table
-  int n = 0;
-  for (int i = 0; i < nseg; i++)
-    if (rows[i]) {
-      P.seg[n] = segs[i];
-      rows[n++] = segs[i].rows;
-    }
-  P.nseg = n;
-  P.k = k;
-  P.nb = k / 256;
-  P.nsub = k / cx_sub(type);
-  P.row_bytes = P.nb * cx_bpb(type);
-  P.tstride = P.nsub + 4;
+  uint32_t rows[4], total;
+  int rc = gemv_setup(type, segs, nseg, k, epi, dbg, P, rows, &total);
+  if (rc || !total) return rc;
   P.act = act;
-  P.epi = epi;
-  P.dbg = dbg;
-  switch (type) {
-    case CX_Q2_K: return launch_t<CX_Q2_K>(P, rows, s);
-    case CX_Q3_K: return launch_t<CX_Q3_K>(P, rows, s);
-    case CX_Q4_K: return launch_t<CX_Q4_K>(P, rows, s);
-    case CX_Q5_K: return launch_t<CX_Q5_K>(P, rows, s);
-    default: return launch_t<CX_Q6_K>(P, rows, s);
-  }
+  return launch_type<false>(type, P, rows, s);
+}
+
+int cx_launch_gemv_norm(int type, const cx_seg* segs, int nseg, uint32_t k, const float* x,
+                        const float* w, float eps, int epi, hipStream_t s) {
+  CX_REQUIRE(x && w, "gemv: missing rmsnorm input");
+  CX_REQUIRE(((uintptr_t)x & 15u) == 0 && ((uintptr_t)w & 15u) == 0,
+             "gemv: the rmsnorm input and weight must be 16-byte aligned");
+  GemvParams P{};
+  uint32_t rows[4], total;
+  int rc = gemv_setup(type, segs, nseg, k, epi, nullptr, P, rows, &total);
+  if (rc || !total) return rc;
+  P.nx = x;
+  P.nw = w;
+  P.eps = eps;
+  return launch_type<true>(type, P, rows, s);
 }
 
 // ------------------------------------------------- activation kernels

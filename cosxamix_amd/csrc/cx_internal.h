@@ -27,6 +27,12 @@ enum cx_epi { CX_EPI_STORE = 0, CX_EPI_ACCUM = 1 };
 // `dbg` (single segment only) receives the integer sub-block sums.
 int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k, const cx_qact& act,
                    int epi, int32_t* dbg, hipStream_t s);
+// The same GEMV with its activation made by every workgroup from f32 x:
+// rmsnorm(x, w, eps) (kernels/mod.rs:511) then quantization (ops.rs:178), in
+// the shadow of the weight loads. For launches of a few hundred workgroups;
+// x and w are 16-byte aligned.
+int cx_launch_gemv_norm(int type, const cx_seg* segs, int nseg, uint32_t k, const float* x,
+                        const float* w, float eps, int epi, hipStream_t s);
 
 // Producers of the i8 activation, one value per lane:
 //   quantize   : rows x k values of x                           (ops.rs:178)

@@ -24,6 +24,9 @@ int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float
                       const float* cos_t, const float* sin_t, uint32_t heads, uint32_t kvh,
                       uint32_t hd, const cx_dstate* st, hipStream_t s);
 size_t cx_attn_splits(size_t cap);
+// floats of the exact path's score buffer (rows padded to 4 floats; the
+// buffer must start 16-byte aligned)
+inline size_t cx_attn_score_floats(size_t heads, size_t cap) { return heads * ((cap + 3) / 4 * 4); }
 
 // One decode step's attention (src/ops.rs:1258-1325 at tokens = 1).
 struct cx_attn_args {

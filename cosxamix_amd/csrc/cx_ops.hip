@@ -206,41 +206,41 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 
 // ------------------------------------------- order-exact decode attention
 // The decode step's attention in the reference's own order, for contexts up
-// to CX_ATT_EXACT_MAX, in two kernels.
+// to CX_ATT_EXACT_MAX, in two kernels. Both stage their cache rows in LDS
+// with direct-to-LDS loads, so a wave keeps up to 63 KiB of the cache in
+// flight instead of waiting on one row at a time.
 //
-// k_attn_scores, workgroup (split, head h): positions [64*split, +64), one
-// lane each: the sequential dot of src/kernels/scalar.rs:16-23 times
-// 1/sqrt(hd), written to sc[h][p]. With rope tables it first rotates q and
-// this step's key (src/ops.rs:1185-1188: a' = a*c - b*s, b' = a*s + b*c,
-// no FMA); the first head of each KV group appends the rotated key and the
-// value to the cache at st->pos (src/forward.rs:454-455). The score at st->pos
-// uses the rotated key from LDS, so no workgroup reads a cache row written in
-// the same launch.
+// k_attn_scores, one wave per (64 positions, head h): the 64 K rows of the
+// head's group are copied into LDS (rows padded by 16 bytes against bank
+// conflicts), then lane p forms the sequential dot of
+// src/kernels/scalar.rs:16-23 times 1/sqrt(hd) and writes sc[h][p]. With
+// rope tables it first rotates q and this step's key (src/ops.rs:1185-1188:
+// a' = a*c - b*s, b' = a*s + b*c, no FMA); the first head of each KV group
+// appends the rotated key and the value to the cache at st->pos
+// (src/forward.rs:454-455). The score at st->pos uses the rotated key from
+// LDS, so no result depends on a cache row written in the same launch.
 //
-// k_attn_seq, one workgroup per head: exact max, e = exp(s - max) (glibc's
-// expf), the sequential sum, p = e * (1/sum) (src/ops.rs:1218-1229), and
-// out[d] = sum over p of prob_p * v_p[d] in position order
-// (src/ops.rs:1316-1321), with V prefetched 32 positions ahead. The head's
-// output is then quantized for the output projection (its head_dim values
-// are whole sub-blocks). Bit-identical to the scalar reference.
-constexpr uint32_t SC_P = 64;  // positions per scores workgroup
+// k_attn_seq, one wave per (head, 64 head dims): the head's scores are
+// copied in, then the softmax in the reference's order: exact max,
+// e = exp(s - max) (glibc's expf), the sum accumulated sequentially from 0,
+// p = e * (1/sum) (src/ops.rs:1211-1229). Meanwhile the V slice streams
+// through a ring of LDS stages; lane d accumulates out[d] = sum over p of
+// prob_p * v_p[d] in position order (src/ops.rs:1316-1321). The output is
+// then quantized for the output projection (64 values are whole
+// sub-blocks). Bit-identical to the scalar reference.
+constexpr uint32_t SC_P = 64;     // positions per scores wave
+constexpr uint32_t PV_DS = 64;    // head dims per softmax-V workgroup (wave 0's lanes)
+constexpr uint32_t PV_STP = 32;   // positions per V stage (8 KiB)
+constexpr uint32_t PV_NST = 16;   // V stages in the LDS ring (128 KiB)
+constexpr uint32_t PV_IPS = PV_STP * PV_DS * 4 / 1024;  // loads per stage: 8
+constexpr uint32_t PV_IPW = PV_IPS / 4;                  // per wave: 2
+// A wave tracks at most 63 outstanding loads (vmcnt is 6 bits): its share
+// of the scores (<= 4 loads for 4096 positions) plus 15 stages ahead (30).
+static_assert(4 + (PV_NST - 1) * PV_IPW <= 63, "too many loads in flight");
 
-template <int HD>
-__device__ inline float seq_dot(const float* a_lds, const float* b) {
-  float4 r[HD / 4];
-#pragma unroll
-  for (int i = 0; i < HD / 4; i++) r[i] = reinterpret_cast<const float4*>(b)[i];
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < HD / 4; i++) {
-    const float4 a = reinterpret_cast<const float4*>(a_lds)[i];
-    s += a.x * r[i].x;
-    s += a.y * r[i].y;
-    s += a.z * r[i].z;
-    s += a.w * r[i].w;
-  }
-  return s;
-}
+__host__ __device__ constexpr uint32_t sc_stride(uint32_t cap) { return (cap + 3) / 4 * 4; }
+// LDS floats for a head's scores: whole 1 KiB loads
+__host__ __device__ constexpr uint32_t sc_lds(uint32_t cap) { return (cap + 255) / 256 * 256; }
 
 template <int HD>
 __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float* knew,
@@ -249,14 +249,28 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
                                                     uint32_t heads, uint32_t kvh,
                                                     const cx_dstate* st, float scale,
                                                     float* sc, uint32_t cap) {
-  __shared__ __align__(16) float qr[HD];
-  __shared__ __align__(16) float kr[HD];
+  constexpr uint32_t ROWB = HD * 4, PADB = ROWB + 16, PADF = PADB / 4;
+  constexpr uint32_t NCH = (SC_P * PADB + 1023) / 1024;
+  extern __shared__ __align__(16) uint8_t sm[];
+  float* kl = reinterpret_cast<float*>(sm);
+  float* qr = reinterpret_cast<float*>(sm + NCH * 1024);
+  float* kr = qr + HD;
   constexpr uint32_t half = HD / 2;
   const uint32_t pos = st->pos, total = pos + 1;
   const uint32_t p0 = blockIdx.x * SC_P, h = blockIdx.y, per = heads / kvh, g = h / per;
   if (p0 >= total) return;
-  const uint32_t kvd = kvh * HD;
+  const uint32_t np = min(SC_P, total - p0), kvd = kvh * HD;
   const int t = threadIdx.x;
+  // 1. the K rows [p0, p0 + np) into LDS; pad bytes and rows past the end
+  //    load a valid dummy that is never read
+  const float* kb = kc + (size_t)p0 * kvd + g * HD;
+  for (uint32_t c = 0; c < NCH; c++) {
+    const uint32_t o = c * 1024 + 16 * t;
+    uint32_t r = o / PADB, b = o % PADB;
+    if (r >= np || b >= ROWB) r = 0, b = 0;
+    cx_dma16(reinterpret_cast<const uint8_t*>(kb + (size_t)r * kvd) + b, sm + c * 1024);
+  }
+  // 2. rope while the rows arrive
   const bool rot = cos_t != nullptr, has_new = rot && pos < p0 + SC_P;
   if (rot) {
     const float* c = cos_t + (size_t)pos * half;
@@ -283,76 +297,162 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
   } else {
     for (uint32_t j = t; j < HD; j += 64) qr[j] = q[h * HD + j];
   }
+  cx_wait_vm<0>();
   __syncthreads();
+  // 3. lane t: position p0 + t
+  if ((uint32_t)t >= np) return;
   const uint32_t p = p0 + t;
-  if (p >= total) return;
-  float s;
-  if (has_new && p == pos) {
-    s = 0.0f;
-    for (int d = 0; d < HD; d++) s += qr[d] * kr[d];
-  } else {
-    s = seq_dot<HD>(qr, kc + (size_t)p * kvd + g * HD);
+  const float4* a4 = reinterpret_cast<const float4*>(qr);
+  const float4* b4 = reinterpret_cast<const float4*>((has_new && p == pos) ? kr : kl + t * PADF);
+  float s = 0.0f;
+#pragma unroll 8
+  for (int i = 0; i < HD / 4; i++) {
+    const float4 a = a4[i], b = b4[i];
+    s += a.x * b.x;
+    s += a.y * b.y;
+    s += a.z * b.z;
+    s += a.w * b.w;
   }
-  sc[(size_t)h * cap + p] = s * scale;
+  sc[(size_t)h * sc_stride(cap) + p] = s * scale;
 }
 
-constexpr int PV_CHUNK = 32;
+// Sequential sum of x[0..n) from 0 (one lane), LDS reads issued a batch ahead
+__device__ inline float seq_sum_lds(const float* x, uint32_t n) {
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const uint32_t n4 = n / 4;
+  float tot = 0.0f;
+  float4 a[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = x4[i];  // may read past n: never used
+  uint32_t b = 0;
+  for (; b + 8 <= n4; b += 8) {
+    float4 nx[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) nx[i] = x4[b + 8 + i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      tot += a[i].x;
+      tot += a[i].y;
+      tot += a[i].z;
+      tot += a[i].w;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) a[i] = nx[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    if (b + i < n4) {
+      tot += a[i].x;
+      tot += a[i].y;
+      tot += a[i].z;
+      tot += a[i].w;
+    }
+  for (uint32_t p = n4 * 4; p < n; p++) tot += x[p];
+  return tot;
+}
 
+// 256 threads: every wave streams its share of the V ring (4x the loads in
+// flight of one wave); wave 0's lanes run the order-exact accumulation.
 template <int HD, int SUB>
 __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
                                                   uint32_t heads, uint32_t kvh,
                                                   const cx_dstate* st, uint32_t cap, float* out,
                                                   int8_t* xq, float* xe, float* xs) {
-  extern __shared__ __align__(16) float e[];
+  extern __shared__ __align__(16) float e[];  // sc_lds(cap) scores, then the V ring
+  float* ring = e + sc_lds(cap);
+  __shared__ uint64_t etab[32];  // exp's table in LDS: no global load after the prefetch
   __shared__ float red[4];
-  __shared__ __align__(16) float os[HD];
   const uint32_t total = st->pos + 1, h = blockIdx.x, g = h / (heads / kvh);
-  const float* sc = sc_all + (size_t)h * cap;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float mx = -INFINITY;
-  for (uint32_t p = tid; p < total; p += 256) {
-    const float s = sc[p];
-    e[p] = s;
-    mx = fmaxf(mx, s);
+  const uint32_t d0 = blockIdx.y * PV_DS, kvd = kvh * HD;
+  const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
+  if (tid == 0) {  // uniform indices: scalar loads, which leave vmcnt alone
+    const uint64_t tab[32] = CX_EXP2_TAB;
+    for (int i = 0; i < 32; i++) etab[i] = tab[i];
   }
-  mx = cx_wave_max(mx);
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  seq_softmax_inplace(e, total, mx, red);
-  if (tid < HD) {
-    const size_t kvd = (size_t)kvh * HD;
-    const float* vp = vc + g * HD + tid;
-    float cur[PV_CHUNK], nxt[PV_CHUNK];
-#pragma unroll
-    for (int j = 0; j < PV_CHUNK; j++) cur[j] = (uint32_t)j < total ? vp[j * kvd] : 0.0f;
-    float o = 0.0f;
-    for (uint32_t p0 = 0; p0 < total; p0 += PV_CHUNK) {
-      const uint32_t pn = p0 + PV_CHUNK;
-#pragma unroll
-      for (int j = 0; j < PV_CHUNK; j++) nxt[j] = pn + j < total ? vp[(pn + j) * kvd] : 0.0f;
-      if (p0 + PV_CHUNK <= total) {
-#pragma unroll
-        for (int j = 0; j < PV_CHUNK; j++) o += e[p0 + j] * cur[j];
-      } else {
-#pragma unroll
-        for (int j = 0; j < PV_CHUNK; j++)
-          if (p0 + j < total) o += e[p0 + j] * cur[j];
-      }
-#pragma unroll
-      for (int j = 0; j < PV_CHUNK; j++) cur[j] = nxt[j];
+  // 1. the head's scores, then the first V stages, as untracked
+  //    direct-to-LDS loads; a wave's loads complete in issue order, so
+  //    waiting for all but its V loads waits for its scores only
+  const float* srow = sc_all + (size_t)h * sc_stride(cap);
+  const uint32_t nsc = (total + 255) / 256;  // 1 KiB per load
+  for (uint32_t c = w; c < nsc; c += 4) {
+    const uint32_t i = c * 256 + 4 * t;
+    cx_dma16_async(srow + (i < total ? i : 0), e + c * 256);
+  }
+  const uint32_t nstage = (total + PV_STP - 1) / PV_STP;
+  const float* vb = vc + g * HD + d0;
+  auto issue = [&](uint32_t s) {  // wave w's loads of stage s into ring slot s % PV_NST
+    float* dst = ring + (s % PV_NST) * (PV_STP * PV_DS);
+    for (uint32_t j = 0; j < PV_IPW; j++) {
+      const uint32_t i = w + 4 * j;
+      uint32_t p = s * PV_STP + i * 4 + t / 16;  // 4 positions of 256 B per load
+      if (p >= total) p = 0;
+      cx_dma16_async(reinterpret_cast<const uint8_t*>(vb + (size_t)p * kvd) + (t % 16) * 16,
+                     dst + i * 256);
     }
-    out[h * HD + tid] = o;
-    os[tid] = o;
+  };
+  for (uint32_t s = 0; s + 1 < PV_NST && s < nstage; s++) issue(s);
+  if (nstage >= PV_NST - 1)
+    cx_wait_vm<(PV_NST - 1) * PV_IPW>();
+  else
+    cx_wait_vm<0>();
+  if (PV_NST - 1 < nstage) issue(PV_NST - 1);
+  cx_wait_lds();
+  cx_barrier();  // every wave's scores and the exp table are in LDS
+  // 2. softmax over positions [0, total)
+  float mx = -INFINITY;
+  for (uint32_t p = tid; p < total; p += 256) mx = fmaxf(mx, e[p]);
+  mx = cx_wave_max(mx);
+  if (t == 0) red[w] = mx;
+  cx_wait_lds();
+  cx_barrier();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const bool uniform = !isfinite(mx);  // all -inf, or a NaN (src/ops.rs:1214-1219)
+  for (uint32_t p = tid; p < total; p += 256)
+    e[p] = uniform ? 1.0f / (float)total : cx_expf_tab(e[p] - mx, etab);
+  cx_wait_lds();
+  cx_barrier();
+  if (!uniform) {
+    if (tid == 0) red[0] = 1.0f / seq_sum_lds(e, total);
+    cx_wait_lds();
+    cx_barrier();
+    const float inv = red[0];
+    for (uint32_t p = tid; p < total; p += 256) e[p] = e[p] * inv;
+    cx_wait_lds();
+    cx_barrier();
   }
+  // 3. out[d0 + t] over the V ring, position order (wave 0)
+  float o = 0.0f;
+  for (uint32_t s = 0; s < nstage; s++) {
+    if (s + PV_NST <= nstage)
+      cx_wait_vm<(PV_NST - 1) * PV_IPW>();
+    else
+      cx_wait_vm<0>();
+    cx_barrier();  // stage s has landed, from every wave
+    if (w == 0) {
+      const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS) + t;
+      const float* ps = e + s * PV_STP;
+      if ((s + 1) * PV_STP <= total) {
+#pragma unroll
+        for (uint32_t j = 0; j < PV_STP; j++) o += ps[j] * vs[j * PV_DS];
+      } else {
+        for (uint32_t j = 0; s * PV_STP + j < total; j++) o += ps[j] * vs[j * PV_DS];
+      }
+    }
+    cx_wait_lds();
+    cx_barrier();  // the slot is read: refill it
+    if (s + PV_NST < nstage) issue(s + PV_NST);
+  }
+  if (w != 0) return;
+  out[h * HD + d0 + t] = o;
   if (!xq) return;
-  __syncthreads();
-  if (tid < HD / 8) {
+  float* os = ring;  // every load has landed and every read of the ring is done
+  os[t] = o;
+  cx_wait_lds();
+  if (t < (int)(PV_DS / 8)) {
     float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) v[j] = os[8 * tid + j];
-    cx_quant8<SUB>(v, (size_t)h * HD + 8 * tid, xq, xe, xs);
+    for (int j = 0; j < 8; j++) v[j] = os[8 * t + j];
+    cx_quant8<SUB>(v, (size_t)h * HD + d0 + 8 * t, xq, xe, xs);
   }
 }
 
@@ -534,17 +634,19 @@ size_t cx_attn_splits(size_t cap) { return (cap + ATT_P - 1) / ATT_P; }
 namespace {
 template <int HD>
 int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
-  hipLaunchKernelGGL(k_attn_scores<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads), dim3(64), 0, s,
-                     a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads, a.kvh, a.st,
-                     scale, a.sc, a.cap);
+  constexpr size_t sc_bytes = (SC_P * (HD * 4 + 16) + 1023) / 1024 * 1024 + 2 * HD * 4;
+  hipLaunchKernelGGL(k_attn_scores<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads), dim3(64),
+                     sc_bytes, s, a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads,
+                     a.kvh, a.st, scale, a.sc, a.cap);
   CX_HIP(hipGetLastError());
-  const size_t lds = a.cap * sizeof(float);
+  const size_t lds = (sc_lds(a.cap) + PV_NST * PV_STP * PV_DS) * sizeof(float);
+  const dim3 grid(a.heads, HD / PV_DS);
   if (a.sub == 16)
-    hipLaunchKernelGGL((k_attn_seq<HD, 16>), dim3(a.heads), dim3(256), lds, s, a.vc, a.sc, a.heads,
-                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+    hipLaunchKernelGGL((k_attn_seq<HD, 16>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads, a.kvh,
+                       a.st, a.cap, a.out, a.xq, a.xe, a.xs);
   else
-    hipLaunchKernelGGL((k_attn_seq<HD, 32>), dim3(a.heads), dim3(256), lds, s, a.vc, a.sc, a.heads,
-                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+    hipLaunchKernelGGL((k_attn_seq<HD, 32>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads, a.kvh,
+                       a.st, a.cap, a.out, a.xq, a.xe, a.xs);
   CX_HIP(hipGetLastError());
   return CX_OK;
 }
