@@ -137,6 +137,102 @@ def gemv_roofline(F, L, m, iters=360, reps=5):
     return avg, gbps, len(gates)
 
 
+PROBE_COPY_BYTES = 64 << 20
+
+
+def gemv_probe():
+    """The workload the PMC passes count: config-1 Q4_K GEMVs over 36
+    rotating matrices (random bytes with finite f16 scales: traffic does not
+    depend on values), then a 64 MiB device-to-device copy whose HBM bytes
+    are known (64 MiB read + 64 MiB written): the calibration kernel."""
+    import ctypes as C
+    import torch
+    from cosxamix_amd import _lib as L, ops
+    lib = L.load()
+    n, k = 11008, 2048
+    rb = ops.row_bytes(L.Q4_K, k)
+    mats = []
+    for i in range(36):
+        w = torch.randint(0, 256, (n * rb,), dtype=torch.uint8, device="cuda")
+        v = w.view(n * k // 256, 144)
+        v[:, 1] = 0x2C  # d = f16 0x2Cxx, dmin = 0x24xx: finite
+        v[:, 3] = 0x24
+        mats.append(w)
+    x = torch.randn(k, device="cuda")
+    xq, xe, xs = ops.cuantizar_i8_en(x, 32)
+    y = torch.empty(n, device="cuda")
+    s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for _ in range(3):
+        for w in mats:
+            L.check(lib.cx_gemv(L.Q4_K, C.c_void_p(w.data_ptr()), n, k, C.c_void_p(xq.data_ptr()),
+                                C.c_void_p(xe.data_ptr()), C.c_void_p(xs.data_ptr()),
+                                C.c_void_p(y.data_ptr()), s), "gemv")
+    src = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def _pmc_per_dispatch(csv_dir, counter):
+    """Mean counter value (KiB) per dispatch of the GEMV and of the copy."""
+    import csv
+    import glob
+    vals = {"gemv": [], "copy": []}
+    for path in glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name") != counter:
+                    continue
+                name = r.get("Kernel_Name", "")
+                key = "gemv" if "k_gemv" in name else ("copy" if "opy" in name else None)
+                if key:
+                    vals[key].append(float(r["Counter_Value"]))
+    if not vals["gemv"] or not vals["copy"]:
+        return None
+    # the copy runs 3 times: its first dispatch may include page-table warm-up
+    return statistics.median(vals["gemv"]), statistics.median(vals["copy"])
+
+
+def gemv_traffic():
+    """HBM bytes per config-1 GEMV from two rocprofv3 --pmc passes over
+    `bench.py --gemv-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch),
+    each scaled by what the same counter reads for the 64 MiB copy. Returns
+    (bytes, detail) or (None, reason)."""
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None, "rocprofv3 not found"
+    out = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="cx_pmc_", dir="/tmp")
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
+               sys.executable, os.path.abspath(__file__), "--gemv-probe"]
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"),
+                               capture_output=True, text=True, timeout=180)
+        except subprocess.TimeoutExpired:
+            return None, f"rocprofv3 --pmc {counter} timed out"
+        got = _pmc_per_dispatch(d, counter)
+        shutil.rmtree(d, ignore_errors=True)
+        if got is None:
+            return None, f"rocprofv3 --pmc {counter}: no counter rows (rc {r.returncode})"
+        out[counter] = got
+    fetch_g, fetch_c = out["FETCH_SIZE"]
+    write_g, write_c = out["WRITE_SIZE"]
+    f_scale, w_scale = PROBE_COPY_BYTES / fetch_c, PROBE_COPY_BYTES / write_c
+    traffic = fetch_g * f_scale + write_g * w_scale
+    log(f"[bench] PMC: gemv FETCH {fetch_g:.0f} KiB, WRITE {write_g:.0f} KiB per dispatch; "
+        f"64 MiB copy reads {fetch_c:.0f} KiB, writes {write_c:.0f} KiB -> scales "
+        f"{f_scale:.3f} / {w_scale:.3f}; traffic {traffic / 1e6:.3f} MB per GEMV")
+    return traffic, {"fetch_kib": round(fetch_g, 1), "write_kib": round(write_g, 1),
+                     "copy_fetch_kib": round(fetch_c, 1), "copy_write_kib": round(write_c, 1),
+                     "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}
+
+
 def cpu_baseline(F, L, m, prompt, decode_tokens=6):
     import numpy as np
     from oracle import oracle as O
@@ -200,10 +296,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true")
+    ap.add_argument("--gemv-probe", action="store_true")
     ap.add_argument("--trace-summary")
     a = ap.parse_args()
     if a.trace_summary:
         trace_summary(a.trace_summary)
+        return 0
+    if a.gemv_probe:
+        gemv_probe()
         return 0
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the decode loop of "
@@ -220,6 +321,7 @@ def main():
     per_tok_bytes = m.bytes_por_token()
     kv_bytes = 2 * F.DAISS_3B.capas * F.DAISS_3B.dim_kv() * 4 * (a.prompt + a.warmup + a.steps // 2)
     avg, gbps, ncopies = gemv_roofline(F, L, m)
+    traffic, tdetail = (None, "skipped (--no-traffic)") if a.no_traffic else gemv_traffic()
     cpu = None if a.no_cpu else cpu_baseline(F, L, m, prompt)
     out = {
         "metric": METRIC,
@@ -239,7 +341,9 @@ def main():
                                "linears Q4_K, f32 KV cache, random-init weights",
                    "prompt_tokens": a.prompt, "decode_tokens": a.steps, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": None if traffic is None else int(traffic),
+                     "traffic_source": tdetail,
                      "kernel": "k_gemv<Q4_K> config 1 (11008x2048)",
                      "us_per_launch": round(avg * 1e6, 3), "bytes_per_launch": CONFIG1_BYTES,
                      "rotating_matrices": ncopies},

@@ -10,9 +10,11 @@
 // every lane moves 16 consecutive bytes, so a wave reads 1 KiB of contiguous
 // HBM per instruction, no VGPRs hold weight data, and the whole tile is in
 // flight at once. The activation (k bytes + 2*k/sub floats) follows into LDS
-// the same way. R is chosen per launch so that there are >= 2 tiles per CU
-// and a tile fits in 64 KiB of LDS; with several workgroups resident per CU
-// the whole matrix is in flight within one wave of workgroups.
+// the same way, or — for the launches that start a layer half — every
+// workgroup makes it itself from the f32 residual (rmsnorm + quantization)
+// while its weights stream in. R is chosen per launch (see launch_t) so that
+// all tiles are resident at once: the whole matrix is in flight within one
+// wave of workgroups.
 //
 // Arithmetic. One lane handles one super-block (256 values) of one row: it
 // reads the block from LDS, unpacks the quants and the 6-bit scales in
@@ -35,6 +37,7 @@ namespace {
 
 constexpr uint32_t M4 = 0x0F0F0F0Fu, M2 = 0x03030303u, M1 = 0x01010101u;
 constexpr uint32_t TILE_LDS_MAX = 64 * 1024;
+constexpr uint32_t TILE_LDS_NORM_MAX = 80 * 1024;  // two workgroups per CU
 
 __device__ inline int dot4(uint32_t a, int b, int c) {
   return __builtin_amdgcn_sdot4((int)a, b, c, false);
@@ -454,8 +457,9 @@ struct TilePlan {
   uint32_t R, tiles, lds, lds_act, lds_scale, lds_terms, lds_norm;
 };
 
-// LDS layout of a tile of R rows: [16 skew + R*row_bytes + 16 pad] [xq k]
-// [xe, xs] [terms R x (nsub+4)] [norm input x, w: 2k floats]
+// LDS layout of a tile of R rows: [16 skew + R*row_bytes + 16 pad]
+// [xq, 272 bytes per 256] [xe, xs] then one region used first for the
+// rmsnorm input (x, w: 2k floats) and then for the terms (R x (nsub+4))
 TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
                    const uint32_t* rows, int nseg, bool norm) {
   TilePlan t{};
@@ -464,8 +468,9 @@ TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
   t.lds_act = (16 + R * row_bytes + 16 + 15) / 16 * 16;
   t.lds_scale = t.lds_act + (k / 256) * ACT_LDS_BLOCK;
   t.lds_terms = t.lds_scale + (8 * nsub + 15) / 16 * 16;
-  t.lds_norm = t.lds_terms + 4 * R * (nsub + 4);
-  t.lds = t.lds_norm + (norm ? 8 * k : 0);
+  t.lds_norm = t.lds_terms;
+  const uint32_t terms = 4 * R * (nsub + 4), nin = norm ? 8 * k : 0;
+  t.lds = t.lds_terms + (terms > nin ? terms : nin);
   return t;
 }
 
@@ -477,14 +482,28 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
       CX_REQUIRE(((uintptr_t)P.seg[i].w & 15u) == 0,
                  "gemv: %s weights must start 16-byte aligned", T == CX_Q4_K ? "Q4_K" : "Q5_K");
   }
-  // largest tile (<= 64 rows) that fits the LDS budget and leaves >= 2
-  // tiles per CU; small matrices fall back to the smallest tiles
+  // Tile rows (measured on MI355X at the 3B projection shapes):
+  //  - with the rmsnorm prologue every workgroup repeats the activation
+  //    work, so take one tile per CU (R = rows/256) when it fits in LDS, else
+  //    two tiles per CU;
+  //  - otherwise the largest R <= 16 that leaves >= 2 tiles per CU.
+  uint32_t total_rows = 0;
+  for (int i = 0; i < P.nseg; i++) total_rows += rows[i];
   TilePlan best{};
-  for (uint32_t R = 64; R >= 1; R >>= 1) {
-    TilePlan t = plan_tile(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM);
-    if (t.lds > TILE_LDS_MAX) continue;
-    best = t;
-    if (t.tiles >= 512) break;
+  if (NORM) {
+    for (uint32_t per_cu = 1; per_cu <= 8 && !best.R; per_cu *= 2) {
+      uint32_t R = (total_rows + 256 * per_cu - 1) / (256 * per_cu);
+      R = R < 1 ? 1 : (R > 64 ? 64 : R);
+      TilePlan t = plan_tile(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM);
+      if (t.lds <= TILE_LDS_NORM_MAX) best = t;
+    }
+  } else {
+    for (uint32_t R = 16; R >= 1; R >>= 1) {
+      TilePlan t = plan_tile(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM);
+      if (t.lds > TILE_LDS_MAX) continue;
+      best = t;
+      if (t.tiles >= 512) break;
+    }
   }
   CX_REQUIRE(best.R, "gemv: a row of %u values does not fit in LDS", P.k);
   P.R = best.R;

@@ -230,12 +230,12 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 // sub-blocks). Bit-identical to the scalar reference.
 constexpr uint32_t SC_P = 64;     // positions per scores wave
 constexpr uint32_t PV_DS = 64;    // head dims per softmax-V workgroup (wave 0's lanes)
-constexpr uint32_t PV_STP = 32;   // positions per V stage (8 KiB)
-constexpr uint32_t PV_NST = 16;   // V stages in the LDS ring (128 KiB)
+constexpr uint32_t PV_STP = 64;   // positions per V stage (16 KiB)
+constexpr uint32_t PV_NST = 8;    // V stages in the LDS ring (128 KiB)
 constexpr uint32_t PV_IPS = PV_STP * PV_DS * 4 / 1024;  // loads per stage: 8
-constexpr uint32_t PV_IPW = PV_IPS / 4;                  // per wave: 2
+constexpr uint32_t PV_IPW = PV_IPS / 4;                  // per wave: 4
 // A wave tracks at most 63 outstanding loads (vmcnt is 6 bits): its share
-// of the scores (<= 4 loads for 4096 positions) plus 15 stages ahead (30).
+// of the scores (<= 4 loads for 4096 positions) plus 7 stages ahead (28).
 static_assert(4 + (PV_NST - 1) * PV_IPW <= 63, "too many loads in flight");
 
 __host__ __device__ constexpr uint32_t sc_stride(uint32_t cap) { return (cap + 3) / 4 * 4; }
@@ -316,39 +316,62 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
   sc[(size_t)h * sc_stride(cap) + p] = s * scale;
 }
 
-// Sequential sum of x[0..n) from 0 (one lane), LDS reads issued a batch ahead
+// Sequential sum of x[0..n) from 0 (one lane). LDS reads run a batch of 32
+// values ahead, alternating between two register buffers.
+__device__ inline void add32(float& tot, const float4 (&a)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    tot += a[i].x;
+    tot += a[i].y;
+    tot += a[i].z;
+    tot += a[i].w;
+  }
+}
 __device__ inline float seq_sum_lds(const float* x, uint32_t n) {
   const float4* x4 = reinterpret_cast<const float4*>(x);
   const uint32_t n4 = n / 4;
   float tot = 0.0f;
-  float4 a[8];
+  float4 A[8], B[8];
 #pragma unroll
-  for (int i = 0; i < 8; i++) a[i] = x4[i];  // may read past n: never used
+  for (int i = 0; i < 8; i++) A[i] = x4[i];  // may read past n: never used
   uint32_t b = 0;
-  for (; b + 8 <= n4; b += 8) {
-    float4 nx[8];
+  for (;;) {
+    if (b + 8 > n4) break;
 #pragma unroll
-    for (int i = 0; i < 8; i++) nx[i] = x4[b + 8 + i];
+    for (int i = 0; i < 8; i++) B[i] = x4[b + 8 + i];
+    add32(tot, A);
+    b += 8;
+    if (b + 8 > n4) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      tot += a[i].x;
-      tot += a[i].y;
-      tot += a[i].z;
-      tot += a[i].w;
+      for (int i = 0; i < 8; i++) A[i] = B[i];
+      break;
     }
 #pragma unroll
-    for (int i = 0; i < 8; i++) a[i] = nx[i];
+    for (int i = 0; i < 8; i++) A[i] = x4[b + 8 + i];
+    add32(tot, B);
+    b += 8;
   }
 #pragma unroll
   for (int i = 0; i < 8; i++)
     if (b + i < n4) {
-      tot += a[i].x;
-      tot += a[i].y;
-      tot += a[i].z;
-      tot += a[i].w;
+      tot += A[i].x;
+      tot += A[i].y;
+      tot += A[i].z;
+      tot += A[i].w;
     }
   for (uint32_t p = n4 * 4; p < n; p++) tot += x[p];
   return tot;
+}
+
+__device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) {
+  o += p[0].x * v[0];
+  o += p[0].y * v[1];
+  o += p[0].z * v[2];
+  o += p[0].w * v[3];
+  o += p[1].x * v[4];
+  o += p[1].y * v[5];
+  o += p[1].z * v[6];
+  o += p[1].w * v[7];
 }
 
 // 256 threads: every wave streams its share of the V ring (4x the loads in
@@ -432,8 +455,30 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
       const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS) + t;
       const float* ps = e + s * PV_STP;
       if ((s + 1) * PV_STP <= total) {
+        // batches of 8 positions; the next batch's LDS reads are issued
+        // before the current batch's adds, alternating two register buffers
+        const float4* p4 = reinterpret_cast<const float4*>(ps);
+        float va[8], vb[8];
+        float4 pa[2], pb[2];
 #pragma unroll
-        for (uint32_t j = 0; j < PV_STP; j++) o += ps[j] * vs[j * PV_DS];
+        for (int j = 0; j < 8; j++) va[j] = vs[j * PV_DS];
+        pa[0] = p4[0];
+        pa[1] = p4[1];
+#pragma unroll
+        for (uint32_t bt = 0; bt < PV_STP / 8; bt += 2) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) vb[j] = vs[(8 * (bt + 1) + j) * PV_DS];
+          pb[0] = p4[2 * (bt + 1)];
+          pb[1] = p4[2 * (bt + 1) + 1];
+          pv8(o, pa, va);
+          if (bt + 2 < PV_STP / 8) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) va[j] = vs[(8 * (bt + 2) + j) * PV_DS];
+            pa[0] = p4[2 * (bt + 2)];
+            pa[1] = p4[2 * (bt + 2) + 1];
+          }
+          pv8(o, pb, vb);
+        }
       } else {
         for (uint32_t j = 0; s * PV_STP + j < total; j++) o += ps[j] * vs[j * PV_DS];
       }
