@@ -19,7 +19,12 @@ the oracle forward whose Q4_K row kernel is the reference's own compiled
 `cosxamix_q4k_completo` (oracle/_ref), threaded like ops.rs (32-row tasks)
 over the host's cores; same 512-token prompt, then a few timed decode tokens.
 
+Batched (the "batched" object): Q4_K 11008 x 2048 and
+2048 x 11008 times m = 8, 32, 512 activation rows through cx_matmul_auto
+(int8 MFMA), against the reference's per-row CPU matmul.
+
 Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--no-cpu]
+       python bench.py --batched-only
        python bench.py --trace-summary gpurun_out/.../kernel_trace.csv
 """
 from __future__ import annotations
@@ -273,6 +278,92 @@ def cpu_baseline(F, L, m, prompt, decode_tokens=6):
                        f"{threads} threads; CPU: {name}")}
 
 
+CONFIG4_MS = (8, 32, 512)
+
+
+def batched_bench(L, m, with_cpu, calls=20, reps=5):
+    """the model's layer-0 Q4_K ffn_gate (11008 x 2048) and
+    ffn_down (2048 x 11008) times m = 8, 32, 512 seeded N(0, 1) activation
+    rows through cx_matmul_auto (activation quantization + the int8 MFMA
+    contraction), timed as a captured graph of `calls` calls on torch's
+    stream. The CPU side is the reference's per-row path: its compiled Q4_K
+    row kernel (cosxamix_q4k_completo) in the oracle's 32-row task loop."""
+    import ctypes as C
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    lib = L.load()
+    names = [t[0] for t in m.tensores()]
+    mats = []
+    for suffix in ("blk.0.ffn_gate.weight", "blk.0.ffn_down.weight"):
+        i = names.index(suffix)
+        _, t, (k, n), _ = m.tensores()[i]
+        assert t == L.Q4_K
+        mats.append((suffix, i, n, k))
+    ref = O.load_ref() if with_cpu else None
+    _, cores = cpu_info()
+    threads = max(1, min(cores, 16))
+    stream = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    cases = []
+    for name, i, n, k in mats:
+        wp = m.tensor_ptr(i)
+        host_w = m.tensor(i) if with_cpu else None
+        for rows in sorted(CONFIG4_MS, reverse=True):  # the largest first sizes the scratch
+            gen = torch.Generator(device="cuda").manual_seed(rows * 7 + n)
+            x = torch.randn(rows, k, generator=gen, device="cuda", dtype=torch.float32)
+            y = torch.empty(rows, n, device="cuda", dtype=torch.float32)
+
+            def call():
+                L.check(lib.cx_matmul_auto(rows, k, n, C.c_void_p(x.data_ptr()), C.c_void_p(wp),
+                                           L.Q4_K, C.c_void_p(y.data_ptr()), stream()), "matmul_auto")
+
+            for _ in range(3):
+                call()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(calls):
+                    call()
+            g.replay()
+            torch.cuda.synchronize()
+            per = []
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                g.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                per.append(e0.elapsed_time(e1) * 1e-3 / calls)
+            sec = statistics.median(per)
+            case = {"matrix": f"{n}x{k}", "m": rows, "us": round(sec * 1e6, 2),
+                    "int_TOPs": round(2.0 * rows * n * k / sec / 1e12, 2),
+                    "us_per_row": round(sec * 1e6 / rows, 3)}
+            if with_cpu:
+                xh = x.cpu().numpy()
+                kern = O.ref_row_kernel(ref, O.Q4_K) if ref is not None else None
+                runs = []
+                for _ in range(3):
+                    t0 = time.perf_counter()
+                    want = O.matmul_fused(O.Q4_K, xh, host_w, n, threads=threads, kernel=kern)
+                    runs.append(time.perf_counter() - t0)
+                cpu = statistics.median(runs)
+                got = y.cpu().numpy().astype(np.float64)
+                err = float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+                case.update({"cpu_ms": round(cpu * 1e3, 2), "speedup_vs_cpu": round(cpu / sec, 1),
+                             "rel_l2_vs_cpu": float(f"{err:.3g}")})
+            log(f"[bench] config 4 {name} m={rows}: {case}")
+            cases.append(case)
+            del g
+    return {"workload": "BASELINE config 4: layer-0 Q4_K ffn_gate (11008x2048) and ffn_down "
+                        "(2048x11008) of the daiss-3b model x m seeded N(0,1) f32 rows; "
+                        "cx_matmul_auto = activation quantization + int8 MFMA contraction, "
+                        f"median of {reps} replays of a captured graph of {calls} calls",
+            "cases": cases,
+            "cpu": None if not with_cpu else
+            (f"reference per-row path: {'cosxamix_q4k_completo' if ref is not None else 'oracle scalar'}"
+             f" row kernel, 32-row tasks over {threads} threads, median of 3 runs")}
+
+
 def trace_summary(path):
     """Per (kernel, grid) dispatch statistics from a rocprofv3 kernel trace."""
     import csv
@@ -298,6 +389,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true")
     ap.add_argument("--gemv-probe", action="store_true")
+    ap.add_argument("--batched-only", action="store_true",
+                    help="only the config-4 batched contraction (GPU side), e.g. under rocprofv3")
     ap.add_argument("--trace-summary")
     a = ap.parse_args()
     if a.trace_summary:
@@ -316,6 +409,10 @@ def main():
     from cosxamix_amd import _lib as L
     from cosxamix_amd import forward as F
 
+    if a.batched_only:
+        m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)
+        print(json.dumps(batched_bench(L, m, False)), flush=True)
+        return 0
     m, prompt, toks, timed, total_ms = decode_bench(F, L, a.steps, a.warmup, a.prompt)
     tok_s = a.steps / (total_ms * 1e-3)
     per_tok_bytes = m.bytes_por_token()
@@ -323,6 +420,7 @@ def main():
     avg, gbps, ncopies = gemv_roofline(F, L, m)
     traffic, tdetail = (None, "skipped (--no-traffic)") if a.no_traffic else gemv_traffic()
     cpu = None if a.no_cpu else cpu_baseline(F, L, m, prompt)
+    batched = batched_bench(L, m, not a.no_cpu)
     out = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -352,6 +450,7 @@ def main():
                    "weight_bytes_per_token": per_tok_bytes,
                    "effective_GBps": round((per_tok_bytes + kv_bytes) / (total_ms * 1e-3 / a.steps) / 1e9, 1),
                    "first_tokens": [int(t) for t in toks[:8]]},
+        "batched": batched,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -22,8 +22,10 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # MFMA results in VGPRs: no v_accvgpr_read before the f32 epilogue
+         "-mllvm", "-amdgpu-mfma-vgpr-form",
          "-Wall", "-Wno-unused-function", "-I" + os.path.join(ROOT, "include")]
-SOURCES = ["cx_api.hip", "cx_gemv.hip", "cx_ops.hip", "cx_gen.hip"]
+SOURCES = ["cx_api.hip", "cx_gemv.hip", "cx_gemm.hip", "cx_ops.hip", "cx_gen.hip"]
 
 
 def _run(cmd):

@@ -18,24 +18,27 @@
 
 // Each lane holds 8 consecutive values v[0..8) at position i (i % 8 == 0);
 // the SUB/8 lanes of one sub-block are consecutive lanes of one quad and
-// must call this together. Writes 8 bytes of xq and, from the sub-block's
-// first lane, its xe and xs.
+// must call this together. cx_quant8_vals gives the lane's 8 quantized bytes
+// (lo, hi) and the sub-block's xe (d) and integer sum (s); cx_quant8 writes
+// the 8 bytes of xq and, from the sub-block's first lane, its xe and xs.
 template <int SUB>
-__device__ inline void cx_quant8(const float (&v)[8], size_t i, int8_t* xq, float* xe,
-                                 float* xs) {
+__device__ inline void cx_quant8_vals(const float (&v)[8], uint32_t& lo, uint32_t& hi, float& d,
+                                      int32_t& s) {
   static_assert(SUB == 16 || SUB == 32, "sub-blocks of 16 or 32");
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[j]));
   amax = fmaxf(amax, cx_xor1f(amax));
   if (SUB == 32) amax = fmaxf(amax, cx_xor2f(amax));
-  float d = 0.0f, inv = 0.0f;
+  float inv = 0.0f;
+  d = 0.0f;
   if (amax > 0.0f) {
     d = amax / 127.0f;
     inv = 127.0f / amax;
   }
-  int32_t s = 0;
-  uint32_t lo = 0, hi = 0;
+  s = 0;
+  lo = 0;
+  hi = 0;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     const int8_t q = cx_rust_i8(roundf(v[j] * inv));
@@ -47,6 +50,15 @@ __device__ inline void cx_quant8(const float (&v)[8], size_t i, int8_t* xq, floa
   }
   s += cx_xor1(s);
   if (SUB == 32) s += cx_xor2(s);
+}
+
+template <int SUB>
+__device__ inline void cx_quant8(const float (&v)[8], size_t i, int8_t* xq, float* xe,
+                                 float* xs) {
+  uint32_t lo, hi;
+  float d;
+  int32_t s;
+  cx_quant8_vals<SUB>(v, lo, hi, d, s);
   *reinterpret_cast<uint2*>(xq + i) = make_uint2(lo, hi);
   if ((i & (SUB - 1)) == 0) {
     xe[i / SUB] = d;

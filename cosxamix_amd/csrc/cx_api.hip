@@ -206,6 +206,14 @@ extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, co
   CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
   CX_REQUIRE(n < (1u << 31) && k < (1u << 31), "matmul_auto: shape too large");
   if (!m || !n) return CX_OK;
+  // Several rows of a Q4_K/Q5_K matrix: all at once on int8 MFMA, each
+  // output bit-identical to the row-by-row GEMV below.
+  if (m > 1 && cx_gemm_supported(type)) {
+    void* sp = nullptr;
+    int rc = cx_scratch_reserve(cx_gemm_scratch_bytes(m, k), &sp);
+    if (rc) return rc;
+    return cx_launch_gemm(type, w, n, k, lhs, m, dst, sp, STREAM(stream));
+  }
   // Every input row is quantized once (ops.rs:469-483), then each output row
   // is the fused GEMV of its own input row: row by row is exactly the
   // reference's "one row equals a batch" (ops.rs:1364-1393).

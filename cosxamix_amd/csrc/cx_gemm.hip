@@ -1,0 +1,453 @@
+// cx_gemm.hip — multi-row k-quant contraction on int8 MFMA (gfx950):
+// dst[a][r] = fused dot of weight row r with activation row a, for m
+// activation rows at once (ops::matmul_auto with m > 1, src/ops.rs:1056-1093;
+// BASELINE config 4 and prefill-shaped calls).
+//
+// Q4_K and Q5_K, whose 32-value sub-blocks are exactly the K = 32 of
+// v_mfma_i32_16x16x32_i8: one MFMA gives the exact integer sums E_j of one
+// sub-block for a 16 (weight rows) x 16 (activation rows) tile. Each lane
+// applies the scalar kernel's f32 term to its four results,
+//   term_j = xe_j * (d*sc_j * E_j - dmin*mn_j * xs_j),
+// and the terms of one output are added sub-block after sub-block from 0
+// (src/kernels/scalar.rs:132-217), so every output equals the per-row dot bit
+// for bit and a row of a batch equals the row alone (src/ops.rs:1364-1393).
+// The reference's own m >= 24 path (src/ops.rs:607-829) adds in another order
+// within 1e-4 of the maximum (src/ops.rs:1518-1561); keeping the per-row
+// order makes a batched prefill bit-identical to token-by-token.
+//
+// The per-sub-block f32 term (6 VALU operations per output and sub-block)
+// bounds this path, not the MFMA: a 16x16x32 MFMA is followed by 24 VALU
+// instructions per lane.
+//
+// MFMA lane layout (checked on the device): A 16x32 — lane l holds row
+// l%16, k = 8(l/16)..+8 as 8 bytes; B 32x16 — lane l holds column l%16,
+// same k range; C 16x16 — lane l element i is row 4(l/16)+i, column l%16.
+// Activations are the A operand and weights the B operand, so a lane's four
+// results share one weight row (l%16): the lane decodes that row's d, dmin
+// and 6-bit scales itself, from one 16-byte read of the block header, and
+// reads xe, xs of its four activation rows as float4s.
+//
+// Workgroup: 4 or 8 waves over a TW x MT tile (TW = 16 RW weight rows, MT =
+// 16 AW WA activation rows); the waves split rows (RW), activation tiles (AW)
+// and, when a tile is too small to give every wave its own rows, the eight
+// sub-blocks of each super-block (KS). With KS > 1 the waves write their
+// terms to LDS and each thread adds the terms of its outputs in sub-block
+// order. The k loop walks super-blocks through an S-stage ring of
+// direct-to-LDS loads: a stage is the tile's weight bytes of one super-block,
+// the MT activation rows' 256 bytes, and their xe and xs. Every wave issues
+// D loads per stage, so the wait for a stage is a fixed vmcnt; loads beyond
+// the stage's bytes reload a valid address into the stage's tail.
+
+#include "cx_act.h"
+#include "cx_internal.h"
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// The B operand (weights): positions 8g..8g+7 of sub-block j of a block in
+// LDS as 8 i8 values. load() reads the raw bytes, operand() unpacks them.
+template <int T> struct GQ;
+template <> struct GQ<CX_Q4_K> {
+  static constexpr int BPB = 144;
+  struct Raw {
+    uint2 q;  // qs bytes 32(j/2) + 8g .. +8 (low nibbles: even j, high: odd j)
+  };
+  __device__ static Raw load(const uint8_t* blk, int j, int g) {
+    return Raw{*reinterpret_cast<const uint2*>(blk + 16 + 32 * (j >> 1) + 8 * g)};
+  }
+  __device__ static long operand(const Raw& r, int j) {
+    const uint32_t sh = 4 * (j & 1);
+    const uint32_t lo = (r.q.x >> sh) & 0x0F0F0F0Fu, hi = (r.q.y >> sh) & 0x0F0F0F0Fu;
+    return (long)(((uint64_t)hi << 32) | lo);
+  }
+};
+template <> struct GQ<CX_Q5_K> {
+  static constexpr int BPB = 176;
+  struct Raw {
+    uint2 q;  // qs bytes 32(j/2) + 8g .. +8
+    uint2 h;  // qh bytes 8g .. +8: bit j is the fifth bit of sub-block j
+  };
+  __device__ static Raw load(const uint8_t* blk, int j, int g) {
+    return Raw{*reinterpret_cast<const uint2*>(blk + 48 + 32 * (j >> 1) + 8 * g),
+               *reinterpret_cast<const uint2*>(blk + 16 + 8 * g)};
+  }
+  __device__ static long operand(const Raw& r, int j) {
+    const uint32_t sh = 4 * (j & 1);
+    const uint32_t lo = ((r.q.x >> sh) & 0x0F0F0F0Fu) | (((r.h.x >> j) & 0x01010101u) << 4);
+    const uint32_t hi = ((r.q.y >> sh) & 0x0F0F0F0Fu) | (((r.h.y >> j) & 0x01010101u) << 4);
+    return (long)(((uint64_t)hi << 32) | lo);
+  }
+};
+
+// quant::escala_y_minimo (src/quant.rs:108-117) of sub-block j from the 12
+// scale bytes q[0..12) held as the words y (q0..q3), z (q4..q7), w (q8..q11)
+__device__ inline void scale_min(uint32_t y, uint32_t z, uint32_t w, int j, uint32_t& sc,
+                                 uint32_t& mn) {
+  if (j < 4) {
+    const int s = 8 * j;
+    sc = (y >> s) & 63;
+    mn = (z >> s) & 63;
+  } else {
+    const int s = 8 * (j - 4);
+    sc = ((w >> s) & 0xF) | (((y >> (s + 6)) & 3) << 4);
+    mn = ((w >> (s + 4)) & 0xF) | (((z >> (s + 6)) & 3) << 4);
+  }
+}
+
+struct GemmParams {
+  const uint8_t* w;     // n rows x row_bytes, GGUF raw
+  const int8_t* xq;     // m_pad rows x k (rows >= m are zero)
+  const float* xexs;    // per sub-block J: xe of the m_pad rows, then their xs
+  float* dst;           // m x n
+  uint32_t n, k, m, m_pad, nb, row_bytes, row_tiles, act_tiles;
+  const float* lhs;     // m x k f32: the quantizer's input (not read by k_gemm)
+  uint8_t* scratch;     // where xq and xexs are carved (not read by k_gemm)
+};
+
+template <int T, int RW, int AW, int WA, int KS, int NSB>
+struct Shape {
+  static constexpr int NW = RW * AW * KS;  // waves
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  static constexpr int BPB = GQ<T>::BPB;
+  static constexpr int TW = 16 * RW, MT = 16 * AW * WA;
+  static constexpr int NU = 8 * NSB;  // sub-blocks per stage
+  static constexpr int NJ = NU / KS;  // sub-blocks per wave per stage
+  static_assert(NU % KS == 0 && (NJ >= 8 ? NJ % 8 == 0 : 8 % NJ == 0), "even split");
+  static constexpr int NBW = NJ >= 8 ? NJ / 8 : 1;  // blocks a wave touches per stage
+  static constexpr int RB = NSB * BPB;              // LDS bytes per weight row
+  // LDS bytes per activation row: 68 mod 64 words, so the 8-byte A operand
+  // reads of 16 rows x 2 lane groups (one half-wave pass) hit 64 distinct banks
+  static constexpr int XS = NSB * 256 + 16;
+  static constexpr int WB = TW * RB, XB = MT * XS, EB = NU * MT * 8;
+  static constexpr int WCH = WB / 16, XCH = XB / 16, ECH = EB / 16;
+  static constexpr int SLOT = NW * 1024;  // bytes of one load of every wave
+  static constexpr int STAGE = (WB + XB + EB + SLOT - 1) / SLOT * SLOT;
+  static constexpr int D = STAGE / SLOT;  // loads per wave per stage
+  static constexpr int TERMS = KS > 1 ? 2 * NU * TW * MT * 4 : 0;
+  static constexpr size_t lds(int S) { return (size_t)S * STAGE + TERMS; }
+};
+
+// wait until at most `ahead` stages (D loads each) of this wave are in flight
+template <int D, int N>
+__device__ inline void wait_stages(int ahead) {
+  if constexpr (N == 0) {
+    cx_wait_vm<0>();
+  } else {
+    if (ahead >= N)
+      cx_wait_vm<N * D>();
+    else
+      wait_stages<D, N - 1>(ahead);
+  }
+}
+
+template <int T, int RW, int AW, int WA, int KS, int NSB, int S>
+__global__ __launch_bounds__(64 * RW * AW * KS) void k_gemm(GemmParams P) {
+  using SH = Shape<T, RW, AW, WA, KS, NSB>;
+  constexpr int BPB = SH::BPB, TW = SH::TW, MT = SH::MT, NU = SH::NU, NJ = SH::NJ;
+  constexpr int D = SH::D, NW = SH::NW, RB = SH::RB, XS = SH::XS;
+  static_assert(S >= 2 && (S - 2) * D <= 63, "stage waits must fit vmcnt");
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int g = lane >> 4, c16 = lane & 15;
+  const int ks = wave % KS, aw = (wave / KS) % AW, rw = wave / (KS * AW);
+
+  // blockIdx -> (row tile, activation tile): the activation tiles of one row
+  // tile share blockIdx % 8, i.e. one XCD and its L2, which then holds the
+  // row tile's weights for all of them
+  const uint32_t b = blockIdx.x, A = P.act_tiles;
+  const uint32_t rt = b / (8 * A) * 8 + b % 8, at = b / 8 % A;
+  if (rt >= P.row_tiles) return;  // whole workgroup, before any load or barrier
+  const uint32_t r0 = rt * TW, a0 = at * MT;
+
+  // this lane's load sources: slot s carries chunk NW*64 s + 64 wave + lane
+  // of a stage, i.e. LDS bytes [16 c, 16 c + 16) of the stage; the chunk
+  // belongs to super-block bis[s] of the stage (a stage past the last
+  // super-block loads a valid dummy address instead)
+  const uint8_t* src[D];
+  uint32_t inc[D];
+  uint32_t bis[D];
+#pragma unroll
+  for (int s = 0; s < D; s++) {
+    const uint32_t c = NW * 64 * s + 64 * wave + lane;
+    src[s] = P.w;
+    inc[s] = 0;
+    bis[s] = 0;
+    if (c < (uint32_t)SH::WCH) {
+      const uint32_t r = c / (RB / 16), part = c % (RB / 16);
+      const uint32_t row = r0 + r < P.n ? r0 + r : P.n - 1;  // past the end: a valid row
+      src[s] = P.w + (size_t)row * P.row_bytes + 16 * part;
+      inc[s] = RB;
+      bis[s] = part / (BPB / 16);
+    } else if (c < (uint32_t)(SH::WCH + SH::XCH)) {
+      const uint32_t cc = c - SH::WCH, a = cc / (XS / 16);
+      uint32_t part = cc % (XS / 16);
+      if (part == 16 * NSB) part = 0;  // the row's pad chunk
+      src[s] = reinterpret_cast<const uint8_t*>(P.xq) + (size_t)(a0 + a) * P.k + 16 * part;
+      inc[s] = 256 * NSB;
+      bis[s] = part / 16;
+    } else if (c < (uint32_t)(SH::WCH + SH::XCH + SH::ECH)) {
+      // sub-block u of the stage: MT xe, then MT xs
+      const uint32_t cc = c - SH::WCH - SH::XCH, u = cc / (MT / 2);
+      const uint32_t h = cc % (MT / 2) / (MT / 4), part = cc % (MT / 4);
+      src[s] = reinterpret_cast<const uint8_t*>(P.xexs + (size_t)(2 * u + h) * P.m_pad + a0) +
+               16 * part;
+      inc[s] = NU * 2 * P.m_pad * 4;
+      bis[s] = u / 8;
+    }
+  }
+  const uint32_t nb = P.nb, nst = (nb + NSB - 1) / NSB;
+  auto issue = [&](uint32_t sb) {
+    uint8_t* base = lds + (sb % S) * SH::STAGE + 1024 * wave;
+#pragma unroll
+    for (int s = 0; s < D; s++) {
+      const uint8_t* p = sb * NSB + bis[s] < nb ? src[s] + (size_t)sb * inc[s] : P.w;
+      cx_dma16_async(p, base + SH::SLOT * s);
+    }
+  };
+
+  float* terms = reinterpret_cast<float*>(lds + S * SH::STAGE);  // [2][NU][TW][MT]
+  constexpr int NQ = TW * MT;  // outputs of the tile
+  constexpr int PP = KS > 1 ? (NQ + 64 * NW - 1) / (64 * NW) : 1;  // outputs chained per thread
+  float acc[WA][4];
+  float cacc[PP];
+#pragma unroll
+  for (int t = 0; t < WA; t++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PP; i++) cacc[i] = 0.0f;
+  // thread `tid` adds, sub-block by sub-block, the terms of outputs
+  // q = tid + 64 NW i (weight row q / MT, activation row q % MT) over the
+  // first `nu` sub-blocks of a stage
+  auto chain = [&](const float* tb, uint32_t nu) {
+#pragma unroll
+    for (int i = 0; i < PP; i++) {
+      const int q = tid + 64 * NW * i;
+      if (NQ % (64 * NW) == 0 || q < NQ) {
+        float v[NU];  // every load first (all in the buffer), then the adds in order
+#pragma unroll
+        for (int u = 0; u < NU; u++) v[u] = tb[u * NQ + q];
+#pragma unroll
+        for (int u = 0; u < NU; u++)
+          if ((uint32_t)u < nu) cacc[i] += v[u];
+      }
+    }
+  };
+  auto valid_sub = [&](uint32_t sb) { return 8 * (nb - sb * NSB < NSB ? nb - sb * NSB : NSB); };
+
+  for (uint32_t st = 0; st < (uint32_t)(S - 1) && st < nst; st++) issue(st);
+  for (uint32_t sb = 0; sb < nst; sb++) {
+    const uint32_t last = sb + S - 2 < nst - 1 ? sb + S - 2 : nst - 1;
+    wait_stages<D, S - 2>((int)(last - sb));
+    cx_wait_lds();  // this wave's reads of the previous stage are done
+    cx_barrier();   // stage sb is in LDS for every wave; slot (sb - 1) % S is free
+    if (sb + S - 1 < nst) issue(sb + S - 1);
+    const uint8_t* cur = lds + (sb % S) * SH::STAGE;
+    const uint8_t* X = cur + SH::WB;
+    const float* E = reinterpret_cast<const float*>(cur + SH::WB + SH::XB);
+    float* tb = terms + (sb & 1) * (NU * NQ);
+    const int ub = ks * NJ;  // this wave's first sub-block of the stage
+#pragma unroll
+    for (int bb = 0; bb < SH::NBW; bb++) {
+      const int bi = (ub >> 3) + bb;  // super-block of the stage
+      if (sb * NSB + bi >= nb) break;
+      // this lane's weight row: d, dmin and the 12 scale bytes in one read
+      const uint8_t* wrow = cur + (16 * rw + c16) * RB + bi * BPB;
+      const uint4 hd = *reinterpret_cast<const uint4*>(wrow);
+      constexpr int NJB = NJ < 8 ? NJ : 8;  // sub-blocks of this block for this wave
+      // every operand of the block first when few (one round of LDS latency),
+      // else per sub-block
+      constexpr bool BATCH = NJB * WA <= 8;
+      typename GQ<T>::Raw wr[BATCH ? NJB : 1];
+      long axb[BATCH ? NJB : 1][WA];
+      float4 xeb[BATCH ? NJB : 1][WA], xsb[BATCH ? NJB : 1][WA];
+      auto fetch = [&](int slot, int u, int j) {
+        wr[slot] = GQ<T>::load(wrow, j, g);
+#pragma unroll
+        for (int t = 0; t < WA; t++) {
+          const int ab = 16 * (aw * WA + t);  // first activation row of the MFMA tile
+          axb[slot][t] = *reinterpret_cast<const long*>(X + (ab + c16) * XS + 32 * u + 8 * g);
+          xeb[slot][t] = *reinterpret_cast<const float4*>(E + u * 2 * MT + ab + 4 * g);
+          xsb[slot][t] = *reinterpret_cast<const float4*>(E + u * 2 * MT + MT + ab + 4 * g);
+        }
+      };
+      if constexpr (BATCH) {
+#pragma unroll
+        for (int jj = 0; jj < NJB; jj++) fetch(jj, ub + 8 * bb + jj, (ub + 8 * bb + jj) & 7);
+      }
+      const float d = cx_h2f(hd.x & 0xFFFFu), dmin = cx_h2f(hd.x >> 16);
+#pragma unroll
+      for (int jj = 0; jj < NJB; jj++) {
+        const int u = ub + 8 * bb + jj, j = u & 7, sl = BATCH ? jj : 0;
+        if constexpr (!BATCH) fetch(0, u, j);
+        uint32_t sc, mn;
+        scale_min(hd.y, hd.z, hd.w, j, sc, mn);
+        const float ds = d * (float)sc, dm = dmin * (float)mn;
+        const long bw = GQ<T>::operand(wr[sl], j);
+#pragma unroll
+        for (int t = 0; t < WA; t++) {
+          const int ab = 16 * (aw * WA + t);
+          v4i e = {0, 0, 0, 0};
+          e = __builtin_amdgcn_mfma_i32_16x16x32_i8(axb[sl][t], bw, e, 0, 0, 0);
+          const float4 xe = xeb[sl][t], xs = xsb[sl][t];
+          const float xev[4] = {xe.x, xe.y, xe.z, xe.w}, xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+          float tv[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) tv[i] = xev[i] * (ds * (float)e[i] - dm * xsv[i]);
+          if constexpr (KS == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[t][i] += tv[i];
+          } else {
+            *reinterpret_cast<float4*>(tb + (u * TW + 16 * rw + c16) * MT + ab + 4 * g) =
+                make_float4(tv[0], tv[1], tv[2], tv[3]);
+          }
+        }
+      }
+    }
+    if constexpr (KS > 1) {
+      if (sb > 0) chain(terms + ((sb - 1) & 1) * (NU * NQ), valid_sub(sb - 1));
+    }
+  }
+
+  if constexpr (KS > 1) {
+    cx_wait_lds();
+    cx_barrier();
+    chain(terms + ((nst - 1) & 1) * (NU * NQ), valid_sub(nst - 1));
+#pragma unroll
+    for (int i = 0; i < PP; i++) {
+      const int q = tid + 64 * NW * i;
+      const uint32_t a = a0 + q % MT, r = r0 + q / MT;
+      if (q < NQ && a < P.m && r < P.n) P.dst[(size_t)a * P.n + r] = cacc[i];
+    }
+  } else {
+    // lane: weight row r, activation rows 4g .. 4g+3 of each MFMA tile
+    const uint32_t r = r0 + 16 * rw + c16;
+    if (r < P.n) {
+#pragma unroll
+      for (int t = 0; t < WA; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const uint32_t a = a0 + 16 * (aw * WA + t) + 4 * g + i;
+          if (a < P.m) P.dst[(size_t)a * P.n + r] = acc[t][i];
+        }
+    }
+  }
+}
+
+// ops::cuantizar_i8_en (src/ops.rs:178-198) of m rows into the layout above:
+// xq rows [m, m_pad) and their xe, xs are zero
+__global__ __launch_bounds__(256) void k_quantize_gemm(const float* x, uint32_t m, uint32_t k,
+                                                       uint32_t m_pad, int8_t* xq, float* xexs) {
+  const size_t i = 8 * (blockIdx.x * 256ull + threadIdx.x);
+  if (i >= (size_t)m_pad * k) return;
+  const uint32_t a = (uint32_t)(i / k), col = (uint32_t)(i % k);
+  float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (a < m) cx_load8(x + i, v);
+  uint32_t lo, hi;
+  float d;
+  int32_t s;
+  cx_quant8_vals<32>(v, lo, hi, d, s);
+  *reinterpret_cast<uint2*>(xq + i) = make_uint2(lo, hi);
+  if ((col & 31) == 0) {
+    float* e = xexs + (size_t)(col / 32) * 2 * m_pad + a;
+    e[0] = d;
+    e[m_pad] = (float)s;
+  }
+}
+
+struct Config {
+  int tw, mt, threads;
+  size_t lds;
+};
+
+typedef void (*gemm_kernel)(GemmParams);
+
+template <int T, int RW, int AW, int WA, int KS, int NSB, int S>
+Config make_config(gemm_kernel* k) {
+  using SH = Shape<T, RW, AW, WA, KS, NSB>;
+  static_assert(SH::lds(S) <= 160 * 1024, "LDS of one CU");
+  *k = k_gemm<T, RW, AW, WA, KS, NSB, S>;
+  return Config{SH::TW, SH::MT, 64 * SH::NW, SH::lds(S)};
+}
+
+// The tile shapes: weight rows x activation rows, waves, super-blocks per
+// stage, ring stages. Each is the fastest of a sweep for some (n, m) of
+// BASELINE config 4 (11008 x 2048 and 2048 x 11008, m = 2 .. 512).
+template <int T>
+Config config(int id, gemm_kernel* k) {
+  switch (id) {
+    case 0: return make_config<T, 1, 1, 1, 8, 4, 2>(k);  // 16 x 16, 8 waves split k
+    case 1: return make_config<T, 1, 1, 1, 8, 2, 3>(k);  // 16 x 16, 8 waves split k
+    case 2: return make_config<T, 4, 1, 1, 1, 2, 3>(k);  // 64 x 16
+    case 3: return make_config<T, 4, 2, 1, 1, 2, 2>(k);  // 64 x 32, 8 waves
+    case 4: return make_config<T, 2, 2, 1, 1, 2, 2>(k);  // 32 x 32
+    case 5: return make_config<T, 4, 2, 2, 1, 1, 3>(k);  // 64 x 64, 8 waves
+    default: return make_config<T, 8, 1, 4, 1, 1, 2>(k);  // 128 x 64, 8 waves
+  }
+}
+
+// Few weight rows (n < 4096: 2048 x 11008, the q/o/k/v shapes) leave too few
+// row tiles for a workgroup per CU, so small m splits k over the waves.
+int choose(uint32_t n, uint32_t m) {
+  if (n >= 4096) return m <= 16 ? 2 : m <= 32 ? 3 : m <= 64 ? 5 : 6;
+  return m <= 32 ? 0 : m <= 64 ? 1 : m <= 128 ? 4 : 5;
+}
+
+template <int T>
+int launch(GemmParams& P, hipStream_t s) {
+  gemm_kernel k = nullptr;
+  const Config c = config<T>(choose(P.n, P.m), &k);
+  // activation rows padded to the tile height (zero rows quantize to zero)
+  P.m_pad = (P.m + c.mt - 1) / c.mt * c.mt;
+  const size_t qgrid = ((size_t)P.m_pad * P.k / 8 + 255) / 256;
+  CX_REQUIRE(qgrid < (1ull << 31), "gemm: %zu activation values is too many",
+             (size_t)P.m_pad * P.k);
+  int8_t* xq = reinterpret_cast<int8_t*>(P.scratch);
+  float* xexs = reinterpret_cast<float*>(P.scratch + ((size_t)P.m_pad * P.k + 255) / 256 * 256);
+  hipLaunchKernelGGL(k_quantize_gemm, dim3((unsigned)qgrid), dim3(256), 0, s, P.lhs, P.m, P.k,
+                     P.m_pad, xq, xexs);
+  CX_HIP(hipGetLastError());
+  P.xq = xq;
+  P.xexs = xexs;
+  P.row_tiles = (P.n + c.tw - 1) / c.tw;
+  P.act_tiles = (P.m + c.mt - 1) / c.mt;
+  const size_t grid = (size_t)(P.row_tiles + 7) / 8 * 8 * P.act_tiles;
+  CX_REQUIRE(grid < (1ull << 31), "gemm: %u x %u is too large", P.n, P.m);
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(c.threads), c.lds, s, P);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+}  // namespace
+
+bool cx_gemm_supported(int type) { return type == CX_Q4_K || type == CX_Q5_K; }
+
+size_t cx_gemm_scratch_bytes(size_t m, size_t k) {
+  const size_t m_pad = (m + 63) / 64 * 64;
+  return (m_pad * k + 255) / 256 * 256 + m_pad * (k / 32) * 8;
+}
+
+int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* lhs, size_t m,
+                   float* dst, void* scratch, hipStream_t s) {
+  CX_REQUIRE(cx_gemm_supported(type), "gemm: type %d has no MFMA path", type);
+  CX_REQUIRE(w && lhs && dst && scratch, "gemm: null pointer");
+  CX_REQUIRE(k % 256 == 0 && k > 0, "gemm: k=%zu is not a multiple of 256", k);
+  CX_REQUIRE(n < (1u << 31) && m < (1u << 24) && k < (1u << 24), "gemm: shape too large");
+  CX_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)lhs & 15) == 0 &&
+                 ((uintptr_t)scratch & 255) == 0,
+             "gemm: weights and activations must be 16-byte aligned");
+  if (!n || !m) return CX_OK;
+  GemmParams P{};
+  P.lhs = lhs;
+  P.scratch = reinterpret_cast<uint8_t*>(scratch);
+  P.w = w;
+  P.dst = dst;
+  P.n = (uint32_t)n;
+  P.k = (uint32_t)k;
+  P.m = (uint32_t)m;
+  P.nb = (uint32_t)(k / 256);
+  P.row_bytes = P.nb * cx_bpb(type);
+  return type == CX_Q4_K ? launch<CX_Q4_K>(P, s) : launch<CX_Q5_K>(P, s);
+}

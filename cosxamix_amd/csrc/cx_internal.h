@@ -46,3 +46,11 @@ int cx_launch_norm_quant(const float* x, const float* w, size_t n, float eps, in
                          int8_t* xq, float* xe, float* xs, hipStream_t s);
 int cx_launch_rmsnorm(float* out, const float* in, const float* w, size_t rows, size_t n,
                       float eps, hipStream_t s);
+
+// m activation rows at once on int8 MFMA (Q4_K, Q5_K): lhs[m][k] f32 is
+// quantized into `scratch` (cx_gemm_scratch_bytes, 256-byte aligned), then
+// dst[m][n] is formed, every value bit-identical to the per-row GEMV.
+bool cx_gemm_supported(int type);
+size_t cx_gemm_scratch_bytes(size_t m, size_t k);
+int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* lhs, size_t m,
+                   float* dst, void* scratch, hipStream_t s);

@@ -159,6 +159,36 @@ def test_matmul_auto_rows_equal_single_rows(cx, dev):  # src/ops.rs:1364-1393
         ops.matmul_auto((m, k, n), T(lhs, dev), T(w, dev), O.Q4_K, one)
 
 
+@pytest.mark.parametrize("t,n,k,ms", [
+    (O.Q4_K, 11008, 2048, (8, 32, 40, 70, 512)),  # BASELINE config 4, first matrix
+    (O.Q4_K, 2048, 11008, (8, 32)),                # config 4, second matrix (43 blocks)
+    (O.Q5_K, 1000, 4096, (3, 17, 64, 100, 200)),   # ragged n, partial tiles
+])
+def test_batched_mfma_bit_identical_to_rows_and_oracle(cx, dev, t, n, k, ms):
+    """matmul_auto with m > 1 (int8 MFMA path) against the single-row GEMV
+    (bit-identical: same integer sums, same f32 terms in scalar order) and,
+    on sampled outputs, against the oracle's scalar row dot (src/ops.rs:1364-1393:
+    a row of a batch equals the row alone)."""
+    ops, _ = cx
+    w = random_rows(t, n, k, n + k)
+    wd = T(w, dev)
+    rng = np.random.default_rng(k)
+    for m in ms:
+        lhs = rng.normal(0, 1, (m, k)).astype(np.float32)
+        lhs[0, :32] = 0.0  # an all-zero sub-block
+        dst = torch.empty((m, n), dtype=torch.float32, device=dev)
+        ops.matmul_auto((m, k, n), T(lhs, dev), wd, t, dst)
+        xq, xe, xs = ops.cuantizar_i8_en(T(lhs, dev), O.SUB[t])
+        got = dst.cpu().numpy()
+        for a in range(m):
+            y = ops.gemv(t, wd, n, k, xq[a].contiguous(), xe[a].contiguous(), xs[a].contiguous())
+            assert np.array_equal(got[a].view(np.uint32), y.cpu().numpy().view(np.uint32)), (m, a)
+        q, e, s = (v.cpu().numpy() for v in (xq, xe, xs))
+        for a, r in ((0, 0), (m - 1, n - 1), (m // 2, n // 3)):
+            want = O.dot_row(t, w[r], q[a], e[a], s[a])
+            assert np.float32(want).view(np.uint32) == got[a, r].view(np.uint32), (m, a, r)
+
+
 def test_multi_1row_bit_identical_to_single_calls(cx, dev):  # src/ops.rs:1614-1670
     ops, _ = cx
     k = 2048
