@@ -98,17 +98,34 @@ template <> struct KQ<CX_Q4_K> {
     if (dbg) dbg[j] = e;
     to[j] = xe[j] * (d * (float)sc * (float)e - dm * (float)mn * xs[j]);
   }
+  // The bytes of half h: the 16-byte header and the qs of pairs 2h, 2h+1
+  // (64 bytes at 16 + 64h), from LDS or straight from global memory.
+  struct Regs {
+    uint4 hd, u[4];
+  };
+  static constexpr int NLOAD = 5;  // 16-byte loads per Regs
+  __device__ static void load(const uint8_t* blk, int h, Regs& r) {
+    const uint4* bw = reinterpret_cast<const uint4*>(blk);
+    r.hd = bw[0];
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.u[i] = bw[1 + 4 * h + i];
+  }
   __device__ static void half(const uint8_t* lds, uint32_t off, int h, const int8_t* xb,
                               const float* xe, const float* xs, int32_t* dbg, float* to) {
-    const uint4* bw = reinterpret_cast<const uint4*>(lds + off);
-    const uint4 hd = bw[0];
+    Regs r;
+    load(lds + off, h, r);
+    half_regs(r, h, xb, xe, xs, dbg, to);
+  }
+  __device__ static void half_regs(const Regs& r, int h, const int8_t* xb, const float* xe,
+                                   const float* xs, int32_t* dbg, float* to) {
+    const uint4 hd = r.hd;
     const float d = cx_h2f(hd.x & 0xFFFF), dm = cx_h2f(hd.x >> 16);
     uint32_t sc4, mn4;
     scales_mins(h, hd.y, hd.z, hd.w, sc4, mn4);
 #pragma unroll
     for (int pp = 0; pp < 2; pp++) {
       const int p = 2 * h + pp;
-      const uint4 u0 = bw[1 + 2 * p], u1 = bw[2 + 2 * p];
+      const uint4 u0 = r.u[2 * pp], u1 = r.u[2 * pp + 1];
       const uint32_t q[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
       int xa[8], xc[8];
       act8(xb + 64 * p, xa);
@@ -131,10 +148,28 @@ template <> struct KQ<CX_Q4_K> {
 template <> struct KQ<CX_Q5_K> {
   static constexpr int BPB = 176, SUB = 32;
   static constexpr bool ALIGNED = true;
+  // header, qh (32 bytes) and the qs of pairs 2h, 2h+1 (64 bytes at 48 + 64h)
+  struct Regs {
+    uint4 hd, h0, h1, u[4];
+  };
+  static constexpr int NLOAD = 7;
+  __device__ static void load(const uint8_t* blk, int h, Regs& r) {
+    const uint4* bw = reinterpret_cast<const uint4*>(blk);
+    r.hd = bw[0];
+    r.h0 = bw[1];
+    r.h1 = bw[2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.u[i] = bw[3 + 4 * h + i];
+  }
   __device__ static void half(const uint8_t* lds, uint32_t off, int h, const int8_t* xb,
                               const float* xe, const float* xs, int32_t* dbg, float* to) {
-    const uint4* bw = reinterpret_cast<const uint4*>(lds + off);
-    const uint4 hd = bw[0], h0 = bw[1], h1 = bw[2];
+    Regs r;
+    load(lds + off, h, r);
+    half_regs(r, h, xb, xe, xs, dbg, to);
+  }
+  __device__ static void half_regs(const Regs& r, int h, const int8_t* xb, const float* xe,
+                                   const float* xs, int32_t* dbg, float* to) {
+    const uint4 hd = r.hd, h0 = r.h0, h1 = r.h1;
     const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
     const float d = cx_h2f(hd.x & 0xFFFF), dm = cx_h2f(hd.x >> 16);
     uint32_t sc4, mn4;
@@ -142,7 +177,7 @@ template <> struct KQ<CX_Q5_K> {
 #pragma unroll
     for (int pp = 0; pp < 2; pp++) {
       const int p = 2 * h + pp;
-      const uint4 u0 = bw[3 + 2 * p], u1 = bw[4 + 2 * p];
+      const uint4 u0 = r.u[2 * pp], u1 = r.u[2 * pp + 1];
       const uint32_t q[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
       int xa[8], xc[8];
       act8(xb + 64 * p, xa);
@@ -354,6 +389,36 @@ __device__ inline void wait_all_but(uint32_t n) {
   else cx_wait_vm<0>();
 }
 
+// total = 0; total += term_s for s = 0 .. n-1 (n % 4 == 0), in that order.
+// The terms are read eight float4s at a time before they are added, so the
+// LDS latency is paid once per 32 adds, not once per 4.
+__device__ inline float row_sum(const float* terms, uint32_t n) {
+  const float4* t = reinterpret_cast<const float4*>(terms);
+  const uint32_t n4 = n / 4;
+  float acc = 0.0f;
+  uint32_t s = 0;
+  for (; s + 8 <= n4; s += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = t[s + i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      acc += v[i].x;
+      acc += v[i].y;
+      acc += v[i].z;
+      acc += v[i].w;
+    }
+  }
+  for (; s < n4; s++) {
+    const float4 v = t[s];
+    acc += v.x;
+    acc += v.y;
+    acc += v.z;
+    acc += v.w;
+  }
+  return acc;
+}
+
 template <int T, bool NORM>
 __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
   using Q = KQ<T>;
@@ -436,15 +501,68 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
   // 3. the row's sum in the scalar spec's order: total = 0; total += term_s
   //    for s = 0, 1, ... (src/kernels/scalar.rs:141-167)
   if ((uint32_t)tid < rows) {
-    const float4* t = reinterpret_cast<const float4*>(terms + tid * P.tstride);
-    float acc = 0.0f;
-    for (uint32_t s = 0; s < P.nsub / 4; s++) {
-      const float4 v = t[s];
-      acc += v.x;
-      acc += v.y;
-      acc += v.z;
-      acc += v.w;
-    }
+    const float acc = row_sum(terms + tid * P.tstride, P.nsub);
+    const uint32_t row = row0 + tid;
+    if (P.epi == CX_EPI_ACCUM)
+      S.y[row] += acc;
+    else
+      S.y[row] = S.bias ? acc + S.bias[row] : acc;
+  }
+}
+
+// The same GEMV for Q4_K/Q5_K (16-byte aligned blocks) with the weights
+// loaded straight into VGPRs: each weight byte is used once, so staging it in
+// LDS only costs LDS bandwidth (the direct-load write and the read). Each
+// lane loads the bytes of its (row, super-block, half) items — the first
+// one's loads are in flight from the start, each later one is loaded while
+// the previous one is computed — and LDS holds only the shared activation and
+// the terms.
+template <int T>
+__global__ __launch_bounds__(256) void k_gemv_reg(GemvParams P) {
+  using Q = KQ<T>;
+  constexpr int SPB = 256 / Q::SUB;
+  extern __shared__ __align__(16) uint8_t lds[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t tile = blockIdx.x;
+  int sg = 0;
+  while (tile >= P.tile_end[sg]) sg++;
+  if (sg) tile -= P.tile_end[sg - 1];
+  const cx_seg S = P.seg[sg];
+  const uint32_t row0 = tile * P.R;
+  const uint32_t rows = min(P.R, S.rows - row0);
+  int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
+  float* se = reinterpret_cast<float*>(lds + P.lds_scale);
+  float* ss = se + P.nsub;
+  float* terms = reinterpret_cast<float*>(lds + P.lds_terms);
+
+  copy_act_padded(P.act.xq, sq, P.nb, wave, lane);
+  copy_to_lds(P.act.xe, se, P.nsub / 4, wave, lane);
+  copy_to_lds(P.act.xs, ss, P.nsub / 4, wave, lane);
+  const uint32_t items = 2 * rows * P.nb;
+  auto block_of = [&](uint32_t it) {
+    const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
+    return S.w + (size_t)(row0 + r) * P.row_bytes + (size_t)blk * Q::BPB;
+  };
+  typename Q::Regs cur{}, nxt{};
+  uint32_t it = tid;
+  if (it < items) Q::load(block_of(it), (int)(it & 1), cur);
+  cx_wait_vm<Q::NLOAD>();  // the activation's direct loads (issued first) have landed
+  cx_barrier();
+  for (; it < items; it += 256) {
+    const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
+    const int h = (int)(it & 1);
+    if (it + 256 < items) Q::load(block_of(it + 256), (int)((it + 256) & 1), nxt);
+    int32_t* dbg = P.dbg ? P.dbg + (size_t)(row0 + r) * P.nsub + blk * SPB : nullptr;
+    Q::half_regs(cur, h, sq + blk * ACT_LDS_BLOCK, se + blk * SPB, ss + blk * SPB, dbg,
+                 terms + r * P.tstride + blk * SPB);
+    cur = nxt;
+  }
+  __syncthreads();
+
+  // the row's sum in the scalar spec's order (src/kernels/scalar.rs:141-167)
+  if ((uint32_t)tid < rows) {
+    const float acc = row_sum(terms + tid * P.tstride, P.nsub);
     const uint32_t row = row0 + tid;
     if (P.epi == CX_EPI_ACCUM)
       S.y[row] += acc;
@@ -461,11 +579,11 @@ struct TilePlan {
 // [xq, 272 bytes per 256] [xe, xs] then one region used first for the
 // rmsnorm input (x, w: 2k floats) and then for the terms (R x (nsub+4))
 TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
-                   const uint32_t* rows, int nseg, bool norm) {
+                   const uint32_t* rows, int nseg, bool norm, bool reg = false) {
   TilePlan t{};
   t.R = R;
   for (int i = 0; i < nseg; i++) t.tiles += (rows[i] + R - 1) / R;
-  t.lds_act = (16 + R * row_bytes + 16 + 15) / 16 * 16;
+  t.lds_act = reg ? 0 : (16 + R * row_bytes + 16 + 15) / 16 * 16;
   t.lds_scale = t.lds_act + (k / 256) * ACT_LDS_BLOCK;
   t.lds_terms = t.lds_scale + (8 * nsub + 15) / 16 * 16;
   t.lds_norm = t.lds_terms;
@@ -477,6 +595,8 @@ TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
 template <int T, bool NORM>
 int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   using Q = KQ<T>;
+  // Q4_K/Q5_K with a ready activation: weights straight into registers
+  constexpr bool REG = !NORM && (T == CX_Q4_K || T == CX_Q5_K);
   if (Q::ALIGNED) {
     for (int i = 0; i < P.nseg; i++)
       CX_REQUIRE(((uintptr_t)P.seg[i].w & 15u) == 0,
@@ -499,7 +619,7 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
     }
   } else {
     for (uint32_t R = 16; R >= 1; R >>= 1) {
-      TilePlan t = plan_tile(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM);
+      TilePlan t = plan_tile(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM, REG);
       if (t.lds > TILE_LDS_MAX) continue;
       best = t;
       if (t.tiles >= 512) break;
@@ -516,7 +636,10 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
     acc += (rows[i] + best.R - 1) / best.R;
     P.tile_end[i] = acc;
   }
-  hipLaunchKernelGGL((k_gemv<T, NORM>), dim3(best.tiles), dim3(256), best.lds, s, P);
+  if constexpr (REG)
+    hipLaunchKernelGGL((k_gemv_reg<T>), dim3(best.tiles), dim3(256), best.lds, s, P);
+  else
+    hipLaunchKernelGGL((k_gemv<T, NORM>), dim3(best.tiles), dim3(256), best.lds, s, P);
   CX_HIP(hipGetLastError());
   return CX_OK;
 }
