@@ -49,6 +49,9 @@ SIGNATURES = {
     "cx_gemv": (C.c_int, [C.c_int, _vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp]),
     "cx_gemv_subsums": (C.c_int, [C.c_int, _vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp]),
     "cx_quantize_blocks": (C.c_int, [C.c_int, _vp, _sz, _vp, _vp]),
+    "cx_dequantize": (C.c_int, [C.c_int, _vp, _sz, _vp, _vp]),
+    "cx_dequantize_rows": (C.c_int, [C.c_int, _vp, _sz, _sz, C.POINTER(_sz), _sz, _vp, _vp]),
+    "cx_unpack_i8": (C.c_int, [C.c_int, _vp, _sz, _vp, _vp, _vp, C.POINTER(C.c_int), _vp]),
     "cx_matmul_auto": (C.c_int, [_sz, _sz, _sz, _vp, _vp, C.c_int, _vp, _vp]),
     "cx_matmul_multi_1row": (C.c_int, [_vp, _sz, _sz, C.POINTER(_vp), C.POINTER(C.c_int),
                                        C.POINTER(_sz), C.POINTER(_vp), _vp]),

@@ -199,8 +199,47 @@ static int quant_scratch(size_t rows, size_t k, QuantScratch* q16, QuantScratch*
   return CX_OK;
 }
 
+extern "C" int cx_dequantize(int type, const uint8_t* bytes, size_t n, float* y, void* stream) {
+  return cx_launch_dequantize(type, bytes, n, y, STREAM(stream));
+}
+
+extern "C" int cx_dequantize_rows(int type, const uint8_t* data, size_t width, size_t total_rows,
+                                  const size_t* rows, size_t n_rows, float* y, void* stream) {
+  CX_REQUIRE(rows || !n_rows, "dequantize rows: null row list");
+  CX_REQUIRE(width < (1u << 31) && total_rows < (1ull << 32), "dequantize rows: shape too large");
+  std::vector<uint32_t> ids(n_rows);
+  for (size_t i = 0; i < n_rows; i++) {
+    // src/quant.rs:194-197: a row past the data is an error, not a read
+    CX_REQUIRE(rows[i] < total_rows, "dequantize rows: row %zu is past the %zu rows of the data",
+               rows[i], total_rows);
+    ids[i] = (uint32_t)rows[i];
+  }
+  if (!n_rows) return CX_OK;
+  void* sp = nullptr;
+  int rc = cx_scratch_reserve(n_rows * 4, &sp);
+  if (rc) return rc;
+  CX_HIP(hipMemcpyAsync(sp, ids.data(), n_rows * 4, hipMemcpyHostToDevice, STREAM(stream)));
+  rc = cx_launch_dequantize_rows(type, data, (uint32_t)width, (const uint32_t*)sp, n_rows, y,
+                                 STREAM(stream));
+  // the host copy of the indices must outlive the (possibly asynchronous) upload
+  if (!rc) CX_HIP(hipStreamSynchronize(STREAM(stream)));
+  return rc;
+}
+
+extern "C" int cx_unpack_i8(int type, const uint8_t* bytes, size_t n, int8_t* q, float* esc,
+                            float* off, int* sub, void* stream) {
+  int rc = cx_launch_unpack_i8(type, bytes, n, q, esc, off, STREAM(stream));
+  if (!rc && sub) *sub = cx_sub(type);
+  return rc;
+}
+
 extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, const uint8_t* w,
                               int type, float* dst, void* stream) {
+  // src/ops.rs:1064-1071: the unquantized formats take the f32 path
+  if (type == CX_F32 || type == CX_F16) {
+    CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
+    return cx_launch_matmul_f(type, w, n, k, lhs, m, dst, STREAM(stream));
+  }
   CX_REQUIRE(cx_is_kquant(type), "matmul_auto: type %d has no k-quant path here", type);
   CX_REQUIRE(k % 256 == 0, "matmul_auto: a row of %zu is not a multiple of the block of 256", k);
   CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");

@@ -54,3 +54,15 @@ bool cx_gemm_supported(int type);
 size_t cx_gemm_scratch_bytes(size_t m, size_t k);
 int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* lhs, size_t m,
                    float* dst, void* scratch, hipStream_t s);
+
+// Format conversion (cx_quant.hip): bit-identical to quant::descuantizar,
+// descuantizar_filas and desempaquetar_i8; rows[] are device indices.
+int cx_launch_dequantize(int type, const uint8_t* b, size_t n, float* y, hipStream_t s);
+int cx_launch_dequantize_rows(int type, const uint8_t* b, uint32_t width, const uint32_t* rows,
+                              size_t nrows, float* y, hipStream_t s);
+int cx_launch_unpack_i8(int type, const uint8_t* b, size_t n, int8_t* q, float* esc, float* off,
+                        hipStream_t s);
+// dst[m][n] = x[m][k] . W^T for F32/F16 weight rows (ops::matmul's
+// unquantized path, src/ops.rs:87-156)
+int cx_launch_matmul_f(int type, const uint8_t* w, size_t n, size_t k, const float* x, size_t m,
+                       float* dst, hipStream_t s);

@@ -91,6 +91,46 @@ def cuantizar_bloques(tipo: int, x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def descuantizar(tipo: int, bloques: torch.Tensor, n: int) -> torch.Tensor:
+    """quant::descuantizar (src/quant.rs:124-162): n values of GGUF bytes to f32."""
+    vpb = VALUES_PER_BLOCK.get(tipo)
+    if vpb is None:
+        raise ValueError(f"tipo {tipo}: sin descuantizador")
+    if n % vpb:
+        raise ValueError(f"pedí {n} valores y el bloque es de {vpb}")
+    if bloques.numel() < row_bytes(tipo, n):
+        raise ValueError("faltan bytes")
+    y = torch.empty(n, dtype=torch.float32, device=bloques.device)
+    _call(_lib.cx_dequantize, tipo, _ptr(bloques), n, _ptr(y), _stream(), what="descuantizar")
+    return y
+
+
+def descuantizar_filas(tipo: int, datos: torch.Tensor, ancho: int, filas) -> torch.Tensor:
+    """quant::descuantizar_filas (src/quant.rs:172-205): the rows `filas` of a
+    row-major matrix of `ancho` values per row, as f32 [len(filas), ancho]."""
+    total = datos.numel() // row_bytes(tipo, ancho)
+    ids = (C.c_size_t * len(filas))(*[int(f) for f in filas])
+    y = torch.empty((len(filas), ancho), dtype=torch.float32, device=datos.device)
+    _call(_lib.cx_dequantize_rows, tipo, _ptr(datos), ancho, total, ids, len(filas), _ptr(y),
+          _stream(), what="descuantizar_filas")
+    return y
+
+
+def desempaquetar_i8(tipo: int, bloques: torch.Tensor, n: int):
+    """quant::desempaquetar_i8 (src/quant.rs:238-468): (q i8[n], escalas,
+    desplazamientos f32[n/sub], sub) with value = escala*q + desplazamiento."""
+    sub = sub_block(tipo)
+    if sub is None:
+        raise ValueError(f"tipo {tipo}: sin desempaquetado directo a i8")
+    q = torch.empty(n, dtype=torch.int8, device=bloques.device)
+    esc = torch.empty(n // sub, dtype=torch.float32, device=bloques.device)
+    off = torch.empty(n // sub, dtype=torch.float32, device=bloques.device)
+    out = C.c_int(0)
+    _call(_lib.cx_unpack_i8, tipo, _ptr(bloques), n, _ptr(q), _ptr(esc), _ptr(off), C.byref(out),
+          _stream(), what="desempaquetar_i8")
+    return q, esc, off, out.value
+
+
 def matmul_auto(mkn, lhs: torch.Tensor, pesos: torch.Tensor, tipo: int, dst: torch.Tensor) -> None:
     """ops::matmul_auto (src/ops.rs:1056-1093): dst[m,n] = lhs[m,k] . W[n,k]^T."""
     m, k, n = mkn

@@ -114,8 +114,33 @@ int cx_gemv_subsums(int type, const uint8_t *w, size_t n, size_t k,
 int cx_quantize_blocks(int type, const float *x, size_t n, uint8_t *out,
                        void *stream);
 
+/* quant::descuantizar (src/quant.rs:124-162; formats 501-679): n values
+ * (whole blocks) of GGUF bytes of `type` to f32. F32, F16, Q8_0, Q5_0,
+ * Q2_K..Q6_K. Bit-identical to the reference. `y` 16-byte aligned. */
+int cx_dequantize(int type, const uint8_t *bytes, size_t n, float *y,
+                  void *stream);
+
+/* quant::descuantizar_filas (src/quant.rs:172-205): rows[i] (HOST array of
+ * n_rows indices below total_rows) of a row-major matrix of `width` values
+ * per row, into y[n_rows][width] (device). Same types as cx_dequantize. */
+int cx_dequantize_rows(int type, const uint8_t *data, size_t width,
+                       size_t total_rows, const size_t *rows, size_t n_rows,
+                       float *y, void *stream);
+
+/* quant::desempaquetar_i8 (src/quant.rs:238-468): n values of `type` to
+ * i8 q[n] and per sub-block scale esc[n/sub] and offset off[n/sub]
+ * (value = esc*q + off; off = 0 for the formats without a minimum). *sub
+ * (host) receives the sub-block size (src/quant.rs:213-219). Q8_0, Q5_0,
+ * Q2_K..Q6_K. Bit-identical to the reference. */
+int cx_unpack_i8(int type, const uint8_t *bytes, size_t n, int8_t *q,
+                 float *esc, float *off, int *sub, void *stream);
+
 /* ops::matmul_auto (src/ops.rs:1056-1093): dst[m,n] = lhs[m,k] . W[n,k]^T,
- * lhs/dst f32 row-major, W GGUF raw rows. Quantizes lhs internally. */
+ * lhs/dst f32 row-major, W GGUF raw rows. k-quants: quantizes lhs
+ * internally (m = 1: the GEMV; m > 1 of Q4_K/Q5_K: the int8 MFMA
+ * contraction; both bit-identical to the row-by-row fused dot). F32/F16
+ * (ops::matmul, src/ops.rs:87-156): f32 dot of each lhs row with the
+ * widened weight row, equal to the reference within f32 rounding; k % 4 == 0. */
 int cx_matmul_auto(size_t m, size_t k, size_t n, const float *lhs,
                    const uint8_t *w, int type, float *dst, void *stream);
 
