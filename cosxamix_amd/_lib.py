@@ -34,6 +34,13 @@ class CxConfig(C.Structure):
                 ("ctx", C.c_uint32), ("eps", C.c_float), ("rope_base", C.c_float)]
 
 
+class CxGgufTensor(C.Structure):
+    """InfoTensor (src/gguf.rs:172-194) as cx_gguf_tensor."""
+    _fields_ = [("name", C.c_char * 128), ("type", C.c_int), ("n_dims", C.c_uint32),
+                ("dims", C.c_uint64 * 4), ("offset", C.c_uint64), ("elements", C.c_uint64),
+                ("bytes", C.c_uint64)]
+
+
 # name -> (restype, argtypes); every symbol include/cosxamix_hip.h declares
 SIGNATURES = {
     "cx_last_error": (C.c_char_p, []),
@@ -63,6 +70,19 @@ SIGNATURES = {
     "cx_attention": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp]),
     "cx_attention_decode": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, C.c_int, _vp, _vp]),
     "cx_argmax": (C.c_int, [_vp, _sz, _vp, _vp]),
+    "cx_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "cx_gguf_free": (None, [_vp]),
+    "cx_gguf_header": (C.c_int, [_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                                 C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                 C.POINTER(C.c_uint64)]),
+    "cx_gguf_meta_int": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "cx_gguf_meta_float": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_double)]),
+    "cx_gguf_meta_str": (C.c_int, [_vp, C.c_char_p, C.c_long, C.c_char_p, _sz, C.POINTER(_sz)]),
+    "cx_gguf_meta_type": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_uint32),
+                                    C.POINTER(C.c_uint64)]),
+    "cx_gguf_find": (C.c_int, [_vp, C.c_char_p]),
+    "cx_gguf_tensor_info": (C.c_int, [_vp, C.c_int, C.POINTER(CxGgufTensor)]),
+    "cx_gguf_tensor_read": (C.c_int, [_vp, C.POINTER(CxGgufTensor), _vp, _sz]),
     "cx_model_create_daiss": (C.c_int, [C.POINTER(CxConfig), C.c_int, C.c_int, C.c_int,
                                         C.c_uint64, C.POINTER(_vp)]),
     "cx_model_free": (None, [_vp]),

@@ -1,6 +1,10 @@
 // cx_internal.h — launch-level interfaces shared between translation units.
 #pragma once
 
+#include <cstdio>
+#include <string>
+#include <vector>
+
 #include "cx_common.h"
 
 // One matrix of a (possibly multi-matrix) GEMV launch. All segments of one
@@ -66,3 +70,22 @@ int cx_launch_unpack_i8(int type, const uint8_t* b, size_t n, int8_t* q, float* 
 // unquantized path, src/ops.rs:87-156)
 int cx_launch_matmul_f(int type, const uint8_t* w, size_t n, size_t k, const float* x, size_t m,
                        float* dst, hipStream_t s);
+
+// GGUF (cx_gguf.hip)
+int cx_gguf_read(const char* path, cx_gguf** out);
+void cx_gguf_release(cx_gguf* g);
+const cx_gguf_tensor* cx_gguf_tensors(const cx_gguf* g, size_t* n);
+// [data_start + offset, + bytes) checked against overflow and the file size
+int cx_gguf_range(const cx_gguf* g, const cx_gguf_tensor& t, uint64_t* from);
+int cx_gguf_read_bytes(const cx_gguf* g, uint64_t from, void* host, size_t n, FILE* f);
+// one metadata entry to write: type 4 (u32: u), 10 (u64: u), 6 (f32: f), 8 (string: s)
+struct cx_gguf_meta {
+  std::string key;
+  uint32_t type;
+  uint64_t u;
+  double f;
+  std::string s;
+};
+int cx_gguf_write(const char* path, const std::vector<cx_gguf_meta>& meta,
+                  const std::vector<cx_gguf_tensor>& tensors,
+                  const std::vector<const void*>& host_data);

@@ -193,6 +193,53 @@ int cx_attention_decode(const float *q, const float *k, const float *v,
  * *out is a DEVICE uint32. */
 int cx_argmax(const float *v, size_t n, uint32_t *out, void *stream);
 
+/* ============================================================ GGUF files
+ * Host-only (no device work). Gguf::abrir and Pesos (src/gguf.rs:119-436). */
+
+typedef struct cx_gguf cx_gguf;
+
+/* InfoTensor (src/gguf.rs:172-194): dims as stored (fastest-varying first:
+ * a weight matrix is [row width, rows]); offset from the data section;
+ * bytes = elements / values_per_block * bytes_per_block. */
+typedef struct {
+  char name[128];
+  int type;
+  uint32_t n_dims;
+  uint64_t dims[4];
+  uint64_t offset;
+  uint64_t elements;
+  uint64_t bytes;
+} cx_gguf_tensor;
+
+/* Gguf::abrir (src/gguf.rs:274-342): header, metadata and tensor table of a
+ * GGUF v2/v3 file; the weights are not read. Errors as the reference: not a
+ * GGUF, unknown version, a truncated header, > 4 dims, an unknown type. */
+int cx_gguf_open(const char *path, cx_gguf **out);
+void cx_gguf_free(cx_gguf *g);
+/* version, counts, the aligned start of the data section and the alignment
+ * (general.alignment, default 32) */
+int cx_gguf_header(const cx_gguf *g, uint32_t *version, uint64_t *n_tensors,
+                   uint64_t *n_meta, uint64_t *data_start, uint64_t *alignment);
+/* Gguf::meta_entero / meta_decimal (src/gguf.rs:348-355; Valor::entero,
+ * decimal at 143-163): CX_EINVAL when the key is missing or not a number. */
+int cx_gguf_meta_int(const cx_gguf *g, const char *key, uint64_t *out);
+int cx_gguf_meta_float(const cx_gguf *g, const char *key, double *out);
+/* Valor::texto: a string value (index < 0) or element `index` of a list of
+ * strings; *len gets its length, buf (cap bytes) a NUL-terminated copy. */
+int cx_gguf_meta_str(const cx_gguf *g, const char *key, long index, char *buf,
+                     size_t cap, size_t *len);
+/* GGUF value type (0..12) of a key and its element count if a list (else 1) */
+int cx_gguf_meta_type(const cx_gguf *g, const char *key, uint32_t *type,
+                      uint64_t *count);
+/* Gguf::tensor (src/gguf.rs:344-346): index of the named tensor or -1 */
+int cx_gguf_find(const cx_gguf *g, const char *name);
+int cx_gguf_tensor_info(const cx_gguf *g, int idx, cx_gguf_tensor *out);
+/* Gguf::datos_de / Pesos::de (src/gguf.rs:357-436): the tensor's bytes into
+ * a host buffer of `cap` bytes; a tensor reaching past the end of the file
+ * (every offset sum checked for overflow) is an error, not a read. */
+int cx_gguf_tensor_read(const cx_gguf *g, const cx_gguf_tensor *t, void *host,
+                        size_t cap);
+
 /* ================================================================ 3. model */
 
 /* forward::Config (src/forward.rs:36-55) */
