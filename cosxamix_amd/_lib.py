@@ -85,6 +85,8 @@ SIGNATURES = {
     "cx_gguf_tensor_read": (C.c_int, [_vp, C.POINTER(CxGgufTensor), _vp, _sz]),
     "cx_model_create_daiss": (C.c_int, [C.POINTER(CxConfig), C.c_int, C.c_int, C.c_int,
                                         C.c_uint64, C.POINTER(_vp)]),
+    "cx_model_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "cx_model_save_gguf": (C.c_int, [_vp, C.c_char_p]),
     "cx_model_free": (None, [_vp]),
     "cx_model_config": (C.c_int, [_vp, C.POINTER(CxConfig)]),
     "cx_model_tensor_count": (C.c_int, [_vp]),

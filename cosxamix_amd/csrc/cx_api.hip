@@ -407,26 +407,32 @@ namespace {
 struct Tensor {
   std::string name;
   int type;
-  uint64_t dims[2];  // width, rows
+  uint64_t dims[2];  // width, rows (1 for a vector)
+  uint32_t n_dims;   // as stored in GGUF
   size_t bytes;
-  size_t offset;
+  size_t offset;     // in the model's pool
 };
+// one layer (src/forward.rs:139-156, Capa): every matrix with its own type, as
+// in real GGUF files (Q4_K_M keeps some attn_v / ffn_down in Q6_K); biases
+// may be absent (architectures without them)
 struct Layer {
   const float *attn_norm, *q_bias, *k_bias, *v_bias, *ffn_norm;
   const uint8_t *q, *k, *v, *o, *gate, *up, *down;
+  int t_q, t_k, t_v, t_o, t_gate, t_up, t_down;
 };
 }  // namespace
 
 struct cx_model {
   cx_config cfg;
   int device;
-  int t_lin, t_down, t_out;
+  int t_embd, t_out;
+  bool tied;  // no output.weight: the lm_head is token_embd (src/forward.rs:218-227)
   hipStream_t stream;
   uint8_t* pool;
   size_t pool_bytes;
   std::vector<Tensor> tensors;
   std::vector<Layer> layers;
-  const float* embd;
+  const uint8_t* embd;
   const float* out_norm;
   const uint8_t* out;
   float *cos_t, *sin_t;
@@ -465,8 +471,145 @@ extern "C" void cx_model_free(cx_model* m) {
   if (m->api) (void)hipFree(m->api);
   if (m->amax_out) (void)hipFree(m->amax_out);
   if (m->pool) (void)hipFree(m->pool);
-  (void)hipStreamDestroy(m->stream);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
+}
+
+static cx_model* model_new(const cx_config& c) {
+  if (hipSetDevice(g_device) != hipSuccess) {
+    cx_set_error("model: no HIP device %d", g_device);
+    return nullptr;
+  }
+  cx_model* m = new cx_model();
+  m->cfg = c;
+  m->device = g_device;
+  if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
+    m->stream = nullptr;
+    cx_model_free(m);
+    cx_set_error("model: stream");
+    return nullptr;
+  }
+  return m;
+}
+
+static size_t tensor_bytes(int t, uint64_t w, uint64_t r) {
+  return (size_t)(w / (uint64_t)cx_vpb(t) * (uint64_t)cx_bpb(t) * r);
+}
+
+// Views of the model's tensors by name (src/forward.rs:210-247), with the
+// shapes and types this path computes: matrices in a GEMV type (Q2_K..Q6_K),
+// norms and biases F32, token_embd in any type with a dequantizer, the lm_head
+// a GEMV type or F32/F16 (tied to token_embd when output.weight is absent).
+static int bind_views(cx_model* m) {
+  cx_config& c = m->cfg;
+  auto find = [&](const std::string& n) -> const Tensor* {
+    for (const Tensor& T : m->tensors)
+      if (T.name == n) return &T;
+    return nullptr;
+  };
+  const Tensor* E = find("token_embd.weight");
+  CX_REQUIRE(E, "model: missing tensor token_embd.weight");
+  CX_REQUIRE(E->dims[0] == c.dim, "model: token_embd rows of %llu values, dim is %u",
+             (unsigned long long)E->dims[0], c.dim);
+  c.vocab = (uint32_t)E->dims[1];
+  CX_REQUIRE(c.vocab > 0 && cx_vpb(E->type) > 0, "model: token_embd of type %d", E->type);
+  m->t_embd = E->type;
+  m->embd = (const uint8_t*)pool_at(m, E->offset);
+  CX_REQUIRE(c.heads && c.kv_heads && c.dim % c.heads == 0 && c.heads % c.kv_heads == 0,
+             "model: %u heads / %u kv heads do not divide dim %u", c.heads, c.kv_heads, c.dim);
+  const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd;
+  CX_REQUIRE(hd == 64 || hd == 128, "model: head_dim %u (the decode attention supports 64 and 128)",
+             hd);
+  CX_REQUIRE(D % 256 == 0, "model: dim %u is not a multiple of 256 (k-quant rows)", D);
+  auto vec = [&](const std::string& n, uint64_t len, bool optional,
+                 const float** p) -> int {
+    const Tensor* T = find(n);
+    if (!T && optional) {
+      *p = nullptr;
+      return CX_OK;
+    }
+    CX_REQUIRE(T, "model: missing tensor %s", n.c_str());
+    CX_REQUIRE(T->type == CX_F32 && T->dims[0] * T->dims[1] == len,
+               "model: %s must be F32 of %llu values", n.c_str(), (unsigned long long)len);
+    *p = (const float*)pool_at(m, T->offset);
+    return CX_OK;
+  };
+  auto mat = [&](const std::string& n, uint64_t w, uint64_t r, const uint8_t** p,
+                 int* t) -> int {
+    const Tensor* T = find(n);
+    CX_REQUIRE(T, "model: missing tensor %s", n.c_str());
+    CX_REQUIRE(cx_is_kquant(T->type), "model: %s is of type %d; the GEMV reads Q2_K..Q6_K",
+               n.c_str(), T->type);
+    CX_REQUIRE(T->dims[0] == w && T->dims[1] == r, "model: %s is %llux%llu, expected %llux%llu",
+               n.c_str(), (unsigned long long)T->dims[0], (unsigned long long)T->dims[1],
+               (unsigned long long)w, (unsigned long long)r);
+    *p = (const uint8_t*)pool_at(m, T->offset);
+    *t = T->type;
+    return CX_OK;
+  };
+  const Tensor* G0 = find("blk.0.ffn_gate.weight");
+  CX_REQUIRE(G0, "model: missing tensor blk.0.ffn_gate.weight");
+  c.ffn = (uint32_t)G0->dims[1];
+  CX_REQUIRE(c.ffn % 256 == 0, "model: ffn %u is not a multiple of 256", c.ffn);
+  const uint32_t I = c.ffn;
+  m->layers.clear();
+  int rc;
+  for (uint32_t i = 0; i < c.layers; i++) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    Layer L{};
+    if ((rc = vec(p + "attn_norm.weight", D, false, &L.attn_norm)) ||
+        (rc = mat(p + "attn_q.weight", D, D, &L.q, &L.t_q)) ||
+        (rc = vec(p + "attn_q.bias", D, true, &L.q_bias)) ||
+        (rc = mat(p + "attn_k.weight", D, kvd, &L.k, &L.t_k)) ||
+        (rc = vec(p + "attn_k.bias", kvd, true, &L.k_bias)) ||
+        (rc = mat(p + "attn_v.weight", D, kvd, &L.v, &L.t_v)) ||
+        (rc = vec(p + "attn_v.bias", kvd, true, &L.v_bias)) ||
+        (rc = mat(p + "attn_output.weight", D, D, &L.o, &L.t_o)) ||
+        (rc = vec(p + "ffn_norm.weight", D, false, &L.ffn_norm)) ||
+        (rc = mat(p + "ffn_gate.weight", D, I, &L.gate, &L.t_gate)) ||
+        (rc = mat(p + "ffn_up.weight", D, I, &L.up, &L.t_up)) ||
+        (rc = mat(p + "ffn_down.weight", I, D, &L.down, &L.t_down)))
+      return rc;
+    m->layers.push_back(L);
+  }
+  if ((rc = vec("output_norm.weight", D, false, &m->out_norm))) return rc;
+  const Tensor* O = find("output.weight");
+  m->tied = O == nullptr;
+  if (!O) O = E;
+  CX_REQUIRE(cx_is_kquant(O->type) || O->type == CX_F32 || O->type == CX_F16,
+             "model: the output matrix is of type %d (GEMV types or F32/F16)", O->type);
+  CX_REQUIRE(O->dims[0] == D && O->dims[1] == c.vocab, "model: output.weight shape");
+  m->t_out = O->type;
+  m->out = (const uint8_t*)pool_at(m, O->offset);
+  return CX_OK;
+}
+
+// rope tables and the per-step buffers of a model whose views are bound
+static int model_finish(cx_model* m) {
+  const cx_config& c = m->cfg;
+  const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn, V = c.vocab;
+  CX_REQUIRE(c.ctx > 0, "model: zero context");
+  // rope tables on the host, exactly as src/ops.rs:1108-1129, then uploaded
+  const size_t n = (size_t)c.ctx * (hd / 2);
+  std::vector<float> hc(n), hs(n);
+  cx_rope_tables(hd, c.rope_base, c.ctx, hc.data(), hs.data());
+  if (hipMalloc(&m->cos_t, n * 4) != hipSuccess || hipMalloc(&m->sin_t, n * 4) != hipSuccess ||
+      hipMemcpy(m->cos_t, hc.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(m->sin_t, hs.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+    cx_set_error("model: rope tables");
+    return CX_ENOMEM;
+  }
+  const size_t parts = cx_argmax_parts(V);
+  if (hipMalloc(&m->x, D * 4) || hipMalloc(&m->q, D * 4) || hipMalloc(&m->k, kvd * 4) ||
+      hipMalloc(&m->v, kvd * 4) || hipMalloc(&m->att, D * 4) || hipMalloc(&m->g, I * 4) ||
+      hipMalloc(&m->u, I * 4) || hipMalloc(&m->logits, (size_t)V * 4) ||
+      hipMalloc(&m->apv, parts * 4) || hipMalloc(&m->api, parts * 4) ||
+      hipMalloc(&m->amax_out, 4) || hipMalloc(&m->xq, (D > I ? D : I)) ||
+      hipMalloc(&m->xe, (D > I ? D : I) / 16 * 4) || hipMalloc(&m->xs, (D > I ? D : I) / 16 * 4)) {
+    cx_set_error("model: activation buffers");
+    return CX_ENOMEM;
+  }
+  return CX_OK;
 }
 
 // src/daiss.rs:396-407 (inicio_de)
@@ -496,22 +639,13 @@ extern "C" int cx_model_create_daiss(const cx_config* cfg, int t_lin, int t_down
   CX_REQUIRE(cx_is_kquant(t_lin) && cx_is_kquant(t_down) && cx_is_kquant(t_out) &&
                  t_lin != CX_Q6_K && t_down != CX_Q6_K && t_out != CX_Q6_K,
              "model: weights must be Q2_K..Q5_K (the quantizers the reference has)");
-  CX_HIP(hipSetDevice(g_device));
-  cx_model* m = new cx_model();
-  m->cfg = c;
-  m->device = g_device;
-  m->t_lin = t_lin;
-  m->t_down = t_down;
-  m->t_out = t_out;
-  if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
-    delete m;
-    cx_set_error("model: stream");
-    return CX_EHIP;
-  }
+  cx_model* m = model_new(c);
+  if (!m) return CX_EHIP;
   const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn, V = c.vocab;
-  // tensor table in the order of src/daiss.rs:236-303
+  // tensor table in the order of src/daiss.rs:236-303; token_embd F32 (the
+  // BASELINE fixtures keep embeddings f32)
   auto add = [&](const std::string& n, int t, uint64_t w, uint64_t r) {
-    Tensor T{n, t, {w, r}, (size_t)(w / cx_vpb(t) * cx_bpb(t) * r), 0};
+    Tensor T{n, t, {w, r}, r == 1 ? 1u : 2u, tensor_bytes(t, w, r), 0};
     m->tensors.push_back(T);
   };
   add("token_embd.weight", CX_F32, D, V);
@@ -575,52 +709,177 @@ extern "C" int cx_model_create_daiss(const cx_config* cfg, int t_lin, int t_down
   }
   (void)hipFree(tmp);
   tmp = nullptr;
-  // named views
-  size_t ti = 0;
-  auto nextp = [&]() { return pool_at(m, m->tensors[ti++].offset); };
-  m->embd = (const float*)nextp();
-  for (uint32_t i = 0; i < c.layers; i++) {
-    Layer L;
-    L.attn_norm = (const float*)nextp();
-    L.q = (const uint8_t*)nextp();
-    L.q_bias = (const float*)nextp();
-    L.k = (const uint8_t*)nextp();
-    L.k_bias = (const float*)nextp();
-    L.v = (const uint8_t*)nextp();
-    L.v_bias = (const float*)nextp();
-    L.o = (const uint8_t*)nextp();
-    L.ffn_norm = (const float*)nextp();
-    L.gate = (const uint8_t*)nextp();
-    L.up = (const uint8_t*)nextp();
-    L.down = (const uint8_t*)nextp();
-    m->layers.push_back(L);
-  }
-  m->out_norm = (const float*)nextp();
-  m->out = (const uint8_t*)nextp();
-  // rope tables on the host, exactly as src/ops.rs:1108-1129, then uploaded
-  {
-    const size_t n = (size_t)c.ctx * (hd / 2);
-    std::vector<float> hc(n), hs(n);
-    cx_rope_tables(hd, c.rope_base, c.ctx, hc.data(), hs.data());
-    if (hipMalloc(&m->cos_t, n * 4) != hipSuccess || hipMalloc(&m->sin_t, n * 4) != hipSuccess ||
-        hipMemcpy(m->cos_t, hc.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(m->sin_t, hs.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess) {
-      cx_set_error("model: rope tables");
-      return fail(CX_ENOMEM);
-    }
-  }
-  const size_t parts = cx_argmax_parts(V);
-  if (hipMalloc(&m->x, D * 4) || hipMalloc(&m->q, D * 4) || hipMalloc(&m->k, kvd * 4) ||
-      hipMalloc(&m->v, kvd * 4) || hipMalloc(&m->att, D * 4) || hipMalloc(&m->g, I * 4) ||
-      hipMalloc(&m->u, I * 4) || hipMalloc(&m->logits, (size_t)V * 4) ||
-      hipMalloc(&m->apv, parts * 4) || hipMalloc(&m->api, parts * 4) ||
-      hipMalloc(&m->amax_out, 4) || hipMalloc(&m->xq, (D > I ? D : I)) ||
-      hipMalloc(&m->xe, (D > I ? D : I) / 16 * 4) || hipMalloc(&m->xs, (D > I ? D : I) / 16 * 4)) {
-    cx_set_error("model: activation buffers");
-    return fail(CX_ENOMEM);
-  }
+  if ((rc = bind_views(m)) || (rc = model_finish(m))) return fail(rc);
   *out = m;
   return CX_OK;
+}
+
+// The tensors of a Qwen2-style model (src/forward.rs:210-247); anything else
+// in the file is not loaded
+static bool model_tensor_name(const std::string& n) {
+  static const char* top[] = {"token_embd.weight", "output_norm.weight", "output.weight"};
+  for (const char* t : top)
+    if (n == t) return true;
+  if (n.compare(0, 4, "blk.") != 0) return false;
+  static const char* per[] = {".attn_norm.weight", ".attn_q.weight", ".attn_q.bias",
+                              ".attn_k.weight",    ".attn_k.bias",   ".attn_v.weight",
+                              ".attn_v.bias",      ".attn_output.weight", ".ffn_norm.weight",
+                              ".ffn_gate.weight",  ".ffn_up.weight", ".ffn_down.weight"};
+  for (const char* t : per) {
+    const size_t l = strlen(t);
+    if (n.size() > l && n.compare(n.size() - l, l, t) == 0) return true;
+  }
+  return false;
+}
+
+// Modelo::abrir (src/forward.rs:187-266): config from the <arch>.* metadata
+// (the reference reads qwen2.*; general.architecture names the prefix), every
+// tensor the forward uses uploaded to one HBM pool unchanged (the kernels
+// read GGUF bytes as they are), read through a pinned staging buffer.
+extern "C" int cx_model_open(const char* path, cx_model** out) {
+  CX_REQUIRE(path && out, "model: null argument");
+  *out = nullptr;
+  cx_gguf* g = nullptr;
+  int rc = cx_gguf_read(path, &g);
+  if (rc) return rc;
+  struct Closer {
+    cx_gguf* g;
+    ~Closer() { cx_gguf_release(g); }
+  } closer{g};
+  char arch[64] = "qwen2";
+  size_t alen = 0;
+  if (cx_gguf_meta_str(g, "general.architecture", -1, arch, sizeof arch, &alen) != CX_OK)
+    snprintf(arch, sizeof arch, "qwen2");
+  const std::string A = arch;
+  auto meta_u = [&](const char* key, uint32_t* v) -> int {
+    uint64_t x;
+    int r = cx_gguf_meta_int(g, (A + "." + key).c_str(), &x);
+    if (r) return r;
+    CX_REQUIRE(x < (1ull << 32), "model: %s.%s = %llu", A.c_str(), key, (unsigned long long)x);
+    *v = (uint32_t)x;
+    return CX_OK;
+  };
+  cx_config c{};
+  if ((rc = meta_u("block_count", &c.layers)) || (rc = meta_u("embedding_length", &c.dim)) ||
+      (rc = meta_u("attention.head_count", &c.heads)) ||
+      (rc = meta_u("attention.head_count_kv", &c.kv_heads)) ||
+      (rc = meta_u("context_length", &c.ctx)))
+    return rc;
+  double eps = 1e-6, base = 10000.0;
+  (void)cx_gguf_meta_float(g, (A + ".attention.layer_norm_rms_epsilon").c_str(), &eps);
+  (void)cx_gguf_meta_float(g, (A + ".rope.freq_base").c_str(), &base);
+  c.eps = (float)eps;
+  c.rope_base = (float)base;
+  CX_REQUIRE(c.layers && c.dim && c.heads && c.kv_heads && c.ctx, "model: zero-sized config");
+  cx_model* m = model_new(c);
+  if (!m) return CX_EHIP;
+  uint8_t* stage = nullptr;
+  FILE* f = nullptr;
+  auto fail = [&](int code) {
+    if (stage) (void)hipHostFree(stage);
+    if (f) fclose(f);
+    cx_model_free(m);
+    return code;
+  };
+  size_t n = 0;
+  const cx_gguf_tensor* gt = cx_gguf_tensors(g, &n);
+  std::vector<uint64_t> from;
+  size_t off = 0;
+  for (size_t i = 0; i < n; i++) {
+    const cx_gguf_tensor& t = gt[i];
+    if (!model_tensor_name(t.name)) continue;
+    if (t.n_dims < 1 || t.n_dims > 2 || cx_vpb(t.type) == 0) {
+      cx_set_error("model: %s has %u dims of type %d", t.name, t.n_dims, t.type);
+      return fail(CX_EINVAL);
+    }
+    uint64_t at;
+    if ((rc = cx_gguf_range(g, t, &at))) return fail(rc);
+    Tensor T{t.name, t.type, {t.dims[0], t.n_dims == 2 ? t.dims[1] : 1}, t.n_dims,
+             (size_t)t.bytes, off};
+    if (T.dims[0] % (uint64_t)cx_vpb(t.type) != 0) {
+      cx_set_error("model: %s rows of %llu values are not whole blocks", t.name,
+                   (unsigned long long)T.dims[0]);
+      return fail(CX_EINVAL);
+    }
+    m->tensors.push_back(T);
+    from.push_back(at);
+    off += (T.bytes + 255) / 256 * 256;
+  }
+  m->pool_bytes = off;
+  if (hipMalloc(&m->pool, off) != hipSuccess) {
+    cx_set_error("model: cannot allocate %zu bytes of weights", off);
+    return fail(CX_ENOMEM);
+  }
+  const size_t STAGE = 64u << 20;
+  if (hipHostMalloc((void**)&stage, STAGE) != hipSuccess) {
+    stage = nullptr;
+    cx_set_error("model: cannot allocate the staging buffer");
+    return fail(CX_ENOMEM);
+  }
+  f = fopen(path, "rb");
+  if (!f) {
+    cx_set_error("model: cannot open %s", path);
+    return fail(CX_EINVAL);
+  }
+  for (size_t i = 0; i < m->tensors.size(); i++) {
+    const Tensor& T = m->tensors[i];
+    for (size_t done = 0; done < T.bytes; done += STAGE) {
+      const size_t len = T.bytes - done < STAGE ? T.bytes - done : STAGE;
+      if ((rc = cx_gguf_read_bytes(g, from[i] + done, stage, len, f))) return fail(rc);
+      if (hipMemcpy(m->pool + T.offset + done, stage, len, hipMemcpyHostToDevice) != hipSuccess) {
+        cx_set_error("model: upload of %s failed", T.name.c_str());
+        return fail(CX_EHIP);
+      }
+    }
+  }
+  fclose(f);
+  f = nullptr;
+  (void)hipHostFree(stage);
+  stage = nullptr;
+  if ((rc = bind_views(m)) || (rc = model_finish(m))) return fail(rc);
+  *out = m;
+  return CX_OK;
+}
+
+// The model as a GGUF file (the daiss writer's metadata, src/daiss.rs:422-468,
+// and Escritor::escribir's layout): tensors in table order, bytes as in HBM.
+extern "C" int cx_model_save_gguf(const cx_model* m, const char* path) {
+  CX_REQUIRE(m && path, "model: null argument");
+  const cx_config& c = m->cfg;
+  auto u32m = [](const char* k, uint64_t v) { return cx_gguf_meta{k, 4, v, 0.0, ""}; };
+  std::vector<cx_gguf_meta> meta = {
+      {"general.architecture", 8, 0, 0.0, "qwen2"},
+      {"general.name", 8, 0, 0.0, "cosxamix-hip"},
+      u32m("qwen2.block_count", c.layers),
+      u32m("qwen2.context_length", c.ctx),
+      u32m("qwen2.embedding_length", c.dim),
+      u32m("qwen2.feed_forward_length", c.ffn),
+      u32m("qwen2.attention.head_count", c.heads),
+      u32m("qwen2.attention.head_count_kv", c.kv_heads),
+      {"qwen2.attention.layer_norm_rms_epsilon", 6, 0, (double)c.eps, ""},
+      {"qwen2.rope.freq_base", 6, 0, (double)c.rope_base, ""},
+  };
+  std::vector<cx_gguf_tensor> ts;
+  std::vector<std::vector<uint8_t>> host(m->tensors.size());
+  std::vector<const void*> ptrs;
+  CX_HIP(hipSetDevice(m->device));
+  CX_HIP(hipStreamSynchronize(m->stream));
+  for (size_t i = 0; i < m->tensors.size(); i++) {
+    const Tensor& T = m->tensors[i];
+    cx_gguf_tensor t{};
+    snprintf(t.name, sizeof t.name, "%s", T.name.c_str());
+    t.type = T.type;
+    t.n_dims = T.n_dims;
+    t.dims[0] = T.dims[0];
+    t.dims[1] = T.n_dims == 2 ? T.dims[1] : 1;
+    t.elements = T.dims[0] * T.dims[1];
+    t.bytes = T.bytes;
+    ts.push_back(t);
+    host[i].resize(T.bytes);
+    CX_HIP(hipMemcpy(host[i].data(), m->pool + T.offset, T.bytes, hipMemcpyDeviceToHost));
+    ptrs.push_back(host[i].data());
+  }
+  return cx_gguf_write(path, meta, ts, ptrs);
 }
 
 extern "C" int cx_model_config(const cx_model* m, cx_config* out) {
@@ -659,7 +918,9 @@ extern "C" size_t cx_model_weight_bytes(const cx_model* m) {
   size_t b = 0;
   for (const Tensor& T : m->tensors)
     if (T.name != "token_embd.weight") b += T.bytes;
-  return b + (size_t)m->cfg.dim * 4;  // one embedding row
+  // one embedding row; a tied lm_head reads the whole table
+  const size_t row = tensor_bytes(m->t_embd, m->cfg.dim, 1);
+  return b + row + (m->tied ? tensor_bytes(m->t_embd, m->cfg.dim, m->cfg.vocab) : 0);
 }
 
 // ------------------------------------------------------------------ cache
@@ -710,23 +971,44 @@ extern "C" void cx_cache_free(cx_cache* c) {
 // src/forward.rs:420-501 for one token at position st->pos, then argmax and
 // the position advance. Every kernel reads the position from the device
 // state, so the sequence is captured once per cache and replayed.
+// The fused-norm GEMV over matrices that share an input, one launch per
+// weight type (proyectar_varias, src/forward.rs:333-368): rmsnorm(x, w) then
+// the projections; segments of one launch share the type.
+static int gemv_norm_by_type(const int* types, const cx_seg* segs, int n, uint32_t k,
+                             const float* x, const float* w, float eps, hipStream_t s) {
+  bool done[4] = {false, false, false, false};
+  for (int i = 0; i < n; i++) {
+    if (done[i]) continue;
+    cx_seg group[4];
+    int ng = 0;
+    for (int j = i; j < n; j++)
+      if (!done[j] && types[j] == types[i]) {
+        group[ng++] = segs[j];
+        done[j] = true;
+      }
+    int rc = cx_launch_gemv_norm(types[i], group, ng, k, x, w, eps, CX_EPI_STORE, s);
+    if (rc) return rc;
+  }
+  return CX_OK;
+}
+
 static int enqueue_step(cx_cache* C) {
   cx_model* m = C->m;
   const cx_config& c = m->cfg;
   hipStream_t s = m->stream;
   const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn;
-  const int sl = cx_sub(m->t_lin), sd = cx_sub(m->t_down), so = cx_sub(m->t_out);
   const cx_qact act{m->xq, m->xe, m->xs};
-  int rc = cx_launch_embed(m->embd, D, C->st, C->hist, m->x, s);
+  int rc = cx_launch_embed(m->t_embd, m->embd, D, C->st, C->hist, m->x, s);
   if (rc) return rc;
   for (uint32_t li = 0; li < c.layers; li++) {
     const Layer& L = m->layers[li];
     float* kc = C->kv + (size_t)li * 2 * C->cap * kvd;
     float* vc = kc + C->cap * kvd;
     // src/forward.rs:422-464: rmsnorm, q/k/v with bias, rope, attention
-    cx_seg qkv[3] = {{L.q, m->q, L.q_bias, D}, {L.k, m->k, L.k_bias, kvd}, {L.v, m->v, L.v_bias, kvd}};
-    if ((rc = cx_launch_gemv_norm(m->t_lin, qkv, 3, D, m->x, L.attn_norm, c.eps, CX_EPI_STORE, s)))
-      return rc;
+    const cx_seg qkv[3] = {{L.q, m->q, L.q_bias, D}, {L.k, m->k, L.k_bias, kvd},
+                           {L.v, m->v, L.v_bias, kvd}};
+    const int tqkv[3] = {L.t_q, L.t_k, L.t_v};
+    if ((rc = gemv_norm_by_type(tqkv, qkv, 3, D, m->x, L.attn_norm, c.eps, s))) return rc;
     cx_attn_args a{};
     a.q = m->q;
     a.knew = m->k;
@@ -748,24 +1030,32 @@ static int enqueue_step(cx_cache* C) {
     a.xq = m->xq;  // the output projection's activation
     a.xe = m->xe;
     a.xs = m->xs;
-    a.sub = sl;
+    a.sub = cx_sub(L.t_o);
     if ((rc = cx_launch_attn_decode(a, s))) return rc;
     // src/forward.rs:466-469: output projection added to the residual
     cx_seg o{L.o, m->x, nullptr, D};
-    if ((rc = cx_launch_gemv(m->t_lin, &o, 1, D, act, CX_EPI_ACCUM, nullptr, s))) return rc;
+    if ((rc = cx_launch_gemv(L.t_o, &o, 1, D, act, CX_EPI_ACCUM, nullptr, s))) return rc;
     // src/forward.rs:472-491: rmsnorm, gate/up, SwiGLU, down added to the residual
-    cx_seg gu[2] = {{L.gate, m->g, nullptr, I}, {L.up, m->u, nullptr, I}};
-    if ((rc = cx_launch_gemv_norm(m->t_lin, gu, 2, D, m->x, L.ffn_norm, c.eps, CX_EPI_STORE, s)))
+    const cx_seg gu[2] = {{L.gate, m->g, nullptr, I}, {L.up, m->u, nullptr, I}};
+    const int tgu[2] = {L.t_gate, L.t_up};
+    if ((rc = gemv_norm_by_type(tgu, gu, 2, D, m->x, L.ffn_norm, c.eps, s))) return rc;
+    if ((rc = cx_launch_swiglu_quant(m->g, m->u, I, cx_sub(L.t_down), m->xq, m->xe, m->xs, s)))
       return rc;
-    if ((rc = cx_launch_swiglu_quant(m->g, m->u, I, sd, m->xq, m->xe, m->xs, s))) return rc;
     cx_seg dn{L.down, m->x, nullptr, D};
-    if ((rc = cx_launch_gemv(m->t_down, &dn, 1, I, act, CX_EPI_ACCUM, nullptr, s))) return rc;
+    if ((rc = cx_launch_gemv(L.t_down, &dn, 1, I, act, CX_EPI_ACCUM, nullptr, s))) return rc;
   }
   // src/forward.rs:495-501: final rmsnorm and the output projection
-  if ((rc = cx_launch_norm_quant(m->x, m->out_norm, D, c.eps, so, m->xq, m->xe, m->xs, s)))
-    return rc;
-  cx_seg lm{m->out, m->logits, nullptr, c.vocab};
-  if ((rc = cx_launch_gemv(m->t_out, &lm, 1, D, act, CX_EPI_STORE, nullptr, s))) return rc;
+  if (cx_is_kquant(m->t_out)) {
+    if ((rc = cx_launch_norm_quant(m->x, m->out_norm, D, c.eps, cx_sub(m->t_out), m->xq, m->xe,
+                                   m->xs, s)))
+      return rc;
+    cx_seg lm{m->out, m->logits, nullptr, c.vocab};
+    if ((rc = cx_launch_gemv(m->t_out, &lm, 1, D, act, CX_EPI_STORE, nullptr, s))) return rc;
+  } else {  // an unquantized (tied) lm_head: the f32 path (src/ops.rs:1064-1071)
+    if ((rc = cx_launch_rmsnorm(m->att, m->x, m->out_norm, 1, D, c.eps, s))) return rc;
+    if ((rc = cx_launch_matmul_f(m->t_out, m->out, c.vocab, D, m->att, 1, m->logits, s)))
+      return rc;
+  }
   return cx_launch_argmax(m->logits, c.vocab, m->apv, m->api, m->amax_out, C->st, C->hist, s);
 }
 

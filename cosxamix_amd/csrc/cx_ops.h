@@ -18,8 +18,9 @@ struct cx_dstate {
 // where the sequential sums would dominate the step.
 #define CX_ATT_EXACT_MAX 4096
 
-int cx_launch_embed(const float* embd, uint32_t dim, const cx_dstate* st, const uint32_t* hist,
-                    float* x, hipStream_t s);
+// x = row hist[st->pos] of the embedding table (GGUF bytes of `type`), dequantized
+int cx_launch_embed(int type, const uint8_t* embd, uint32_t dim, const cx_dstate* st,
+                    const uint32_t* hist, float* x, hipStream_t s);
 int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc,
                       const float* cos_t, const float* sin_t, uint32_t heads, uint32_t kvh,
                       uint32_t hd, const cx_dstate* st, hipStream_t s);

@@ -1,6 +1,6 @@
 // cx_ops.hip — the per-token ops around the GEMV, for gfx950.
 //
-//   embedding row copy           src/forward.rs:391-405
+//   embedding row lookup         src/forward.rs:391-405 (descuantizar_filas of one row)
 //   RoPE (split halves) + KV     src/ops.rs:1150-1193, src/forward.rs:440-456
 //   decode attention (split-K)   src/ops.rs:1258-1325 at tokens = 1
 //   causal GQA attention         src/ops.rs:1258-1325
@@ -9,16 +9,29 @@
 //   argmax + token loop state    src/sampler.rs:129-137, src/forward.rs:544-557
 #include "cx_ops.h"
 #include "cx_act.h"
+#include "cx_dequant.h"
 
 namespace {
 
 // ---------------------------------------------------------- embedding
-__global__ __launch_bounds__(256) void k_embed(const float* embd, uint32_t dim,
+// the token's row of an embedding table of any GGUF type, dequantized
+// (quant::descuantizar_filas, src/quant.rs:172-205), 8 values a lane
+template <int T>
+__global__ __launch_bounds__(256) void k_embed(const uint8_t* embd, uint32_t dim,
                                                const cx_dstate* st, const uint32_t* hist,
                                                float* x) {
+  constexpr int VPB = T == CX_F32 || T == CX_F16 ? 1 : (T == CX_Q8_0 || T == CX_Q5_0 ? 32 : 256);
+  constexpr int BPB = T == CX_F32 ? 4 : T == CX_F16 ? 2 : T == CX_Q8_0 ? 34 : T == CX_Q5_0 ? 22
+                    : T == CX_Q2_K ? 84 : T == CX_Q3_K ? 110 : T == CX_Q4_K ? 144
+                    : T == CX_Q5_K ? 176 : 210;
   const uint32_t tok = hist[st->pos];
-  const float* row = embd + (size_t)tok * dim;
-  for (uint32_t i = threadIdx.x; i < dim; i += 256) x[i] = row[i];
+  const uint8_t* row = embd + (size_t)tok * (dim / VPB) * BPB;
+  for (uint32_t i = 8 * threadIdx.x; i < dim; i += 2048) {
+    float v[8];
+    cxq::dequant8<T>(row + i / VPB * BPB, i % VPB, v);
+#pragma unroll
+    for (int j = 0; j < 8; j++) x[i + j] = v[j];
+  }
 }
 
 // ------------------------------------------------------ rope + KV append
@@ -658,9 +671,23 @@ int cx_launch_rope(float* x, size_t tokens, size_t heads, size_t hd, const float
   CX_HIP(hipGetLastError());
   return CX_OK;
 }
-int cx_launch_embed(const float* embd, uint32_t dim, const cx_dstate* st, const uint32_t* hist,
-                    float* x, hipStream_t s) {
-  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, embd, dim, st, hist, x);
+int cx_launch_embed(int type, const uint8_t* embd, uint32_t dim, const cx_dstate* st,
+                    const uint32_t* hist, float* x, hipStream_t s) {
+  CX_REQUIRE(dim % 8 == 0 && dim % (uint32_t)cx_vpb(type) == 0,
+             "embedding: a row of %u values is not whole blocks of type %d", dim, type);
+  const dim3 g(1), wg(256);
+  switch (type) {
+    case CX_F32: hipLaunchKernelGGL(k_embed<CX_F32>, g, wg, 0, s, embd, dim, st, hist, x); break;
+    case CX_F16: hipLaunchKernelGGL(k_embed<CX_F16>, g, wg, 0, s, embd, dim, st, hist, x); break;
+    case CX_Q8_0: hipLaunchKernelGGL(k_embed<CX_Q8_0>, g, wg, 0, s, embd, dim, st, hist, x); break;
+    case CX_Q5_0: hipLaunchKernelGGL(k_embed<CX_Q5_0>, g, wg, 0, s, embd, dim, st, hist, x); break;
+    case CX_Q2_K: hipLaunchKernelGGL(k_embed<CX_Q2_K>, g, wg, 0, s, embd, dim, st, hist, x); break;
+    case CX_Q3_K: hipLaunchKernelGGL(k_embed<CX_Q3_K>, g, wg, 0, s, embd, dim, st, hist, x); break;
+    case CX_Q4_K: hipLaunchKernelGGL(k_embed<CX_Q4_K>, g, wg, 0, s, embd, dim, st, hist, x); break;
+    case CX_Q5_K: hipLaunchKernelGGL(k_embed<CX_Q5_K>, g, wg, 0, s, embd, dim, st, hist, x); break;
+    case CX_Q6_K: hipLaunchKernelGGL(k_embed<CX_Q6_K>, g, wg, 0, s, embd, dim, st, hist, x); break;
+    default: cx_set_error("embedding: type %d has no dequantizer", type); return CX_EINVAL;
+  }
   CX_HIP(hipGetLastError());
   return CX_OK;
 }

@@ -54,7 +54,8 @@ def bytes_de_cache_por_token(cfg: Config) -> int:
 
 
 class Modelo:
-    """A Qwen2 model resident in HBM with daiss-style seeded weights."""
+    """A Qwen2 model resident in HBM: daiss-style seeded weights made on the
+    GPU (the constructor), or a GGUF file (``Modelo.abrir``)."""
 
     def __init__(self, cfg: Config, tipo=L.Q4_K, semilla: int = 42, tipo_down=None,
                  tipo_salida=None):
@@ -65,10 +66,28 @@ class Modelo:
                 "Modelo")
         self._h = h
 
+    @classmethod
+    def abrir(cls, ruta) -> "Modelo":
+        """Modelo::abrir (src/forward.rs:187-266): a GGUF file into HBM."""
+        h = C.c_void_p()
+        if _lib.cx_model_open(str(ruta).encode(), C.byref(h)) != 0:
+            raise ValueError(L.last_error())
+        m = cls.__new__(cls)
+        m._h = h
+        c = L.CxConfig()
+        L.check(_lib.cx_model_config(h, C.byref(c)), "Modelo")
+        m.cfg = Config(c.layers, c.dim, c.heads, c.kv_heads, c.ffn, c.vocab, c.ctx, c.eps,
+                       c.rope_base)
+        return m
+
+    def guardar(self, ruta) -> None:
+        """The model as a GGUF file (the daiss writer's metadata, src/daiss.rs:422-468)."""
+        L.check(_lib.cx_model_save_gguf(self._h, str(ruta).encode()), "guardar")
+
     def close(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and _lib is not None:
             _lib.cx_model_free(self._h)
-            self._h = None
+        self._h = None
 
     def __del__(self):
         self.close()
@@ -154,9 +173,9 @@ class Cache:
         _lib.cx_cache_clear(self._h)
 
     def close(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and _lib is not None:
             _lib.cx_cache_free(self._h)
-            self._h = None
+        self._h = None
 
     def __del__(self):
         self.close()

@@ -259,6 +259,20 @@ typedef struct cx_cache cx_cache;
  * (src/forward.rs:187-266); here the tensors are made where they are used. */
 int cx_model_create_daiss(const cx_config *cfg, int linear_type, int down_type,
                           int out_type, uint64_t seed, cx_model **out);
+/* Modelo::abrir (src/forward.rs:187-266): a Qwen2-architecture GGUF file
+ * into HBM. Config from <general.architecture>.* metadata (block_count,
+ * embedding_length, attention.head_count[_kv], context_length,
+ * layer_norm_rms_epsilon = 1e-6 and rope.freq_base = 10000 if absent);
+ * vocab and ffn from the tensors. Per-tensor types: matrices Q2_K..Q6_K
+ * (mixed per tensor, as Q*_K_M files are), norms and biases F32 (biases may
+ * be absent), token_embd any type cx_dequantize reads, output.weight a
+ * matrix type or F32/F16 and tied to token_embd when absent
+ * (src/forward.rs:218-227). The bytes are uploaded unchanged. */
+int cx_model_open(const char *path, cx_model **out);
+/* The model as a GGUF file: the reference daiss writer's metadata
+ * (src/daiss.rs:422-468) and Escritor::escribir's layout (src/gguf_write.rs),
+ * tensors in table order with their bytes as held in HBM. */
+int cx_model_save_gguf(const cx_model *m, const char *path);
 void cx_model_free(cx_model *m);
 int cx_model_config(const cx_model *m, cx_config *out);
 
