@@ -98,6 +98,25 @@ def decode_bench(F, L, steps, warmup, prompt_len):
     return m, prompt, toks, timed, total_ms
 
 
+def prefill_bench(m, prompt, reps=5):
+    """Modelo::forward of the whole prompt on an empty cache (the batched
+    prefill): the median wall time of `reps` calls after one warm-up call,
+    each ending with the last token's logits on the host."""
+    cache = m.nueva_cache(len(prompt) + 1)
+    m.forward(prompt, cache)  # allocates the prefill buffers
+    times = []
+    for _ in range(reps):
+        cache.truncar(0)
+        t0 = time.perf_counter()
+        m.forward(prompt, cache)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    out = {"prompt_tokens": len(prompt), "median_ms": round(med * 1e3, 3),
+           "tok_per_s": round(len(prompt) / med, 1), "reps": reps}
+    log(f"[bench] prefill of {len(prompt)} tokens: {med * 1e3:.2f} ms ({out['tok_per_s']} tok/s)")
+    return out
+
+
 def gemv_roofline(F, L, m, iters=360, reps=5):
     import torch
     from cosxamix_amd import ops
@@ -417,6 +436,7 @@ def main():
     tok_s = a.steps / (total_ms * 1e-3)
     per_tok_bytes = m.bytes_por_token()
     kv_bytes = 2 * F.DAISS_3B.capas * F.DAISS_3B.dim_kv() * 4 * (a.prompt + a.warmup + a.steps // 2)
+    prefill = prefill_bench(m, prompt)
     avg, gbps, ncopies = gemv_roofline(F, L, m)
     traffic, tdetail = (None, "skipped (--no-traffic)") if a.no_traffic else gemv_traffic()
     cpu = None if a.no_cpu else cpu_baseline(F, L, m, prompt)
@@ -451,6 +471,7 @@ def main():
                    "effective_GBps": round((per_tok_bytes + kv_bytes) / (total_ms * 1e-3 / a.steps) / 1e9, 1),
                    "first_tokens": [int(t) for t in toks[:8]]},
         "batched": batched,
+        "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -445,6 +445,16 @@ struct cx_model {
   float *xe, *xs;
 };
 
+// The batched prefill's buffers: T tokens of every activation, the
+// contraction's quantized rows, and T query tokens of attention scratch.
+// Made at a cache's first multi-token forward.
+struct cx_prefill {
+  uint32_t T;
+  float *x, *nrm, *q, *k, *v, *att, *g, *u, *tmp;  // nrm also holds the SwiGLU rows
+  float *sc, *pm, *pl, *po;
+  void* scratch;
+};
+
 struct cx_cache {
   cx_model* m;
   size_t cap, len;
@@ -455,6 +465,7 @@ struct cx_cache {
   float* sc;            // scores of the order-exact attention, heads x cap
   hipGraphExec_t exec;
   bool have_graph;
+  cx_prefill pf;
 };
 
 static void* pool_at(cx_model* m, size_t off) { return m->pool + off; }
@@ -961,7 +972,9 @@ extern "C" void cx_cache_free(cx_cache* c) {
   (void)hipSetDevice(c->m->device);
   (void)hipStreamSynchronize(c->m->stream);
   if (c->have_graph) (void)hipGraphExecDestroy(c->exec);
-  void* bufs[] = {c->kv, c->hist, c->st, c->pm, c->pl, c->po, c->sc};
+  const cx_prefill& P = c->pf;
+  void* bufs[] = {c->kv, c->hist, c->st, c->pm, c->pl, c->po, c->sc, P.x, P.nrm, P.q, P.k,
+                  P.v, P.att, P.g, P.u, P.tmp, P.sc, P.pm, P.pl, P.po, P.scratch};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   delete c;
@@ -992,13 +1005,15 @@ static int gemv_norm_by_type(const int* types, const cx_seg* segs, int n, uint32
   return CX_OK;
 }
 
+static int enqueue_tail(cx_cache* C);
+
 static int enqueue_step(cx_cache* C) {
   cx_model* m = C->m;
   const cx_config& c = m->cfg;
   hipStream_t s = m->stream;
   const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn;
   const cx_qact act{m->xq, m->xe, m->xs};
-  int rc = cx_launch_embed(m->t_embd, m->embd, D, C->st, C->hist, m->x, s);
+  int rc = cx_launch_embed(m->t_embd, m->embd, D, C->st, C->hist, m->x, 1, s);
   if (rc) return rc;
   for (uint32_t li = 0; li < c.layers; li++) {
     const Layer& L = m->layers[li];
@@ -1044,7 +1059,19 @@ static int enqueue_step(cx_cache* C) {
     cx_seg dn{L.down, m->x, nullptr, D};
     if ((rc = cx_launch_gemv(L.t_down, &dn, 1, I, act, CX_EPI_ACCUM, nullptr, s))) return rc;
   }
-  // src/forward.rs:495-501: final rmsnorm and the output projection
+  return enqueue_tail(C);
+}
+
+// src/forward.rs:495-501: the final rmsnorm and the output projection of the
+// residual m->x, then the argmax, which writes the next token at st->pos + 1
+// (when past the prompt) and advances st->pos
+static int enqueue_tail(cx_cache* C) {
+  cx_model* m = C->m;
+  const cx_config& c = m->cfg;
+  hipStream_t s = m->stream;
+  const uint32_t D = c.dim;
+  const cx_qact act{m->xq, m->xe, m->xs};
+  int rc;
   if (cx_is_kquant(m->t_out)) {
     if ((rc = cx_launch_norm_quant(m->x, m->out_norm, D, c.eps, cx_sub(m->t_out), m->xq, m->xe,
                                    m->xs, s)))
@@ -1105,6 +1132,171 @@ static int run_steps(cx_cache* C, size_t prompt_end, size_t steps, float* step_m
   return CX_OK;
 }
 
+// ------------------------------------------------------ batched prefill
+// Modelo::forward over several tokens (src/forward.rs:375-505) as one pass
+// per layer over a chunk of up to T tokens. The GEMVs become the int8 MFMA
+// contraction for Q4_K/Q5_K (other types run the GEMV row by row), and the
+// attention runs the decode step's kernels with one query token per grid
+// slice. Every value equals what token-by-token decoding computes:
+// - the contraction is bit-identical to the GEMV;
+// - the rows are normalized in the fused GEMV prologue's tree;
+// - the quantization of a row is a function of its values alone;
+// - bias and residual adds are the same single f32 adds as the epilogues;
+// - the attention kernels and their path (exact or split-K, by capacity)
+//   are the decode step's.
+// So a prompt gives the same logits, cache and tokens either way.
+static const size_t kPrefillMaxT = 256;
+static const size_t kPrefillAttnBytes = 256ull << 20;  // attention scratch bound
+
+static int prefill_alloc(cx_cache* C) {
+  cx_prefill& P = C->pf;
+  if (P.T) return CX_OK;
+  const cx_config& c = C->m->cfg;
+  const size_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn, H = c.heads;
+  const size_t ns = cx_attn_splits(C->cap);
+  const bool exact = C->cap <= CX_ATT_EXACT_MAX;
+  const size_t per_tok = exact ? cx_attn_score_floats(H, C->cap) * 4 : ns * H * (hd + 2) * 4;
+  size_t T = kPrefillAttnBytes / per_tok;
+  T = T > kPrefillMaxT ? kPrefillMaxT : T < 16 ? 16 : T / 16 * 16;
+  if (T > C->cap) T = C->cap;
+  const size_t wide = D > I ? D : I;
+  struct Want {
+    float** p;
+    size_t floats;
+  } want[] = {{&P.x, T * D},   {&P.nrm, T * wide}, {&P.q, T * D},   {&P.k, T * kvd},
+              {&P.v, T * kvd}, {&P.att, T * D},    {&P.g, T * I},   {&P.u, T * I},
+              {&P.tmp, T * D}};
+  for (const Want& w : want)
+    if (hipMalloc(w.p, w.floats * 4) != hipSuccess) goto fail;
+  if (exact) {
+    if (hipMalloc(&P.sc, T * cx_attn_score_floats(H, C->cap) * 4) != hipSuccess) goto fail;
+  } else if (hipMalloc(&P.pm, T * ns * H * 4) != hipSuccess ||
+             hipMalloc(&P.pl, T * ns * H * 4) != hipSuccess ||
+             hipMalloc(&P.po, T * ns * H * hd * 4) != hipSuccess) {
+    goto fail;
+  }
+  if (hipMalloc(&P.scratch, cx_gemm_scratch_bytes(T, wide)) != hipSuccess) goto fail;
+  P.T = (uint32_t)T;
+  return CX_OK;
+fail:
+  for (void* b : {(void*)P.x, (void*)P.nrm, (void*)P.q, (void*)P.k, (void*)P.v, (void*)P.att,
+                  (void*)P.g, (void*)P.u, (void*)P.tmp, (void*)P.sc, (void*)P.pm, (void*)P.pl,
+                  (void*)P.po, P.scratch})
+    if (b) (void)hipFree(b);
+  P = cx_prefill{};
+  cx_set_error("prefill: cannot allocate the buffers of %zu tokens", T);
+  return CX_ENOMEM;
+}
+
+// out[r] = W . in[r] for `rows` rows of width k. Q4_K/Q5_K: the contraction,
+// quantizing `in` unless *quantized says an earlier call of the same input
+// did; other types: the GEMV row by row on the step's activation buffers.
+static int prefill_matmul(cx_cache* C, int type, const uint8_t* w, uint32_t n, uint32_t k,
+                          const float* in, uint32_t rows, float* out, bool* quantized) {
+  cx_model* m = C->m;
+  hipStream_t s = m->stream;
+  int rc;
+  if (cx_gemm_supported(type)) {
+    if (!*quantized && (rc = cx_gemm_quantize(in, rows, k, C->pf.scratch, s))) return rc;
+    *quantized = true;
+    return cx_gemm_apply(type, w, n, k, rows, out, C->pf.scratch, s);
+  }
+  const cx_qact act{m->xq, m->xe, m->xs};
+  for (uint32_t r = 0; r < rows; r++) {
+    if ((rc = cx_launch_quantize(in + (size_t)r * k, 1, k, cx_sub(type), m->xq, m->xe, m->xs, s)))
+      return rc;
+    cx_seg seg{w, out + (size_t)r * n, nullptr, n};
+    if ((rc = cx_launch_gemv(type, &seg, 1, k, act, CX_EPI_STORE, nullptr, s))) return rc;
+  }
+  return CX_OK;
+}
+
+// tokens at positions [st->pos, st->pos + nt), already in hist: the layers
+static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
+  cx_model* m = C->m;
+  cx_prefill& P = C->pf;
+  const cx_config& c = m->cfg;
+  hipStream_t s = m->stream;
+  const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn;
+  int rc = cx_launch_embed(m->t_embd, m->embd, D, C->st, C->hist, P.x, nt, s);
+  if (rc) return rc;
+  for (uint32_t li = 0; li < c.layers; li++) {
+    const Layer& L = m->layers[li];
+    float* kc = C->kv + (size_t)li * 2 * C->cap * kvd;
+    float* vc = kc + C->cap * kvd;
+    // src/forward.rs:422-464
+    bool qd = false;
+    if ((rc = cx_launch_norm_rows(P.x, L.attn_norm, nt, D, c.eps, P.nrm, s)) ||
+        (rc = prefill_matmul(C, L.t_q, L.q, D, D, P.nrm, nt, P.q, &qd)) ||
+        (rc = prefill_matmul(C, L.t_k, L.k, kvd, D, P.nrm, nt, P.k, &qd)) ||
+        (rc = prefill_matmul(C, L.t_v, L.v, kvd, D, P.nrm, nt, P.v, &qd)))
+      return rc;
+    if ((L.q_bias && (rc = cx_launch_add_rows(P.q, L.q_bias, nt, D, 1, s))) ||
+        (L.k_bias && (rc = cx_launch_add_rows(P.k, L.k_bias, nt, kvd, 1, s))) ||
+        (L.v_bias && (rc = cx_launch_add_rows(P.v, L.v_bias, nt, kvd, 1, s))))
+      return rc;
+    if ((rc = cx_launch_rope_kv(P.q, P.k, P.v, kc, vc, m->cos_t, m->sin_t, c.heads, c.kv_heads,
+                                hd, C->st, nt, s)))
+      return rc;
+    cx_attn_args a{};
+    a.q = P.q;
+    a.kc = kc;
+    a.vc = vc;
+    a.heads = c.heads;
+    a.kvh = c.kv_heads;
+    a.hd = hd;
+    a.cap = (uint32_t)C->cap;
+    a.st = C->st;
+    a.pm = P.pm;
+    a.pl = P.pl;
+    a.po = P.po;
+    a.sc = P.sc;
+    a.out = P.att;
+    a.tokens = nt;
+    if ((rc = cx_launch_attn_decode(a, s))) return rc;
+    // src/forward.rs:466-491
+    qd = false;
+    if ((rc = prefill_matmul(C, L.t_o, L.o, D, D, P.att, nt, P.tmp, &qd)) ||
+        (rc = cx_launch_add_rows(P.x, P.tmp, nt, D, nt, s)) ||
+        (rc = cx_launch_norm_rows(P.x, L.ffn_norm, nt, D, c.eps, P.nrm, s)))
+      return rc;
+    qd = false;
+    if ((rc = prefill_matmul(C, L.t_gate, L.gate, I, D, P.nrm, nt, P.g, &qd)) ||
+        (rc = prefill_matmul(C, L.t_up, L.up, I, D, P.nrm, nt, P.u, &qd)) ||
+        (rc = cx_launch_swiglu_rows(P.g, P.u, (size_t)nt * I, P.nrm, s)))
+      return rc;
+    qd = false;
+    if ((rc = prefill_matmul(C, L.t_down, L.down, D, I, P.nrm, nt, P.tmp, &qd)) ||
+        (rc = cx_launch_add_rows(P.x, P.tmp, nt, D, nt, s)))
+      return rc;
+  }
+  return CX_OK;
+}
+
+// Positions [C->len, C->len + t) of hist through the model, in chunks; then
+// the last token's logits and argmax (the argmax writes hist[len + t]).
+static int prefill(cx_cache* C, size_t t) {
+  cx_model* m = C->m;
+  hipStream_t s = m->stream;
+  int rc = prefill_alloc(C);
+  if (rc) return rc;
+  const cx_prefill& P = C->pf;
+  const uint32_t D = m->cfg.dim, end = (uint32_t)(C->len + t), cap = (uint32_t)C->cap;
+  uint32_t last = 0;
+  for (size_t c0 = 0; c0 < t; c0 += P.T) {
+    const uint32_t nt = (uint32_t)(t - c0 < P.T ? t - c0 : P.T);
+    if ((rc = cx_launch_set_state(C->st, (uint32_t)(C->len + c0), end, cap, s)) ||
+        (rc = enqueue_prefill_chunk(C, nt)))
+      return rc;
+    last = nt - 1;
+  }
+  CX_HIP(hipMemcpyAsync(m->x, P.x + (size_t)last * D, (size_t)D * 4, hipMemcpyDeviceToDevice, s));
+  if ((rc = cx_launch_set_state(C->st, end - 1, end, cap, s)) || (rc = enqueue_tail(C))) return rc;
+  CX_HIP(hipStreamSynchronize(s));
+  C->len = end;
+  return CX_OK;
+}
+
 extern "C" int cx_forward(cx_model* m, cx_cache* C, const uint32_t* toks, size_t t,
                           float* logits_host, uint32_t* argmax_out) {
   CX_REQUIRE(m && C && C->m == m, "forward: model/cache mismatch");
@@ -1115,7 +1307,7 @@ extern "C" int cx_forward(cx_model* m, cx_cache* C, const uint32_t* toks, size_t
                m->cfg.vocab);
   CX_HIP(hipSetDevice(m->device));
   CX_HIP(hipMemcpyAsync(C->hist + C->len, toks, t * 4, hipMemcpyHostToDevice, m->stream));
-  int rc = run_steps(C, C->len + t, t, nullptr);
+  int rc = t > 1 ? prefill(C, t) : run_steps(C, C->len + t, t, nullptr);
   if (rc) return rc;
   if (logits_host)
     CX_HIP(hipMemcpy(logits_host, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
@@ -1141,7 +1333,7 @@ extern "C" int cx_generate(cx_model* m, cx_cache* C, const uint32_t* prompt, siz
     CX_REQUIRE(prompt[i] < m->cfg.vocab, "generate: token %u is not in the vocabulary", prompt[i]);
   CX_HIP(hipSetDevice(m->device));
   CX_HIP(hipMemcpyAsync(C->hist + start, prompt, n * 4, hipMemcpyHostToDevice, m->stream));
-  int rc = run_steps(C, start + n, n, nullptr);
+  int rc = n > 1 ? prefill(C, n) : run_steps(C, start + n, n, nullptr);
   if (rc) return rc;
   rc = run_steps(C, start + n, steps - n, step_ms);
   if (rc) return rc;

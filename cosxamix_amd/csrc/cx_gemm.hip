@@ -395,22 +395,32 @@ int choose(uint32_t n, uint32_t m) {
   return m <= 32 ? 0 : m <= 64 ? 1 : m <= 128 ? 4 : 5;
 }
 
+// xq and xexs of m_pad quantized rows in scratch
+inline int8_t* scratch_xq(uint8_t* scratch) { return reinterpret_cast<int8_t*>(scratch); }
+inline float* scratch_xexs(uint8_t* scratch, size_t m_pad, size_t k) {
+  return reinterpret_cast<float*>(scratch + (m_pad * k + 255) / 256 * 256);
+}
+
+int quantize(const float* lhs, uint32_t m, uint32_t k, uint32_t m_pad, uint8_t* scratch,
+             hipStream_t s) {
+  const size_t qgrid = ((size_t)m_pad * k / 8 + 255) / 256;
+  CX_REQUIRE(qgrid < (1ull << 31), "gemm: %zu activation values is too many", (size_t)m_pad * k);
+  hipLaunchKernelGGL(k_quantize_gemm, dim3((unsigned)qgrid), dim3(256), 0, s, lhs, m, k, m_pad,
+                     scratch_xq(scratch), scratch_xexs(scratch, m_pad, k));
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+// the contraction over rows quantized with a row count m_pad that is a
+// multiple of the chosen tile's height
 template <int T>
-int launch(GemmParams& P, hipStream_t s) {
+int contract(GemmParams& P, hipStream_t s) {
   gemm_kernel k = nullptr;
   const Config c = config<T>(choose(P.n, P.m), &k);
-  // activation rows padded to the tile height (zero rows quantize to zero)
-  P.m_pad = (P.m + c.mt - 1) / c.mt * c.mt;
-  const size_t qgrid = ((size_t)P.m_pad * P.k / 8 + 255) / 256;
-  CX_REQUIRE(qgrid < (1ull << 31), "gemm: %zu activation values is too many",
-             (size_t)P.m_pad * P.k);
-  int8_t* xq = reinterpret_cast<int8_t*>(P.scratch);
-  float* xexs = reinterpret_cast<float*>(P.scratch + ((size_t)P.m_pad * P.k + 255) / 256 * 256);
-  hipLaunchKernelGGL(k_quantize_gemm, dim3((unsigned)qgrid), dim3(256), 0, s, P.lhs, P.m, P.k,
-                     P.m_pad, xq, xexs);
-  CX_HIP(hipGetLastError());
-  P.xq = xq;
-  P.xexs = xexs;
+  CX_REQUIRE(P.m_pad % c.mt == 0 && P.m_pad >= P.m, "gemm: %u padded rows for tiles of %d",
+             P.m_pad, c.mt);
+  P.xq = scratch_xq(P.scratch);
+  P.xexs = scratch_xexs(P.scratch, P.m_pad, P.k);
   P.row_tiles = (P.n + c.tw - 1) / c.tw;
   P.act_tiles = (P.m + c.mt - 1) / c.mt;
   const size_t grid = (size_t)(P.row_tiles + 7) / 8 * 8 * P.act_tiles;
@@ -419,6 +429,19 @@ int launch(GemmParams& P, hipStream_t s) {
   CX_HIP(hipGetLastError());
   return CX_OK;
 }
+
+template <int T>
+int launch(GemmParams& P, hipStream_t s) {
+  gemm_kernel k = nullptr;
+  const Config c = config<T>(choose(P.n, P.m), &k);
+  // activation rows padded to the tile height (zero rows quantize to zero)
+  P.m_pad = (P.m + c.mt - 1) / c.mt * c.mt;
+  int rc = quantize(P.lhs, P.m, P.k, P.m_pad, P.scratch, s);
+  return rc ? rc : contract<T>(P, s);
+}
+
+// every tile height (16, 32 or 64 rows) divides 64
+inline uint32_t pad64(size_t m) { return (uint32_t)((m + 63) / 64 * 64); }
 
 }  // namespace
 
@@ -450,4 +473,35 @@ int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* 
   P.nb = (uint32_t)(k / 256);
   P.row_bytes = P.nb * cx_bpb(type);
   return type == CX_Q4_K ? launch<CX_Q4_K>(P, s) : launch<CX_Q5_K>(P, s);
+}
+
+int cx_gemm_quantize(const float* lhs, size_t m, size_t k, void* scratch, hipStream_t s) {
+  CX_REQUIRE(lhs && scratch, "gemm: null pointer");
+  CX_REQUIRE(k % 256 == 0 && k > 0 && k < (1u << 24) && m < (1u << 24), "gemm: %zu x %zu", m, k);
+  CX_REQUIRE(((uintptr_t)lhs & 15) == 0 && ((uintptr_t)scratch & 255) == 0,
+             "gemm: activations must be 16-byte and scratch 256-byte aligned");
+  if (!m) return CX_OK;
+  return quantize(lhs, (uint32_t)m, (uint32_t)k, pad64(m), reinterpret_cast<uint8_t*>(scratch), s);
+}
+
+int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, float* dst,
+                  const void* scratch, hipStream_t s) {
+  CX_REQUIRE(cx_gemm_supported(type), "gemm: type %d has no MFMA path", type);
+  CX_REQUIRE(w && dst && scratch, "gemm: null pointer");
+  CX_REQUIRE(k % 256 == 0 && k > 0, "gemm: k=%zu is not a multiple of 256", k);
+  CX_REQUIRE(n < (1u << 31) && m < (1u << 24) && k < (1u << 24), "gemm: shape too large");
+  CX_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)scratch & 255) == 0,
+             "gemm: weights must be 16-byte and scratch 256-byte aligned");
+  if (!n || !m) return CX_OK;
+  GemmParams P{};
+  P.scratch = const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(scratch));
+  P.w = w;
+  P.dst = dst;
+  P.n = (uint32_t)n;
+  P.k = (uint32_t)k;
+  P.m = (uint32_t)m;
+  P.m_pad = pad64(m);
+  P.nb = (uint32_t)(k / 256);
+  P.row_bytes = P.nb * cx_bpb(type);
+  return type == CX_Q4_K ? contract<CX_Q4_K>(P, s) : contract<CX_Q5_K>(P, s);
 }

@@ -760,6 +760,65 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float* x, const float*
   }
 }
 
+// rmsnorm of row blockIdx.x of x[rows][k] in the tree of k_gemv's fused
+// prologue: 8 consecutive values a lane (stride 2048), f64 squares, wave
+// sums, then ((w0 + w1) + w2) + w3; v = (x as f64 * scale) as f32 * w. Rows
+// normalized here are bit for bit the values the decode step's fused GEMV
+// quantizes, so a batched prefill matches token-by-token decoding.
+__global__ __launch_bounds__(256) void k_norm_rows(const float* x, const float* w, uint32_t k,
+                                                   float eps, float* out) {
+  __shared__ double red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* xr = x + (size_t)blockIdx.x * k;
+  float* yr = out + (size_t)blockIdx.x * k;
+  double sum = 0.0;
+  for (uint32_t i = 8 * tid; i < k; i += 2048) {
+    float v[8];
+    cx_load8(xr + i, v);
+#pragma unroll
+    for (int j = 0; j < 8; j++) sum += (double)v[j] * (double)v[j];
+  }
+  sum = cx_wave_sum_d(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  const double tot = ((red[0] + red[1]) + red[2]) + red[3];
+  const double scale = 1.0 / sqrt(tot / (double)k + (double)eps);
+  for (uint32_t i = 8 * tid; i < k; i += 2048) {
+    float v[8], nw[8];
+    cx_load8(xr + i, v);
+    cx_load8(w + i, nw);
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = (float)((double)v[j] * scale) * nw[j];
+    reinterpret_cast<float4*>(yr + i)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(yr + i)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// silu(g) * u elementwise (src/forward.rs:483-487), 8 values a lane
+__global__ __launch_bounds__(256) void k_swiglu_rows(const float* g, const float* u, size_t n,
+                                                     float* out) {
+  const size_t i = 8 * (blockIdx.x * 256ull + threadIdx.x);
+  if (i >= n) return;
+  float a[8], b[8];
+  cx_load8(g + i, a);
+  cx_load8(u + i, b);
+#pragma unroll
+  for (int j = 0; j < 8; j++) a[j] = cx_swiglu(a[j], b[j]);
+  reinterpret_cast<float4*>(out + i)[0] = make_float4(a[0], a[1], a[2], a[3]);
+  reinterpret_cast<float4*>(out + i)[1] = make_float4(a[4], a[5], a[6], a[7]);
+}
+
+// y[r][i] += a[r % a_rows][i]: the residual add (a_rows = rows) and the bias
+// add (a_rows = 1) of src/forward.rs:316-322, 467-469, 489-491, one f32 add
+// each, as the GEMV epilogues do
+__global__ __launch_bounds__(256) void k_add_rows(float* y, const float* a, uint32_t n,
+                                                  uint32_t a_rows, size_t total) {
+  const size_t i = blockIdx.x * 256ull + threadIdx.x;
+  if (i >= total) return;
+  const size_t r = i / n;
+  y[i] = y[i] + a[(r % a_rows) * n + i % n];
+}
+
 __global__ __launch_bounds__(256) void k_rmsnorm(float* out, const float* in, const float* w,
                                                  uint32_t n, float eps) {
   __shared__ double red[4];
@@ -810,6 +869,40 @@ int cx_launch_norm_quant(const float* x, const float* w, size_t n, float eps, in
     hipLaunchKernelGGL(k_norm_quant<16>, dim3(1), dim3(256), 0, s, x, w, (uint32_t)n, eps, xq, xe, xs);
   else
     hipLaunchKernelGGL(k_norm_quant<32>, dim3(1), dim3(256), 0, s, x, w, (uint32_t)n, eps, xq, xe, xs);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_norm_rows(const float* x, const float* w, size_t rows, size_t k, float eps,
+                        float* out, hipStream_t s) {
+  CX_REQUIRE(x && w && out, "norm rows: null pointer");
+  CX_REQUIRE(k % 8 == 0 && rows < (1u << 31), "norm rows: %zu x %zu", rows, k);
+  if (!rows || !k) return CX_OK;
+  hipLaunchKernelGGL(k_norm_rows, dim3((unsigned)rows), dim3(256), 0, s, x, w, (uint32_t)k, eps,
+                     out);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_swiglu_rows(const float* g, const float* u, size_t n, float* out, hipStream_t s) {
+  CX_REQUIRE(g && u && out && n % 8 == 0, "swiglu rows: %zu values", n);
+  if (!n) return CX_OK;
+  const size_t grid = (n / 8 + 255) / 256;
+  CX_REQUIRE(grid < (1ull << 31), "swiglu rows: %zu values is too many", n);
+  hipLaunchKernelGGL(k_swiglu_rows, dim3((unsigned)grid), dim3(256), 0, s, g, u, n, out);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_add_rows(float* y, const float* a, size_t rows, size_t n, size_t a_rows,
+                       hipStream_t s) {
+  CX_REQUIRE(y && a && n && a_rows && n < (1u << 31) && a_rows < (1u << 31),
+             "add rows: bad arguments");
+  const size_t total = rows * n, grid = (total + 255) / 256;
+  if (!total) return CX_OK;
+  CX_REQUIRE(grid < (1ull << 31), "add rows: %zu values is too many", total);
+  hipLaunchKernelGGL(k_add_rows, dim3((unsigned)grid), dim3(256), 0, s, y, a, (uint32_t)n,
+                     (uint32_t)a_rows, total);
   CX_HIP(hipGetLastError());
   return CX_OK;
 }

@@ -50,6 +50,14 @@ int cx_launch_norm_quant(const float* x, const float* w, size_t n, float eps, in
                          int8_t* xq, float* xe, float* xs, hipStream_t s);
 int cx_launch_rmsnorm(float* out, const float* in, const float* w, size_t rows, size_t n,
                       float eps, hipStream_t s);
+// Row forms of the decode step's ops, for the batched prefill: rmsnorm of
+// rows in the fused GEMV prologue's f64 tree (bit-identical to it); SwiGLU;
+// y[r] += a[r % a_rows] (residual: a_rows = rows; bias: a_rows = 1)
+int cx_launch_norm_rows(const float* x, const float* w, size_t rows, size_t k, float eps,
+                        float* out, hipStream_t s);
+int cx_launch_swiglu_rows(const float* g, const float* u, size_t n, float* out, hipStream_t s);
+int cx_launch_add_rows(float* y, const float* a, size_t rows, size_t n, size_t a_rows,
+                       hipStream_t s);
 
 // m activation rows at once on int8 MFMA (Q4_K, Q5_K): lhs[m][k] f32 is
 // quantized into `scratch` (cx_gemm_scratch_bytes, 256-byte aligned), then
@@ -58,6 +66,12 @@ bool cx_gemm_supported(int type);
 size_t cx_gemm_scratch_bytes(size_t m, size_t k);
 int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* lhs, size_t m,
                    float* dst, void* scratch, hipStream_t s);
+// The same in two steps, for several matrices over one activation: quantize
+// lhs once into scratch, then contract any number of Q4_K/Q5_K matrices of
+// width k against it (scratch of cx_gemm_scratch_bytes(m, k)).
+int cx_gemm_quantize(const float* lhs, size_t m, size_t k, void* scratch, hipStream_t s);
+int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, float* dst,
+                  const void* scratch, hipStream_t s);
 
 // Format conversion (cx_quant.hip): bit-identical to quant::descuantizar,
 // descuantizar_filas and desempaquetar_i8; rows[] are device indices.

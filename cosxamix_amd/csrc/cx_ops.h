@@ -12,18 +12,24 @@ struct cx_dstate {
   uint32_t pad;
 };
 
+int cx_launch_set_state(cx_dstate* st, uint32_t pos, uint32_t prompt_end, uint32_t cap,
+                        hipStream_t s);
+
 #define CX_ATT_MAX_TOTAL 16000  // general attention keeps scores in LDS
 // Decode attention runs in the reference's exact order (bit-identical) for
 // caches up to this many tokens, and as split-K ("flash decoding") above it,
 // where the sequential sums would dominate the step.
 #define CX_ATT_EXACT_MAX 4096
 
-// x = row hist[st->pos] of the embedding table (GGUF bytes of `type`), dequantized
+// x[r] = row hist[st->pos + r] of the embedding table (GGUF bytes of
+// `type`), dequantized, for r < rows
 int cx_launch_embed(int type, const uint8_t* embd, uint32_t dim, const cx_dstate* st,
-                    const uint32_t* hist, float* x, hipStream_t s);
+                    const uint32_t* hist, float* x, uint32_t rows, hipStream_t s);
+// rows tokens at positions st->pos + r: q[r] rotated in place, k[r] rotated
+// into K[pos], v[r] into V[pos]
 int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc,
                       const float* cos_t, const float* sin_t, uint32_t heads, uint32_t kvh,
-                      uint32_t hd, const cx_dstate* st, hipStream_t s);
+                      uint32_t hd, const cx_dstate* st, uint32_t rows, hipStream_t s);
 size_t cx_attn_splits(size_t cap);
 // floats of the exact path's score buffer (rows padded to 4 floats; the
 // buffer must start 16-byte aligned)
@@ -46,6 +52,11 @@ struct cx_attn_args {
   float *xe, *xs;
   int sub;
   int mode;                    // 0: by cap, 1: order-exact, 2: split-K
+  // query tokens (0 or 1: one). T > 1: token z at position st->pos + z,
+  // q/out rows of heads*hd, sc and the split partials T times their
+  // one-token size; q already rotated and the caches already filled
+  // (cos_t null), no quantized output.
+  uint32_t tokens;
 };
 int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s);
 int cx_launch_attention(const float* q, const float* k, const float* v, size_t tokens,

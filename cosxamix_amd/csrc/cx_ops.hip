@@ -15,7 +15,8 @@ namespace {
 
 // ---------------------------------------------------------- embedding
 // the token's row of an embedding table of any GGUF type, dequantized
-// (quant::descuantizar_filas, src/quant.rs:172-205), 8 values a lane
+// (quant::descuantizar_filas, src/quant.rs:172-205), 8 values a lane;
+// workgroup r makes the row of position st->pos + r into x[r]
 template <int T>
 __global__ __launch_bounds__(256) void k_embed(const uint8_t* embd, uint32_t dim,
                                                const cx_dstate* st, const uint32_t* hist,
@@ -24,8 +25,9 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* embd, uint32_t dim
   constexpr int BPB = T == CX_F32 ? 4 : T == CX_F16 ? 2 : T == CX_Q8_0 ? 34 : T == CX_Q5_0 ? 22
                     : T == CX_Q2_K ? 84 : T == CX_Q3_K ? 110 : T == CX_Q4_K ? 144
                     : T == CX_Q5_K ? 176 : 210;
-  const uint32_t tok = hist[st->pos];
+  const uint32_t tok = hist[st->pos + blockIdx.x];
   const uint8_t* row = embd + (size_t)tok * (dim / VPB) * BPB;
+  x += (size_t)blockIdx.x * dim;
   for (uint32_t i = 8 * threadIdx.x; i < dim; i += 2048) {
     float v[8];
     cxq::dequant8<T>(row + i / VPB * BPB, i % VPB, v);
@@ -35,15 +37,18 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* embd, uint32_t dim
 }
 
 // ------------------------------------------------------ rope + KV append
-// One token at position st->pos: q (H heads) rotated in place, k (Hkv heads)
-// rotated and written to K[pos], v copied to V[pos]. Rotation as
-// src/ops.rs:1185-1188: a' = a*c - b*s, b' = a*s + b*c (no FMA).
+// Token r (workgroup r) at position st->pos + r: q (H heads) rotated in
+// place, k (Hkv heads) rotated and written to K[pos], v copied to V[pos].
+// Rotation as src/ops.rs:1185-1188: a' = a*c - b*s, b' = a*s + b*c (no FMA).
 __global__ __launch_bounds__(256) void k_rope_kv(float* q, const float* k, const float* v,
                                                  float* kc, float* vc, const float* cos_t,
                                                  const float* sin_t, uint32_t heads,
                                                  uint32_t kvh, uint32_t hd,
                                                  const cx_dstate* st) {
-  const uint32_t pos = st->pos, half = hd / 2, kvd = kvh * hd;
+  const uint32_t pos = st->pos + blockIdx.x, half = hd / 2, kvd = kvh * hd;
+  q += (size_t)blockIdx.x * heads * hd;
+  k += (size_t)blockIdx.x * kvd;
+  v += (size_t)blockIdx.x * kvd;
   const float* c = cos_t + (size_t)pos * half;
   const float* s = sin_t + (size_t)pos * half;
   float* kd = kc + (size_t)pos * kvd;
@@ -81,7 +86,12 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* q, const float*
                                                     float* pm, float* pl, float* po,
                                                     uint32_t max_splits) {
   extern __shared__ __align__(16) float sh[];
-  const uint32_t total = st->pos + 1;
+  // query token z (blockIdx.z) sits at position st->pos + z
+  const uint32_t z = blockIdx.z, total = st->pos + z + 1;
+  q += (size_t)z * heads * hd;
+  pm += (size_t)z * max_splits * heads;
+  pl += (size_t)z * max_splits * heads;
+  po += (size_t)z * max_splits * heads * hd;
   const uint32_t split = blockIdx.x, g = blockIdx.y, per = heads / kvh;
   const uint32_t p0 = split * ATT_P;
   if (p0 >= total) return;
@@ -137,8 +147,12 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* q, const float*
 // out = (sum w_s o_s) * (1 / sum w_s l_s).
 __global__ void k_attn_combine(const float* pm, const float* pl, const float* po,
                                uint32_t heads, uint32_t hd, const cx_dstate* st,
-                               float* out) {
-  const uint32_t total = st->pos + 1, ns = (total + ATT_P - 1) / ATT_P;
+                               float* out, uint32_t max_splits) {
+  const uint32_t z = blockIdx.z, total = st->pos + z + 1, ns = (total + ATT_P - 1) / ATT_P;
+  pm += (size_t)z * max_splits * heads;
+  pl += (size_t)z * max_splits * heads;
+  po += (size_t)z * max_splits * heads * hd;
+  out += (size_t)z * heads * hd;
   const uint32_t h = blockIdx.x;
   float M = -INFINITY;
   for (uint32_t s = 0; s < ns; s++) M = fmaxf(M, pm[(size_t)s * heads + h]);
@@ -269,10 +283,17 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
   float* qr = reinterpret_cast<float*>(sm + NCH * 1024);
   float* kr = qr + HD;
   constexpr uint32_t half = HD / 2;
-  const uint32_t pos = st->pos, total = pos + 1;
+  // query token z (blockIdx.z) sits at position st->pos + z
+  const uint32_t z = blockIdx.z, pos = st->pos + z, total = pos + 1;
   const uint32_t p0 = blockIdx.x * SC_P, h = blockIdx.y, per = heads / kvh, g = h / per;
   if (p0 >= total) return;
   const uint32_t np = min(SC_P, total - p0), kvd = kvh * HD;
+  q += (size_t)z * heads * HD;
+  if (cos_t) {
+    knew += (size_t)z * kvd;
+    vnew += (size_t)z * kvd;
+  }
+  sc += (size_t)z * heads * sc_stride(cap);
   const int t = threadIdx.x;
   // 1. the K rows [p0, p0 + np) into LDS; pad bytes and rows past the end
   //    load a valid dummy that is never read
@@ -398,8 +419,11 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   float* ring = e + sc_lds(cap);
   __shared__ uint64_t etab[32];  // exp's table in LDS: no global load after the prefetch
   __shared__ float red[4];
-  const uint32_t total = st->pos + 1, h = blockIdx.x, g = h / (heads / kvh);
+  // query token z (blockIdx.z) sits at position st->pos + z
+  const uint32_t z = blockIdx.z, total = st->pos + z + 1, h = blockIdx.x, g = h / (heads / kvh);
   const uint32_t d0 = blockIdx.y * PV_DS, kvd = kvh * HD;
+  sc_all += (size_t)z * heads * sc_stride(cap);
+  out += (size_t)z * heads * HD;
   const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
   if (tid == 0) {  // uniform indices: scalar loads, which leave vmcnt alone
     const uint64_t tab[32] = CX_EXP2_TAB;
@@ -653,7 +677,19 @@ __global__ __launch_bounds__(256) void k_rope(float* x, uint32_t tokens, uint32_
 
 }  // namespace
 
+// the token loop's device state, set in stream order
+__global__ void k_set_state(cx_dstate* st, uint32_t pos, uint32_t prompt_end, uint32_t cap) {
+  if (threadIdx.x == 0) *st = cx_dstate{pos, prompt_end, cap, 0};
+}
+
 // ================================================================ launchers
+int cx_launch_set_state(cx_dstate* st, uint32_t pos, uint32_t prompt_end, uint32_t cap,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(k_set_state, dim3(1), dim3(64), 0, s, st, pos, prompt_end, cap);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
 int cx_launch_argmax_one(const float* v, size_t n, uint32_t* out, hipStream_t s) {
   CX_REQUIRE(v && out && n > 0 && n < 0xFFFFFFFFull, "argmax: bad arguments (n=%zu)", n);
   hipLaunchKernelGGL(k_argmax_one, dim3(1), dim3(1024), 0, s, v, (uint32_t)n, out);
@@ -672,10 +708,11 @@ int cx_launch_rope(float* x, size_t tokens, size_t heads, size_t hd, const float
   return CX_OK;
 }
 int cx_launch_embed(int type, const uint8_t* embd, uint32_t dim, const cx_dstate* st,
-                    const uint32_t* hist, float* x, hipStream_t s) {
+                    const uint32_t* hist, float* x, uint32_t rows, hipStream_t s) {
   CX_REQUIRE(dim % 8 == 0 && dim % (uint32_t)cx_vpb(type) == 0,
              "embedding: a row of %u values is not whole blocks of type %d", dim, type);
-  const dim3 g(1), wg(256);
+  CX_REQUIRE(rows >= 1, "embedding: no rows");
+  const dim3 g(rows), wg(256);
   switch (type) {
     case CX_F32: hipLaunchKernelGGL(k_embed<CX_F32>, g, wg, 0, s, embd, dim, st, hist, x); break;
     case CX_F16: hipLaunchKernelGGL(k_embed<CX_F16>, g, wg, 0, s, embd, dim, st, hist, x); break;
@@ -694,8 +731,9 @@ int cx_launch_embed(int type, const uint8_t* embd, uint32_t dim, const cx_dstate
 
 int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc,
                       const float* cos_t, const float* sin_t, uint32_t heads, uint32_t kvh,
-                      uint32_t hd, const cx_dstate* st, hipStream_t s) {
-  hipLaunchKernelGGL(k_rope_kv, dim3(1), dim3(256), 0, s, q, k, v, kc, vc, cos_t, sin_t, heads,
+                      uint32_t hd, const cx_dstate* st, uint32_t rows, hipStream_t s) {
+  CX_REQUIRE(rows >= 1, "rope: no rows");
+  hipLaunchKernelGGL(k_rope_kv, dim3(rows), dim3(256), 0, s, q, k, v, kc, vc, cos_t, sin_t, heads,
                      kvh, hd, st);
   CX_HIP(hipGetLastError());
   return CX_OK;
@@ -707,12 +745,13 @@ namespace {
 template <int HD>
 int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
   constexpr size_t sc_bytes = (SC_P * (HD * 4 + 16) + 1023) / 1024 * 1024 + 2 * HD * 4;
-  hipLaunchKernelGGL(k_attn_scores<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads), dim3(64),
+  const uint32_t T = a.tokens ? a.tokens : 1;
+  hipLaunchKernelGGL(k_attn_scores<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads, T), dim3(64),
                      sc_bytes, s, a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads,
                      a.kvh, a.st, scale, a.sc, a.cap);
   CX_HIP(hipGetLastError());
   const size_t lds = (sc_lds(a.cap) + PV_NST * PV_STP * PV_DS) * sizeof(float);
-  const dim3 grid(a.heads, HD / PV_DS);
+  const dim3 grid(a.heads, HD / PV_DS, T);
   if (a.sub == 16)
     hipLaunchKernelGGL((k_attn_seq<HD, 16>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads, a.kvh,
                        a.st, a.cap, a.out, a.xq, a.xe, a.xs);
@@ -732,6 +771,10 @@ int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s) {
   CX_REQUIRE(!a.xq || ((a.sub == 16 || a.sub == 32) && a.xe && a.xs),
              "attention: quantized output needs sub 16 or 32");
   CX_REQUIRE(!a.cos_t || (a.knew && a.vnew && a.sin_t), "attention: rope needs the new k/v");
+  const uint32_t T = a.tokens ? a.tokens : 1;
+  CX_REQUIRE(T == 1 || (!a.cos_t && !a.xq),
+             "attention: several query tokens take rotated q and filled caches, f32 output");
+  CX_REQUIRE(a.st && T <= 65535, "attention: %u query tokens", T);
   const float scale = 1.0f / sqrtf((float)hd);
   const bool exact = a.mode == 1 || (a.mode == 0 && a.cap <= CX_ATT_EXACT_MAX);
   if (exact) {
@@ -740,15 +783,15 @@ int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s) {
   }
   int rc;
   if (a.cos_t && (rc = cx_launch_rope_kv(a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, heads,
-                                         kvh, hd, a.st, s)))
+                                         kvh, hd, a.st, 1, s)))
     return rc;
   const uint32_t ns = (uint32_t)cx_attn_splits(a.cap), per = heads / kvh;
   const size_t lds = sizeof(float) * (per * hd + ATT_P * (hd + 1) + per * ATT_P);
-  hipLaunchKernelGGL(k_attn_split, dim3(ns, kvh), dim3(256), lds, s, a.q, a.kc, a.vc, heads, kvh,
-                     hd, a.st, scale, a.pm, a.pl, a.po, ns);
+  hipLaunchKernelGGL(k_attn_split, dim3(ns, kvh, T), dim3(256), lds, s, a.q, a.kc, a.vc, heads,
+                     kvh, hd, a.st, scale, a.pm, a.pl, a.po, ns);
   CX_HIP(hipGetLastError());
-  hipLaunchKernelGGL(k_attn_combine, dim3(heads), dim3(128), 0, s, a.pm, a.pl, a.po, heads, hd,
-                     a.st, a.out);
+  hipLaunchKernelGGL(k_attn_combine, dim3(heads, 1, T), dim3(128), 0, s, a.pm, a.pl, a.po, heads,
+                     hd, a.st, a.out, ns);
   CX_HIP(hipGetLastError());
   if (a.xq) return cx_launch_quantize(a.out, 1, (size_t)heads * hd, a.sub, a.xq, a.xe, a.xs, s);
   return CX_OK;
