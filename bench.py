@@ -98,6 +98,45 @@ def decode_bench(F, L, steps, warmup, prompt_len):
     return m, prompt, toks, timed, total_ms
 
 
+def config5_bench(F, L, steps=256, warmup=8, prefix=8192):
+    """the Llama-3-8B shape (qwen2 architecture, zero
+    biases), Q4_K linears, Q5_K ffn_down, Q4_K lm_head; an 8192-token seeded
+    random prefix prefilled into the f32 KV cache, then `steps` greedy
+    tokens, timed per step with HIP events after `warmup` untimed ones."""
+    import numpy as np
+    cfg = F.LLAMA3_8B
+    t0 = time.perf_counter()
+    m = F.Modelo(cfg, tipo=L.Q4_K, semilla=8, tipo_down=L.Q5_K, tipo_salida=L.Q4_K)
+    gen_s = time.perf_counter() - t0
+    prompt = prompt_tokens(prefix, cfg.vocab, seed=5)
+    cache = m.nueva_cache(prefix + warmup + steps + 1)
+    t0 = time.perf_counter()
+    first = int(m.forward(prompt, cache, logits=False)[1])  # the prefix's next token
+    prefill_s = time.perf_counter() - t0
+    toks, ms = m.generar(np.array([first], np.uint32), warmup + steps, cache, tiempos=True)
+    timed = [float(v) for v in ms[warmup:warmup + steps]]
+    total = sum(timed) * 1e-3
+    w = m.bytes_por_token()
+    ctx_mid = prefix + 1 + warmup + steps // 2
+    kv = 2 * cfg.capas * cfg.dim_kv() * 4 * ctx_mid
+    out = {"workload": "BASELINE config 5: Llama-3-8B-shape daiss model (32 layers, hidden 4096, "
+                       "32/8 heads x 128, SwiGLU 14336, vocab 128256, rope 5e5), Q4_K linears, "
+                       "Q5_K ffn_down, Q4_K lm_head, f32 KV cache (split-K attention), "
+                       f"{prefix}-token seeded random prefix, greedy decode",
+           "prefix_tokens": prefix, "decode_tokens": steps, "warmup": warmup,
+           "tok_per_s": round(steps / total, 2),
+           "median_us_per_token": round(statistics.median(timed) * 1000, 2),
+           "weight_bytes_per_token": w, "kv_bytes_per_token_mid": kv,
+           "effective_GBps": round((w + kv) / (total / steps) / 1e9, 1),
+           "prefill_s": round(prefill_s, 3), "prefill_tok_per_s": round(prefix / prefill_s, 1),
+           "model_generation_s": round(gen_s, 2)}
+    log(f"[bench] config 5: prefill {prefix} tokens {prefill_s:.2f}s; {steps} tokens at "
+        f"{out['tok_per_s']} tok/s ({out['median_us_per_token']} us median), "
+        f"{out['effective_GBps']} GB/s effective")
+    m.close()
+    return out
+
+
 def prefill_bench(m, prompt, reps=5):
     """Modelo::forward of the whole prompt on an empty cache (the batched
     prefill): the median wall time of `reps` calls after one warm-up call,
@@ -411,6 +450,8 @@ def main():
     ap.add_argument("--batched-only", action="store_true",
                     help="only the config-4 batched contraction (GPU side), e.g. under rocprofv3")
     ap.add_argument("--trace-summary")
+    ap.add_argument("--config5-only", action="store_true",
+                    help="only BASELINE config 5 (8B shape, 8K context)")
     a = ap.parse_args()
     if a.trace_summary:
         trace_summary(a.trace_summary)
@@ -428,6 +469,9 @@ def main():
     from cosxamix_amd import _lib as L
     from cosxamix_amd import forward as F
 
+    if a.config5_only:
+        print(json.dumps(config5_bench(F, L)), flush=True)
+        return 0
     if a.batched_only:
         m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)
         print(json.dumps(batched_bench(L, m, False)), flush=True)

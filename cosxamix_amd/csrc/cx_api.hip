@@ -356,14 +356,13 @@ extern "C" int cx_attention_decode(const float* q, const float* k, const float* 
                                    void* stream) {
   CX_REQUIRE(q && k && v && out && total > 0, "attention_decode: bad arguments");
   CX_REQUIRE(mode >= 0 && mode <= 2, "attention_decode: mode %d", mode);
-  CX_REQUIRE(mode != 1 || total <= CX_ATT_EXACT_MAX, "attention_decode: exact mode up to %d",
-             CX_ATT_EXACT_MAX);
   const size_t cap = total;
   const size_t ns = cx_attn_splits(cap);
   auto up = [](size_t n) { return (n + 255) / 256 * 256; };
   const size_t o_pm = 256, o_pl = o_pm + up(ns * heads * 4), o_po = o_pl + up(ns * heads * 4),
                o_sc = o_po + up(ns * heads * hd * 4),
-               bytes = o_sc + up(cx_attn_score_floats(heads, cap) * 4);
+               o_cm = o_sc + up(cx_attn_score_floats(heads, cap) * 4),
+               bytes = o_cm + up(cx_attn_chunk_floats(heads, cap) * 4);
   void* sp = nullptr;
   int rc = cx_scratch_reserve(bytes, &sp);
   if (rc) return rc;
@@ -373,6 +372,7 @@ extern "C" int cx_attention_decode(const float* q, const float* k, const float* 
   float* pl = (float*)(b + o_pl);
   float* po = (float*)(b + o_po);
   float* sc = (float*)(b + o_sc);
+  float* cm = (float*)(b + o_cm);
   hipStream_t s = STREAM(stream);
   // the kernels read the position from device state: pos = total - 1
   cx_dstate h{(uint32_t)(total - 1), 0u, (uint32_t)cap, 0u};
@@ -390,6 +390,7 @@ extern "C" int cx_attention_decode(const float* q, const float* k, const float* 
   a.pl = pl;
   a.po = po;
   a.sc = sc;
+  a.cm = cm;
   a.out = out;
   a.mode = mode;
   rc = cx_launch_attn_decode(a, s);
@@ -451,7 +452,7 @@ struct cx_model {
 struct cx_prefill {
   uint32_t T;
   float *x, *nrm, *q, *k, *v, *att, *g, *u, *tmp;  // nrm also holds the SwiGLU rows
-  float *sc, *pm, *pl, *po;
+  float *sc, *cm;
   void* scratch;
 };
 
@@ -463,6 +464,7 @@ struct cx_cache {
   cx_dstate* st;
   float *pm, *pl, *po;  // split-K partials
   float* sc;            // scores of the order-exact attention, heads x cap
+  float* cm;            // and their maxima per chunk of positions
   hipGraphExec_t exec;
   bool have_graph;
   cx_prefill pf;
@@ -949,7 +951,8 @@ extern "C" int cx_cache_new(cx_model* m, size_t cap, cx_cache** out) {
   if (hipMalloc(&C->kv, (size_t)c.layers * 2 * cap * kvd * 4) || hipMalloc(&C->hist, (cap + 1) * 4) ||
       hipMalloc(&C->st, sizeof(cx_dstate)) || hipMalloc(&C->pm, ns * c.heads * 4) ||
       hipMalloc(&C->pl, ns * c.heads * 4) || hipMalloc(&C->po, ns * c.heads * (c.dim / c.heads) * 4) ||
-      hipMalloc(&C->sc, cx_attn_score_floats(c.heads, cap) * 4)) {
+      hipMalloc(&C->sc, cx_attn_score_floats(c.heads, cap) * 4) ||
+      hipMalloc(&C->cm, cx_attn_chunk_floats(c.heads, cap) * 4)) {
     cx_cache_free(C);
     cx_set_error("cache: cannot allocate %zu tokens", cap);
     return CX_ENOMEM;
@@ -973,8 +976,8 @@ extern "C" void cx_cache_free(cx_cache* c) {
   (void)hipStreamSynchronize(c->m->stream);
   if (c->have_graph) (void)hipGraphExecDestroy(c->exec);
   const cx_prefill& P = c->pf;
-  void* bufs[] = {c->kv, c->hist, c->st, c->pm, c->pl, c->po, c->sc, P.x, P.nrm, P.q, P.k,
-                  P.v, P.att, P.g, P.u, P.tmp, P.sc, P.pm, P.pl, P.po, P.scratch};
+  void* bufs[] = {c->kv, c->hist, c->st, c->pm, c->pl, c->po, c->sc, c->cm, P.x, P.nrm, P.q,
+                  P.k, P.v, P.att, P.g, P.u, P.tmp, P.sc, P.cm, P.scratch};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   delete c;
@@ -1041,6 +1044,7 @@ static int enqueue_step(cx_cache* C) {
     a.pl = C->pl;
     a.po = C->po;
     a.sc = C->sc;
+    a.cm = C->cm;
     a.out = m->att;
     a.xq = m->xq;  // the output projection's activation
     a.xe = m->xe;
@@ -1153,9 +1157,7 @@ static int prefill_alloc(cx_cache* C) {
   if (P.T) return CX_OK;
   const cx_config& c = C->m->cfg;
   const size_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn, H = c.heads;
-  const size_t ns = cx_attn_splits(C->cap);
-  const bool exact = C->cap <= CX_ATT_EXACT_MAX;
-  const size_t per_tok = exact ? cx_attn_score_floats(H, C->cap) * 4 : ns * H * (hd + 2) * 4;
+  const size_t per_tok = (cx_attn_score_floats(H, C->cap) + cx_attn_chunk_floats(H, C->cap)) * 4;
   size_t T = kPrefillAttnBytes / per_tok;
   T = T > kPrefillMaxT ? kPrefillMaxT : T < 16 ? 16 : T / 16 * 16;
   if (T > C->cap) T = C->cap;
@@ -1168,20 +1170,15 @@ static int prefill_alloc(cx_cache* C) {
               {&P.tmp, T * D}};
   for (const Want& w : want)
     if (hipMalloc(w.p, w.floats * 4) != hipSuccess) goto fail;
-  if (exact) {
-    if (hipMalloc(&P.sc, T * cx_attn_score_floats(H, C->cap) * 4) != hipSuccess) goto fail;
-  } else if (hipMalloc(&P.pm, T * ns * H * 4) != hipSuccess ||
-             hipMalloc(&P.pl, T * ns * H * 4) != hipSuccess ||
-             hipMalloc(&P.po, T * ns * H * hd * 4) != hipSuccess) {
+  if (hipMalloc(&P.sc, T * cx_attn_score_floats(H, C->cap) * 4) != hipSuccess ||
+      hipMalloc(&P.cm, T * cx_attn_chunk_floats(H, C->cap) * 4) != hipSuccess)
     goto fail;
-  }
   if (hipMalloc(&P.scratch, cx_gemm_scratch_bytes(T, wide)) != hipSuccess) goto fail;
   P.T = (uint32_t)T;
   return CX_OK;
 fail:
   for (void* b : {(void*)P.x, (void*)P.nrm, (void*)P.q, (void*)P.k, (void*)P.v, (void*)P.att,
-                  (void*)P.g, (void*)P.u, (void*)P.tmp, (void*)P.sc, (void*)P.pm, (void*)P.pl,
-                  (void*)P.po, P.scratch})
+                  (void*)P.g, (void*)P.u, (void*)P.tmp, (void*)P.sc, (void*)P.cm, P.scratch})
     if (b) (void)hipFree(b);
   P = cx_prefill{};
   cx_set_error("prefill: cannot allocate the buffers of %zu tokens", T);
@@ -1247,10 +1244,8 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
     a.hd = hd;
     a.cap = (uint32_t)C->cap;
     a.st = C->st;
-    a.pm = P.pm;
-    a.pl = P.pl;
-    a.po = P.po;
     a.sc = P.sc;
+    a.cm = P.cm;
     a.out = P.att;
     a.tokens = nt;
     if ((rc = cx_launch_attn_decode(a, s))) return rc;

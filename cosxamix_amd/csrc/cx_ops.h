@@ -16,10 +16,10 @@ int cx_launch_set_state(cx_dstate* st, uint32_t pos, uint32_t prompt_end, uint32
                         hipStream_t s);
 
 #define CX_ATT_MAX_TOTAL 16000  // general attention keeps scores in LDS
-// Decode attention runs in the reference's exact order (bit-identical) for
-// caches up to this many tokens, and as split-K ("flash decoding") above it,
-// where the sequential sums would dominate the step.
-#define CX_ATT_EXACT_MAX 4096
+// Decode attention holds a head's scores in LDS for caches up to this many
+// tokens (cx_ops.hip) and streams them above it (cx_attn.hip); both paths
+// are order-exact.
+#define CX_ATT_LDS_MAX 4096
 
 // x[r] = row hist[st->pos + r] of the embedding table (GGUF bytes of
 // `type`), dequantized, for r < rows
@@ -32,10 +32,14 @@ int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float
                       uint32_t hd, const cx_dstate* st, uint32_t rows, hipStream_t s);
 size_t cx_attn_splits(size_t cap);
 // floats of the exact path's score buffer (rows padded to 4 floats; the
-// buffer must start 16-byte aligned)
+// buffer must start 16-byte aligned) and of its per-chunk maxima
 inline size_t cx_attn_score_floats(size_t heads, size_t cap) { return heads * ((cap + 3) / 4 * 4); }
+size_t cx_attn_chunk_floats(size_t heads, size_t cap);
 
-// One decode step's attention (src/ops.rs:1258-1325 at tokens = 1).
+// One decode step's attention (src/ops.rs:1258-1325 at tokens = 1). The
+// order-exact path (modes 0 and 1, cx_attn.hip) is bit-identical to the
+// reference for any cache length; split-K (mode 2) combines partial
+// softmaxes in another order.
 struct cx_attn_args {
   float* q;                    // heads*hd; rotated in place by the split-K path
   const float* knew;           // this step's k and v (kvh*hd), used with rope
@@ -46,12 +50,13 @@ struct cx_attn_args {
   const float* sin_t;          //   already hold position st->pos
   uint32_t heads, kvh, hd, cap;
   const cx_dstate* st;
-  float *pm, *pl, *po, *sc;    // split-K partials, exact-path scores
+  float *pm, *pl, *po;         // split-K partials
+  float *sc, *cm;              // exact path: scores, per-chunk maxima
   float* out;                  // heads*hd
   int8_t* xq;                  // optional: out quantized for the next GEMV
   float *xe, *xs;
   int sub;
-  int mode;                    // 0: by cap, 1: order-exact, 2: split-K
+  int mode;                    // 0 or 1: order-exact, 2: split-K
   // query tokens (0 or 1: one). T > 1: token z at position st->pos + z,
   // q/out rows of heads*hd, sc and the split partials T times their
   // one-token size; q already rotated and the caches already filled
@@ -59,6 +64,7 @@ struct cx_attn_args {
   uint32_t tokens;
 };
 int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s);
+int cx_launch_attn_exact(const cx_attn_args& a, float scale, hipStream_t s);
 int cx_launch_attention(const float* q, const float* k, const float* v, size_t tokens,
                         size_t total, size_t heads, size_t kvh, size_t hd, float* out,
                         hipStream_t s);

@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 
 // ------------------------------------------- order-exact decode attention
 // The decode step's attention in the reference's own order, for contexts up
-// to CX_ATT_EXACT_MAX, in two kernels. Both stage their cache rows in LDS
+// to CX_ATT_LDS_MAX, in two kernels. Both stage their cache rows in LDS
 // with direct-to-LDS loads, so a wave keeps up to 63 KiB of the cache in
 // flight instead of waiting on one row at a time.
 //
@@ -741,6 +741,7 @@ int cx_launch_rope_kv(float* q, const float* k, const float* v, float* kc, float
 
 size_t cx_attn_splits(size_t cap) { return (cap + ATT_P - 1) / ATT_P; }
 
+
 namespace {
 template <int HD>
 int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
@@ -765,8 +766,9 @@ int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
 
 int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s) {
   const uint32_t heads = a.heads, kvh = a.kvh, hd = a.hd;
-  CX_REQUIRE(kvh && heads % kvh == 0 && heads / kvh <= ATT_MAXG, "attention: %u heads / %u groups",
-             heads, kvh);
+  CX_REQUIRE(kvh && heads % kvh == 0, "attention: %u heads / %u groups", heads, kvh);
+  CX_REQUIRE(a.mode != 2 || heads / kvh <= ATT_MAXG,
+             "attention: split-K takes at most %d query heads per KV group", ATT_MAXG);
   CX_REQUIRE(hd == 64 || hd == 128, "attention: head_dim %u (64 or 128 supported)", hd);
   CX_REQUIRE(!a.xq || ((a.sub == 16 || a.sub == 32) && a.xe && a.xs),
              "attention: quantized output needs sub 16 or 32");
@@ -776,10 +778,12 @@ int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s) {
              "attention: several query tokens take rotated q and filled caches, f32 output");
   CX_REQUIRE(a.st && T <= 65535, "attention: %u query tokens", T);
   const float scale = 1.0f / sqrtf((float)hd);
-  const bool exact = a.mode == 1 || (a.mode == 0 && a.cap <= CX_ATT_EXACT_MAX);
-  if (exact) {
-    CX_REQUIRE(a.cap <= CX_ATT_EXACT_MAX, "attention: exact path up to %d tokens", CX_ATT_EXACT_MAX);
-    return hd == 64 ? launch_exact<64>(a, scale, s) : launch_exact<128>(a, scale, s);
+  if (a.mode != 2) {
+    // two order-exact designs: the cache's scores held in LDS (short
+    // caches: fewer, lighter stages), or streamed (any length)
+    if (a.cap <= CX_ATT_LDS_MAX && heads / kvh <= ATT_MAXG)
+      return hd == 64 ? launch_exact<64>(a, scale, s) : launch_exact<128>(a, scale, s);
+    return cx_launch_attn_exact(a, scale, s);
   }
   int rc;
   if (a.cos_t && (rc = cx_launch_rope_kv(a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, heads,

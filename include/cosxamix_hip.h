@@ -182,9 +182,9 @@ int cx_attention(const float *q, const float *k, const float *v, size_t tokens,
 
 /* ops::atencion at tokens = 1 (src/ops.rs:1258-1325) with the decode-step
  * kernels of the model: q[H*hd] of the token at position total-1 against
- * k/v[total][Hkv*hd]. mode 0: as the model chooses (order-exact up to 4096
- * cached tokens, split-K above); 1: order-exact (bit-identical to the
- * reference's scalar order, total <= 4096); 2: split-K. */
+ * k/v[total][Hkv*hd]. mode 0 or 1: order-exact, bit-identical to the
+ * reference's scalar order at any length (what the model runs); 2: split-K
+ * (partial softmaxes combined: equal within f32 rounding). */
 int cx_attention_decode(const float *q, const float *k, const float *v,
                         size_t total, size_t heads, size_t kv_heads,
                         size_t head_dim, int mode, float *out, void *stream);

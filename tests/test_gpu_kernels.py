@@ -280,13 +280,14 @@ def test_softmax_silu_argmax(cx, dev):
     assert ops.argmax(T(big, dev)) == 100
 
 
-@pytest.mark.parametrize("heads,kvh", [(16, 2), (32, 8), (4, 2)])
-def test_decode_attention_paths(cx, dev, heads, kvh):
+@pytest.mark.parametrize("heads,kvh,hd", [(16, 2, 128), (32, 8, 128), (4, 2, 64), (28, 4, 128),
+                                          (8, 8, 64), (32, 2, 128)])
+def test_decode_attention_paths(cx, dev, heads, kvh, hd):
     """The model's decode attention: order-exact mode bit-identical to the
-    oracle (src/ops.rs:1258-1325); split-K mode within f32 rounding."""
+    oracle (src/ops.rs:1258-1325) at any length, for 1, 2, 4, 7, 8 and 16
+    query heads per KV group; split-K mode within f32 rounding."""
     ops, _ = cx
-    hd = 128
-    for total in (1, 2, 37, 63, 64, 65, 100, 150, 640, 1000):
+    for total in (1, 2, 37, 63, 64, 65, 100, 150, 255, 256, 257, 640, 1000, 4097, 8300):
         rng = np.random.default_rng(total + heads)
         q = rng.normal(0, 1, heads * hd).astype(np.float32)
         k = rng.normal(0, 1, total * kvh * hd).astype(np.float32)

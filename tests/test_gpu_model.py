@@ -107,14 +107,11 @@ def test_config3_shape_bit_identical_to_oracle(F):
     assert np.array_equal(got, exp), (got, exp)
 
 
-def test_split_k_attention_path_logit_statistics(F):
-    """Caches above 4096 tokens use split-K decode attention, whose f32 sums
-    run in another order (the kernel itself is within rtol 1e-5 of the
-    oracle: test_decode_attention_paths). At the model level most steps are
-    within the north star's 1e-3; a step whose attention output crosses an
-    i8 rounding boundary of the next quantization moves by up to ~3e-2.
-    Bars: >= 75% of 24 teacher-forced steps within 1e-3, all within 5e-2,
-    and the argmax agrees wherever the oracle's top-2 gap exceeds 5e-2."""
+def test_long_cache_attention_path_bit_identical_to_oracle(F):
+    """Caches above 4096 tokens stream the scores through LDS instead of
+    holding them (cx_attn.hip); the arithmetic order is still the
+    reference's, so logits stay bit-identical: a 4200-token cache, a
+    150-token prefill and 24 teacher-forced steps, then greedy tokens."""
     c = F.Config(capas=1, dim=2048, cabezas=16, cabezas_kv=2, ffn=2048, vocab=800,
                  contexto=5000, rope=1e6)
     m = F.Modelo(c, semilla=5)
@@ -123,18 +120,14 @@ def test_split_k_attention_path_logit_statistics(F):
     cache, rc = m.nueva_cache(4200), ref.new_cache(4200)
     lg, _ = m.forward(prompt, cache)
     want = ref.forward(prompt, rc)
-    errs = []
     for step in range(24):
-        errs.append(float(np.max(np.abs(lg - want))))
-        top = np.sort(want)
-        if top[-1] - top[-2] > 5e-2:
-            assert O.argmax(lg) == O.argmax(want), step
+        assert np.array_equal(lg.view(np.uint32), want.view(np.uint32)), step
         tok = O.argmax(want)
         lg, _ = m.forward([tok], cache)
         want = ref.forward([tok], rc)
-    errs = np.array(errs)
-    assert np.mean(errs <= 1e-3) >= 0.75, errs
-    assert errs.max() <= 5e-2, errs
+    got = m.generar(prompt, 12, m.nueva_cache(4200))
+    exp = ref.generate(prompt, 12, ref.new_cache(4200))
+    assert np.array_equal(got, exp)
 
 
 def test_cache_truncate_and_prefix_reuse(F):  # src/forward.rs:98-127

@@ -4,8 +4,8 @@ tokens (the int8 MFMA contraction for Q4_K/Q5_K, the GEMV row by row for
 other types, the decode attention kernels with one query per grid slice).
 It must give what feeding the same tokens one at a time gives, bit for bit:
 the logits of the last token, and through the KV cache every later step.
-Both attention paths are covered (order-exact for caches up to 4096
-tokens, split-K above), prompts longer than one chunk, a prefill that
+Both attention paths are covered (scores held in LDS for caches up to
+4096 tokens, streamed above), prompts longer than one chunk, a prefill that
 starts at a nonzero cache length, and a model whose matrices take the
 row-by-row fallback."""
 import numpy as np
@@ -54,7 +54,7 @@ def check_model(F, m, cap, n_prompt, n_more, seed):
     return prompt
 
 
-@pytest.mark.parametrize("cap", [512, 4160], ids=["exact", "split-k"])
+@pytest.mark.parametrize("cap", [512, 4160], ids=["lds-scores", "streamed-scores"])
 def test_prefill_equals_token_by_token_daiss(F, cap):
     # Q5_K attention and gate/up (contraction), Q3_K ffn_down (row by row),
     # Q4_K lm_head; 300 tokens = two chunks
