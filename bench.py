@@ -452,6 +452,7 @@ def main():
     ap.add_argument("--trace-summary")
     ap.add_argument("--config5-only", action="store_true",
                     help="only BASELINE config 5 (8B shape, 8K context)")
+    ap.add_argument("--no-config5", action="store_true")
     a = ap.parse_args()
     if a.trace_summary:
         trace_summary(a.trace_summary)
@@ -485,6 +486,8 @@ def main():
     traffic, tdetail = (None, "skipped (--no-traffic)") if a.no_traffic else gemv_traffic()
     cpu = None if a.no_cpu else cpu_baseline(F, L, m, prompt)
     batched = batched_bench(L, m, not a.no_cpu)
+    m.close()
+    config5 = None if a.no_config5 else config5_bench(F, L)
     out = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -516,6 +519,7 @@ def main():
                    "first_tokens": [int(t) for t in toks[:8]]},
         "batched": batched,
         "prefill": prefill,
+        "config5": config5,
     }
     print(json.dumps(out), flush=True)
     return 0

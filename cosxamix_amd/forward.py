@@ -8,6 +8,7 @@ of the last one; ``generar`` is the greedy token loop of Modelo::generar.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -65,6 +66,7 @@ class Modelo:
                                            tipo_salida or tipo, semilla, C.byref(h)),
                 "Modelo")
         self._h = h
+        self._caches = weakref.WeakSet()
 
     @classmethod
     def abrir(cls, ruta) -> "Modelo":
@@ -74,6 +76,7 @@ class Modelo:
             raise ValueError(L.last_error())
         m = cls.__new__(cls)
         m._h = h
+        m._caches = weakref.WeakSet()
         c = L.CxConfig()
         L.check(_lib.cx_model_config(h, C.byref(c)), "Modelo")
         m.cfg = Config(c.layers, c.dim, c.heads, c.kv_heads, c.ffn, c.vocab, c.ctx, c.eps,
@@ -85,6 +88,9 @@ class Modelo:
         L.check(_lib.cx_model_save_gguf(self._h, str(ruta).encode()), "guardar")
 
     def close(self):
+        """Frees the model and, first, every cache still open on it."""
+        for c in list(getattr(self, "_caches", ())):
+            c.close()
         if getattr(self, "_h", None) and _lib is not None:
             _lib.cx_model_free(self._h)
         self._h = None
@@ -162,6 +168,7 @@ class Cache:
         h = C.c_void_p()
         L.check(_lib.cx_cache_new(modelo._h, capacidad, C.byref(h)), "Cache")
         self._h = h
+        modelo._caches.add(self)
 
     def largo(self) -> int:
         return int(_lib.cx_cache_len(self._h))
