@@ -137,6 +137,21 @@ def config5_bench(F, L, steps=256, warmup=8, prefix=8192):
     return out
 
 
+def sampled_bench(m, prompt, steps=64, warmup=8, temp=0.8, top_p=0.9):
+    """The same token loop with Muestreador(42, temp, top_p) drawing on the
+    GPU inside the captured step: median per-token time."""
+    from cosxamix_amd import sampler
+    cache = m.nueva_cache(len(prompt) + warmup + steps + 1)
+    toks, ms = m.generar(prompt, warmup + steps, cache, tiempos=True,
+                         muestreador=sampler.Muestreador(42, temp, top_p))
+    timed = [float(v) for v in ms[warmup:warmup + steps]]
+    med = statistics.median(timed)
+    out = {"temperature": temp, "top_p": top_p, "median_us_per_token": round(med * 1000, 2),
+           "tok_per_s": round(1000.0 / med, 2), "first_tokens": [int(t) for t in toks[:8]]}
+    log(f"[bench] sampled decode (t={temp}, top_p={top_p}): {out['median_us_per_token']} us/token")
+    return out
+
+
 def prefill_bench(m, prompt, reps=5):
     """Modelo::forward of the whole prompt on an empty cache (the batched
     prefill): the median wall time of `reps` calls after one warm-up call,
@@ -482,6 +497,7 @@ def main():
     per_tok_bytes = m.bytes_por_token()
     kv_bytes = 2 * F.DAISS_3B.capas * F.DAISS_3B.dim_kv() * 4 * (a.prompt + a.warmup + a.steps // 2)
     prefill = prefill_bench(m, prompt)
+    sampled = sampled_bench(m, prompt)
     avg, gbps, ncopies = gemv_roofline(F, L, m)
     traffic, tdetail = (None, "skipped (--no-traffic)") if a.no_traffic else gemv_traffic()
     cpu = None if a.no_cpu else cpu_baseline(F, L, m, prompt)
@@ -519,6 +535,7 @@ def main():
                    "first_tokens": [int(t) for t in toks[:8]]},
         "batched": batched,
         "prefill": prefill,
+        "sampled_decode": sampled,
         "config5": config5,
     }
     print(json.dumps(out), flush=True)

@@ -103,6 +103,10 @@ SIGNATURES = {
     "cx_forward": (C.c_int, [_vp, _vp, _u32p, _sz, _f32p, _u32p]),
     "cx_generate": (C.c_int, [_vp, _vp, _u32p, _sz, _sz, C.c_uint32, _u32p, C.POINTER(_sz),
                               _f32p]),
+    "cx_generate_sampled": (C.c_int, [_vp, _vp, _u32p, _sz, _sz, C.c_uint32, C.c_uint64, C.c_float,
+                                      C.c_float, _u32p, C.POINTER(_sz), _f32p]),
+    "cx_sample": (C.c_int, [_vp, _sz, C.c_float, C.c_float, C.POINTER(C.c_uint64),
+                            C.POINTER(C.c_uint32), _vp]),
 }
 
 

@@ -403,6 +403,60 @@ extern "C" int cx_argmax(const float* v, size_t n, uint32_t* out, void* stream) 
   return cx_launch_argmax_one(v, n, out, STREAM(stream));
 }
 
+// Muestreador::nuevo (src/sampler.rs:38-47): Azar::con_semilla (a zero seed
+// is remapped, src/daiss.rs:322-328), 1/temperature, top_p clamped to [0, 1]
+// (a NaN stays NaN, as f32::clamp leaves it)
+static cx_samp_state sampler_state(uint64_t seed, float temperature, float top_p) {
+  cx_samp_state h{};
+  h.azar = seed ? seed : 0x9E3779B97F4A7C15ull;
+  h.inv = 1.0f / temperature;
+  h.top_p = top_p < 0.0f ? 0.0f : (top_p > 1.0f ? 1.0f : top_p);
+  return h;
+}
+
+// Muestreador::elegir (src/sampler.rs:61-125) on device logits; the
+// generator's state is the caller's (host), advanced by one draw when
+// temperature > 0. Returns when *out (host) holds the token.
+extern "C" int cx_sample(const float* logits, size_t n, float temperature, float top_p,
+                         uint64_t* state, uint32_t* out, void* stream) {
+  CX_REQUIRE(state && out, "sample: null state or output");
+  if (n == 0) {  // src/sampler.rs:62-64
+    *out = 0;
+    return CX_OK;
+  }
+  CX_REQUIRE(logits && n < (1u << 31), "sample: bad logits (n=%zu)", n);
+  hipStream_t s = STREAM(stream);
+  auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+  // (the chains' 16-byte loads may reach 3 floats past the last value)
+  const size_t o_pb = 256, o_part = o_pb + up((n + 4) * 4),
+               o_ord = o_part + up(cx_sample_parts(n) * 4), o_ordp = o_ord + up(n * 4),
+               o_tok = o_ordp + up((n + 4) * 4), bytes = o_tok + 256;
+  void* sp = nullptr;
+  int rc = cx_scratch_reserve(bytes, &sp);
+  if (rc) return rc;
+  uint8_t* b = (uint8_t*)sp;
+  uint32_t* tok = (uint32_t*)(b + o_tok);
+  if (temperature <= 0.0f) {  // greedy: the argmax, no draw
+    if ((rc = cx_launch_argmax_one(logits, n, tok, s))) return rc;
+    CX_HIP(hipMemcpyAsync(out, tok, 4, hipMemcpyDeviceToHost, s));
+    CX_HIP(hipStreamSynchronize(s));
+    return CX_OK;
+  }
+  cx_samp_state h = sampler_state(1, temperature, top_p);
+  h.azar = *state;  // the caller's generator, as it stands
+  cx_samp_state* sd = (cx_samp_state*)b;
+  CX_HIP(hipMemcpyAsync(sd, &h, sizeof h, hipMemcpyHostToDevice, s));
+  if ((rc = cx_launch_sample(logits, n, sd, (float*)(b + o_pb), (float*)(b + o_part),
+                             (uint32_t*)(b + o_ord), (float*)(b + o_ordp), tok, nullptr, nullptr,
+                             s)))
+    return rc;
+  CX_HIP(hipMemcpyAsync(&h, sd, sizeof h, hipMemcpyDeviceToHost, s));
+  CX_HIP(hipStreamSynchronize(s));
+  *state = h.azar;
+  *out = h.token;
+  return CX_OK;
+}
+
 // ================================================================ 3. model
 namespace {
 struct Tensor {
@@ -465,8 +519,15 @@ struct cx_cache {
   float *pm, *pl, *po;  // split-K partials
   float* sc;            // scores of the order-exact attention, heads x cap
   float* cm;            // and their maxima per chunk of positions
-  hipGraphExec_t exec;
+  hipGraphExec_t exec;    // the captured step (greedy tail)
   bool have_graph;
+  hipGraphExec_t exec_s;  // the captured step with the sampler's tail
+  bool have_graph_s;
+  bool sampling;          // steps and prefills take the sampler's tail
+  // the sampler's state and scratch, made at the first sampled generation
+  cx_samp_state* sd;
+  float *spb, *spart, *sordp;
+  uint32_t* sord;
   cx_prefill pf;
 };
 
@@ -975,9 +1036,12 @@ extern "C" void cx_cache_free(cx_cache* c) {
   (void)hipSetDevice(c->m->device);
   (void)hipStreamSynchronize(c->m->stream);
   if (c->have_graph) (void)hipGraphExecDestroy(c->exec);
+  if (c->have_graph_s) (void)hipGraphExecDestroy(c->exec_s);
   const cx_prefill& P = c->pf;
-  void* bufs[] = {c->kv, c->hist, c->st, c->pm, c->pl, c->po, c->sc, c->cm, P.x, P.nrm, P.q,
-                  P.k, P.v, P.att, P.g, P.u, P.tmp, P.sc, P.cm, P.scratch};
+  void* bufs[] = {c->kv,   c->hist, c->st,   c->pm,    c->pl,    c->po,  c->sc,    c->cm,
+                  c->sd,   c->spb,  c->spart, c->sordp, c->sord,  P.x,    P.nrm,    P.q,
+                  P.k,     P.v,     P.att,   P.g,      P.u,      P.tmp,  P.sc,     P.cm,
+                  P.scratch};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   delete c;
@@ -1067,8 +1131,9 @@ static int enqueue_step(cx_cache* C) {
 }
 
 // src/forward.rs:495-501: the final rmsnorm and the output projection of the
-// residual m->x, then the argmax, which writes the next token at st->pos + 1
-// (when past the prompt) and advances st->pos
+// residual m->x, then the argmax (or, while sampling, Muestreador::elegir),
+// which writes the next token at st->pos + 1 (when past the prompt) and
+// advances st->pos
 static int enqueue_tail(cx_cache* C) {
   cx_model* m = C->m;
   const cx_config& c = m->cfg;
@@ -1087,11 +1152,17 @@ static int enqueue_tail(cx_cache* C) {
     if ((rc = cx_launch_matmul_f(m->t_out, m->out, c.vocab, D, m->att, 1, m->logits, s)))
       return rc;
   }
+  if (C->sampling)
+    return cx_launch_sample(m->logits, c.vocab, C->sd, C->spb, C->spart, C->sord, C->sordp,
+                            m->amax_out, C->st, C->hist, s);
   return cx_launch_argmax(m->logits, c.vocab, m->apv, m->api, m->amax_out, C->st, C->hist, s);
 }
 
+// the step graph of the current tail (greedy or sampling), captured once
 static int ensure_graph(cx_cache* C) {
-  if (C->have_graph) return CX_OK;
+  bool& have = C->sampling ? C->have_graph_s : C->have_graph;
+  hipGraphExec_t& exec = C->sampling ? C->exec_s : C->exec;
+  if (have) return CX_OK;
   cx_model* m = C->m;
   hipGraph_t g;
   CX_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
@@ -1102,10 +1173,10 @@ static int ensure_graph(cx_cache* C) {
     return rc;
   }
   CX_HIP(e);
-  hipError_t ie = hipGraphInstantiate(&C->exec, g, nullptr, nullptr, 0);
+  hipError_t ie = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
   (void)hipGraphDestroy(g);
   CX_HIP(ie);
-  C->have_graph = true;
+  have = true;
   return CX_OK;
 }
 
@@ -1123,8 +1194,9 @@ static int run_steps(cx_cache* C, size_t prompt_end, size_t steps, float* step_m
     for (auto& e : ev) CX_HIP(hipEventCreate(&e));
     CX_HIP(hipEventRecord(ev[0], m->stream));
   }
+  hipGraphExec_t exec = C->sampling ? C->exec_s : C->exec;
   for (size_t i = 0; i < steps; i++) {
-    CX_HIP(hipGraphLaunch(C->exec, m->stream));
+    CX_HIP(hipGraphLaunch(exec, m->stream));
     if (step_ms) CX_HIP(hipEventRecord(ev[i + 1], m->stream));
   }
   CX_HIP(hipStreamSynchronize(m->stream));
@@ -1310,9 +1382,8 @@ extern "C" int cx_forward(cx_model* m, cx_cache* C, const uint32_t* toks, size_t
   return CX_OK;
 }
 
-extern "C" int cx_generate(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n,
-                           size_t max_new, uint32_t eos, uint32_t* out, size_t* n_out,
-                           float* step_ms) {
+static int generate(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n, size_t max_new,
+                    uint32_t eos, uint32_t* out, size_t* n_out, float* step_ms) {
   CX_REQUIRE(m && C && C->m == m && n_out, "generate: bad arguments");
   CX_REQUIRE(prompt && n > 0, "generate: empty prompt");
   *n_out = 0;
@@ -1346,4 +1417,41 @@ extern "C" int cx_generate(cx_model* m, cx_cache* C, const uint32_t* prompt, siz
   // forwarding it: the cache holds the prompt plus the pushed tokens.
   if (k < made) C->len = start + n + k;
   return CX_OK;
+}
+
+extern "C" int cx_generate(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n,
+                           size_t max_new, uint32_t eos, uint32_t* out, size_t* n_out,
+                           float* step_ms) {
+  return generate(m, C, prompt, n, max_new, eos, out, n_out, step_ms);
+}
+
+static int sampler_buffers(cx_cache* C) {
+  if (C->sd) return CX_OK;
+  const size_t V = C->m->cfg.vocab;
+  // the chains' 16-byte loads may reach 3 floats past the last value
+  if (hipMalloc(&C->sd, sizeof(cx_samp_state)) != hipSuccess ||
+      hipMalloc(&C->spb, (V + 4) * 4) != hipSuccess ||
+      hipMalloc(&C->spart, cx_sample_parts(V) * 4) != hipSuccess ||
+      hipMalloc(&C->sord, V * 4) != hipSuccess || hipMalloc(&C->sordp, (V + 4) * 4) != hipSuccess) {
+    cx_set_error("sample: cannot allocate the sampler's buffers");
+    return CX_ENOMEM;
+  }
+  return CX_OK;
+}
+
+extern "C" int cx_generate_sampled(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n,
+                                   size_t max_new, uint32_t eos, uint64_t seed, float temperature,
+                                   float top_p, uint32_t* out, size_t* n_out, float* step_ms) {
+  // src/sampler.rs:65-66: temperature <= 0 is greedy, with no draw
+  if (temperature <= 0.0f) return generate(m, C, prompt, n, max_new, eos, out, n_out, step_ms);
+  CX_REQUIRE(m && C && C->m == m, "generate: bad arguments");
+  CX_HIP(hipSetDevice(m->device));
+  int rc = sampler_buffers(C);
+  if (rc) return rc;
+  const cx_samp_state h = sampler_state(seed, temperature, top_p);
+  CX_HIP(hipMemcpyAsync(C->sd, &h, sizeof h, hipMemcpyHostToDevice, m->stream));
+  C->sampling = true;
+  rc = generate(m, C, prompt, n, max_new, eos, out, n_out, step_ms);
+  C->sampling = false;
+  return rc;
 }

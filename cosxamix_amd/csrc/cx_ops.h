@@ -15,6 +15,24 @@ struct cx_dstate {
 int cx_launch_set_state(cx_dstate* st, uint32_t pos, uint32_t prompt_end, uint32_t cap,
                         hipStream_t s);
 
+// Device state of the sampler (cx_sample.hip): the Azar state, 1/temperature
+// and top_p set by the host; u, 1/S and the uniform flag written per call.
+struct cx_samp_state {
+  uint64_t azar;
+  float inv, top_p;
+  float u, inv_s;
+  uint32_t uniform, token;
+};
+// floats of the per-block maxima of a vocabulary of n
+size_t cx_sample_parts(size_t n);
+// One Muestreador::elegir with temperature on device logits[n]: pb (n
+// floats), part (cx_sample_parts(n)), ord (n), ordp (n floats) are scratch;
+// the token goes to *out (device, optional) and, with st, to hist[pos + 1]
+// with the position advanced (the token loop's argmax step).
+int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb, float* part,
+                     uint32_t* ord, float* ordp, uint32_t* out, cx_dstate* st, uint32_t* hist,
+                     hipStream_t s);
+
 #define CX_ATT_MAX_TOTAL 16000  // general attention keeps scores in LDS
 // Decode attention holds a head's scores in LDS for caches up to this many
 // tokens (cx_ops.hip) and streams them above it (cx_attn.hip); both paths

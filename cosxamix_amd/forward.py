@@ -145,17 +145,36 @@ class Modelo:
         return lg, am.value
 
     def generar(self, prompt, max_nuevos: int, cache: "Cache", fin: int | None = None,
-                tiempos: bool = False):
-        """Modelo::generar with the greedy sampler. Returns the tokens, and the
-        per-token decode times in ms if `tiempos`."""
+                tiempos: bool = False, muestreador=None):
+        """Modelo::generar (src/forward.rs:533-559): greedy, or with a
+        ``sampler.Muestreador`` (its seed, temperature and top_p; the draws
+        happen on the GPU). Returns the tokens, and the per-token decode times
+        in ms if `tiempos`."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
         out = np.zeros(max(max_nuevos, 1), np.uint32)
         n = C.c_size_t()
         ms = np.zeros(max(max_nuevos, 1), np.float32) if tiempos else None
-        L.check(_lib.cx_generate(self._h, cache._h, p.ctypes.data_as(L._u32p), p.size, max_nuevos,
-                                 0xFFFFFFFF if fin is None else fin, out.ctypes.data_as(L._u32p),
-                                 C.byref(n), ms.ctypes.data_as(L._f32p) if tiempos else None),
-                "generar")
+        eos = 0xFFFFFFFF if fin is None else fin
+        if muestreador is None:
+            L.check(_lib.cx_generate(self._h, cache._h, p.ctypes.data_as(L._u32p), p.size,
+                                     max_nuevos, eos, out.ctypes.data_as(L._u32p), C.byref(n),
+                                     ms.ctypes.data_as(L._f32p) if tiempos else None),
+                    "generar")
+        else:
+            # the sampler's generator as it stands; afterwards it is advanced
+            # by the draws the reference makes: one per token, one more for
+            # the end token, none past the context
+            inicio = cache.largo()
+            L.check(_lib.cx_generate_sampled(self._h, cache._h, p.ctypes.data_as(L._u32p), p.size,
+                                             max_nuevos, eos, muestreador.estado,
+                                             muestreador.temperatura, muestreador.top_p,
+                                             out.ctypes.data_as(L._u32p), C.byref(n),
+                                             ms.ctypes.data_as(L._f32p) if tiempos else None),
+                    "generar")
+            if muestreador.temperatura > 0.0:
+                pasos = min(p.size + max_nuevos, self.cfg.contexto - inicio)
+                hechos = min(max_nuevos, pasos - p.size + 1)
+                muestreador.avanzar(n.value + (1 if n.value < hechos else 0))
         toks = out[: n.value].copy()
         return (toks, ms) if tiempos else toks
 

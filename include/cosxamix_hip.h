@@ -193,6 +193,17 @@ int cx_attention_decode(const float *q, const float *k, const float *v,
  * *out is a DEVICE uint32. */
 int cx_argmax(const float *v, size_t n, uint32_t *out, void *stream);
 
+/* sampler::Muestreador::elegir (src/sampler.rs:61-152) on device logits[n]:
+ * temperature <= 0 is the argmax with no draw; otherwise one draw of the
+ * xorshift64* generator whose state *state (HOST) holds (Azar::siguiente,
+ * src/daiss.rs:330-337; seed it as Azar::con_semilla does: a zero seed is
+ * 0x9E3779B97F4A7C15), the softmax of logits/temperature, and top-p (clamped
+ * to [0, 1]; >= 1 samples the whole vocabulary in index order). *out (HOST)
+ * receives the token. Equal probabilities are ordered by ascending index
+ * (the reference's unstable sort leaves that order unspecified). */
+int cx_sample(const float *logits, size_t n, float temperature, float top_p,
+              uint64_t *state, uint32_t *out, void *stream);
+
 /* ============================================================ GGUF files
  * Host-only (no device work). Gguf::abrir and Pesos (src/gguf.rs:119-436). */
 
@@ -310,6 +321,13 @@ int cx_forward(cx_model *m, cx_cache *c, const uint32_t *toks, size_t t,
 int cx_generate(cx_model *m, cx_cache *c, const uint32_t *prompt, size_t n,
                 size_t max_new, uint32_t eos, uint32_t *out, size_t *n_out,
                 float *step_ms);
+/* Modelo::generar with Muestreador::nuevo(seed, temperature, top_p)
+ * (src/forward.rs:533-559, src/sampler.rs:38-47): as cx_generate, each
+ * token drawn by the sampler on the GPU inside the captured step. */
+int cx_generate_sampled(cx_model *m, cx_cache *c, const uint32_t *prompt,
+                        size_t n, size_t max_new, uint32_t eos, uint64_t seed,
+                        float temperature, float top_p, uint32_t *out,
+                        size_t *n_out, float *step_ms);
 
 #ifdef __cplusplus
 }

@@ -1399,3 +1399,108 @@ int orc_generate(const orc_model *M, const uint32_t *prompt, size_t n,
   free(lg);
   return rc;
 }
+
+/* ------------------------------------------------------------- sampler */
+/* src/sampler.rs:38-47 */
+void orc_sampler_init(orc_sampler *s, uint64_t seed, float temp, float top_p) {
+  orc_azar_seed(&s->azar, seed);
+  s->temp = temp;
+  /* f32::clamp(0, 1): a NaN passes through */
+  s->top_p = top_p < 0.0f ? 0.0f : (top_p > 1.0f ? 1.0f : top_p);
+}
+
+/* f32::total_cmp as an unsigned key: larger key, larger value */
+static uint32_t total_key(float p) {
+  uint32_t b;
+  memcpy(&b, &p, 4);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+static const float *g_sort_p; /* qsort has no context argument */
+/* descending probability (total_cmp), then ascending index */
+static int by_prob_desc(const void *a, const void *b) {
+  const uint32_t i = *(const uint32_t *)a, j = *(const uint32_t *)b;
+  const uint32_t ki = total_key(g_sort_p[i]), kj = total_key(g_sort_p[j]);
+  if (ki != kj) return ki > kj ? -1 : 1;
+  return i < j ? -1 : (i > j);
+}
+
+/* src/sampler.rs:139-152 */
+static uint32_t sample_running(const float *probs, const uint32_t *idx, size_t len,
+                               float u) {
+  float acc = 0.0f;
+  uint32_t last = 0;
+  for (size_t k = 0; k < len; k++) {
+    const uint32_t t = idx ? idx[k] : (uint32_t)k;
+    acc += probs[t];
+    last = t;
+    if (acc > u) return t;
+  }
+  return last;
+}
+
+/* src/sampler.rs:61-125 */
+uint32_t orc_sample(orc_sampler *s, const float *logits, size_t n) {
+  if (n == 0) return 0;
+  if (s->temp <= 0.0f) return orc_argmax(logits, n);
+  const float u = (float)(orc_azar_next(&s->azar) >> 40) / 16777216.0f;
+  float *probs = (float *)malloc(n * 4);
+  uint32_t *ord = (uint32_t *)malloc(n * 4);
+  if (!probs || !ord) {
+    free(probs);
+    free(ord);
+    return 0;
+  }
+  const float inv = 1.0f / s->temp;
+  for (size_t i = 0; i < n; i++) probs[i] = logits[i] * inv;
+  orc_softmax(probs, n, n);
+  uint32_t tok;
+  if (s->top_p >= 1.0f) {
+    tok = sample_running(probs, NULL, n, u);
+  } else {
+    /* the CANDIDATOS = 1024 most probable, sorted (the top k of a total
+     * order are the first k of the full sort), their mass, and the full
+     * order when they fall short */
+    for (size_t i = 0; i < n; i++) ord[i] = (uint32_t)i;
+    g_sort_p = probs;
+    qsort(ord, n, 4, by_prob_desc);
+    const size_t k = n < 1024 ? n : 1024;
+    float masa = 0.0f;
+    for (size_t i = 0; i < k; i++) masa += probs[ord[i]];
+    size_t len = k;
+    if (masa < s->top_p && k < n) len = n;
+    float acc = 0.0f;
+    size_t corte = len;
+    for (size_t i = 0; i < len; i++) {
+      acc += probs[ord[i]];
+      if (acc >= s->top_p) {
+        corte = i + 1;
+        break;
+      }
+    }
+    float total = 0.0f;
+    for (size_t i = 0; i < corte; i++) total += probs[ord[i]];
+    tok = sample_running(probs, ord, corte, u * total);
+  }
+  free(probs);
+  free(ord);
+  return tok;
+}
+
+/* src/forward.rs:533-559 */
+int orc_generate_sampled(const orc_model *M, const uint32_t *prompt, size_t n,
+                         size_t max_new, orc_sampler *s, uint32_t eos,
+                         orc_cache *c, uint32_t *out, size_t *n_out) {
+  float *lg = (float *)malloc(M->cfg.vocab * 4);
+  if (!lg) return -1;
+  *n_out = 0;
+  int rc = orc_forward(M, prompt, n, c, lg);
+  for (size_t i = 0; rc == 0 && i < max_new; i++) {
+    uint32_t t = orc_sample(s, lg, M->cfg.vocab);
+    if (t == eos) break;
+    out[(*n_out)++] = t;
+    if (c->len >= M->cfg.ctx) break;
+    rc = orc_forward(M, &t, 1, c, lg);
+  }
+  free(lg);
+  return rc;
+}

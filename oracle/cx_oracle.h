@@ -176,6 +176,21 @@ int orc_forward(const orc_model *m, const uint32_t *toks, size_t t,
 int orc_generate(const orc_model *m, const uint32_t *prompt, size_t n,
                  size_t max_new, orc_cache *c, uint32_t *out, size_t *n_out);
 
+/* sampler::Muestreador (src/sampler.rs:27-152): temperature and top-p
+ * sampling with Azar. Equal probabilities are ordered by ascending index
+ * (the reference's unstable sort leaves their order unspecified). */
+typedef struct {
+  orc_azar azar;
+  float temp, top_p;
+} orc_sampler;
+void orc_sampler_init(orc_sampler *s, uint64_t seed, float temp, float top_p);
+uint32_t orc_sample(orc_sampler *s, const float *logits, size_t n);
+/* Modelo::generar (src/forward.rs:533-559) with the sampler and an end
+ * token (UINT32_MAX: none) */
+int orc_generate_sampled(const orc_model *m, const uint32_t *prompt, size_t n,
+                         size_t max_new, orc_sampler *s, uint32_t eos,
+                         orc_cache *c, uint32_t *out, size_t *n_out);
+
 const char *orc_last_error(void);
 
 #ifdef __cplusplus

@@ -105,6 +105,11 @@ def _load():
                                   _f32p]),
         "orc_generate": (C.c_int, [C.POINTER(OrcModel), _u32p, C.c_size_t, C.c_size_t,
                                    C.POINTER(OrcCache), _u32p, C.POINTER(C.c_size_t)]),
+        "orc_sampler_init": (None, [C.c_void_p, C.c_uint64, C.c_float, C.c_float]),
+        "orc_sample": (C.c_uint32, [C.c_void_p, _f32p, C.c_size_t]),
+        "orc_generate_sampled": (C.c_int, [C.POINTER(OrcModel), _u32p, C.c_size_t, C.c_size_t,
+                                           C.c_void_p, C.c_uint32, C.POINTER(OrcCache), _u32p,
+                                           C.POINTER(C.c_size_t)]),
         "orc_last_error": (C.c_char_p, []),
     }
     for name, (res, args) in sig.items():
@@ -411,3 +416,35 @@ def ref_row_kernel(r, t: int):
     name = {Q2_K: "cosxamix_q2k_asm", Q3_K: "cosxamix_q3k_completo", Q4_K: "cxref_q4k_row",
             Q5_K: "cosxamix_q5k_asm"}[t]
     return C.cast(getattr(r, name), ROW_KERNEL)
+
+
+class OrcSampler(C.Structure):
+    _fields_ = [("azar", C.c_uint64), ("temp", C.c_float), ("top_p", C.c_float)]
+
+
+class Sampler:
+    """sampler::Muestreador (src/sampler.rs:27-152), restated in C."""
+
+    def __init__(self, seed: int, temp: float, top_p: float):
+        self.s = OrcSampler()
+        lib.orc_sampler_init(C.byref(self.s), seed & (2**64 - 1), temp, top_p)
+
+    @property
+    def state(self) -> int:
+        return self.s.azar
+
+    def choose(self, logits) -> int:
+        x = np.ascontiguousarray(logits, np.float32)
+        return int(lib.orc_sample(C.byref(self.s), _p(x, _f32p), x.size))
+
+
+def generate_sampled(model: "Model", prompt, max_new: int, sampler: Sampler, cache: "Cache",
+                     eos: int = 0xFFFFFFFF):
+    p = np.ascontiguousarray(prompt, np.uint32)
+    out = np.zeros(max(max_new, 1), np.uint32)
+    n = C.c_size_t(0)
+    if lib.orc_generate_sampled(C.byref(model.m), _p(p, _u32p), p.size, max_new,
+                                C.byref(sampler.s), eos, C.byref(cache.c), _p(out, _u32p),
+                                C.byref(n)):
+        raise RuntimeError(err())
+    return out[: n.value]
