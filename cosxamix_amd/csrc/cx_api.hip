@@ -240,8 +240,9 @@ extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, co
     CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
     return cx_launch_matmul_f(type, w, n, k, lhs, m, dst, STREAM(stream));
   }
-  CX_REQUIRE(cx_is_kquant(type), "matmul_auto: type %d has no k-quant path here", type);
-  CX_REQUIRE(k % 256 == 0, "matmul_auto: a row of %zu is not a multiple of the block of 256", k);
+  CX_REQUIRE(cx_has_gemv(type), "matmul_auto: type %d has no quantized path here", type);
+  CX_REQUIRE(k % (size_t)cx_vpb(type) == 0, "matmul_auto: a row of %zu is not a multiple of the block of %d",
+             k, cx_vpb(type));
   CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
   CX_REQUIRE(n < (1u << 31) && k < (1u << 31), "matmul_auto: shape too large");
   if (!m || !n) return CX_OK;
@@ -274,11 +275,12 @@ extern "C" int cx_matmul_multi_1row(const float* x, size_t k, size_t count,
                                     const uint8_t* const* w, const int* types, const size_t* ns,
                                     float* const* dsts, void* stream) {
   CX_REQUIRE(x && w && types && ns && dsts, "multi: null pointer");
-  CX_REQUIRE(k % 256 == 0, "multi: a row of %zu is not a multiple of 256", k);
   // the row quantized once per sub-block size in use (16 and/or 32)
   bool need16 = false, need32 = false;
   for (size_t i = 0; i < count; i++) {
-    CX_REQUIRE(cx_is_kquant(types[i]), "multi: type %d has no k-quant path here", types[i]);
+    CX_REQUIRE(cx_has_gemv(types[i]), "multi: type %d has no quantized path here", types[i]);
+    CX_REQUIRE(k % (size_t)cx_vpb(types[i]) == 0, "multi: a row of %zu is not whole blocks of type %d",
+               k, types[i]);
     (cx_sub(types[i]) == 16 ? need16 : need32) = true;
   }
   QuantScratch q16, q32;
@@ -571,7 +573,8 @@ static size_t tensor_bytes(int t, uint64_t w, uint64_t r) {
 }
 
 // Views of the model's tensors by name (src/forward.rs:210-247), with the
-// shapes and types this path computes: matrices in a GEMV type (Q2_K..Q6_K),
+// shapes and types this path computes: matrices in a GEMV type (Q2_K..Q6_K
+// on widths of whole 256-value blocks, Q8_0/Q5_0 on widths of 32),
 // norms and biases F32, token_embd in any type with a dequantizer, the lm_head
 // a GEMV type or F32/F16 (tied to token_embd when output.weight is absent).
 static int bind_views(cx_model* m) {
@@ -594,7 +597,7 @@ static int bind_views(cx_model* m) {
   const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd;
   CX_REQUIRE(hd == 64 || hd == 128, "model: head_dim %u (the decode attention supports 64 and 128)",
              hd);
-  CX_REQUIRE(D % 256 == 0, "model: dim %u is not a multiple of 256 (k-quant rows)", D);
+  CX_REQUIRE(D % 32 == 0, "model: dim %u is not a multiple of 32", D);
   auto vec = [&](const std::string& n, uint64_t len, bool optional,
                  const float** p) -> int {
     const Tensor* T = find(n);
@@ -612,8 +615,11 @@ static int bind_views(cx_model* m) {
                  int* t) -> int {
     const Tensor* T = find(n);
     CX_REQUIRE(T, "model: missing tensor %s", n.c_str());
-    CX_REQUIRE(cx_is_kquant(T->type), "model: %s is of type %d; the GEMV reads Q2_K..Q6_K",
-               n.c_str(), T->type);
+    CX_REQUIRE(cx_has_gemv(T->type),
+               "model: %s is of type %d; the GEMV reads Q2_K..Q6_K, Q8_0 and Q5_0", n.c_str(),
+               T->type);
+    CX_REQUIRE(w % (uint64_t)cx_vpb(T->type) == 0, "model: %s rows of %llu values are not whole blocks",
+               n.c_str(), (unsigned long long)w);
     CX_REQUIRE(T->dims[0] == w && T->dims[1] == r, "model: %s is %llux%llu, expected %llux%llu",
                n.c_str(), (unsigned long long)T->dims[0], (unsigned long long)T->dims[1],
                (unsigned long long)w, (unsigned long long)r);
@@ -624,7 +630,7 @@ static int bind_views(cx_model* m) {
   const Tensor* G0 = find("blk.0.ffn_gate.weight");
   CX_REQUIRE(G0, "model: missing tensor blk.0.ffn_gate.weight");
   c.ffn = (uint32_t)G0->dims[1];
-  CX_REQUIRE(c.ffn % 256 == 0, "model: ffn %u is not a multiple of 256", c.ffn);
+  CX_REQUIRE(c.ffn % 32 == 0, "model: ffn %u is not a multiple of 32", c.ffn);
   const uint32_t I = c.ffn;
   m->layers.clear();
   int rc;
@@ -650,8 +656,10 @@ static int bind_views(cx_model* m) {
   const Tensor* O = find("output.weight");
   m->tied = O == nullptr;
   if (!O) O = E;
-  CX_REQUIRE(cx_is_kquant(O->type) || O->type == CX_F32 || O->type == CX_F16,
+  CX_REQUIRE(cx_has_gemv(O->type) || O->type == CX_F32 || O->type == CX_F16,
              "model: the output matrix is of type %d (GEMV types or F32/F16)", O->type);
+  CX_REQUIRE(D % (uint32_t)cx_vpb(O->type) == 0, "model: output rows of %u values are not whole blocks",
+             D);
   CX_REQUIRE(O->dims[0] == D && O->dims[1] == c.vocab, "model: output.weight shape");
   m->t_out = O->type;
   m->out = (const uint8_t*)pool_at(m, O->offset);
@@ -707,12 +715,17 @@ extern "C" int cx_model_create_daiss(const cx_config* cfg, int t_lin, int t_down
   CX_REQUIRE(c.layers && c.dim && c.heads && c.kv_heads && c.ffn && c.vocab && c.ctx,
              "model: zero-sized config");
   CX_REQUIRE(c.dim % c.heads == 0 && c.heads % c.kv_heads == 0, "model: heads do not divide");
-  CX_REQUIRE(c.dim % 256 == 0 && c.ffn % 256 == 0, "model: dim and ffn must be multiples of 256");
   CX_REQUIRE(c.dim / c.heads == 64 || c.dim / c.heads == 128,
              "model: head_dim %u (the decode attention supports 64 and 128)", c.dim / c.heads);
-  CX_REQUIRE(cx_is_kquant(t_lin) && cx_is_kquant(t_down) && cx_is_kquant(t_out) &&
-                 t_lin != CX_Q6_K && t_down != CX_Q6_K && t_out != CX_Q6_K,
-             "model: weights must be Q2_K..Q5_K (the quantizers the reference has)");
+  // the quantizers the reference has (src/quant.rs:744-805): Q8_0 on rows of
+  // 32 values, Q2_K..Q5_K on rows of 256 (Config::admite_kquants,
+  // src/daiss.rs:210-220)
+  for (int t : {t_lin, t_down, t_out}) {
+    CX_REQUIRE(t == CX_Q8_0 || (cx_is_kquant(t) && t != CX_Q6_K),
+               "model: weights must be Q8_0 or Q2_K..Q5_K (the quantizers the reference has)");
+    CX_REQUIRE(c.dim % cx_vpb(t) == 0 && c.ffn % cx_vpb(t) == 0,
+               "model: dim %u and ffn %u are not whole blocks of type %d", c.dim, c.ffn, t);
+  }
   cx_model* m = model_new(c);
   if (!m) return CX_EHIP;
   const uint32_t D = c.dim, hd = D / c.heads, kvd = c.kv_heads * hd, I = c.ffn, V = c.vocab;
@@ -1141,7 +1154,7 @@ static int enqueue_tail(cx_cache* C) {
   const uint32_t D = c.dim;
   const cx_qact act{m->xq, m->xe, m->xs};
   int rc;
-  if (cx_is_kquant(m->t_out)) {
+  if (cx_has_gemv(m->t_out)) {
     if ((rc = cx_launch_norm_quant(m->x, m->out_norm, D, c.eps, cx_sub(m->t_out), m->xq, m->xe,
                                    m->xs, s)))
       return rc;

@@ -66,6 +66,11 @@ __host__ __device__ inline int cx_sub(int t) {
 inline bool cx_is_kquant(int t) {
   return t == CX_Q2_K || t == CX_Q3_K || t == CX_Q4_K || t == CX_Q5_K || t == CX_Q6_K;
 }
+// the 32-value block formats without a minimum (Q8_0, Q5_0): GGUF's choice
+// for matrices whose width is not a multiple of 256 (src/gguf.rs:80-82)
+inline bool cx_is_block32(int t) { return t == CX_Q8_0 || t == CX_Q5_0; }
+// every format the GEMV reads: the k-quants and the 32-value blocks
+inline bool cx_has_gemv(int t) { return cx_is_kquant(t) || cx_is_block32(t); }
 
 // ------------------------------------------------------ device helpers
 __device__ inline float cx_h2f(uint32_t h16) {

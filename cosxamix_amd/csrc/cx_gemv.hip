@@ -1,8 +1,10 @@
-// cx_gemv.hip — batch-1 k-quant GEMV for gfx950 (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K).
+// cx_gemv.hip — batch-1 GEMV for gfx950: the k-quants (Q2_K, Q3_K, Q4_K,
+// Q5_K, Q6_K) and the 32-value block formats (Q8_0, Q5_0).
 //
 // y[r] = sum over super-blocks of row r of the reference's fused dot
 // (src/kernels/scalar.rs:132-324, src/kernels/q2k.rs:41-69) against an i8
-// activation quantized beforehand (xq, xe, xs).
+// activation quantized beforehand (xq, xe, xs). Q8_0/Q5_0 rows take the
+// reference's buffer path instead (k_gemv32 below).
 //
 // Data movement. A workgroup owns a tile of R consecutive rows, i.e. one
 // contiguous byte range of the matrix. Its four waves copy that range into
@@ -571,6 +573,150 @@ __global__ __launch_bounds__(256) void k_gemv_reg(GemvParams P) {
   }
 }
 
+// total = 0; total += term_s for s = 0 .. n-1 (any n), in that order
+__device__ inline float row_sum_any(const float* terms, uint32_t n) {
+  float acc = row_sum(terms, n & ~3u);
+  for (uint32_t s = n & ~3u; s < n; s++) acc += terms[s];
+  return acc;
+}
+
+// ------------------------------------------- 32-value blocks (Q8_0, Q5_0)
+// The buffer path of the reference for these formats (ops::matmul_i8_directo
+// and matmul_varias_una_fila, src/ops.rs:310-414, 968-993): the row unpacked
+// to i8 quants and one scale d per 32 values (quant::desempaquetar_i8,
+// src/quant.rs:270-330; no offset term), then kernels::dot_i8_escalado
+// (src/kernels/scalar.rs:95-109):
+//   total = 0; total += (d_b * xe_b) * (f32)E_b   for b = 0, 1, ...
+// with E_b the exact i32 dot of the block's quants and the i8 activation.
+// One lane per (row, block): it reads the block from LDS at any byte offset,
+// forms E_b with v_dot4c_i32_i8 and stores the term; one lane per row adds
+// them in block order.
+template <int T> struct B32;
+
+// Q8_0, 34 B: d (f16) then 32 signed quants
+template <> struct B32<CX_Q8_0> {
+  static constexpr int BPB = 34;
+  __device__ static float dot(const uint8_t* lds, uint32_t off, const int8_t* xb, int& e) {
+    uint32_t dw[1], q[8];
+    lds_words<1>(lds, off, dw);
+    lds_words<8>(lds, off + 2, q);
+    int x[8];
+    act8(xb, x);
+    e = 0;
+#pragma unroll
+    for (int w = 0; w < 8; w++) e = dot4(q[w], x[w], e);
+    return cx_h2f(dw[0] & 0xFFFF);
+  }
+};
+
+// Q5_0, 22 B: d (f16), qh (u32: bit i is the fifth bit of value i), qs (16):
+// value i < 16 is the low nibble of qs[i], value 16 + i the high one;
+// quant = (nibble | fifth bit << 4) - 16
+template <> struct B32<CX_Q5_0> {
+  static constexpr int BPB = 22;
+  __device__ static float dot(const uint8_t* lds, uint32_t off, const int8_t* xb, int& e) {
+    uint32_t hw[2], qs[4];
+    lds_words<2>(lds, off, hw);
+    lds_words<4>(lds, off + 6, qs);
+    const uint32_t qh = (hw[0] >> 16) | (hw[1] << 16);
+    int x[8];
+    act8(xb, x);
+    e = 0;
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+      const uint32_t nib = w < 4 ? (qs[w] & M4) : ((qs[w - 4] >> 4) & M4);
+      const uint32_t t = (qh >> (4 * w)) & 0xFu;  // fifth bits of values 4w..4w+3
+      const uint32_t hi = ((t & 1u) << 4) | ((t & 2u) << 11) | ((t & 4u) << 18) | ((t & 8u) << 25);
+      // (u - 16) in every byte, u in 0..31: bias by 128 so no byte borrows
+      const uint32_t v = (((nib | hi) | 0x80808080u) - 0x10101010u) ^ 0x80808080u;
+      e = dot4(v, x[w], e);
+    }
+    return cx_h2f(hw[0] & 0xFFFF);
+  }
+};
+
+template <int T, bool NORM>
+__global__ __launch_bounds__(256) void k_gemv32(GemvParams P) {
+  using Q = B32<T>;
+  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ double red[4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t tile = blockIdx.x;
+  int sg = 0;
+  while (tile >= P.tile_end[sg]) sg++;
+  if (sg) tile -= P.tile_end[sg - 1];
+  const cx_seg S = P.seg[sg];
+  const uint32_t row0 = tile * P.R;
+  const uint32_t rows = min(P.R, S.rows - row0);
+  int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
+  float* se = reinterpret_cast<float*>(lds + P.lds_scale);
+  float* ss = se + P.nsub;
+  float* sx = reinterpret_cast<float*>(lds + P.lds_norm);
+
+  // 1. the rmsnorm input (if any), the tile's rows (`skew` bytes into LDS:
+  //    34- and 22-byte blocks leave rows at any even offset) and the
+  //    quantized activation, by direct loads; xe by ordinary loads
+  if (NORM) {
+    copy_to_lds(P.nx, sx, P.k / 4, wave, lane);
+    copy_to_lds(P.nw, sx + P.k, P.k / 4, wave, lane);
+  }
+  const uint8_t* src = S.w + (size_t)row0 * P.row_bytes;
+  const uint32_t skew = (uint32_t)((uintptr_t)src & 15u);
+  const uint32_t ntile =
+      copy_to_lds(src - skew, lds, (skew + rows * P.row_bytes + 15) >> 4, wave, lane);
+  if (!NORM) {
+    copy_to_lds(P.act.xq, sq, P.k / 16, wave, lane);
+    for (uint32_t i = tid; i < P.nsub; i += 256) se[i] = P.act.xe[i];
+  } else {
+    // rmsnorm then quantization, as k_gemv's prologue (the same f64 tree)
+    wait_all_but(ntile);
+    cx_barrier();
+    const float* sw = sx + P.k;
+    double sum = 0.0;
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048)
+#pragma unroll
+      for (int j = 0; j < 8; j++) sum += (double)sx[i + j] * (double)sx[i + j];
+    sum = cx_wave_sum_d(sum);
+    if (lane == 0) red[wave] = sum;
+    cx_wait_lds();
+    cx_barrier();
+    const double tot = ((red[0] + red[1]) + red[2]) + red[3];
+    const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = (float)((double)sx[i + j] * scale) * sw[i + j];
+      cx_quant8<32>(v, i, sq, se, ss);
+    }
+  }
+  cx_wait_vm<0>();
+  cx_wait_lds();
+  __syncthreads();
+
+  // 2. one (row, block) a lane: E_b exactly, then (d_b * xe_b) * E_b
+  float* terms = reinterpret_cast<float*>(lds + P.lds_terms);
+  const uint32_t items = rows * P.nsub;
+  for (uint32_t it = tid; it < items; it += 256) {
+    const uint32_t r = it / P.nsub, b = it - r * P.nsub;
+    int e;
+    const float d = Q::dot(lds, skew + r * P.row_bytes + b * Q::BPB, sq + 32 * b, e);
+    if (P.dbg) P.dbg[(size_t)(row0 + r) * P.nsub + b] = e;
+    terms[r * P.tstride + b] = d * se[b] * (float)e;
+  }
+  __syncthreads();
+
+  // 3. the row's sum in block order from 0 (src/kernels/scalar.rs:97-107)
+  if ((uint32_t)tid < rows) {
+    const float acc = row_sum_any(terms + tid * P.tstride, P.nsub);
+    const uint32_t row = row0 + tid;
+    if (P.epi == CX_EPI_ACCUM)
+      S.y[row] += acc;
+    else
+      S.y[row] = S.bias ? acc + S.bias[row] : acc;
+  }
+}
+
 struct TilePlan {
   uint32_t R, tiles, lds, lds_act, lds_scale, lds_terms, lds_norm;
 };
@@ -644,9 +790,66 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   return CX_OK;
 }
 
+// LDS of a 32-value-block tile: [16 skew + R*row_bytes + 16 pad] [xq, k
+// bytes] [xe, xs] then the rmsnorm input (2k floats) or the terms
+// (R x (nsub+4))
+TilePlan plan_tile32(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
+                     const uint32_t* rows, int nseg, bool norm) {
+  TilePlan t{};
+  t.R = R;
+  for (int i = 0; i < nseg; i++) t.tiles += (rows[i] + R - 1) / R;
+  t.lds_act = (16 + R * row_bytes + 16 + 15) / 16 * 16;
+  t.lds_scale = t.lds_act + (k + 15) / 16 * 16;
+  t.lds_terms = t.lds_scale + (8 * nsub + 15) / 16 * 16;
+  t.lds_norm = t.lds_terms;
+  const uint32_t terms = 4 * R * (nsub + 4), nin = norm ? 8 * k : 0;
+  t.lds = t.lds_terms + (terms > nin ? terms : nin);
+  return t;
+}
+
+template <int T, bool NORM>
+int launch_b32(GemvParams& P, const uint32_t* rows, hipStream_t s) {
+  uint32_t total_rows = 0;
+  for (int i = 0; i < P.nseg; i++) total_rows += rows[i];
+  // the k-quant GEMV's tile choice: with the prologue one or two tiles per
+  // CU, otherwise the largest R <= 16 that leaves >= 2 tiles per CU
+  TilePlan best{};
+  if (NORM) {
+    for (uint32_t per_cu = 1; per_cu <= 8 && !best.R; per_cu *= 2) {
+      uint32_t R = (total_rows + 256 * per_cu - 1) / (256 * per_cu);
+      R = R < 1 ? 1 : (R > 64 ? 64 : R);
+      TilePlan t = plan_tile32(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM);
+      if (t.lds <= TILE_LDS_NORM_MAX) best = t;
+    }
+  } else {
+    for (uint32_t R = 16; R >= 1; R >>= 1) {
+      TilePlan t = plan_tile32(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM);
+      if (t.lds > TILE_LDS_MAX) continue;
+      best = t;
+      if (t.tiles >= 512) break;
+    }
+  }
+  CX_REQUIRE(best.R, "gemv: a row of %u values does not fit in LDS", P.k);
+  P.R = best.R;
+  P.lds_act = best.lds_act;
+  P.lds_scale = best.lds_scale;
+  P.lds_terms = best.lds_terms;
+  P.lds_norm = best.lds_norm;
+  uint32_t acc = 0;
+  for (int i = 0; i < P.nseg; i++) {
+    acc += (rows[i] + best.R - 1) / best.R;
+    P.tile_end[i] = acc;
+  }
+  hipLaunchKernelGGL((k_gemv32<T, NORM>), dim3(best.tiles), dim3(256), best.lds, s, P);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
 template <bool NORM>
 int launch_type(int type, GemvParams& P, const uint32_t* rows, hipStream_t s) {
   switch (type) {
+    case CX_Q8_0: return launch_b32<CX_Q8_0, NORM>(P, rows, s);
+    case CX_Q5_0: return launch_b32<CX_Q5_0, NORM>(P, rows, s);
     case CX_Q2_K: return launch_t<CX_Q2_K, NORM>(P, rows, s);
     case CX_Q3_K: return launch_t<CX_Q3_K, NORM>(P, rows, s);
     case CX_Q4_K: return launch_t<CX_Q4_K, NORM>(P, rows, s);
@@ -660,8 +863,9 @@ int launch_type(int type, GemvParams& P, const uint32_t* rows, hipStream_t s) {
 int gemv_setup(int type, const cx_seg* segs, int nseg, uint32_t k, int epi, int32_t* dbg,
                GemvParams& P, uint32_t* rows, uint32_t* total) {
   CX_REQUIRE(nseg >= 1 && nseg <= 4, "gemv: 1..4 matrices per launch");
-  CX_REQUIRE(cx_is_kquant(type), "gemv: type %d has no fused GEMV", type);
-  CX_REQUIRE(k > 0 && k % 256 == 0, "gemv: k=%u is not a multiple of 256", k);
+  CX_REQUIRE(cx_has_gemv(type), "gemv: type %d has no GEMV", type);
+  const uint32_t vpb = (uint32_t)cx_vpb(type);
+  CX_REQUIRE(k > 0 && k % vpb == 0, "gemv: k=%u is not a multiple of %u", k, vpb);
   CX_REQUIRE(!dbg || nseg == 1, "gemv: sub-block sums need a single matrix");
   *total = 0;
   int n = 0;
@@ -675,7 +879,7 @@ int gemv_setup(int type, const cx_seg* segs, int nseg, uint32_t k, int epi, int3
   }
   P.nseg = n;
   P.k = k;
-  P.nb = k / 256;
+  P.nb = k / vpb;
   P.nsub = k / cx_sub(type);
   P.row_bytes = P.nb * cx_bpb(type);
   P.tstride = P.nsub + 4;
@@ -689,9 +893,11 @@ int gemv_setup(int type, const cx_seg* segs, int nseg, uint32_t k, int epi, int3
 int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k, const cx_qact& act,
                    int epi, int32_t* dbg, hipStream_t s) {
   CX_REQUIRE(act.xq && act.xe && act.xs, "gemv: missing quantized activation");
-  CX_REQUIRE(((uintptr_t)act.xq & 15u) == 0 && ((uintptr_t)act.xe & 15u) == 0 &&
-                 ((uintptr_t)act.xs & 15u) == 0,
-             "gemv: xq, xe and xs must be 16-byte aligned");
+  // the 32-value block kernel reads xe with ordinary loads (and no xs)
+  const uintptr_t ealign = cx_is_block32(type) ? 3u : 15u;
+  CX_REQUIRE(((uintptr_t)act.xq & 15u) == 0 && ((uintptr_t)act.xe & ealign) == 0 &&
+                 ((uintptr_t)act.xs & ealign) == 0,
+             "gemv: xq must be 16-byte aligned, xe and xs %d-byte", (int)ealign + 1);
   GemvParams P{};
   uint32_t rows[4], total;
   int rc = gemv_setup(type, segs, nseg, k, epi, dbg, P, rows, &total);
@@ -864,7 +1070,8 @@ int cx_launch_swiglu_quant(const float* g, const float* u, size_t n, int sub, in
 int cx_launch_norm_quant(const float* x, const float* w, size_t n, float eps, int sub,
                          int8_t* xq, float* xe, float* xs, hipStream_t s) {
   CX_REQUIRE(sub == 16 || sub == 32, "norm: sub must be 16 or 32, got %d", sub);
-  CX_REQUIRE(n % 256 == 0 && n < (1u << 31), "norm: width %zu must be a multiple of 256", n);
+  CX_REQUIRE(n % (size_t)sub == 0 && n < (1u << 31), "norm: width %zu must be whole sub-blocks of %d",
+             n, sub);
   if (sub == 16)
     hipLaunchKernelGGL(k_norm_quant<16>, dim3(1), dim3(256), 0, s, x, w, (uint32_t)n, eps, xq, xe, xs);
   else

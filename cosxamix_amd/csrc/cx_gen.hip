@@ -376,6 +376,23 @@ __global__ __launch_bounds__(64) void k_quant_blocks(const float* x, size_t nblo
   if (T == CX_Q5_K) block_q5k(xb, out + b * 176);
 }
 
+// quant::cuantizar_bloques for Q8_0 (src/quant.rs:765-780), one 32-value
+// block a lane: d = max|x| / 127 stored as f16, the quants made with the
+// scale as it will be read back, round half away, clamped to [-127, 127]
+__global__ __launch_bounds__(64) void k_quant_q8_0(const float* x, size_t nblocks, uint8_t* out) {
+  const size_t b = blockIdx.x * 64ull + threadIdx.x;
+  if (b >= nblocks) return;
+  const float* c = x + b * 32;
+  uint8_t* o = out + b * 34;
+  float amax = 0.0f;
+  for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(c[j]));
+  const uint16_t h = f32_to_f16(amax / 127.0f);
+  put16(o, h);
+  const float read = f16_to_f32(h);
+  const float inv = read > 0.0f ? 1.0f / read : 0.0f;
+  for (int j = 0; j < 32; j++) o[2 + j] = (uint8_t)(int8_t)clampi(entero(c[j] * inv), -127, 127);
+}
+
 }  // namespace
 
 uint64_t cx_fnv_name(const char* name) {
@@ -405,6 +422,14 @@ int cx_gen_fill(float* out, size_t n, float v, hipStream_t s) {
 }
 
 int cx_quantize_blocks_dev(int type, const float* x, size_t n, uint8_t* out, hipStream_t s) {
+  if (type == CX_Q8_0) {
+    CX_REQUIRE(n % 32 == 0, "quantize_blocks: %zu values are not whole blocks of 32", n);
+    const size_t nb = n / 32;
+    if (!nb) return CX_OK;
+    hipLaunchKernelGGL(k_quant_q8_0, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, s, x, nb, out);
+    CX_HIP(hipGetLastError());
+    return CX_OK;
+  }
   CX_REQUIRE(n % 256 == 0, "quantize_blocks: %zu values are not whole blocks", n);
   const size_t nb = n / 256;
   if (!nb) return CX_OK;

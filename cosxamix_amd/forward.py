@@ -43,6 +43,9 @@ class Config:
                           self.contexto, self.eps, self.rope)
 
 
+# daiss-0.5b (src/daiss.rs:91-102): dim 896 is 3.5 blocks of 256, so its
+# matrices are Q8_0 (the reference's writer) or Q5_0 (real Qwen2.5-0.5B GGUFs)
+DAISS_0_5B = Config(24, 896, 14, 2, 4864, 151936, 32768, 1e-6, 1_000_000.0)
 # daiss-3b (src/daiss.rs:103-114) = the Qwen2.5-3B shape of the benchmark
 DAISS_3B = Config(36, 2048, 16, 2, 11008, 151936, 32768, 1e-6, 1_000_000.0)
 # Llama-3-8B shape written as a qwen2-architecture model (zero biases)

@@ -95,7 +95,11 @@ int cx_quantize_act(const float *x, size_t rows, size_t k, int sub,
 
 /* y[r] = row r of W (n rows, GGUF raw bytes) . activation, for r < n.
  * The per-row fused dot of ops::matmul_i8_fusionado with m = 1
- * (src/ops.rs:435-522). Q2_K, Q3_K, Q4_K, Q5_K, Q6_K. */
+ * (src/ops.rs:435-522) for Q2_K, Q3_K, Q4_K, Q5_K, Q6_K (k % 256 == 0);
+ * for Q8_0 and Q5_0 (k % 32 == 0) the buffer path of
+ * ops::matmul_i8_directo (src/ops.rs:310-414: desempaquetar_i8, then
+ * kernels::dot_i8_escalado's block-order sum, scalar.rs:95-109). xq 16-byte
+ * aligned; xe/xs 16-byte (k-quants) or 4-byte (Q8_0/Q5_0) aligned. */
 int cx_gemv(int type, const uint8_t *w, size_t n, size_t k, const int8_t *xq,
             const float *xe, const float *xs, float *y, void *stream);
 
@@ -107,10 +111,10 @@ int cx_gemv_subsums(int type, const uint8_t *w, size_t n, size_t k,
                     const int8_t *xq, const float *xe, const float *xs,
                     int32_t *out, void *stream);
 
-/* quant::cuantizar_bloques for the k-quants (src/quant.rs:744-805 ->
- * src/quant_kquants.rs:160-399): n f32 values (n % 256 == 0) -> GGUF blocks,
- * one GPU thread per 256-value block. Q2_K, Q3_K, Q4_K, Q5_K. The same bytes
- * as the reference's quantizers for the same input. */
+/* quant::cuantizar_bloques (src/quant.rs:744-805 ->
+ * src/quant_kquants.rs:160-399): n f32 values (whole blocks) -> GGUF blocks,
+ * one GPU thread per block. Q8_0, Q2_K, Q3_K, Q4_K, Q5_K. The same bytes as
+ * the reference's quantizers for the same input. */
 int cx_quantize_blocks(int type, const float *x, size_t n, uint8_t *out,
                        void *stream);
 
@@ -138,7 +142,8 @@ int cx_unpack_i8(int type, const uint8_t *bytes, size_t n, int8_t *q,
 /* ops::matmul_auto (src/ops.rs:1056-1093): dst[m,n] = lhs[m,k] . W[n,k]^T,
  * lhs/dst f32 row-major, W GGUF raw rows. k-quants: quantizes lhs
  * internally (m = 1: the GEMV; m > 1 of Q4_K/Q5_K: the int8 MFMA
- * contraction; both bit-identical to the row-by-row fused dot). F32/F16
+ * contraction; both bit-identical to the row-by-row fused dot). Q8_0/Q5_0
+ * (k % 32 == 0): the buffer path (matmul_i8_directo), row by row. F32/F16
  * (ops::matmul, src/ops.rs:87-156): f32 dot of each lhs row with the
  * widened weight row, equal to the reference within f32 rounding; k % 4 == 0. */
 int cx_matmul_auto(size_t m, size_t k, size_t n, const float *lhs,

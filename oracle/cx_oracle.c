@@ -1242,17 +1242,89 @@ int orc_matmul_fused(size_t m, size_t k, size_t n, const float *lhs,
   return 0;
 }
 
+/* src/kernels/scalar.rs:95-109 (dot_i8_escalado): per block of `block`
+ * values the exact i32 dot, then total += (esc_a * esc_b) * (f32)dot, in
+ * block order from 0 */
+float orc_dot_i8_scaled(const int8_t *a, const int8_t *b, const float *esc_a,
+                        const float *esc_b, size_t n, int block) {
+  float total = 0.0f;
+  for (size_t i = 0, r = 0; r < n; i++, r += (size_t)block) {
+    size_t to = r + (size_t)block < n ? r + (size_t)block : n;
+    int32_t part = 0;
+    for (size_t j = r; j < to; j++) part += (int32_t)a[j] * (int32_t)b[j];
+    total += esc_a[i] * esc_b[i] * (float)part;
+  }
+  return total;
+}
+
+/* One weight row of the buffer path (src/ops.rs:377-407, 968-993): unpack
+ * the row to (q, scale, offset) per sub-block, the scaled dot, then the
+ * offset term when the format has one. A row that does not unpack is left
+ * at 0. */
+static float direct_row(int type, const uint8_t *row, size_t k, int sub, const int8_t *xq,
+                        const float *xe, const float *xs, int8_t *cq, float *ce, float *cd) {
+  if (orc_unpack_i8(type, row, k, cq, ce, cd) < 0) return 0.0f;
+  size_t nsub = k / (size_t)sub;
+  float total = orc_dot_i8_scaled(cq, xq, ce, xe, k, sub);
+  int has_off = 0;
+  for (size_t b = 0; b < nsub; b++) has_off |= cd[b] != 0.0f;
+  if (has_off)
+    for (size_t b = 0; b < nsub; b++) total += cd[b] * xe[b] * xs[b];
+  return total;
+}
+
+/* src/ops.rs:310-414 (matmul_i8_directo): every format with an i8 unpack
+ * (Q8_0, Q5_0 and the k-quants); the path matmul_auto takes for Q8_0/Q5_0
+ * below its blocked threshold (src/ops.rs:1072-1092) */
+int orc_matmul_direct(size_t m, size_t k, size_t n, const float *lhs, const uint8_t *w,
+                      int type, float *dst, int threads) {
+  int sub = orc_sub_block(type);
+  size_t vpb = orc_values_per_block(type), bpb = orc_bytes_per_block(type);
+  if (!sub || !vpb) { set_err("matmul_direct: type has no i8 unpack"); return -1; }
+  if (k % vpb || k % (size_t)sub) { set_err("matmul_direct: a row is not whole blocks"); return -1; }
+  size_t nsub = k / (size_t)sub, rowb = k / vpb * bpb;
+  act_buf a;
+  if (act_alloc(&a, m, k, sub)) { act_free(&a); set_err("alloc"); return -1; }
+  for (size_t f = 0; f < m; f++)
+    orc_quantize_act(lhs + f * k, k, sub, a.q + f * k, a.e + f * nsub, a.s + f * nsub);
+  size_t tasks = (n + ROWS_PER_TASK - 1) / ROWS_PER_TASK;
+  int err = 0;
+  if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(dynamic) num_threads(threads)
+  for (size_t t = 0; t < tasks; t++) {
+    int8_t *cq = (int8_t *)malloc(k);
+    float *ce = (float *)malloc(nsub * 4), *cd = (float *)malloc(nsub * 4);
+    if (!cq || !ce || !cd) {
+      err = 1;
+    } else {
+      size_t r0 = t * ROWS_PER_TASK, r1 = r0 + ROWS_PER_TASK;
+      if (r1 > n) r1 = n;
+      for (size_t r = r0; r < r1; r++)
+        for (size_t f = 0; f < m; f++)
+          dst[f * n + r] = direct_row(type, w + r * rowb, k, sub, a.q + f * k, a.e + f * nsub,
+                                      a.s + f * nsub, cq, ce, cd);
+    }
+    free(cq); free(ce); free(cd);
+  }
+  act_free(&a);
+  if (err) { set_err("matmul_direct: alloc"); return -1; }
+  return 0;
+}
+
 /* src/ops.rs:895-1009 (matmul_varias_una_fila) — one activation quantization
- * per sub size, then every 32-row task of every matrix in one region. */
+ * per sub size, then every 32-row task of every matrix in one region: the
+ * fused row kernel where the format has one (src/ops.rs:950-966), the
+ * buffer path otherwise (968-993). */
 int orc_matmul_multi_1row(const float *x, size_t k, size_t count,
                           const uint8_t *const *ws, const int *types,
                           const size_t *ns, float *const *dsts, int threads) {
-  if (k % 256) { set_err("multi: k"); return -1; }
   act_buf a16 = {0}, a32 = {0};
   int need16 = 0, need32 = 0;
   for (size_t i = 0; i < count; i++) {
     int s = orc_sub_block(types[i]);
-    if (!orc_row_kernel_for(types[i])) { set_err("multi: type"); return -1; }
+    size_t vpb = orc_values_per_block(types[i]);
+    if (!s || !vpb) { set_err("multi: type"); return -1; }
+    if (k % vpb || k % (size_t)s) { set_err("multi: a row is not whole blocks"); return -1; }
     if (s == 16) need16 = 1; else need32 = 1;
   }
   if (need16) { act_alloc(&a16, 1, k, 16); orc_quantize_act(x, k, 16, a16.q, a16.e, a16.s); }
@@ -1267,12 +1339,23 @@ int orc_matmul_multi_1row(const float *x, size_t k, size_t count,
       tt -= (ns[i] + ROWS_PER_TASK - 1) / ROWS_PER_TASK;
       i++;
     }
-    const act_buf *a = orc_sub_block(types[i]) == 16 ? &a16 : &a32;
-    orc_row_kernel kern = orc_row_kernel_for(types[i]);
-    size_t rowb = k / 256 * orc_bytes_per_block(types[i]);
+    const int sub = orc_sub_block(types[i]);
+    const act_buf *a = sub == 16 ? &a16 : &a32;
+    orc_row_kernel kern = k % 256 == 0 ? orc_row_kernel_for(types[i]) : NULL;
+    size_t rowb = k / orc_values_per_block(types[i]) * orc_bytes_per_block(types[i]);
     size_t r0 = tt * ROWS_PER_TASK, r1 = r0 + ROWS_PER_TASK;
     if (r1 > ns[i]) r1 = ns[i];
-    for (size_t r = r0; r < r1; r++) dsts[i][r] = kern(ws[i] + r * rowb, a->q, a->e, a->s, k / 256);
+    if (kern) {
+      for (size_t r = r0; r < r1; r++) dsts[i][r] = kern(ws[i] + r * rowb, a->q, a->e, a->s, k / 256);
+      continue;
+    }
+    size_t nsub = k / (size_t)sub;
+    int8_t *cq = (int8_t *)malloc(k);
+    float *ce = (float *)malloc(nsub * 4), *cd = (float *)malloc(nsub * 4);
+    if (cq && ce && cd)
+      for (size_t r = r0; r < r1; r++)
+        dsts[i][r] = direct_row(types[i], ws[i] + r * rowb, k, sub, a->q, a->e, a->s, cq, ce, cd);
+    free(cq); free(ce); free(cd);
   }
   if (need16) act_free(&a16);
   if (need32) act_free(&a32);
@@ -1325,7 +1408,13 @@ void orc_cache_truncate(orc_cache *c, size_t n) { if (n < c->len) c->len = n; }
 static int proj(const orc_model *M, const float *x, size_t t, size_t k, size_t n,
                 const uint8_t *w, int type, const float *bias, float *dst) {
   orc_row_kernel kern = M->kern_override && type == ORC_Q4_K ? M->kern_override : NULL;
-  if (orc_matmul_fused(t, k, n, x, w, type, dst, kern, M->threads, 2)) return -1;
+  /* matmul_auto (src/ops.rs:1056-1093): the fused row kernel for the
+   * k-quants, the buffer path for Q8_0/Q5_0 */
+  if (orc_row_kernel_for(type) && k % 256 == 0) {
+    if (orc_matmul_fused(t, k, n, x, w, type, dst, kern, M->threads, 2)) return -1;
+  } else if (orc_matmul_direct(t, k, n, x, w, type, dst, M->threads)) {
+    return -1;
+  }
   if (bias)
     for (size_t r = 0; r < t; r++)
       for (size_t i = 0; i < n; i++) dst[r * n + i] += bias[i];

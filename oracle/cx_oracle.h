@@ -129,6 +129,10 @@ int orc_matmul_fused(size_t m, size_t k, size_t n, const float *lhs,
                      const uint8_t *w, int type, float *dst,
                      orc_row_kernel kern, int threads, int prefetch);
 /* src/ops.rs:895-1009 (matmul_varias_una_fila) */
+float orc_dot_i8_scaled(const int8_t *a, const int8_t *b, const float *esc_a,
+                        const float *esc_b, size_t n, int block);
+int orc_matmul_direct(size_t m, size_t k, size_t n, const float *lhs, const uint8_t *w,
+                      int type, float *dst, int threads);
 int orc_matmul_multi_1row(const float *x, size_t k, size_t count,
                           const uint8_t *const *ws, const int *types,
                           const size_t *ns, float *const *dsts, int threads);

@@ -93,6 +93,8 @@ def _load():
         "orc_attention": (C.c_int, [_f32p, _f32p, _f32p] + [C.c_size_t] * 5 + [_f32p]),
         "orc_matmul_fused": (C.c_int, [C.c_size_t] * 3 + [_f32p, _u8p, C.c_int, _f32p,
                                                           C.c_void_p, C.c_int, C.c_int]),
+        "orc_matmul_direct": (C.c_int, [C.c_size_t] * 3 + [_f32p, _u8p, C.c_int, _f32p, C.c_int]),
+        "orc_dot_i8_scaled": (C.c_float, [_i8p, _i8p, _f32p, _f32p, C.c_size_t, C.c_int]),
         "orc_matmul_multi_1row": (C.c_int, [_f32p, C.c_size_t, C.c_size_t, C.POINTER(_u8p),
                                             C.POINTER(C.c_int), C.POINTER(C.c_size_t),
                                             C.POINTER(_f32p), C.c_int]),
@@ -223,6 +225,18 @@ def matmul_fused(t: int, lhs: np.ndarray, w: np.ndarray, n: int, threads: int = 
     kp = C.cast(kernel, C.c_void_p) if kernel is not None else None
     if lib.orc_matmul_fused(m, k, n, _p(lhs, _f32p), _p(w, _u8p), t, _p(dst, _f32p), kp,
                             threads, prefetch):
+        raise ValueError(err())
+    return dst
+
+
+def matmul_direct(t: int, lhs: np.ndarray, w: np.ndarray, n: int, threads: int = 1) -> np.ndarray:
+    """dst[m, n] = lhs[m, k] . W^T by the buffer path (ops::matmul_i8_directo,
+    src/ops.rs:310-414): Q8_0, Q5_0 and the k-quants."""
+    lhs = np.ascontiguousarray(lhs, dtype=np.float32)
+    m, k = lhs.shape if lhs.ndim == 2 else (1, lhs.size)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    dst = np.zeros((m, n), dtype=np.float32)
+    if lib.orc_matmul_direct(m, k, n, _p(lhs, _f32p), _p(w, _u8p), t, _p(dst, _f32p), threads):
         raise ValueError(err())
     return dst
 

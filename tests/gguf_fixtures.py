@@ -48,11 +48,22 @@ def q6k_bytes(rows, width, seed):
     return b.reshape(rows, -1)
 
 
-def mixed_model(seed=5, override=None, ctx=None):
-    """A 2-layer qwen2 GGUF: per-tensor k-quant types (overridable), a Q4_K
-    token_embd tied to the lm_head, q/k/v biases in layer 0 only. Returns
-    (file bytes, host tensors by name, types by name)."""
-    c = dict(MINI, ctx=ctx or MINI["ctx"])
+def q5_0_bytes(rows, width, seed):
+    """Q5_0 rows with any quants and small finite scales (the reference has
+    no Q5_0 quantizer)."""
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (rows * width // 32, 22), dtype=np.uint8)
+    h = rng.integers(0x1000, 0x1800, rows * width // 32)
+    b[:, 0], b[:, 1] = h & 0xFF, h >> 8
+    return b.reshape(rows, -1)
+
+
+def mixed_model(seed=5, override=None, ctx=None, shape=None, embd=None):
+    """A 2-layer qwen2 GGUF: per-tensor types (k-quants by default,
+    overridable), a token_embd (Q4_K by default) tied to the lm_head, q/k/v
+    biases in layer 0 only. `shape` overrides MINI's dims. Returns (file
+    bytes, host tensors by name, types by name)."""
+    c = dict(MINI, ctx=ctx or MINI["ctx"], **(shape or {}))
     D, I, V = c["dim"], c["ffn"], c["vocab"]
     kvd = c["kv_heads"] * D // c["heads"]
     rng = np.random.default_rng(seed)
@@ -61,6 +72,8 @@ def mixed_model(seed=5, override=None, ctx=None):
     def quant(name, t, rows, width, sigma):
         if t == O.Q6_K:
             b = q6k_bytes(rows, width, seed + len(host))
+        elif t == O.Q5_0:
+            b = q5_0_bytes(rows, width, seed + len(host))
         else:
             b = O.daiss_matrix(seed, name, rows, width, sigma, t)
         host[name], types[name] = b, t
@@ -71,7 +84,7 @@ def mixed_model(seed=5, override=None, ctx=None):
         host[name], types[name] = v, O.F32
         gg.append((name, [n], O.F32, v.tobytes()))
 
-    quant("token_embd.weight", O.Q4_K, V, D, 1.0)
+    quant("token_embd.weight", embd or O.Q4_K, V, D, 1.0)
     mats = {"attn_q": O.Q4_K, "attn_k": O.Q5_K, "attn_v": O.Q6_K, "attn_output": O.Q3_K,
             "ffn_gate": O.Q4_K, "ffn_up": O.Q5_K, "ffn_down": O.Q6_K}
     mats.update(override or {})
@@ -100,16 +113,16 @@ def mixed_model(seed=5, override=None, ctx=None):
     return gguf_bytes(meta, gg), host, types
 
 
-def oracle_of(host, types, ctx=None):
+def oracle_of(host, types, ctx=None, shape=None):
     """The oracle forward of the mixed model: embedding dequantized to f32,
     the tied lm_head as token_embd's bytes, zero biases where absent."""
-    c = dict(MINI, ctx=ctx or MINI["ctx"])
+    c = dict(MINI, ctx=ctx or MINI["ctx"], **(shape or {}))
     D, kvd = c["dim"], c["kv_heads"] * c["dim"] // c["heads"]
     t = dict(host)
     ty = dict(types)
-    emb = host["token_embd.weight"]
-    t["token_embd.weight"] = O.dequantize(O.Q4_K, emb.reshape(-1), c["vocab"] * D)
-    t["output.weight"], ty["output.weight"] = emb, O.Q4_K
+    emb, et = host["token_embd.weight"], types["token_embd.weight"]
+    t["token_embd.weight"] = O.dequantize(et, emb.reshape(-1), c["vocab"] * D)
+    t["output.weight"], ty["output.weight"] = emb, et
     for i in range(c["layers"]):
         for b, n in (("attn_q.bias", D), ("attn_k.bias", kvd), ("attn_v.bias", kvd)):
             t.setdefault(f"blk.{i}.{b}", np.zeros(n, np.float32))

@@ -83,4 +83,12 @@ def test_argument_errors_are_reported_not_crashed(L):
     cfg = L.CxConfig(1, 100, 4, 2, 768, 10, 64, 1e-6, 1e4)
     h = C.c_void_p()
     assert lib.cx_model_create_daiss(C.byref(cfg), O.Q4_K, O.Q4_K, O.Q4_K, 1, C.byref(h)) == -1
-    assert "256" in L.last_error()
+    assert "head_dim" in L.last_error()
+    # daiss-0.5b's dim of 896 is 3.5 blocks of 256: k-quants refused (Q8_0 is its type)
+    cfg = L.CxConfig(1, 896, 14, 2, 4864, 10, 64, 1e-6, 1e4)
+    assert lib.cx_model_create_daiss(C.byref(cfg), O.Q4_K, O.Q4_K, O.Q4_K, 1, C.byref(h)) == -1
+    assert "whole blocks" in L.last_error()
+    assert lib.cx_model_create_daiss(C.byref(cfg), O.Q6_K, O.Q6_K, O.Q6_K, 1, C.byref(h)) == -1
+    assert "quantizers" in L.last_error()
+    assert lib.cx_matmul_auto(1, 100, 4, p, p, O.Q8_0, p, None) == -1
+    assert "32" in L.last_error()

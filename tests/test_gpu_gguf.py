@@ -88,10 +88,14 @@ def test_files_the_path_cannot_run_are_refused(F, tmp_path):
     p.write_bytes(cut)
     with pytest.raises(ValueError, match="ffn_up"):
         F.Modelo.abrir(p)
-    # a matrix in a type the GEMV does not read (Q8_0)
+    # a matrix in a type the reference cannot unpack either (Q4_0): the Q8_0
+    # file with the type id changed, its 34-byte blocks read as 18-byte ones
     data, _, _ = mixed_model(seed=9, override={"attn_output": O.Q8_0})
-    p2 = tmp_path / "q8.gguf"
-    p2.write_bytes(data)
+    name = b"blk.0.attn_output.weight"
+    i = data.index(name) + len(name) + 4 + 16  # n_dims, two dims: the type
+    assert struct.unpack("<I", data[i:i + 4])[0] == O.Q8_0
+    p2 = tmp_path / "q4_0.gguf"
+    p2.write_bytes(data[:i] + struct.pack("<I", 2) + data[i + 4:])
     with pytest.raises(ValueError, match="attn_output"):
         F.Modelo.abrir(p2)
     # a matrix of the wrong shape: ffn_up declared with one row less
