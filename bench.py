@@ -23,6 +23,10 @@ Batched (the "batched" object): Q4_K 11008 x 2048 and
 2048 x 11008 times m = 8, 32, 512 activation rows through cx_matmul_auto
 (int8 MFMA), against the reference's per-row CPU matmul.
 
+Q8_0 (the "decode_0_5b_q8_0" object): daiss-0.5b, whose 896-wide matrices
+only the 32-value block formats can hold, written in Q8_0 and decoded by the
+same loop.
+
 Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--no-cpu]
        python bench.py --batched-only
        python bench.py --trace-summary gpurun_out/.../kernel_trace.csv
@@ -133,6 +137,34 @@ def config5_bench(F, L, steps=256, warmup=8, prefix=8192):
     log(f"[bench] config 5: prefill {prefix} tokens {prefill_s:.2f}s; {steps} tokens at "
         f"{out['tok_per_s']} tok/s ({out['median_us_per_token']} us median), "
         f"{out['effective_GBps']} GB/s effective")
+    m.close()
+    return out
+
+
+def small_model_bench(F, L, steps=128, warmup=8, prompt_len=512):
+    """daiss-0.5b (src/daiss.rs:91-102: dim 896, 24 layers, 14/2 heads of
+    64, SwiGLU 4864) written in Q8_0, the reference writer's type: every
+    matrix is 896 or 4864 values wide and runs the Q8_0 GEMV. Same loop as
+    the headline: 512-token prompt, `warmup` untimed tokens, `steps` timed."""
+    cfg = F.DAISS_0_5B
+    m = F.Modelo(cfg, tipo=L.Q8_0, semilla=42)
+    prompt = prompt_tokens(prompt_len, cfg.vocab)
+    cache = m.nueva_cache(prompt_len + warmup + steps + 1)
+    toks, ms = m.generar(prompt, warmup + steps, cache, tiempos=True)
+    timed = [float(v) for v in ms[warmup:warmup + steps]]
+    total = sum(timed) * 1e-3
+    w = m.bytes_por_token()
+    kv = 2 * cfg.capas * cfg.dim_kv() * 4 * (prompt_len + warmup + steps // 2)
+    out = {"workload": "daiss-0.5b (24 layers, hidden 896, 14/2 heads x 64, SwiGLU 4864, vocab "
+                       "151936), every matrix Q8_0 (896- and 4864-wide rows), f32 KV cache, "
+                       "512-token seeded prompt, greedy decode",
+           "decode_tokens": steps, "tok_per_s": round(steps / total, 2),
+           "median_us_per_token": round(statistics.median(timed) * 1000, 2),
+           "weight_bytes_per_token": w,
+           "effective_GBps": round((w + kv) / (total / steps) / 1e9, 1),
+           "first_tokens": [int(t) for t in toks[:8]]}
+    log(f"[bench] daiss-0.5b Q8_0: {out['tok_per_s']} tok/s ({out['median_us_per_token']} us "
+        f"median), {out['effective_GBps']} GB/s effective")
     m.close()
     return out
 
@@ -468,6 +500,8 @@ def main():
     ap.add_argument("--config5-only", action="store_true",
                     help="only BASELINE config 5 (8B shape, 8K context)")
     ap.add_argument("--no-config5", action="store_true")
+    ap.add_argument("--small-only", action="store_true",
+                    help="only the daiss-0.5b Q8_0 decode (the 32-value block GEMV)")
     a = ap.parse_args()
     if a.trace_summary:
         trace_summary(a.trace_summary)
@@ -488,6 +522,9 @@ def main():
     if a.config5_only:
         print(json.dumps(config5_bench(F, L)), flush=True)
         return 0
+    if a.small_only:
+        print(json.dumps(small_model_bench(F, L, a.steps, a.warmup, a.prompt)), flush=True)
+        return 0
     if a.batched_only:
         m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)
         print(json.dumps(batched_bench(L, m, False)), flush=True)
@@ -504,6 +541,7 @@ def main():
     batched = batched_bench(L, m, not a.no_cpu)
     m.close()
     config5 = None if a.no_config5 else config5_bench(F, L)
+    small = small_model_bench(F, L)
     out = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -537,6 +575,7 @@ def main():
         "prefill": prefill,
         "sampled_decode": sampled,
         "config5": config5,
+        "decode_0_5b_q8_0": small,
     }
     print(json.dumps(out), flush=True)
     return 0
