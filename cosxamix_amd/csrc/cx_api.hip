@@ -1132,11 +1132,18 @@ static int enqueue_step(cx_cache* C) {
     cx_seg o{L.o, m->x, nullptr, D};
     if ((rc = cx_launch_gemv(L.t_o, &o, 1, D, act, CX_EPI_ACCUM, nullptr, s))) return rc;
     // src/forward.rs:472-491: rmsnorm, gate/up, SwiGLU, down added to the residual
-    const cx_seg gu[2] = {{L.gate, m->g, nullptr, I}, {L.up, m->u, nullptr, I}};
-    const int tgu[2] = {L.t_gate, L.t_up};
-    if ((rc = gemv_norm_by_type(tgu, gu, 2, D, m->x, L.ffn_norm, c.eps, s))) return rc;
-    if ((rc = cx_launch_swiglu_quant(m->g, m->u, I, cx_sub(L.t_down), m->xq, m->xe, m->xs, s)))
-      return rc;
+    if (L.t_gate == L.t_up && cx_glu_supported(L.t_gate) && I % 32 == 0 && D <= 8192) {
+      // gate, up and SwiGLU in one launch, bit-identical to the three below
+      if ((rc = cx_launch_gemv_glu(L.t_gate, L.gate, L.up, I, D, m->x, L.ffn_norm, c.eps,
+                                   cx_sub(L.t_down), m->xq, m->xe, m->xs, s)))
+        return rc;
+    } else {
+      const cx_seg gu[2] = {{L.gate, m->g, nullptr, I}, {L.up, m->u, nullptr, I}};
+      const int tgu[2] = {L.t_gate, L.t_up};
+      if ((rc = gemv_norm_by_type(tgu, gu, 2, D, m->x, L.ffn_norm, c.eps, s))) return rc;
+      if ((rc = cx_launch_swiglu_quant(m->g, m->u, I, cx_sub(L.t_down), m->xq, m->xe, m->xs, s)))
+        return rc;
+    }
     cx_seg dn{L.down, m->x, nullptr, D};
     if ((rc = cx_launch_gemv(L.t_down, &dn, 1, I, act, CX_EPI_ACCUM, nullptr, s))) return rc;
   }

@@ -580,6 +580,122 @@ __device__ inline float row_sum_any(const float* terms, uint32_t n) {
   return acc;
 }
 
+// ------------------------------------- gate/up + SwiGLU in one launch
+// The MLP's first half of one decode step (src/forward.rs:472-487) for
+// gate and up of one type (Q4_K or Q5_K): tile t holds gate rows
+// [32t, 32t+32) and the same rows of up. Every workgroup makes the rmsnorm +
+// quantization of x itself (the prologue of k_gemv, the same f64 tree) while
+// its weights stream straight into registers (as k_gemv_reg), forms the 64
+// rows' terms and row sums in the reference's order, then
+// act[i] = silu(gate[i]) * up[i] for its 32 values and their i8 quantization
+// (sub-blocks of the down projection's size, 16 or 32) — the bytes
+// k_gemv_norm + k_swiglu_quant would write, without the launch between them.
+struct GluParams {
+  const uint8_t* wg;
+  const uint8_t* wu;
+  const float* nx;
+  const float* nw;
+  float eps;
+  uint32_t k, nb, nsub, row_bytes, tstride;
+  uint32_t lds_scale, lds_terms, lds_gu;
+  int8_t* xq;  // the down projection's activation
+  float* xe;
+  float* xs;
+};
+constexpr uint32_t GLU_ROWS = 32;
+
+// Every thread keeps GLU_DEPTH items' weights in flight: all of them at
+// k = 2048 (4 items a thread), a ring refilled one item behind at larger k.
+constexpr int GLU_DEPTH = 4;
+
+template <int T, int SUB>
+__global__ __launch_bounds__(256) void k_gemv_glu(GluParams P) {
+  using Q = KQ<T>;
+  constexpr int SPB = 256 / Q::SUB;
+  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ double red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t row0 = blockIdx.x * GLU_ROWS;
+  int8_t* sq = reinterpret_cast<int8_t*>(lds);
+  float* se = reinterpret_cast<float*>(lds + P.lds_scale);
+  float* ss = se + P.nsub;
+  float* sx = reinterpret_cast<float*>(lds + P.lds_terms);  // the norm input, then the terms
+  float* terms = sx;
+  float* gu = reinterpret_cast<float*>(lds + P.lds_gu);
+
+  // 1. x and the norm weight by direct loads, then this thread's first
+  //    item's weights into registers
+  copy_to_lds(P.nx, sx, P.k / 4, wave, lane);
+  copy_to_lds(P.nw, sx + P.k, P.k / 4, wave, lane);
+  const uint32_t items = 2 * (2 * GLU_ROWS) * P.nb;
+  auto block_of = [&](uint32_t it) {
+    const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
+    const uint8_t* w = r < GLU_ROWS ? P.wg : P.wu;
+    return w + (size_t)(row0 + (r & (GLU_ROWS - 1))) * P.row_bytes + (size_t)blk * Q::BPB;
+  };
+  typename Q::Regs buf[GLU_DEPTH];
+  uint32_t issued = 0;  // wave-uniform: items is a multiple of 128
+#pragma unroll
+  for (int d = 0; d < GLU_DEPTH; d++) {
+    const uint32_t it = tid + 256u * d;
+    if (it < items) {
+      Q::load(block_of(it), (int)(it & 1), buf[d]);
+      issued++;
+    }
+  }
+  wait_all_but(issued * Q::NLOAD);  // x and w (issued first) have landed
+  cx_barrier();
+  // 2. rmsnorm + quantization of the activation (k_gemv's prologue)
+  {
+    const float* sw = sx + P.k;
+    double sum = 0.0;
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048)
+#pragma unroll
+      for (int j = 0; j < 8; j++) sum += (double)sx[i + j] * (double)sx[i + j];
+    sum = cx_wave_sum_d(sum);
+    if (lane == 0) red[wave] = sum;
+    cx_wait_lds();
+    cx_barrier();
+    const double tot = ((red[0] + red[1]) + red[2]) + red[3];
+    const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = (float)((double)sx[i + j] * scale) * sw[i + j];
+      cx_quant8_padded<Q::SUB>(v, i, sq, se, ss);
+    }
+  }
+  cx_wait_lds();
+  cx_barrier();  // the activation is in LDS; x and w are read: the region becomes the terms
+  // 3. the 64 rows' terms; slot d of the ring holds items d, d + DEPTH, ...
+  for (uint32_t base = tid; base < items; base += 256u * GLU_DEPTH) {
+#pragma unroll
+    for (int d = 0; d < GLU_DEPTH; d++) {
+      const uint32_t it = base + 256u * d;
+      if (it < items) {
+        const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
+        Q::half_regs(buf[d], (int)(it & 1), sq + blk * ACT_LDS_BLOCK, se + blk * SPB,
+                     ss + blk * SPB, nullptr, terms + r * P.tstride + blk * SPB);
+        const uint32_t nx = it + 256u * GLU_DEPTH;
+        if (nx < items) Q::load(block_of(nx), (int)(nx & 1), buf[d]);
+      }
+    }
+  }
+  __syncthreads();
+  // 4. row sums in the scalar spec's order; SwiGLU one value a lane; then
+  //    the quantization, 8 values a lane
+  if ((uint32_t)tid < 2 * GLU_ROWS) gu[tid] = row_sum(terms + tid * P.tstride, P.nsub);
+  __syncthreads();
+  if (tid < (int)GLU_ROWS) gu[tid] = cx_swiglu(gu[tid], gu[GLU_ROWS + tid]);
+  __syncthreads();
+  if (tid < (int)(GLU_ROWS / 8)) {
+    float a[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) a[j] = gu[8 * tid + j];
+    cx_quant8<SUB>(a, row0 + 8 * tid, P.xq, P.xe, P.xs);
+  }
+}
+
 // ------------------------------------------- 32-value blocks (Q8_0, Q5_0)
 // The buffer path of the reference for these formats (ops::matmul_i8_directo
 // and matmul_varias_una_fila, src/ops.rs:310-414, 968-993): the row unpacked
@@ -919,6 +1035,52 @@ int cx_launch_gemv_norm(int type, const cx_seg* segs, int nseg, uint32_t k, cons
   P.nw = w;
   P.eps = eps;
   return launch_type<true>(type, P, rows, s);
+}
+
+bool cx_glu_supported(int type) { return type == CX_Q4_K || type == CX_Q5_K; }
+
+int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t I, uint32_t k,
+                       const float* x, const float* w, float eps, int sub, int8_t* xq, float* xe,
+                       float* xs, hipStream_t s) {
+  CX_REQUIRE(cx_glu_supported(type), "gemv glu: type %d (Q4_K or Q5_K)", type);
+  CX_REQUIRE(sub == 16 || sub == 32, "gemv glu: sub-blocks of 16 or 32, not %d", sub);
+  CX_REQUIRE(k > 0 && k % 256 == 0 && k <= 8192, "gemv glu: k=%u (a multiple of 256, at most 8192)", k);
+  CX_REQUIRE(I > 0 && I % GLU_ROWS == 0, "gemv glu: %u rows are not tiles of %u", I, GLU_ROWS);
+  CX_REQUIRE(wg && wu && x && w && xq && xe && xs, "gemv glu: null pointer");
+  CX_REQUIRE(((uintptr_t)wg & 15) == 0 && ((uintptr_t)wu & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
+                 ((uintptr_t)w & 15) == 0 && ((uintptr_t)xq & 7) == 0,
+             "gemv glu: weights, x and w 16-byte aligned, xq 8-byte");
+  GluParams P{};
+  P.wg = wg;
+  P.wu = wu;
+  P.nx = x;
+  P.nw = w;
+  P.eps = eps;
+  P.k = k;
+  P.nb = k / 256;
+  P.nsub = k / cx_sub(type);
+  P.row_bytes = P.nb * cx_bpb(type);
+  P.tstride = P.nsub + 4;
+  P.xq = xq;
+  P.xe = xe;
+  P.xs = xs;
+  // LDS: [xq, 272 bytes per 256][xe, xs][norm input (2k floats), then the
+  // terms (64 x (nsub + 4))][64 row sums]
+  P.lds_scale = P.nb * ACT_LDS_BLOCK;
+  P.lds_terms = P.lds_scale + (8 * P.nsub + 15) / 16 * 16;
+  const uint32_t terms = 4 * 2 * GLU_ROWS * P.tstride, nin = 8 * k;
+  P.lds_gu = P.lds_terms + (terms > nin ? terms : nin);
+  const uint32_t lds = P.lds_gu + 4 * 2 * GLU_ROWS;
+  const dim3 grid(I / GLU_ROWS);
+  if (type == CX_Q4_K) {
+    if (sub == 32) hipLaunchKernelGGL((k_gemv_glu<CX_Q4_K, 32>), grid, dim3(256), lds, s, P);
+    else hipLaunchKernelGGL((k_gemv_glu<CX_Q4_K, 16>), grid, dim3(256), lds, s, P);
+  } else {
+    if (sub == 32) hipLaunchKernelGGL((k_gemv_glu<CX_Q5_K, 32>), grid, dim3(256), lds, s, P);
+    else hipLaunchKernelGGL((k_gemv_glu<CX_Q5_K, 16>), grid, dim3(256), lds, s, P);
+  }
+  CX_HIP(hipGetLastError());
+  return CX_OK;
 }
 
 // ------------------------------------------------- activation kernels

@@ -48,6 +48,11 @@ CASES = [
                                   vocab=2000, contexto=200, rope=5e5), O.Q4_K, O.Q5_K),
     ("mini-q2k", dict(capas=2, dim=512, cabezas=8, cabezas_kv=2, ffn=1536, vocab=1500,
                       contexto=200, rope=10000.0), O.Q2_K, O.Q3_K),
+    # gate/up/SwiGLU in one launch, quantizing for a down of 16-value sub-blocks
+    ("mini-q5k-q3kdown", dict(capas=2, dim=512, cabezas=8, cabezas_kv=2, ffn=1536, vocab=1500,
+                              contexto=200, rope=10000.0), O.Q5_K, O.Q3_K),
+    ("mini-q4k-q2kdown", dict(capas=2, dim=768, cabezas=6, cabezas_kv=2, ffn=2304, vocab=900,
+                              contexto=200, rope=10000.0), O.Q4_K, O.Q2_K),
 ]
 
 
