@@ -256,11 +256,13 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 // then quantized for the output projection (64 values are whole
 // sub-blocks). Bit-identical to the scalar reference.
 constexpr uint32_t SC_P = 64;     // positions per scores wave
-constexpr uint32_t PV_DS = 64;    // head dims per softmax-V workgroup (wave 0's lanes)
-constexpr uint32_t PV_STP = 64;   // positions per V stage (16 KiB)
+constexpr uint32_t PV_DS = 32;    // head dims per softmax-V workgroup (wave 0's lanes)
+constexpr uint32_t PV_STP = 128;  // positions per V stage (16 KiB)
 constexpr uint32_t PV_NST = 8;    // V stages in the LDS ring (128 KiB)
-constexpr uint32_t PV_IPS = PV_STP * PV_DS * 4 / 1024;  // loads per stage: 8
-constexpr uint32_t PV_IPW = PV_IPS / 4;                  // per wave: 4
+constexpr uint32_t PV_IPS = PV_STP * PV_DS * 4 / 1024;  // 1 KiB loads per stage
+constexpr uint32_t PV_IPW = PV_IPS / 4;                  // per wave
+constexpr uint32_t PV_LPP = PV_DS / 4;                   // lanes per position in a load
+static_assert(PV_IPW >= 1 && PV_DS % 32 == 0, "whole loads per wave");
 // A wave tracks at most 63 outstanding loads (vmcnt is 6 bits): its share
 // of the scores (<= 4 loads for 4096 positions) plus 7 stages ahead (28).
 static_assert(4 + (PV_NST - 1) * PV_IPW <= 63, "too many loads in flight");
@@ -397,15 +399,23 @@ __device__ inline float seq_sum_lds(const float* x, uint32_t n) {
   return tot;
 }
 
+// o += p[j] * v[j] for 8 positions in order. The 8 products are formed
+// first, pinned there by an empty asm that takes them as operands: left to
+// itself the compiler interleaves each multiply with its add, and the chain
+// then waits for a multiply and an add per position instead of one add.
 __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) {
-  o += p[0].x * v[0];
-  o += p[0].y * v[1];
-  o += p[0].z * v[2];
-  o += p[0].w * v[3];
-  o += p[1].x * v[4];
-  o += p[1].y * v[5];
-  o += p[1].z * v[6];
-  o += p[1].w * v[7];
+  float t0 = p[0].x * v[0], t1 = p[0].y * v[1], t2 = p[0].z * v[2], t3 = p[0].w * v[3];
+  float t4 = p[1].x * v[4], t5 = p[1].y * v[5], t6 = p[1].z * v[6], t7 = p[1].w * v[7];
+  asm volatile("" : "+v"(t0), "+v"(t1), "+v"(t2), "+v"(t3), "+v"(t4), "+v"(t5), "+v"(t6),
+               "+v"(t7));
+  o += t0;
+  o += t1;
+  o += t2;
+  o += t3;
+  o += t4;
+  o += t5;
+  o += t6;
+  o += t7;
 }
 
 // 256 threads: every wave streams its share of the V ring (4x the loads in
@@ -444,9 +454,9 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     float* dst = ring + (s % PV_NST) * (PV_STP * PV_DS);
     for (uint32_t j = 0; j < PV_IPW; j++) {
       const uint32_t i = w + 4 * j;
-      uint32_t p = s * PV_STP + i * 4 + t / 16;  // 4 positions of 256 B per load
+      uint32_t p = s * PV_STP + i * (64 / PV_LPP) + t / PV_LPP;  // 64/LPP positions a load
       if (p >= total) p = 0;
-      cx_dma16_async(reinterpret_cast<const uint8_t*>(vb + (size_t)p * kvd) + (t % 16) * 16,
+      cx_dma16_async(reinterpret_cast<const uint8_t*>(vb + (size_t)p * kvd) + (t % PV_LPP) * 16,
                      dst + i * 256);
     }
   };
@@ -488,34 +498,36 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     else
       cx_wait_vm<0>();
     cx_barrier();  // stage s has landed, from every wave
-    if (w == 0) {
+    if (w == 0 && t < (int)PV_DS) {
       const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS) + t;
       const float* ps = e + s * PV_STP;
       if ((s + 1) * PV_STP <= total) {
-        // batches of 8 positions; the next batch's LDS reads are issued
-        // before the current batch's adds, alternating two register buffers
+        // batches of 32 positions, two register buffers: a batch's LDS
+        // reads are issued before the previous batch's arithmetic, so their
+        // latency hides behind 32 adds
         const float4* p4 = reinterpret_cast<const float4*>(ps);
-        float va[8], vb[8];
-        float4 pa[2], pb[2];
+        float va[32], vb[32];
+        float4 pa[8], pb[8];
+        auto fetch = [&](float (&v)[32], float4 (&pp)[8], int b) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) va[j] = vs[j * PV_DS];
-        pa[0] = p4[0];
-        pa[1] = p4[1];
+          for (int j = 0; j < 32; j++) v[j] = vs[(32 * b + j) * PV_DS];
 #pragma unroll
-        for (uint32_t bt = 0; bt < PV_STP / 8; bt += 2) {
+          for (int i = 0; i < 8; i++) pp[i] = p4[8 * b + i];
+        };
+        auto apply = [&](const float (&v)[32], const float4 (&pp)[8]) {
 #pragma unroll
-          for (int j = 0; j < 8; j++) vb[j] = vs[(8 * (bt + 1) + j) * PV_DS];
-          pb[0] = p4[2 * (bt + 1)];
-          pb[1] = p4[2 * (bt + 1) + 1];
-          pv8(o, pa, va);
-          if (bt + 2 < PV_STP / 8) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) va[j] = vs[(8 * (bt + 2) + j) * PV_DS];
-            pa[0] = p4[2 * (bt + 2)];
-            pa[1] = p4[2 * (bt + 2) + 1];
-          }
-          pv8(o, pb, vb);
-        }
+          for (int q = 0; q < 4; q++) pv8(o, *reinterpret_cast<const float4(*)[2]>(pp + 2 * q),
+                                          *reinterpret_cast<const float(*)[8]>(v + 8 * q));
+        };
+        static_assert(PV_STP == 128, "four batches of 32 a stage");
+        fetch(va, pa, 0);
+        fetch(vb, pb, 1);
+        apply(va, pa);
+        fetch(va, pa, 2);
+        apply(vb, pb);
+        fetch(vb, pb, 3);
+        apply(va, pa);
+        apply(vb, pb);
       } else {
         for (uint32_t j = 0; s * PV_STP + j < total; j++) o += ps[j] * vs[j * PV_DS];
       }
@@ -524,7 +536,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     cx_barrier();  // the slot is read: refill it
     if (s + PV_NST < nstage) issue(s + PV_NST);
   }
-  if (w != 0) return;
+  if (w != 0 || t >= (int)PV_DS) return;
   out[h * HD + d0 + t] = o;
   if (!xq) return;
   float* os = ring;  // every load has landed and every read of the ring is done
