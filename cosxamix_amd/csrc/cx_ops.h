@@ -23,10 +23,11 @@ struct cx_samp_state {
   float u, inv_s;
   uint32_t uniform, token;
 };
-// floats of the per-block maxima of a vocabulary of n
+// 4-byte words of the sampler's `part` scratch for a vocabulary of n (the
+// per-block maxima and the descending-order sort's keys, indices, counts)
 size_t cx_sample_parts(size_t n);
 // One Muestreador::elegir with temperature on device logits[n]: pb (n
-// floats), part (cx_sample_parts(n)), ord (n), ordp (n floats) are scratch;
+// floats), part (cx_sample_parts(n) words), ord (n), ordp (n floats) are scratch;
 // the token goes to *out (device, optional) and, with st, to hist[pos + 1]
 // with the position advanced (the token loop's argmax step).
 int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb, float* part,

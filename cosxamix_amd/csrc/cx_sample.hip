@@ -13,20 +13,24 @@
 //          total = its sum; the first token of the nucleus whose running
 //          sum exceeds u * total (the last one if none does)
 //
-// The reference takes the 1024 most probable tokens first and sorts all of
-// them only when those fall short of top_p; both give the prefix of the
-// descending order, which is what is built here: 1024 tokens, then blocks of
-// 16384 for the flat distributions that need more.
+// The reference takes the 1024 most probable tokens first (the candidates)
+// and sorts every token only when their mass falls short of top_p. Both are
+// prefixes of one descending order, which is built here for every token by
+// a stable device-wide radix sort; the nucleus is then its first 1024 tokens
+// or all of them, by the reference's test on the candidates' mass.
 // Ties: the reference sorts with an unstable sort, which leaves the order of
 // equal probabilities unspecified; here they go by ascending token index.
 //
 // Kernels of one call, each a fixed launch (no host decision between them,
 // so the sequence can sit in a captured graph):
-//   k_samp_z    z_i and per-block maxima                      (grid)
-//   k_samp_e    e_i = exp(z_i - max), or the uniform 1/n       (grid)
-//   k_samp_sum  S sequentially, 1/S, and the draw of u         (1 workgroup)
-//   k_samp_p    p_i = e_i * (1/S)                              (grid)
-//   k_samp_pick the token                                      (1 workgroup)
+//   k_samp_z     z_i and per-block maxima                      (grid)
+//   k_samp_e     e_i = exp(z_i - max), or the uniform 1/n       (grid)
+//   k_samp_sum   S sequentially, 1/S, and the draw of u         (1 workgroup)
+//   k_samp_p     p_i = e_i * (1/S)                              (grid)
+//   k_rs_count, k_rs_scan, k_rs_scatter, four times: the descending order
+//                of p (8-bit digits, least significant first); they return
+//                at once when top_p >= 1 (no order needed)
+//   k_samp_pick  the token                                      (1 workgroup)
 // The sequential sums (S, the running sums) are single-lane chains fed from
 // LDS stages that the other waves fill with direct-to-LDS loads.
 #include "cx_ops.h"
@@ -39,11 +43,12 @@ constexpr uint32_t ZV = 8;           // values per thread of the grid kernels
 constexpr uint32_t CW = 1024;        // threads of the single-workgroup kernels
 constexpr uint32_t SEG = 2048;       // floats per chain stage (8 KiB: one KiB per loader wave)
 constexpr uint32_t NST = 8;          // chain stages in the LDS ring
-constexpr uint32_t TOPK0 = 1024;     // tokens of the first block of the descending order
-constexpr uint32_t TOPK = 16384;     // tokens of a later block (128 KiB of keys)
+constexpr uint32_t CAND = 1024;      // CANDIDATOS (src/sampler.rs): the first nucleus
+constexpr uint32_t RS_T = 256;       // threads of a radix-sort workgroup
+constexpr uint32_t RS_R = 8;         // rounds of RS_T elements a tile
+constexpr uint32_t RS_TILE = RS_T * RS_R;
 
-constexpr size_t PICK_LDS = TOPK * sizeof(uint64_t);  // the keys, or the chains' ring
-static_assert(PICK_LDS >= NST * SEG * sizeof(float), "the ring fits in the keys' LDS");
+constexpr size_t PICK_LDS = NST * SEG * sizeof(float);  // the chains' ring
 
 // total-order key of a probability (f32::total_cmp): larger key, larger value
 __device__ inline uint32_t pkey(float p) {
@@ -164,94 +169,133 @@ __device__ inline void chain_walk(const float* x, uint32_t n, float* lds, F stag
   __syncthreads();
 }
 
-// tot += v[0] + ... + v[m) in order; 32 values a batch, the next batch read
-// before the current is added (v holds whole batches: reads past m stay in
-// the stage)
+// tot += v[0] + ... + v[m) in order; 32 values a batch, two register
+// buffers taking turns: a batch is read while the one before it is added
+// (v holds whole batches: reads past m stay in the stage)
+__device__ inline void add32v(float& tot, const float4 (&a)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    tot += a[i].x;
+    tot += a[i].y;
+    tot += a[i].z;
+    tot += a[i].w;
+  }
+}
+__device__ inline void load32v(float4 (&a)[8], const float4* v4, uint32_t j) {
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = v4[j / 4 + i];
+}
 __device__ inline void stage_sum(float& tot, const float* v, uint32_t m) {
   const float4* v4 = reinterpret_cast<const float4*>(v);
   float4 A[8], B[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) A[i] = v4[i];
+  const uint32_t mb = m / 32 * 32;  // whole batches
   uint32_t j = 0;
-  for (; j + 32 <= m; j += 32) {
-    if (j + 32 < SEG) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) B[i] = v4[j / 4 + 8 + i];
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      tot += A[i].x;
-      tot += A[i].y;
-      tot += A[i].z;
-      tot += A[i].w;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) A[i] = B[i];
+  if (mb) load32v(A, v4, 0);
+  while (j < mb) {
+    if (j + 32 < mb) load32v(B, v4, j + 32);
+    add32v(tot, A);
+    j += 32;
+    if (j >= mb) break;
+    if (j + 32 < mb) load32v(A, v4, j + 32);
+    add32v(tot, B);
+    j += 32;
   }
   for (; j < m; j++) tot += v[j];
 }
 
 // The running sum acc += v[j] in order, stopping at the first j with
-// acc > target (returns j, or m). The sums of a batch of 32 are formed first
-// and checked once: acc never decreases (v >= 0), so the batch crosses iff
-// its last sum does; a NaN sum takes the one-by-one check.
+// acc > target (GE: acc >= target; returns j, or m). The sums of a batch of
+// 32 are formed first and checked once: acc never decreases (v >= 0), so the
+// batch crosses iff its last sum does; a NaN sum takes the one-by-one check.
+template <bool GE>
+__device__ inline bool passes(float a, float target) { return GE ? a >= target : a > target; }
+
+// one batch of 32: true (and acc = the crossing sum, *at = its offset) if it
+// crosses, else acc = the batch's last sum
+template <bool GE>
+__device__ inline bool cross32(float& acc, const float4 (&A)[8], float target, uint32_t* at) {
+  float r[32];
+  float a = acc;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    a += A[i].x;
+    r[4 * i] = a;
+    a += A[i].y;
+    r[4 * i + 1] = a;
+    a += A[i].z;
+    r[4 * i + 2] = a;
+    a += A[i].w;
+    r[4 * i + 3] = a;
+  }
+  if (passes<GE>(a, target) || a != a) {
+#pragma unroll
+    for (int k = 0; k < 32; k++)
+      if (passes<GE>(r[k], target)) {
+        acc = r[k];
+        *at = (uint32_t)k;
+        return true;
+      }
+  }
+  acc = a;
+  return false;
+}
+
+template <bool GE = false>
 __device__ inline uint32_t stage_cross(float& acc, const float* v, uint32_t m, float target) {
   const float4* v4 = reinterpret_cast<const float4*>(v);
   float4 A[8], B[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) A[i] = v4[i];
-  uint32_t j = 0;
-  for (; j + 32 <= m; j += 32) {
-    if (j + 32 < SEG) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) B[i] = v4[j / 4 + 8 + i];
-    }
-    float r[32];
-    float a = acc;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      a += A[i].x;
-      r[4 * i] = a;
-      a += A[i].y;
-      r[4 * i + 1] = a;
-      a += A[i].z;
-      r[4 * i + 2] = a;
-      a += A[i].w;
-      r[4 * i + 3] = a;
-    }
-    if (a > target || a != a) {
-#pragma unroll
-      for (int k = 0; k < 32; k++)
-        if (r[k] > target) {
-          acc = r[k];
-          return j + k;
-        }
-    }
-    acc = a;
-#pragma unroll
-    for (int i = 0; i < 8; i++) A[i] = B[i];
+  const uint32_t mb = m / 32 * 32;
+  uint32_t j = 0, k = 0;
+  if (mb) load32v(A, v4, 0);
+  while (j < mb) {
+    if (j + 32 < mb) load32v(B, v4, j + 32);
+    if (cross32<GE>(acc, A, target, &k)) return j + k;
+    j += 32;
+    if (j >= mb) break;
+    if (j + 32 < mb) load32v(A, v4, j + 32);
+    if (cross32<GE>(acc, B, target, &k)) return j + k;
+    j += 32;
   }
   for (; j < m; j++) {
     acc += v[j];
-    if (acc > target) return j;
+    if (passes<GE>(acc, target)) return j;
   }
   return m;
 }
 
-// the first index of x[0..n) whose running sum exceeds target, or n
-__device__ inline uint32_t chain_cross(const float* x, uint32_t n, float* lds, float target) {
+// The running sum of x[0..n) continued from *acc: the first index where it
+// exceeds target (GE: reaches it), or n; *acc (thread 0) ends as the sum
+// through that index, or through x[n - 1]
+// (*acc in shared memory; every thread sees the result and *acc on return)
+template <bool GE = false>
+__device__ inline uint32_t chain_find(const float* x, uint32_t n, float* lds, float target,
+                                      float* acc) {
   __shared__ uint32_t s_at;
-  float acc = 0.0f;
-  if (threadIdx.x == 0) s_at = n;
+  __syncthreads();  // every read of the last call's s_at and *acc is done
+  float a = 0.0f;
+  if (threadIdx.x == 0) {
+    a = *acc;
+    s_at = n;
+  }
   chain_walk(x, n, lds, [&](const float* v, uint32_t m, uint32_t base) {
-    const uint32_t k = stage_cross(acc, v, m, target);
+    const uint32_t k = stage_cross<GE>(a, v, m, target);
     if (k < m) {
       s_at = base + k;
       return true;
     }
     return false;
   });
+  if (threadIdx.x == 0) *acc = a;
+  __syncthreads();
   return s_at;
+}
+
+// the first index of x[0..n) whose running sum exceeds target, or n
+__device__ inline uint32_t chain_cross(const float* x, uint32_t n, float* lds, float target) {
+  __shared__ float acc;
+  __syncthreads();  // no thread still reads the last call's acc
+  if (threadIdx.x == 0) acc = 0.0f;
+  return chain_find<false>(x, n, lds, target, &acc);
 }
 
 // S = e_0 + e_1 + ... sequentially from 0, then 1/S; and the draw of u
@@ -274,29 +318,128 @@ __global__ __launch_bounds__(CW) void k_samp_sum(const float* pb, uint32_t n, cx
   if (threadIdx.x == 0) sd->inv_s = 1.0f / tot;
 }
 
-// ------------------------------------------------------------------- pick
-// The token (src/sampler.rs:83-125, 139-152), written to *out and, in the
-// token loop, to hist[pos + 1] with the position advanced as the greedy
-// argmax does.
-__device__ inline uint64_t ckey(uint32_t key, uint32_t idx) {  // descending p, then ascending index
-  return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - idx);
-}
-
-__device__ inline float key_p(uint64_t c) {  // the probability back from a composite key
-  const uint32_t k = (uint32_t)(c >> 32);
+// ------------------------------------------------- the descending order
+// A stable LSD radix sort of (key, index) with key = ~total-order key of p:
+// ascending keys are descending probabilities (f32::total_cmp), and equal
+// ones keep ascending index. Four passes of 8-bit digits; a pass counts the
+// digits of each tile of RS_TILE elements, scans the counts (digit-major,
+// then tile), and scatters each tile in index order. Pass 0 reads p itself;
+// the last pass writes the order (ord) and the sorted probabilities (ordp).
+__device__ inline uint32_t rs_key(float p) { return ~pkey(p); }
+__device__ inline float rs_p(uint32_t key) {  // the probability back from its key
+  const uint32_t k = ~key;
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
+template <int D>
+__global__ __launch_bounds__(RS_T) void k_rs_count(const float* pb, const uint32_t* kin, uint32_t n,
+                                                   const cx_samp_state* sd, uint32_t* cnt,
+                                                   uint32_t G) {
+  if (sd->top_p >= 1.0f) return;
+  __shared__ uint32_t h[256];
+  const uint32_t tid = threadIdx.x, base = blockIdx.x * RS_TILE;
+  h[tid] = 0;
+  __syncthreads();
+  for (uint32_t r = 0; r < RS_R; r++) {
+    const uint32_t i = base + r * RS_T + tid;
+    if (i < n) {
+      const uint32_t key = D == 0 ? rs_key(pb[i]) : kin[i];
+      atomicAdd(&h[(key >> (8 * D)) & 255u], 1u);
+    }
+  }
+  __syncthreads();
+  cnt[tid * G + blockIdx.x] = h[tid];
+}
+
+// exclusive prefix sum of cnt[0..e) in place, one workgroup of CW threads.
+// With LDS (e <= RS_SCAN_LDS words) the counts are staged there by coalesced
+// loads, each thread scans a contiguous chunk, and the result goes back
+// coalesced; otherwise the chunks are read from global memory.
+constexpr uint32_t RS_SCAN_LDS = 32768;
+template <bool LDS>
+__global__ __launch_bounds__(CW) void k_rs_scan(uint32_t* cnt, uint32_t e, const cx_samp_state* sd) {
+  if (sd->top_p >= 1.0f) return;
+  extern __shared__ uint32_t stage[];
+  __shared__ uint32_t part[CW];
+  const uint32_t tid = threadIdx.x, per = (e + CW - 1) / CW;
+  const uint32_t lo = min(e, tid * per), hi = min(e, lo + per);
+  uint32_t* c = LDS ? stage : cnt;
+  if (LDS) {
+    for (uint32_t i = tid; i < e; i += CW) stage[i] = cnt[i];
+    __syncthreads();
+  }
+  uint32_t sum = 0;
+  for (uint32_t i = lo; i < hi; i++) sum += c[i];
+  part[tid] = sum;
+  __syncthreads();
+  for (uint32_t off = 1; off < CW; off <<= 1) {  // inclusive scan of the parts
+    const uint32_t v = tid >= off ? part[tid - off] : 0u;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  uint32_t run = part[tid] - sum;
+  for (uint32_t i = lo; i < hi; i++) {
+    const uint32_t x = c[i];
+    c[i] = run;
+    run += x;
+  }
+  if (LDS) {
+    __syncthreads();
+    for (uint32_t i = tid; i < e; i += CW) cnt[i] = stage[i];
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(RS_T) void k_rs_scatter(const float* pb, const uint32_t* kin,
+                                                     const uint32_t* iin, uint32_t n,
+                                                     const cx_samp_state* sd, const uint32_t* off,
+                                                     uint32_t G, uint32_t* kout, uint32_t* iout,
+                                                     float* pout) {
+  if (sd->top_p >= 1.0f) return;
+  __shared__ uint32_t run[256];     // next position of each digit in this tile
+  __shared__ uint32_t wc[4][256];   // digit counts of each wave in this round
+  const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, base = blockIdx.x * RS_TILE;
+  const uint64_t below = (1ull << lane) - 1;
+  run[tid] = off[tid * G + blockIdx.x];
+  for (uint32_t r = 0; r < RS_R; r++) {
+    const uint32_t i = base + r * RS_T + tid;
+    const bool valid = i < n;
+    const uint32_t key = valid ? (D == 0 ? rs_key(pb[i]) : kin[i]) : 0u;
+    const uint32_t idx = D == 0 ? i : (valid ? iin[i] : 0u);
+    const uint32_t dig = (key >> (8 * D)) & 255u;
+    // the lanes of this wave with the same digit
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int bt = 0; bt < 8; bt++) {
+      const uint64_t bb = __ballot((dig >> bt) & 1u);
+      m &= ((dig >> bt) & 1u) ? bb : ~bb;
+    }
+    __syncthreads();  // the last round's reads of wc[] and updates of run[] are done
+    for (uint32_t d = lane; d < 256; d += 64) wc[w][d] = 0;
+    __syncthreads();
+    if (valid && (m & below) == 0) wc[w][dig] = (uint32_t)__popcll(m);
+    __syncthreads();
+    if (valid) {
+      uint32_t pos = run[dig] + (uint32_t)__popcll(m & below);
+      for (uint32_t v = 0; v < w; v++) pos += wc[v][dig];
+      if (kout) kout[pos] = key;
+      iout[pos] = idx;
+      if (pout) pout[pos] = rs_p(key);
+    }
+    __syncthreads();  // every read of run[] is done
+    run[tid] += wc[0][tid] + wc[1][tid] + wc[2][tid] + wc[3][tid];
+  }
+}
+
+// --------------------------------------------------------------------- pick
+// The token (src/sampler.rs:83-125, 139-152), written to *out and, in the
+// token loop, to hist[pos + 1] with the position advanced as the greedy
+// argmax does.
 __global__ __launch_bounds__(CW) void k_samp_pick(const float* pb, uint32_t n, cx_samp_state* sd,
-                                                  uint32_t* ord, float* ordp, uint32_t* out,
-                                                  cx_dstate* st, uint32_t* hist) {
+                                                  const uint32_t* ord, const float* ordp,
+                                                  uint32_t* out, cx_dstate* st, uint32_t* hist) {
   extern __shared__ __align__(16) float ring[];
-  // a block's keys share the LDS of the chains' ring, used after the blocks
-  uint64_t* keys = reinterpret_cast<uint64_t*>(ring);
-  __shared__ uint32_t hw[CW / 64][256];  // per-wave digit histograms
-  __shared__ uint32_t hist8[256];
-  __shared__ uint32_t wsum[CW / 64];
-  __shared__ uint32_t s_prefix, s_need, s_ngt, s_cut, s_done;
   __shared__ float s_acc;
   const uint32_t tid = threadIdx.x;
   const float u = sd->u, top_p = sd->top_p;
@@ -305,157 +448,27 @@ __global__ __launch_bounds__(CW) void k_samp_pick(const float* pb, uint32_t n, c
     const uint32_t at = chain_cross(pb, n, ring, u);
     tok = at < n ? at : n - 1;
   } else {
-    // the descending order, TOPK tokens at a time, until the running sum of
-    // p reaches top_p; ord[] receives the order
-    if (tid == 0) {
-      s_acc = 0.0f;
-      s_done = 0;
-      s_cut = n;
-    }
-    uint64_t bound = ~0ull;  // strictly below this composite key
-    uint32_t m = 0;
+    // the candidates' running sum to top_p (the crossing token enters)
+    const uint32_t k = min(CAND, n);
+    if (tid == 0) s_acc = 0.0f;
     __syncthreads();
-    while (!s_done) {
-      const uint32_t kk = min(m == 0 ? TOPK0 : TOPK, n - m);
-      const uint32_t sortn = kk <= TOPK0 ? TOPK0 : TOPK;  // a power of two
-      // radix select of the kk-th largest 32-bit key among the eligible,
-      // most significant byte first
-      if (tid == 0) {
-        s_prefix = 0;
-        s_need = kk;
-      }
-      __syncthreads();
-      uint32_t mask = 0;
-      const uint32_t wv = tid >> 6;
-      for (int d = 3; d >= 0; d--) {
-        for (uint32_t b = tid; b < (CW / 64) * 256; b += CW) (&hw[0][0])[b] = 0;
-        __syncthreads();
-        const uint32_t prefix = s_prefix;
-        for (uint32_t i = tid; i < n; i += CW) {
-          const uint32_t k = pkey(pb[i]);
-          if (ckey(k, i) < bound && (k & mask) == prefix) atomicAdd(&hw[wv][(k >> (8 * d)) & 255], 1u);
-        }
-        __syncthreads();
-        for (uint32_t b = tid; b < 256; b += CW) {
-          uint32_t c = 0;
-          for (uint32_t w = 0; w < CW / 64; w++) c += hw[w][b];
-          hist8[b] = c;
-        }
-        __syncthreads();
-        if (tid == 0) {
-          uint32_t need = s_need, above = 0;
-          int D = 255;
-          for (; D > 0; D--) {
-            if (above + hist8[D] >= need) break;
-            above += hist8[D];
-          }
-          s_need = need - above;
-          s_prefix = prefix | ((uint32_t)D << (8 * d));
-        }
-        mask |= 255u << (8 * d);
-        __syncthreads();
-      }
-      // the kk tokens: every eligible key above T, then the first `need` keys
-      // equal to T in index order. Wave w owns a contiguous range of indices
-      // and reads it 64 at a time (coalesced); a tie's rank is the ties
-      // before it: earlier waves, earlier reads, lower lanes.
-      const uint32_t T = s_prefix, need = s_need;
-      if (tid == 0) s_ngt = 0;
-      const uint32_t lane = tid & 63;
-      const uint32_t span = ((n + CW / 64 - 1) / (CW / 64) + 63) / 64 * 64;
-      const uint32_t w0 = min(n, wv * span), w1 = min(n, w0 + span);
-      const uint64_t below = (1ull << lane) - 1;
-      uint32_t ties = 0;
-      for (uint32_t b0 = w0; b0 < w1; b0 += 64) {
-        const uint32_t i = b0 + lane;
-        bool tie = false;
-        if (i < w1) {
-          const uint32_t k = pkey(pb[i]);
-          tie = k == T && ckey(k, i) < bound;
-        }
-        ties += __popcll(__ballot(tie));
-      }
-      if (lane == 0) wsum[wv] = ties;
-      __syncthreads();
-      uint32_t run = 0;
-      for (uint32_t w = 0; w < wv; w++) run += wsum[w];
-      const uint32_t ngt = kk - need;  // keys above T, all taken
-      for (uint32_t b0 = w0; b0 < w1; b0 += 64) {
-        const uint32_t i = b0 + lane;
-        bool tie = false;
-        uint64_t c = 0;
-        if (i < w1) {
-          const uint32_t k = pkey(pb[i]);
-          c = ckey(k, i);
-          if (c < bound) {
-            if (k > T) keys[atomicAdd(&s_ngt, 1u)] = c;
-            tie = k == T;
-          }
-        }
-        const uint64_t tm = __ballot(tie);
-        const uint32_t r = run + __popcll(tm & below);
-        if (tie && r < need) keys[ngt + r] = c;
-        run += __popcll(tm);
-      }
-      for (uint32_t j = kk + tid; j < sortn; j += CW) keys[j] = 0;  // sorts last
-      __syncthreads();
-      // bitonic sort, descending
-      for (uint32_t size = 2; size <= sortn; size <<= 1)
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-          for (uint32_t i = tid; i < sortn; i += CW) {
-            const uint32_t j = i ^ stride;
-            if (j > i) {
-              const bool desc = (i & size) == 0;
-              const uint64_t a = keys[i], b = keys[j];
-              if ((a < b) == desc) {
-                keys[i] = b;
-                keys[j] = a;
-              }
-            }
-          }
-          __syncthreads();
-        }
-      for (uint32_t j = tid; j < kk; j += CW) {
-        ord[m + j] = 0xFFFFFFFFu - (uint32_t)keys[j];
-        ordp[m + j] = key_p(keys[j]);
-      }
-      __threadfence();  // ord/ordp are read back through other waves' loads
-      // the running sum over this block, in order, 32 sums at a time (it
-      // never decreases: a batch reaches top_p iff its last sum does)
-      if (tid == 0) {
-        float acc = s_acc;
-        for (uint32_t j = 0; j < kk && !s_done; j += 32) {
-          float r[32];
-          float a = acc;
-          const uint32_t nb = min(32u, kk - j);
-#pragma unroll
-          for (uint32_t k = 0; k < 32; k++) {
-            if (k < nb) a += key_p(keys[j + k]);
-            r[k] = a;
-          }
-          if (a >= top_p || a != a) {
-            for (uint32_t k = 0; k < nb; k++)
-              if (r[k] >= top_p) {
-                s_cut = m + j + k + 1;
-                s_done = 1;
-                a = r[k];
-                break;
-              }
-          }
-          acc = a;
-        }
-        s_acc = acc;
-        if (m + kk == n) s_done = 1;  // never reached: the nucleus is every token
-      }
-      bound = keys[kk - 1];
-      m += kk;
-      __syncthreads();
+    uint32_t at = chain_find<true>(ordp, k, ring, top_p, &s_acc);
+    uint32_t cut;
+    if (at < k) {
+      cut = at + 1;
+    } else if (s_acc < top_p && k < n) {
+      // their mass falls short: the nucleus comes from every token's order
+      at = chain_find<true>(ordp + k, n - k, ring, top_p, &s_acc);
+      cut = at < n - k ? k + at + 1 : n;
+    } else {
+      cut = k;  // a NaN top_p: the candidates, whole
     }
+    __syncthreads();
     // total = the nucleus's sum (the running sum where it stopped); then the
     // first token of the nucleus whose running sum exceeds u * total (the
     // last one of the nucleus if none does)
-    const uint32_t cut = s_cut;
-    const uint32_t at = chain_cross(ordp, cut, ring, u * s_acc);
+    const float total = s_acc;
+    at = chain_cross(ordp, cut, ring, u * total);
     tok = ord[at < cut ? at : cut - 1];
   }
   if (tid == 0) {
@@ -469,9 +482,24 @@ __global__ __launch_bounds__(CW) void k_samp_pick(const float* pb, uint32_t n, c
   }
 }
 
+// the layout of `part`: the per-block maxima, then the sort's keys and
+// indices (two buffers of each but the final indices, which are ord) and the
+// digit counts
+struct SortScratch {
+  uint32_t nparts, n4, tiles;
+  size_t words() const { return (size_t)(nparts + 63) / 64 * 64 + 3 * (size_t)n4 + 256 * (size_t)tiles; }
+};
+inline SortScratch sort_scratch(size_t n) {
+  SortScratch S;
+  S.nparts = (uint32_t)((n + ZB * ZV - 1) / (ZB * ZV));
+  S.n4 = (uint32_t)((n + 63) / 64 * 64);
+  S.tiles = (uint32_t)((n + RS_TILE - 1) / RS_TILE);
+  return S;
+}
+
 }  // namespace
 
-size_t cx_sample_parts(size_t n) { return (n + ZB * ZV - 1) / (ZB * ZV); }
+size_t cx_sample_parts(size_t n) { return sort_scratch(n).words(); }
 
 int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb, float* part,
                      uint32_t* ord, float* ordp, uint32_t* out, cx_dstate* st, uint32_t* hist,
@@ -480,18 +508,45 @@ int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb
              "sample: bad arguments (n=%zu)", n);
   CX_REQUIRE(((uintptr_t)pb & 15) == 0 && ((uintptr_t)ordp & 15) == 0,
              "sample: the probability buffers must be 16-byte aligned");
-  const unsigned g = (unsigned)cx_sample_parts(n);
+  const SortScratch S = sort_scratch(n);
+  const unsigned g = S.nparts, G = S.tiles;
+  const uint32_t N = (uint32_t)n;
+  uint32_t* kA = reinterpret_cast<uint32_t*>(part) + (S.nparts + 63) / 64 * 64;
+  uint32_t* iA = kA + S.n4;
+  uint32_t* kB = iA + S.n4;
+  uint32_t* cnt = kB + S.n4;
   const size_t ring = (size_t)NST * SEG * sizeof(float);
-  hipLaunchKernelGGL(k_samp_z, dim3(g), dim3(ZB), 0, s, logits, (uint32_t)n, sd, pb, part);
+  hipLaunchKernelGGL(k_samp_z, dim3(g), dim3(ZB), 0, s, logits, N, sd, pb, part);
   CX_HIP(hipGetLastError());
-  hipLaunchKernelGGL(k_samp_e, dim3(g), dim3(ZB), 0, s, pb, (uint32_t)n, part, g, sd);
+  hipLaunchKernelGGL(k_samp_e, dim3(g), dim3(ZB), 0, s, pb, N, part, g, sd);
   CX_HIP(hipGetLastError());
-  hipLaunchKernelGGL(k_samp_sum, dim3(1), dim3(CW), ring, s, pb, (uint32_t)n, sd);
+  hipLaunchKernelGGL(k_samp_sum, dim3(1), dim3(CW), ring, s, pb, N, sd);
   CX_HIP(hipGetLastError());
-  hipLaunchKernelGGL(k_samp_p, dim3(g), dim3(ZB), 0, s, pb, (uint32_t)n, sd);
+  hipLaunchKernelGGL(k_samp_p, dim3(g), dim3(ZB), 0, s, pb, N, sd);
   CX_HIP(hipGetLastError());
-  hipLaunchKernelGGL(k_samp_pick, dim3(1), dim3(CW), PICK_LDS, s, pb, (uint32_t)n, sd, ord, ordp, out,
-                     st, hist);
+  // the descending order: pb -> (kA, iA) -> (kB, ord) -> (kA, iA) -> ord, ordp
+  const uint32_t E = 256 * G;
+  auto pass = [&](auto count, auto scatter, const uint32_t* ki, const uint32_t* ii, uint32_t* ko,
+                  uint32_t* io, float* po) -> int {
+    hipLaunchKernelGGL(count, dim3(G), dim3(RS_T), 0, s, pb, ki, N, sd, cnt, G);
+    CX_HIP(hipGetLastError());
+    if (E <= RS_SCAN_LDS)
+      hipLaunchKernelGGL(k_rs_scan<true>, dim3(1), dim3(CW), E * 4, s, cnt, E, sd);
+    else
+      hipLaunchKernelGGL(k_rs_scan<false>, dim3(1), dim3(CW), 0, s, cnt, E, sd);
+    CX_HIP(hipGetLastError());
+    hipLaunchKernelGGL(scatter, dim3(G), dim3(RS_T), 0, s, pb, ki, ii, N, sd, cnt, G, ko, io, po);
+    CX_HIP(hipGetLastError());
+    return CX_OK;
+  };
+  int rc;
+  if ((rc = pass(k_rs_count<0>, k_rs_scatter<0>, nullptr, nullptr, kA, iA, nullptr)) ||
+      (rc = pass(k_rs_count<1>, k_rs_scatter<1>, kA, iA, kB, ord, nullptr)) ||
+      (rc = pass(k_rs_count<2>, k_rs_scatter<2>, kB, ord, kA, iA, nullptr)) ||
+      (rc = pass(k_rs_count<3>, k_rs_scatter<3>, kA, iA, nullptr, ord, ordp)))
+    return rc;
+  hipLaunchKernelGGL(k_samp_pick, dim3(1), dim3(CW), PICK_LDS, s, pb, N, sd, ord, ordp, out, st,
+                     hist);
   CX_HIP(hipGetLastError());
   return CX_OK;
 }

@@ -30,6 +30,8 @@ def logits_of(kind, n, seed):
         return np.ones(n, np.float32)
     if kind == "steps":  # many exact ties at several levels
         return (rng.integers(0, 6, n) * 0.5).astype(np.float32)
+    if kind == "soft":  # nearly flat and untied: the random-init model's logits
+        return rng.normal(0, 0.3, n).astype(np.float32)
     raise ValueError(kind)
 
 
@@ -37,7 +39,8 @@ CASES = [
     ("normal", 151936, 0.8, 0.9), ("normal", 151936, 1.0, 1.0), ("normal", 151936, 1.5, 0.5),
     ("peaked", 151936, 0.7, 0.95), ("normal", 3000, 1.0, 0.0), ("flat", 5000, 1.0, 0.9),
     ("steps", 4000, 1.0, 0.7), ("normal", 1, 1.0, 0.9), ("normal", 7, 2.0, 1.0),
-    ("peaked", 128256, 0.6, 1.0),
+    ("peaked", 128256, 0.6, 1.0), ("flat", 151936, 0.8, 0.9), ("soft", 151936, 0.8, 0.9),
+    ("soft", 151936, 1.0, 0.999), ("steps", 100000, 1.0, 0.95),
 ]
 
 
@@ -53,6 +56,20 @@ def test_sampler_matches_oracle(S, dev, kind, n, temp, top_p):
     want = [o.choose(lg) for _ in range(draws)]
     assert got == want
     assert g.estado == o.state
+
+
+def test_a_nan_top_p_keeps_the_candidates(S, dev):
+    """top_p NaN (f32::clamp keeps it): the candidates' mass is not below it,
+    so the nucleus is the 1024 most probable tokens, whole
+    (src/sampler.rs:96-114)."""
+    lg = logits_of("soft", 20000, 3)
+    d = torch.from_numpy(lg).to(dev)
+    g = S.Muestreador(77, 1.0, float("nan"))
+    o = O.Sampler(77, 1.0, float("nan"))
+    got = [g.elegir(d) for _ in range(20)]
+    assert got == [o.choose(lg) for _ in range(20)]
+    order = np.lexsort((np.arange(lg.size), -lg))  # descending logit, then index
+    assert set(got) <= set(order[:1024].tolist())
 
 
 def test_greedy_and_empty(S, dev):
