@@ -256,16 +256,24 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 // then quantized for the output projection (64 values are whole
 // sub-blocks). Bit-identical to the scalar reference.
 constexpr uint32_t SC_P = 64;     // positions per scores wave
-constexpr uint32_t PV_DS = 32;    // head dims per softmax-V workgroup (wave 0's lanes)
-constexpr uint32_t PV_STP = 128;  // positions per V stage (16 KiB)
-constexpr uint32_t PV_NST = 8;    // V stages in the LDS ring (128 KiB)
-constexpr uint32_t PV_IPS = PV_STP * PV_DS * 4 / 1024;  // 1 KiB loads per stage
-constexpr uint32_t PV_IPW = PV_IPS / 4;                  // per wave
-constexpr uint32_t PV_LPP = PV_DS / 4;                   // lanes per position in a load
-static_assert(PV_IPW >= 1 && PV_DS % 32 == 0, "whole loads per wave");
-// A wave tracks at most 63 outstanding loads (vmcnt is 6 bits): its share
-// of the scores (<= 4 loads for 4096 positions) plus 7 stages ahead (28).
-static_assert(4 + (PV_NST - 1) * PV_IPW <= 63, "too many loads in flight");
+constexpr uint32_t PV_STP = 128;  // positions per V stage
+// The softmax-V kernel's shape: DS head dims per workgroup (wave 0's lanes),
+// NST V stages of PV_STP positions in the LDS ring (128 KiB either way).
+// One query token (decode) takes 32 dims: twice the workgroups of 64, so the
+// shared softmax and chains run on more CUs at once; many query tokens
+// (prefill) take 64, which does that shared work half as often.
+template <uint32_t DS>
+struct PvShape {
+  static constexpr uint32_t NST = 32768 / (PV_STP * DS);
+  static constexpr uint32_t IPS = PV_STP * DS * 4 / 1024;  // 1 KiB loads per stage
+  static constexpr uint32_t IPW = IPS / 4;                  // per wave
+  static constexpr uint32_t LPP = DS / 4;                   // lanes per position in a load
+  static_assert(IPW >= 1 && DS % 32 == 0 && NST >= 2, "whole loads per wave");
+  // A wave tracks at most 63 outstanding loads (vmcnt is 6 bits): its share
+  // of the scores (<= 4 loads for 4096 positions) plus NST - 1 stages ahead.
+  static_assert(4 + (NST - 1) * IPW <= 63, "too many loads in flight");
+};
+
 
 __host__ __device__ constexpr uint32_t sc_stride(uint32_t cap) { return (cap + 3) / 4 * 4; }
 // LDS floats for a head's scores: whole 1 KiB loads
@@ -420,7 +428,7 @@ __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) 
 
 // 256 threads: every wave streams its share of the V ring (4x the loads in
 // flight of one wave); wave 0's lanes run the order-exact accumulation.
-template <int HD, int SUB>
+template <int HD, int SUB, uint32_t PV_DS>
 __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
                                                   uint32_t heads, uint32_t kvh,
                                                   const cx_dstate* st, uint32_t cap, float* out,
@@ -431,6 +439,8 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   __shared__ float red[4];
   // query token z (blockIdx.z) sits at position st->pos + z
   const uint32_t z = blockIdx.z, total = st->pos + z + 1, h = blockIdx.x, g = h / (heads / kvh);
+  using PS = PvShape<PV_DS>;
+  constexpr uint32_t PV_NST = PS::NST, PV_IPW = PS::IPW, PV_LPP = PS::LPP;
   const uint32_t d0 = blockIdx.y * PV_DS, kvd = kvh * HD;
   sc_all += (size_t)z * heads * sc_stride(cap);
   out += (size_t)z * heads * HD;
@@ -763,14 +773,20 @@ int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
                      sc_bytes, s, a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads,
                      a.kvh, a.st, scale, a.sc, a.cap);
   CX_HIP(hipGetLastError());
-  const size_t lds = (sc_lds(a.cap) + PV_NST * PV_STP * PV_DS) * sizeof(float);
-  const dim3 grid(a.heads, HD / PV_DS, T);
-  if (a.sub == 16)
-    hipLaunchKernelGGL((k_attn_seq<HD, 16>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads, a.kvh,
-                       a.st, a.cap, a.out, a.xq, a.xe, a.xs);
-  else
-    hipLaunchKernelGGL((k_attn_seq<HD, 32>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads, a.kvh,
-                       a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+  const size_t lds = (sc_lds(a.cap) + 32768) * sizeof(float);  // scores, then the V ring
+  if (T > 1) {  // many query tokens: 64 dims a workgroup, f32 output only
+    const dim3 grid(a.heads, HD / 64, T);
+    hipLaunchKernelGGL((k_attn_seq<HD, 32, 64>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads,
+                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+  } else {
+    const dim3 grid(a.heads, HD / 32, T);
+    if (a.sub == 16)
+      hipLaunchKernelGGL((k_attn_seq<HD, 16, 32>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads,
+                         a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+    else
+      hipLaunchKernelGGL((k_attn_seq<HD, 32, 32>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads,
+                         a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+  }
   CX_HIP(hipGetLastError());
   return CX_OK;
 }
