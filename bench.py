@@ -485,6 +485,40 @@ def trace_summary(path):
               f"{statistics.median(ds) / 1e3:9.2f}")
 
 
+def token_summary(path, ntok=8):
+    """Per decode token from a rocprofv3 kernel trace of a decode run: the
+    kernels between consecutive lm_head launches (the largest GEMV grid),
+    averaged over the last `ntok` tokens."""
+    import collections
+    import csv
+    import re
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            g = int(r.get("Grid_Size_X", r.get("Grid_Size"))) // int(
+                r.get("Workgroup_Size_X", r.get("Workgroup_Size")))
+            rows.append((r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]), g))
+    rows.sort(key=lambda r: r[1])
+    lm_grid = max(r[3] for r in rows if "k_gemv" in r[0])
+    lm = [i for i, r in enumerate(rows) if r[3] == lm_grid and "k_gemv" in r[0]]
+    per = collections.defaultdict(list)
+    spans = []
+    for a, b in zip(lm[-ntok - 1:-1], lm[-ntok:]):
+        seg = rows[a + 1:b + 1]
+        spans.append(seg[-1][2] - rows[a][2])
+        for r in seg:
+            m = re.search(r"(k_[a-z_0-9]+(<[^>]*>)?)", r[0])
+            per[(m.group(1) if m else r[0][:40], r[3])].append(r[2] - r[1])
+    busy = sum(sum(v) for v in per.values()) / ntok
+    print(f"{ntok} tokens: span {statistics.mean(spans) / 1e3:.1f} us per token on the GPU, "
+          f"kernel time {busy / 1e3:.1f} us")
+    print("| kernel | workgroups | calls/token | avg µs | µs/token |")
+    print("|---|---:|---:|---:|---:|")
+    for (k, g), v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| {k} | {g} | {len(v) // ntok} | {statistics.mean(v) / 1e3:.2f} | "
+              f"{sum(v) / 1e3 / ntok:.1f} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -497,6 +531,12 @@ def main():
     ap.add_argument("--batched-only", action="store_true",
                     help="only the config-4 batched contraction (GPU side), e.g. under rocprofv3")
     ap.add_argument("--trace-summary")
+    ap.add_argument("--per-token", type=int, default=0,
+                    help="with --trace-summary: the per-token breakdown of the last N decode tokens")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the headline decode (e.g. under rocprofv3)")
+    ap.add_argument("--sampled-only", action="store_true",
+                    help="only the temperature/top-p decode of the 3B model")
     ap.add_argument("--config5-only", action="store_true",
                     help="only BASELINE config 5 (8B shape, 8K context)")
     ap.add_argument("--no-config5", action="store_true")
@@ -504,7 +544,10 @@ def main():
                     help="only the daiss-0.5b Q8_0 decode (the 32-value block GEMV)")
     a = ap.parse_args()
     if a.trace_summary:
-        trace_summary(a.trace_summary)
+        if a.per_token:
+            token_summary(a.trace_summary, a.per_token)
+        else:
+            trace_summary(a.trace_summary)
         return 0
     if a.gemv_probe:
         gemv_probe()
@@ -522,6 +565,12 @@ def main():
     if a.config5_only:
         print(json.dumps(config5_bench(F, L)), flush=True)
         return 0
+    if a.sampled_only:
+        m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)
+        print(json.dumps(sampled_bench(m, prompt_tokens(a.prompt, F.DAISS_3B.vocab), a.steps,
+                                       a.warmup)), flush=True)
+        m.close()
+        return 0
     if a.small_only:
         print(json.dumps(small_model_bench(F, L, a.steps, a.warmup, a.prompt)), flush=True)
         return 0
@@ -531,6 +580,12 @@ def main():
         return 0
     m, prompt, toks, timed, total_ms = decode_bench(F, L, a.steps, a.warmup, a.prompt)
     tok_s = a.steps / (total_ms * 1e-3)
+    if a.decode_only:
+        print(json.dumps({"decode_tok_per_s": round(tok_s, 2),
+                          "median_us_per_token": round(statistics.median(timed) * 1000, 2)}),
+              flush=True)
+        m.close()
+        return 0
     per_tok_bytes = m.bytes_por_token()
     kv_bytes = 2 * F.DAISS_3B.capas * F.DAISS_3B.dim_kv() * 4 * (a.prompt + a.warmup + a.steps // 2)
     prefill = prefill_bench(m, prompt)
