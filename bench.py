@@ -165,6 +165,7 @@ def small_model_bench(F, L, steps=128, warmup=8, prompt_len=512):
            "first_tokens": [int(t) for t in toks[:8]]}
     log(f"[bench] daiss-0.5b Q8_0: {out['tok_per_s']} tok/s ({out['median_us_per_token']} us "
         f"median), {out['effective_GBps']} GB/s effective")
+    out["prefill"] = prefill_bench(m, prompt)
     m.close()
     return out
 

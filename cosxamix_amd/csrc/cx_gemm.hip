@@ -336,6 +336,119 @@ __global__ __launch_bounds__(64 * RW * AW * KS) void k_gemm(GemmParams P) {
   }
 }
 
+// ------------------------------------------- 32-value blocks (Q8_0, Q5_0)
+// The reference's buffer path (ops::matmul_i8_directo, src/ops.rs:310-414;
+// its m >= 24 blocked path adds in another order, src/ops.rs:726): one
+// v_mfma_i32_16x16x32_i8 per block gives a 16 (activation rows) x 16 (weight
+// rows) tile of exact block dots E; each lane applies the GEMV's term
+// (d * xe) * E to its four outputs and adds them block after block from 0,
+// so every output equals k_gemv32's bit for bit. A workgroup of 4 waves
+// covers 64 weight rows x 16 activation rows; the operands are read
+// straight from global memory (rows of 34- and 22-byte blocks sit at any
+// even offset: 16-bit loads), GB32_DEPTH blocks ahead of the MFMA.
+template <int T> struct GB;
+template <> struct GB<CX_Q8_0> {
+  static constexpr int BPB = 34;
+  struct Raw {
+    uint16_t d, q[4];
+  };
+  // d and the quants at positions 8g .. 8g+7 of the block
+  __device__ static void load(const uint8_t* blk, int g, Raw& r) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+    r.d = h[0];
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.q[i] = h[1 + 4 * g + i];
+  }
+  __device__ static long operand(const Raw& r, int) {
+    const uint32_t lo = (uint32_t)r.q[0] | ((uint32_t)r.q[1] << 16);
+    const uint32_t hi = (uint32_t)r.q[2] | ((uint32_t)r.q[3] << 16);
+    return (long)(((uint64_t)hi << 32) | lo);
+  }
+};
+template <> struct GB<CX_Q5_0> {
+  static constexpr int BPB = 22;
+  struct Raw {
+    uint16_t d, qh[2], qs[4];
+  };
+  // d, the fifth bits and the nibble bytes of positions 8g .. 8g+7: value
+  // i < 16 is the low nibble of qs[i], value 16 + i the high one
+  __device__ static void load(const uint8_t* blk, int g, Raw& r) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+    r.d = h[0];
+    r.qh[0] = h[1];
+    r.qh[1] = h[2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.qs[i] = h[3 + 4 * (g & 1) + i];
+  }
+  __device__ static uint32_t spread4(uint32_t t) {  // bit i -> bit 4 of byte i
+    return ((t & 1u) << 4) | ((t & 2u) << 11) | ((t & 4u) << 18) | ((t & 8u) << 25);
+  }
+  __device__ static long operand(const Raw& r, int g) {
+    const uint32_t qh = (uint32_t)r.qh[0] | ((uint32_t)r.qh[1] << 16);
+    const uint32_t sh = g < 2 ? 0u : 4u;
+    const uint32_t w0 = ((uint32_t)r.qs[0] | ((uint32_t)r.qs[1] << 16)) >> sh;
+    const uint32_t w1 = ((uint32_t)r.qs[2] | ((uint32_t)r.qs[3] << 16)) >> sh;
+    const uint32_t t = (qh >> (8 * g)) & 0xFFu;
+    // (u - 16) in every byte, u in 0..31: biased by 128 so no byte borrows
+    const uint32_t lo = (((w0 & 0x0F0F0F0Fu) | spread4(t & 15u)) | 0x80808080u) - 0x10101010u;
+    const uint32_t hi = (((w1 & 0x0F0F0F0Fu) | spread4(t >> 4)) | 0x80808080u) - 0x10101010u;
+    return (long)(((uint64_t)(hi ^ 0x80808080u) << 32) | (lo ^ 0x80808080u));
+  }
+};
+
+constexpr int GB32_DEPTH = 4;
+
+template <int T>
+__global__ __launch_bounds__(256) void k_gemm32(GemmParams P) {
+  using Q = GB<T>;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  // the activation tiles of one row tile share blockIdx % 8 (one XCD's L2)
+  const uint32_t b = blockIdx.x, A = P.act_tiles;
+  const uint32_t rt = b / (8 * A) * 8 + b % 8, at = b / 8 % A;
+  if (rt >= P.row_tiles) return;
+  const uint32_t r = rt * 64 + 16 * wave + c16;  // this lane's weight row (B column)
+  const uint32_t a0 = at * 16;
+  const uint8_t* wrow = P.w + (size_t)min(r, P.n - 1) * P.row_bytes;  // past the end: a valid row
+  const int8_t* xrow = P.xq + (size_t)(a0 + c16) * P.k + 8 * g;     // A operand: row a0 + c16
+  const float* xe = P.xexs + a0 + 4 * g;  // block J: xe of the tile's rows at J * 2 * m_pad
+  const uint32_t nb = P.k / 32;
+  typename Q::Raw wr[GB32_DEPTH];
+  long ax[GB32_DEPTH];
+  float4 xv[GB32_DEPTH];
+  auto fetch = [&](uint32_t j, int slot) {
+    Q::load(wrow + (size_t)j * Q::BPB, g, wr[slot]);
+    ax[slot] = *reinterpret_cast<const long*>(xrow + 32 * j);
+    xv[slot] = *reinterpret_cast<const float4*>(xe + (size_t)j * 2 * P.m_pad);
+  };
+#pragma unroll
+  for (int d = 0; d < GB32_DEPTH; d++)
+    if ((uint32_t)d < nb) fetch(d, d);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t j0 = 0; j0 < nb; j0 += GB32_DEPTH) {
+#pragma unroll
+    for (int d = 0; d < GB32_DEPTH; d++) {
+      const uint32_t j = j0 + d;
+      if (j < nb) {
+        v4i e = {0, 0, 0, 0};
+        e = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax[d], Q::operand(wr[d], g), e, 0, 0, 0);
+        const float dw = cx_h2f(wr[d].d);
+        const float xs4[4] = {xv[d].x, xv[d].y, xv[d].z, xv[d].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] += dw * xs4[i] * (float)e[i];
+        if (j + GB32_DEPTH < nb) fetch(j + GB32_DEPTH, d);
+      }
+    }
+  }
+  if (r < P.n) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t a = a0 + 4 * g + i;
+      if (a < P.m) P.dst[(size_t)a * P.n + r] = acc[i];
+    }
+  }
+}
+
 // ops::cuantizar_i8_en (src/ops.rs:178-198) of m rows into the layout above:
 // xq rows [m, m_pad) and their xe, xs are zero
 __global__ __launch_bounds__(256) void k_quantize_gemm(const float* x, uint32_t m, uint32_t k,
@@ -443,9 +556,27 @@ int launch(GemmParams& P, hipStream_t s) {
 // every tile height (16, 32 or 64 rows) divides 64
 inline uint32_t pad64(size_t m) { return (uint32_t)((m + 63) / 64 * 64); }
 
+// the 32-value block contraction over rows quantized in scratch (m_pad set)
+int contract32(int type, GemmParams& P, hipStream_t s) {
+  P.xq = scratch_xq(P.scratch);
+  P.xexs = scratch_xexs(P.scratch, P.m_pad, P.k);
+  P.row_tiles = (P.n + 63) / 64;
+  P.act_tiles = (P.m + 15) / 16;
+  const size_t grid = (size_t)(P.row_tiles + 7) / 8 * 8 * P.act_tiles;
+  CX_REQUIRE(grid < (1ull << 31), "gemm: %u x %u is too large", P.n, P.m);
+  if (type == CX_Q8_0)
+    hipLaunchKernelGGL(k_gemm32<CX_Q8_0>, dim3((unsigned)grid), dim3(256), 0, s, P);
+  else
+    hipLaunchKernelGGL(k_gemm32<CX_Q5_0>, dim3((unsigned)grid), dim3(256), 0, s, P);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
 }  // namespace
 
-bool cx_gemm_supported(int type) { return type == CX_Q4_K || type == CX_Q5_K; }
+bool cx_gemm_supported(int type) {
+  return type == CX_Q4_K || type == CX_Q5_K || type == CX_Q8_0 || type == CX_Q5_0;
+}
 
 size_t cx_gemm_scratch_bytes(size_t m, size_t k) {
   const size_t m_pad = (m + 63) / 64 * 64;
@@ -456,11 +587,12 @@ int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* 
                    float* dst, void* scratch, hipStream_t s) {
   CX_REQUIRE(cx_gemm_supported(type), "gemm: type %d has no MFMA path", type);
   CX_REQUIRE(w && lhs && dst && scratch, "gemm: null pointer");
-  CX_REQUIRE(k % 256 == 0 && k > 0, "gemm: k=%zu is not a multiple of 256", k);
+  const size_t vpb = (size_t)cx_vpb(type);
+  CX_REQUIRE(k % vpb == 0 && k > 0, "gemm: k=%zu is not a multiple of %zu", k, vpb);
   CX_REQUIRE(n < (1u << 31) && m < (1u << 24) && k < (1u << 24), "gemm: shape too large");
-  CX_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)lhs & 15) == 0 &&
+  CX_REQUIRE(((uintptr_t)w & (cx_is_block32(type) ? 1 : 15)) == 0 && ((uintptr_t)lhs & 15) == 0 &&
                  ((uintptr_t)scratch & 255) == 0,
-             "gemm: weights and activations must be 16-byte aligned");
+             "gemm: weights (16-byte; Q8_0/Q5_0 2-byte) and activations (16-byte) misaligned");
   if (!n || !m) return CX_OK;
   GemmParams P{};
   P.lhs = lhs;
@@ -470,14 +602,19 @@ int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* 
   P.n = (uint32_t)n;
   P.k = (uint32_t)k;
   P.m = (uint32_t)m;
-  P.nb = (uint32_t)(k / 256);
+  P.nb = (uint32_t)(k / vpb);
   P.row_bytes = P.nb * cx_bpb(type);
+  if (cx_is_block32(type)) {
+    P.m_pad = pad64(m);
+    const int rc = quantize(lhs, P.m, P.k, P.m_pad, P.scratch, s);
+    return rc ? rc : contract32(type, P, s);
+  }
   return type == CX_Q4_K ? launch<CX_Q4_K>(P, s) : launch<CX_Q5_K>(P, s);
 }
 
 int cx_gemm_quantize(const float* lhs, size_t m, size_t k, void* scratch, hipStream_t s) {
   CX_REQUIRE(lhs && scratch, "gemm: null pointer");
-  CX_REQUIRE(k % 256 == 0 && k > 0 && k < (1u << 24) && m < (1u << 24), "gemm: %zu x %zu", m, k);
+  CX_REQUIRE(k % 32 == 0 && k > 0 && k < (1u << 24) && m < (1u << 24), "gemm: %zu x %zu", m, k);
   CX_REQUIRE(((uintptr_t)lhs & 15) == 0 && ((uintptr_t)scratch & 255) == 0,
              "gemm: activations must be 16-byte and scratch 256-byte aligned");
   if (!m) return CX_OK;
@@ -488,10 +625,11 @@ int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, floa
                   const void* scratch, hipStream_t s) {
   CX_REQUIRE(cx_gemm_supported(type), "gemm: type %d has no MFMA path", type);
   CX_REQUIRE(w && dst && scratch, "gemm: null pointer");
-  CX_REQUIRE(k % 256 == 0 && k > 0, "gemm: k=%zu is not a multiple of 256", k);
+  const size_t vpb = (size_t)cx_vpb(type);
+  CX_REQUIRE(k % vpb == 0 && k > 0, "gemm: k=%zu is not a multiple of %zu", k, vpb);
   CX_REQUIRE(n < (1u << 31) && m < (1u << 24) && k < (1u << 24), "gemm: shape too large");
-  CX_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)scratch & 255) == 0,
-             "gemm: weights must be 16-byte and scratch 256-byte aligned");
+  CX_REQUIRE(((uintptr_t)w & (cx_is_block32(type) ? 1 : 15)) == 0 && ((uintptr_t)scratch & 255) == 0,
+             "gemm: weights (16-byte; Q8_0/Q5_0 2-byte) or scratch (256-byte) misaligned");
   if (!n || !m) return CX_OK;
   GemmParams P{};
   P.scratch = const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(scratch));
@@ -501,7 +639,8 @@ int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, floa
   P.k = (uint32_t)k;
   P.m = (uint32_t)m;
   P.m_pad = pad64(m);
-  P.nb = (uint32_t)(k / 256);
+  P.nb = (uint32_t)(k / vpb);
   P.row_bytes = P.nb * cx_bpb(type);
+  if (cx_is_block32(type)) return contract32(type, P, s);
   return type == CX_Q4_K ? contract<CX_Q4_K>(P, s) : contract<CX_Q5_K>(P, s);
 }

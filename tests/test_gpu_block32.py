@@ -92,6 +92,21 @@ def test_matmul_auto_rows_and_multi(ops, dev, t):
         assert torch.equal(o, one), tm
 
 
+@pytest.mark.parametrize("t", B32, ids=["Q8_0", "Q5_0"])
+@pytest.mark.parametrize("m,n,k", [(2, 64, 896), (17, 100, 896), (64, 4864, 896),
+                                   (130, 896, 4864), (33, 257, 2048)])
+def test_mfma_contraction_bit_exact(ops, dev, t, m, n, k):
+    """Several rows (the batched prefill's shape) on the int8 MFMA
+    contraction: every output equals the buffer path's, ragged tiles
+    included."""
+    w = rows_of(t, n, k, m + n)
+    lhs = np.random.default_rng(m * n).normal(0, 1, (m, k)).astype(np.float32)
+    dst = torch.empty((m, n), dtype=torch.float32, device=dev)
+    ops.matmul_auto((m, k, n), T(lhs, dev), T(w, dev), t, dst)
+    want = O.matmul_direct(t, lhs, w, n, threads=8)
+    assert np.array_equal(dst.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
 def test_q8_0_daiss_model_matches_the_oracle(dev):
     """A daiss model written in Q8_0, the reference writer's type
     (src/daiss.rs:206-220), at daiss-0.5b's widths (dim 896, 14/2 heads of
@@ -106,6 +121,12 @@ def test_q8_0_daiss_model_matches_the_oracle(dev):
     assert np.array_equal(lg, want) and top == O.argmax(want)
     got = m.generar(prompt, 24, m.nueva_cache(256))
     assert np.array_equal(got, ref.generate(prompt, 24, ref.new_cache(256)))
+    # the batched prefill (MFMA) equals token-by-token decoding, bit for bit
+    c1, c2 = m.nueva_cache(128), m.nueva_cache(128)
+    l1, _ = m.forward(prompt, c1)
+    for tok in prompt:
+        l2, _ = m.forward([tok], c2)
+    assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
 
 
 def test_qwen_0_5b_style_mixed_file_matches_the_oracle(dev, tmp_path):
