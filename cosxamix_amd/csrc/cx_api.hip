@@ -1277,17 +1277,19 @@ fail:
   return CX_ENOMEM;
 }
 
-// out[r] = W . in[r] for `rows` rows of width k. Q4_K/Q5_K: the contraction,
-// quantizing `in` unless *quantized says an earlier call of the same input
-// did; other types: the GEMV row by row on the step's activation buffers.
+// out[r] = W . in[r] for `rows` rows of width k: the MFMA contraction,
+// quantizing `in` unless *quantized (the sub-block size an earlier call of
+// the same input quantized with, or 0) already matches the type's; the GEMV
+// row by row on the step's activation buffers otherwise.
 static int prefill_matmul(cx_cache* C, int type, const uint8_t* w, uint32_t n, uint32_t k,
-                          const float* in, uint32_t rows, float* out, bool* quantized) {
+                          const float* in, uint32_t rows, float* out, int* quantized) {
   cx_model* m = C->m;
   hipStream_t s = m->stream;
   int rc;
   if (cx_gemm_supported(type)) {
-    if (!*quantized && (rc = cx_gemm_quantize(in, rows, k, C->pf.scratch, s))) return rc;
-    *quantized = true;
+    const int sub = cx_sub(type);
+    if (*quantized != sub && (rc = cx_gemm_quantize(in, rows, k, sub, C->pf.scratch, s))) return rc;
+    *quantized = sub;
     return cx_gemm_apply(type, w, n, k, rows, out, C->pf.scratch, s);
   }
   const cx_qact act{m->xq, m->xe, m->xs};
@@ -1314,7 +1316,7 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
     float* kc = C->kv + (size_t)li * 2 * C->cap * kvd;
     float* vc = kc + C->cap * kvd;
     // src/forward.rs:422-464
-    bool qd = false;
+    int qd = 0;
     if ((rc = cx_launch_norm_rows(P.x, L.attn_norm, nt, D, c.eps, P.nrm, s)) ||
         (rc = prefill_matmul(C, L.t_q, L.q, D, D, P.nrm, nt, P.q, &qd)) ||
         (rc = prefill_matmul(C, L.t_k, L.k, kvd, D, P.nrm, nt, P.k, &qd)) ||
@@ -1342,17 +1344,17 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
     a.tokens = nt;
     if ((rc = cx_launch_attn_decode(a, s))) return rc;
     // src/forward.rs:466-491
-    qd = false;
+    qd = 0;
     if ((rc = prefill_matmul(C, L.t_o, L.o, D, D, P.att, nt, P.tmp, &qd)) ||
         (rc = cx_launch_add_rows(P.x, P.tmp, nt, D, nt, s)) ||
         (rc = cx_launch_norm_rows(P.x, L.ffn_norm, nt, D, c.eps, P.nrm, s)))
       return rc;
-    qd = false;
+    qd = 0;
     if ((rc = prefill_matmul(C, L.t_gate, L.gate, I, D, P.nrm, nt, P.g, &qd)) ||
         (rc = prefill_matmul(C, L.t_up, L.up, I, D, P.nrm, nt, P.u, &qd)) ||
         (rc = cx_launch_swiglu_rows(P.g, P.u, (size_t)nt * I, P.nrm, s)))
       return rc;
-    qd = false;
+    qd = 0;
     if ((rc = prefill_matmul(C, L.t_down, L.down, D, I, P.nrm, nt, P.tmp, &qd)) ||
         (rc = cx_launch_add_rows(P.x, P.tmp, nt, D, nt, s)))
       return rc;

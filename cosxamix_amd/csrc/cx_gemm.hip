@@ -449,8 +449,197 @@ __global__ __launch_bounds__(256) void k_gemm32(GemmParams P) {
   }
 }
 
+// ----------------------------- 16-value sub-blocks (Q2_K, Q3_K, Q6_K)
+// A 32-value group of a super-block holds two sub-blocks: lanes 16..31 of
+// the group's MFMA K range (lane groups g = 0, 1) are sub-block 2G and
+// 32..63 (g = 2, 3) sub-block 2G + 1. Two MFMAs per group, each with the
+// other sub-block's weight bytes zeroed, give the two exact sums; each lane
+// then applies the GEMV's term (k_gemv's KQ<T>) and adds in sub-block order,
+// so every output equals the per-row GEMV bit for bit. Operands come
+// straight from global memory (16-bit loads: 84-, 110- and 210-byte blocks
+// leave rows at any even offset).
+template <int T> struct GK;
+__device__ inline long pack8(uint32_t lo, uint32_t hi) {
+  return (long)(((uint64_t)hi << 32) | lo);
+}
+__device__ inline uint32_t w16(const uint16_t* h) { return (uint32_t)h[0] | ((uint32_t)h[1] << 16); }
+
+// Q2_K, 84 B: scales(16: low nibble scale, high nibble min) qs(64) d dmin;
+// value (qs[32(G/4) + i] >> 2(G%4)) & 3 (src/kernels/q2k.rs:41-69)
+template <> struct GK<CX_Q2_K> {
+  static constexpr int BPB = 84;
+  struct Raw {
+    uint16_t q[4], sc, d, dm;
+  };
+  __device__ static void load(const uint8_t* blk, int G, int g, Raw& r) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+    const int q0 = (16 + 32 * (G / 4) + 8 * g) / 2;
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.q[i] = h[q0 + i];
+    r.sc = h[G];  // the scale bytes of sub-blocks 2G, 2G+1
+    r.d = h[40];
+    r.dm = h[41];
+  }
+  __device__ static long operand(const Raw& r, int G, int) {
+    const uint32_t sh = 2 * (G % 4);
+    return pack8((w16(r.q) >> sh) & 0x03030303u, (w16(r.q + 2) >> sh) & 0x03030303u);
+  }
+  __device__ static float term(const Raw& r, int G, int hf, int e, float xe, float xs) {
+    (void)G;
+    const uint32_t sc = hf ? (r.sc >> 8) : (r.sc & 0xFFu);
+    const float d = cx_h2f(r.d), dm = cx_h2f(r.dm);
+    return xe * (d * (float)(sc & 0xF) * (float)e - dm * (float)(sc >> 4) * xs);
+  }
+};
+
+// Q3_K, 110 B: hmask(32) qs(64) scales(12) d; value (q + 4) =
+// ((qs[32(G/4) + i] >> 2(G%4)) & 3) | ((hmask[i] >> G) & 1) << 2
+// (src/kernels/scalar.rs:236-275), scales as quant::escalas_q3k
+template <> struct GK<CX_Q3_K> {
+  static constexpr int BPB = 110;
+  struct Raw {
+    uint16_t q[4], hm[4], sw[6], d;
+  };
+  __device__ static void load(const uint8_t* blk, int G, int g, Raw& r) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+    const int q0 = (32 + 32 * (G / 4) + 8 * g) / 2;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      r.q[i] = h[q0 + i];
+      r.hm[i] = h[4 * g + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 6; i++) r.sw[i] = h[48 + i];
+    r.d = h[54];
+  }
+  __device__ static long operand(const Raw& r, int G, int) {
+    const uint32_t sh = 2 * (G % 4);
+    const uint32_t lo = ((w16(r.q) >> sh) & 0x03030303u) | (((w16(r.hm) >> G) & 0x01010101u) << 2);
+    const uint32_t hi =
+        ((w16(r.q + 2) >> sh) & 0x03030303u) | (((w16(r.hm + 2) >> G) & 0x01010101u) << 2);
+    return pack8(lo, hi);
+  }
+  // the 6-bit signed scale of sub-block s (src/quant.rs:87-106)
+  __device__ static float esc(const Raw& r, int s) {
+    const uint32_t m1 = 0x03030303u, m2 = 0x0F0F0F0Fu;
+    const uint32_t a0 = w16(r.sw), a1 = w16(r.sw + 2), t = w16(r.sw + 4);
+    uint32_t w;
+    switch (s / 4) {
+      case 0: w = (a0 & m2) | ((t & m1) << 4); break;
+      case 1: w = (a1 & m2) | (((t >> 2) & m1) << 4); break;
+      case 2: w = ((a0 >> 4) & m2) | (((t >> 4) & m1) << 4); break;
+      default: w = ((a1 >> 4) & m2) | (((t >> 6) & m1) << 4); break;
+    }
+    return (float)(int8_t)(uint8_t)(w >> (8 * (s % 4)));
+  }
+  __device__ static float term(const Raw& r, int G, int hf, int e, float xe, float xs) {
+    const float scale = cx_h2f(r.d) * (esc(r, 2 * G + hf) - 32.0f);
+    return xe * scale * ((float)e - 4.0f * xs);
+  }
+};
+
+// Q6_K, 210 B: ql(128) qh(64) scales(16, i8) d. Group G: half = G/4,
+// gi = G%4; value = nibble | ((qh[32 half + i] >> 2gi) & 3) << 4, the nibble
+// low (gi < 2) or high of ql[64 half + 32 (gi%2) + i] (src/kernels/scalar.rs:294-324)
+template <> struct GK<CX_Q6_K> {
+  static constexpr int BPB = 210;
+  struct Raw {
+    uint16_t ql[4], qh[4], sc, d;
+  };
+  __device__ static void load(const uint8_t* blk, int G, int g, Raw& r) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+    const int half = G / 4, gi = G % 4;
+    const int l0 = (64 * half + 32 * (gi % 2) + 8 * g) / 2, h0 = (128 + 32 * half + 8 * g) / 2;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      r.ql[i] = h[l0 + i];
+      r.qh[i] = h[h0 + i];
+    }
+    r.sc = h[96 + G];
+    r.d = h[104];
+  }
+  __device__ static long operand(const Raw& r, int G, int) {
+    const int gi = G % 4;
+    const uint32_t ns = gi < 2 ? 0u : 4u, hs = 2 * gi;
+    const uint32_t lo = ((w16(r.ql) >> ns) & 0x0F0F0F0Fu) | (((w16(r.qh) >> hs) & 0x03030303u) << 4);
+    const uint32_t hi =
+        ((w16(r.ql + 2) >> ns) & 0x0F0F0F0Fu) | (((w16(r.qh + 2) >> hs) & 0x03030303u) << 4);
+    return pack8(lo, hi);
+  }
+  __device__ static float term(const Raw& r, int G, int hf, int e, float xe, float xs) {
+    (void)G;
+    const float scale = cx_h2f(r.d) * (float)(int8_t)(uint8_t)(hf ? (r.sc >> 8) : (r.sc & 0xFFu));
+    return xe * scale * ((float)e - 32.0f * xs);
+  }
+};
+
+constexpr int GK16_DEPTH = 3;
+
+template <int T>
+__global__ __launch_bounds__(256) void k_gemm16(GemmParams P) {
+  using Q = GK<T>;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const uint32_t b = blockIdx.x, A = P.act_tiles;
+  const uint32_t rt = b / (8 * A) * 8 + b % 8, at = b / 8 % A;
+  if (rt >= P.row_tiles) return;
+  const uint32_t r = rt * 64 + 16 * wave + c16;
+  const uint32_t a0 = at * 16;
+  const uint8_t* wrow = P.w + (size_t)min(r, P.n - 1) * P.row_bytes;
+  const int8_t* xrow = P.xq + (size_t)(a0 + c16) * P.k + 8 * g;
+  const float* xe = P.xexs + a0 + 4 * g;  // sub-block J: xe at J * 2 * m_pad, xs m_pad after
+  const uint32_t ng = P.k / 32;          // 32-value groups
+  typename Q::Raw wr[GK16_DEPTH];
+  long ax[GK16_DEPTH];
+  float4 xv[GK16_DEPTH][4];  // xe, xs of sub-block 2j, then of 2j + 1
+  auto fetch = [&](uint32_t j, int slot) {
+    Q::load(wrow + (size_t)(j / 8) * Q::BPB, (int)(j % 8), g, wr[slot]);
+    ax[slot] = *reinterpret_cast<const long*>(xrow + 32 * j);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const float* e = xe + (size_t)(2 * j + h) * 2 * P.m_pad;
+      xv[slot][2 * h] = *reinterpret_cast<const float4*>(e);
+      xv[slot][2 * h + 1] = *reinterpret_cast<const float4*>(e + P.m_pad);
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < GK16_DEPTH; d++)
+    if ((uint32_t)d < ng) fetch(d, d);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t j0 = 0; j0 < ng; j0 += GK16_DEPTH) {
+#pragma unroll
+    for (int d = 0; d < GK16_DEPTH; d++) {
+      const uint32_t j = j0 + d;
+      if (j < ng) {
+        const int G = (int)(j % 8);
+        const long bw = Q::operand(wr[d], G, g);
+        v4i e0 = {0, 0, 0, 0}, e1 = {0, 0, 0, 0};
+        e0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax[d], g < 2 ? bw : 0l, e0, 0, 0, 0);
+        e1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax[d], g < 2 ? 0l : bw, e1, 0, 0, 0);
+        const float4 xe0 = xv[d][0], xs0 = xv[d][1], xe1 = xv[d][2], xs1 = xv[d][3];
+        const float a_e0[4] = {xe0.x, xe0.y, xe0.z, xe0.w}, a_s0[4] = {xs0.x, xs0.y, xs0.z, xs0.w};
+        const float a_e1[4] = {xe1.x, xe1.y, xe1.z, xe1.w}, a_s1[4] = {xs1.x, xs1.y, xs1.z, xs1.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          acc[i] += Q::term(wr[d], G, 0, e0[i], a_e0[i], a_s0[i]);
+          acc[i] += Q::term(wr[d], G, 1, e1[i], a_e1[i], a_s1[i]);
+        }
+        if (j + GK16_DEPTH < ng) fetch(j + GK16_DEPTH, d);
+      }
+    }
+  }
+  if (r < P.n) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t a = a0 + 4 * g + i;
+      if (a < P.m) P.dst[(size_t)a * P.n + r] = acc[i];
+    }
+  }
+}
+
 // ops::cuantizar_i8_en (src/ops.rs:178-198) of m rows into the layout above:
 // xq rows [m, m_pad) and their xe, xs are zero
+template <int SUB>
 __global__ __launch_bounds__(256) void k_quantize_gemm(const float* x, uint32_t m, uint32_t k,
                                                        uint32_t m_pad, int8_t* xq, float* xexs) {
   const size_t i = 8 * (blockIdx.x * 256ull + threadIdx.x);
@@ -461,10 +650,10 @@ __global__ __launch_bounds__(256) void k_quantize_gemm(const float* x, uint32_t 
   uint32_t lo, hi;
   float d;
   int32_t s;
-  cx_quant8_vals<32>(v, lo, hi, d, s);
+  cx_quant8_vals<SUB>(v, lo, hi, d, s);
   *reinterpret_cast<uint2*>(xq + i) = make_uint2(lo, hi);
-  if ((col & 31) == 0) {
-    float* e = xexs + (size_t)(col / 32) * 2 * m_pad + a;
+  if ((col & (SUB - 1)) == 0) {
+    float* e = xexs + (size_t)(col / SUB) * 2 * m_pad + a;
     e[0] = d;
     e[m_pad] = (float)s;
   }
@@ -514,12 +703,16 @@ inline float* scratch_xexs(uint8_t* scratch, size_t m_pad, size_t k) {
   return reinterpret_cast<float*>(scratch + (m_pad * k + 255) / 256 * 256);
 }
 
-int quantize(const float* lhs, uint32_t m, uint32_t k, uint32_t m_pad, uint8_t* scratch,
+int quantize(const float* lhs, uint32_t m, uint32_t k, uint32_t m_pad, int sub, uint8_t* scratch,
              hipStream_t s) {
   const size_t qgrid = ((size_t)m_pad * k / 8 + 255) / 256;
   CX_REQUIRE(qgrid < (1ull << 31), "gemm: %zu activation values is too many", (size_t)m_pad * k);
-  hipLaunchKernelGGL(k_quantize_gemm, dim3((unsigned)qgrid), dim3(256), 0, s, lhs, m, k, m_pad,
-                     scratch_xq(scratch), scratch_xexs(scratch, m_pad, k));
+  if (sub == 16)
+    hipLaunchKernelGGL(k_quantize_gemm<16>, dim3((unsigned)qgrid), dim3(256), 0, s, lhs, m, k,
+                       m_pad, scratch_xq(scratch), scratch_xexs(scratch, m_pad, k));
+  else
+    hipLaunchKernelGGL(k_quantize_gemm<32>, dim3((unsigned)qgrid), dim3(256), 0, s, lhs, m, k,
+                       m_pad, scratch_xq(scratch), scratch_xexs(scratch, m_pad, k));
   CX_HIP(hipGetLastError());
   return CX_OK;
 }
@@ -549,38 +742,42 @@ int launch(GemmParams& P, hipStream_t s) {
   const Config c = config<T>(choose(P.n, P.m), &k);
   // activation rows padded to the tile height (zero rows quantize to zero)
   P.m_pad = (P.m + c.mt - 1) / c.mt * c.mt;
-  int rc = quantize(P.lhs, P.m, P.k, P.m_pad, P.scratch, s);
+  int rc = quantize(P.lhs, P.m, P.k, P.m_pad, 32, P.scratch, s);
   return rc ? rc : contract<T>(P, s);
 }
 
 // every tile height (16, 32 or 64 rows) divides 64
 inline uint32_t pad64(size_t m) { return (uint32_t)((m + 63) / 64 * 64); }
 
-// the 32-value block contraction over rows quantized in scratch (m_pad set)
-int contract32(int type, GemmParams& P, hipStream_t s) {
+// the direct-operand contractions (32-value blocks and 16-value sub-blocks)
+// over rows quantized in scratch with the type's sub-block size (m_pad set)
+bool direct_type(int type) { return cx_is_block32(type) || cx_sub(type) == 16; }
+int contract_direct(int type, GemmParams& P, hipStream_t s) {
   P.xq = scratch_xq(P.scratch);
   P.xexs = scratch_xexs(P.scratch, P.m_pad, P.k);
   P.row_tiles = (P.n + 63) / 64;
   P.act_tiles = (P.m + 15) / 16;
   const size_t grid = (size_t)(P.row_tiles + 7) / 8 * 8 * P.act_tiles;
   CX_REQUIRE(grid < (1ull << 31), "gemm: %u x %u is too large", P.n, P.m);
-  if (type == CX_Q8_0)
-    hipLaunchKernelGGL(k_gemm32<CX_Q8_0>, dim3((unsigned)grid), dim3(256), 0, s, P);
-  else
-    hipLaunchKernelGGL(k_gemm32<CX_Q5_0>, dim3((unsigned)grid), dim3(256), 0, s, P);
+  const dim3 G((unsigned)grid), W(256);
+  switch (type) {
+    case CX_Q8_0: hipLaunchKernelGGL(k_gemm32<CX_Q8_0>, G, W, 0, s, P); break;
+    case CX_Q5_0: hipLaunchKernelGGL(k_gemm32<CX_Q5_0>, G, W, 0, s, P); break;
+    case CX_Q2_K: hipLaunchKernelGGL(k_gemm16<CX_Q2_K>, G, W, 0, s, P); break;
+    case CX_Q3_K: hipLaunchKernelGGL(k_gemm16<CX_Q3_K>, G, W, 0, s, P); break;
+    default: hipLaunchKernelGGL(k_gemm16<CX_Q6_K>, G, W, 0, s, P); break;
+  }
   CX_HIP(hipGetLastError());
   return CX_OK;
 }
 
 }  // namespace
 
-bool cx_gemm_supported(int type) {
-  return type == CX_Q4_K || type == CX_Q5_K || type == CX_Q8_0 || type == CX_Q5_0;
-}
+bool cx_gemm_supported(int type) { return cx_has_gemv(type); }
 
-size_t cx_gemm_scratch_bytes(size_t m, size_t k) {
+size_t cx_gemm_scratch_bytes(size_t m, size_t k) {  // xe and xs for sub-blocks of 16
   const size_t m_pad = (m + 63) / 64 * 64;
-  return (m_pad * k + 255) / 256 * 256 + m_pad * (k / 32) * 8;
+  return (m_pad * k + 255) / 256 * 256 + m_pad * (k / 16) * 8;
 }
 
 int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* lhs, size_t m,
@@ -590,9 +787,9 @@ int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* 
   const size_t vpb = (size_t)cx_vpb(type);
   CX_REQUIRE(k % vpb == 0 && k > 0, "gemm: k=%zu is not a multiple of %zu", k, vpb);
   CX_REQUIRE(n < (1u << 31) && m < (1u << 24) && k < (1u << 24), "gemm: shape too large");
-  CX_REQUIRE(((uintptr_t)w & (cx_is_block32(type) ? 1 : 15)) == 0 && ((uintptr_t)lhs & 15) == 0 &&
+  CX_REQUIRE(((uintptr_t)w & (direct_type(type) ? 1 : 15)) == 0 && ((uintptr_t)lhs & 15) == 0 &&
                  ((uintptr_t)scratch & 255) == 0,
-             "gemm: weights (16-byte; Q8_0/Q5_0 2-byte) and activations (16-byte) misaligned");
+             "gemm: weights (Q4_K/Q5_K 16-byte, others 2-byte) and activations (16-byte) misaligned");
   if (!n || !m) return CX_OK;
   GemmParams P{};
   P.lhs = lhs;
@@ -604,21 +801,23 @@ int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* 
   P.m = (uint32_t)m;
   P.nb = (uint32_t)(k / vpb);
   P.row_bytes = P.nb * cx_bpb(type);
-  if (cx_is_block32(type)) {
+  if (direct_type(type)) {
     P.m_pad = pad64(m);
-    const int rc = quantize(lhs, P.m, P.k, P.m_pad, P.scratch, s);
-    return rc ? rc : contract32(type, P, s);
+    const int rc = quantize(lhs, P.m, P.k, P.m_pad, cx_sub(type), P.scratch, s);
+    return rc ? rc : contract_direct(type, P, s);
   }
   return type == CX_Q4_K ? launch<CX_Q4_K>(P, s) : launch<CX_Q5_K>(P, s);
 }
 
-int cx_gemm_quantize(const float* lhs, size_t m, size_t k, void* scratch, hipStream_t s) {
+int cx_gemm_quantize(const float* lhs, size_t m, size_t k, int sub, void* scratch, hipStream_t s) {
   CX_REQUIRE(lhs && scratch, "gemm: null pointer");
+  CX_REQUIRE(sub == 16 || sub == 32, "gemm: sub-blocks of 16 or 32, not %d", sub);
   CX_REQUIRE(k % 32 == 0 && k > 0 && k < (1u << 24) && m < (1u << 24), "gemm: %zu x %zu", m, k);
   CX_REQUIRE(((uintptr_t)lhs & 15) == 0 && ((uintptr_t)scratch & 255) == 0,
              "gemm: activations must be 16-byte and scratch 256-byte aligned");
   if (!m) return CX_OK;
-  return quantize(lhs, (uint32_t)m, (uint32_t)k, pad64(m), reinterpret_cast<uint8_t*>(scratch), s);
+  return quantize(lhs, (uint32_t)m, (uint32_t)k, pad64(m), sub, reinterpret_cast<uint8_t*>(scratch),
+                  s);
 }
 
 int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, float* dst,
@@ -628,8 +827,8 @@ int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, floa
   const size_t vpb = (size_t)cx_vpb(type);
   CX_REQUIRE(k % vpb == 0 && k > 0, "gemm: k=%zu is not a multiple of %zu", k, vpb);
   CX_REQUIRE(n < (1u << 31) && m < (1u << 24) && k < (1u << 24), "gemm: shape too large");
-  CX_REQUIRE(((uintptr_t)w & (cx_is_block32(type) ? 1 : 15)) == 0 && ((uintptr_t)scratch & 255) == 0,
-             "gemm: weights (16-byte; Q8_0/Q5_0 2-byte) or scratch (256-byte) misaligned");
+  CX_REQUIRE(((uintptr_t)w & (direct_type(type) ? 1 : 15)) == 0 && ((uintptr_t)scratch & 255) == 0,
+             "gemm: weights (Q4_K/Q5_K 16-byte, others 2-byte) or scratch (256-byte) misaligned");
   if (!n || !m) return CX_OK;
   GemmParams P{};
   P.scratch = const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(scratch));
@@ -641,6 +840,6 @@ int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, floa
   P.m_pad = pad64(m);
   P.nb = (uint32_t)(k / vpb);
   P.row_bytes = P.nb * cx_bpb(type);
-  if (cx_is_block32(type)) return contract32(type, P, s);
+  if (direct_type(type)) return contract_direct(type, P, s);
   return type == CX_Q4_K ? contract<CX_Q4_K>(P, s) : contract<CX_Q5_K>(P, s);
 }

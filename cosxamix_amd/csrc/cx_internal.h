@@ -70,17 +70,18 @@ int cx_launch_swiglu_rows(const float* g, const float* u, size_t n, float* out, 
 int cx_launch_add_rows(float* y, const float* a, size_t rows, size_t n, size_t a_rows,
                        hipStream_t s);
 
-// m activation rows at once on int8 MFMA (Q4_K, Q5_K): lhs[m][k] f32 is
-// quantized into `scratch` (cx_gemm_scratch_bytes, 256-byte aligned), then
-// dst[m][n] is formed, every value bit-identical to the per-row GEMV.
+// m activation rows at once on int8 MFMA (every GEMV type): lhs[m][k] f32
+// is quantized into `scratch` (cx_gemm_scratch_bytes, 256-byte aligned),
+// then dst[m][n] is formed, every value bit-identical to the per-row GEMV.
 bool cx_gemm_supported(int type);
 size_t cx_gemm_scratch_bytes(size_t m, size_t k);
 int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* lhs, size_t m,
                    float* dst, void* scratch, hipStream_t s);
 // The same in two steps, for several matrices over one activation: quantize
-// lhs once into scratch, then contract any number of Q4_K/Q5_K matrices of
-// width k against it (scratch of cx_gemm_scratch_bytes(m, k)).
-int cx_gemm_quantize(const float* lhs, size_t m, size_t k, void* scratch, hipStream_t s);
+// lhs once into scratch in sub-blocks of `sub` (cx_sub of the types to come),
+// then contract any number of matrices of width k and that sub-block size
+// against it (scratch of cx_gemm_scratch_bytes(m, k)).
+int cx_gemm_quantize(const float* lhs, size_t m, size_t k, int sub, void* scratch, hipStream_t s);
 int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, float* dst,
                   const void* scratch, hipStream_t s);
 

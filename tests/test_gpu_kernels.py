@@ -163,6 +163,11 @@ def test_matmul_auto_rows_equal_single_rows(cx, dev):  # src/ops.rs:1364-1393
     (O.Q4_K, 11008, 2048, (8, 32, 40, 70, 512)),  # BASELINE config 4, first matrix
     (O.Q4_K, 2048, 11008, (8, 32)),                # config 4, second matrix (43 blocks)
     (O.Q5_K, 1000, 4096, (3, 17, 64, 100, 200)),   # ragged n, partial tiles
+    # the 16-value sub-block formats (two masked MFMAs a 32-value group)
+    (O.Q6_K, 2048, 11008, (2, 17, 64)),             # Q*_K_M down projections
+    (O.Q6_K, 1000, 2048, (5, 130)),
+    (O.Q3_K, 2100, 2048, (3, 33)),
+    (O.Q2_K, 777, 4096, (16, 70)),
 ])
 def test_batched_mfma_bit_identical_to_rows_and_oracle(cx, dev, t, n, k, ms):
     """matmul_auto with m > 1 (int8 MFMA path) against the single-row GEMV
