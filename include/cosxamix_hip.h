@@ -140,10 +140,10 @@ int cx_unpack_i8(int type, const uint8_t *bytes, size_t n, int8_t *q,
                  float *esc, float *off, int *sub, void *stream);
 
 /* ops::matmul_auto (src/ops.rs:1056-1093): dst[m,n] = lhs[m,k] . W[n,k]^T,
- * lhs/dst f32 row-major, W GGUF raw rows. k-quants: quantizes lhs
- * internally (m = 1: the GEMV; m > 1 of Q4_K/Q5_K: the int8 MFMA
- * contraction; both bit-identical to the row-by-row fused dot). Q8_0/Q5_0
- * (k % 32 == 0): the buffer path (matmul_i8_directo), row by row. F32/F16
+ * lhs/dst f32 row-major, W GGUF raw rows. k-quants (k % 256 == 0) and
+ * Q8_0/Q5_0 (k % 32 == 0, the buffer path of matmul_i8_directo): quantizes
+ * lhs internally; m = 1 is the GEMV, m > 1 the int8 MFMA contraction, both
+ * bit-identical to the row-by-row dot. F32/F16
  * (ops::matmul, src/ops.rs:87-156): f32 dot of each lhs row with the
  * widened weight row, equal to the reference within f32 rounding; k % 4 == 0. */
 int cx_matmul_auto(size_t m, size_t k, size_t n, const float *lhs,
