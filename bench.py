@@ -125,7 +125,7 @@ def config5_bench(F, L, steps=256, warmup=8, prefix=8192):
     kv = 2 * cfg.capas * cfg.dim_kv() * 4 * ctx_mid
     out = {"workload": "BASELINE config 5: Llama-3-8B-shape daiss model (32 layers, hidden 4096, "
                        "32/8 heads x 128, SwiGLU 14336, vocab 128256, rope 5e5), Q4_K linears, "
-                       "Q5_K ffn_down, Q4_K lm_head, f32 KV cache (split-K attention), "
+                       "Q5_K ffn_down, Q4_K lm_head, f32 KV cache (order-exact attention), "
                        f"{prefix}-token seeded random prefix, greedy decode",
            "prefix_tokens": prefix, "decode_tokens": steps, "warmup": warmup,
            "tok_per_s": round(steps / total, 2),

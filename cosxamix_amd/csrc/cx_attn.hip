@@ -36,15 +36,17 @@ constexpr uint32_t QK_P = 64;   // positions per scores workgroup
 constexpr uint32_t SV_DS = 32;  // head dims per softmax-V workgroup
 constexpr uint32_t S_SP = 256;  // positions per pass-S stage (one KiB per head)
 constexpr uint32_t S_PAD = S_SP + 36;  // 292 floats: 36 mod 64 banks apart
-constexpr uint32_t P_SP = 64;   // positions per pass-P stage
+constexpr uint32_t P_SP = 256;  // positions per pass-P stage
 constexpr uint32_t P_PAD = P_SP + 4;
+constexpr uint32_t P_VCH = P_SP * SV_DS * 4 / 1024;  // the stage's V: 1 KiB chunks
 constexpr uint32_t NSTS = 6;    // pass-S ring stages
 constexpr uint32_t MAXG = 64;   // query heads per KV group
 
 __host__ __device__ constexpr uint32_t sc_stride(uint32_t cap) { return (cap + 3) / 4 * 4; }
 __host__ __device__ constexpr uint32_t att_chunks(uint32_t cap) { return (cap + QK_P - 1) / QK_P; }
-// pass-P stage: V [P_SP][SV_DS] floats (8 KiB), then the scores [per][P_SP]
-__host__ __device__ constexpr uint32_t p_chunks(uint32_t per) { return 8 + (per + 3) / 4; }
+// pass-P stage: V [P_SP][SV_DS] floats (32 KiB), then the scores [per][P_SP]
+// (one KiB a head)
+__host__ __device__ constexpr uint32_t p_chunks(uint32_t per) { return P_VCH + per * P_SP / 256; }
 __host__ __device__ constexpr uint32_t chain_waves(uint32_t per) { return (per + 1) / 2; }
 
 // s_waitcnt vmcnt(n) for a wave-uniform n: at most n of this wave's vector
@@ -339,11 +341,11 @@ __global__ __launch_bounds__(768) void k_att_sv(const float* vc, const float* sc
     for (uint32_t ch = wave - ncw; ch < pch; ch += nhp) {
       const uint32_t j = ch * 64 + lane;  // 16-byte slot of the stage
       const float* src = sc;              // dummy: any valid address
-      if (ch < 8) {                       // V[p][0..32) of 8 positions per chunk
+      if (ch < P_VCH) {                   // V[p][0..32) of 8 positions per chunk
         const uint32_t p = s * P_SP + j / 8;
         if (p < total) src = vb + (size_t)p * kvd + 4 * (j % 8);
       } else {                            // scores[h][p]
-        const uint32_t k = j - 8 * 64, h = k / 16, p = s * P_SP + 4 * (k % 16);
+        const uint32_t k = j - P_VCH * 64, h = k / (P_SP / 4), p = s * P_SP + 4 * (k % (P_SP / 4));
         if (h < nh && p < total) src = sc + (size_t)h * stride + p;
       }
       cx_dma16_async(src, base + ch * 256);
@@ -439,9 +441,9 @@ __global__ __launch_bounds__(768) void k_att_sv(const float* vc, const float* sc
     // refill the slot the chains read in the last iteration
     if (s >= 2 && s - 2 + nstp < nsp) issue_p(s - 2 + nstp);
     if (wave >= ncw && active && s < nsp) {
-      const float* rs = ring_p + (s % nstp) * pch * 256 + 8 * 256;
+      const float* rs = ring_p + (s % nstp) * pch * 256 + P_VCH * 256;
       float* pb = pbuf + (s & 1) * nh * P_PAD;
-      // one probability a lane: at most one per helper lane per stage
+      // the stage's probabilities over the helper lanes (up to four a lane)
       for (uint32_t i = tid - 64 * ncw; i < nh * P_SP; i += 64 * nhp) {
         const uint32_t h = i / P_SP, p = i % P_SP;
         float pr = 0.0f;
@@ -455,7 +457,8 @@ __global__ __launch_bounds__(768) void k_att_sv(const float* vc, const float* sc
       const float* vs = ring_p + ((s - 1) % nstp) * pch * 256 + dd;
       const uint32_t n = min(P_SP, total - (s - 1) * P_SP);
       if (n == P_SP) {
-        pv_stage64(o, pb, vs);
+#pragma unroll 1
+        for (uint32_t b = 0; b < P_SP; b += 64) pv_stage64(o, pb + b, vs + b * SV_DS);
       } else {
         for (uint32_t p = 0; p < n; p++) o += pb[p] * vs[p * SV_DS];
       }
