@@ -1127,12 +1127,16 @@ static int enqueue_step(cx_cache* C) {
     a.xe = m->xe;
     a.xs = m->xs;
     a.sub = cx_sub(L.t_o);
+    const bool glu = L.t_gate == L.t_up && cx_glu_supported(L.t_gate) && I % 32 == 0 && D <= 8192;
+    // the attention's spare CUs pull the o-proj's and gate/up's weights into L2
+    (void)cx_gemv_prefetch_plan(L.t_o, L.o, D, D, &a.pf.job[0]);
+    if (glu) (void)cx_glu_prefetch_plan(L.t_gate, L.gate, L.up, I, D, &a.pf.job[1]);
     if ((rc = cx_launch_attn_decode(a, s))) return rc;
     // src/forward.rs:466-469: output projection added to the residual
     cx_seg o{L.o, m->x, nullptr, D};
     if ((rc = cx_launch_gemv(L.t_o, &o, 1, D, act, CX_EPI_ACCUM, nullptr, s))) return rc;
     // src/forward.rs:472-491: rmsnorm, gate/up, SwiGLU, down added to the residual
-    if (L.t_gate == L.t_up && cx_glu_supported(L.t_gate) && I % 32 == 0 && D <= 8192) {
+    if (glu) {
       // gate, up and SwiGLU in one launch, bit-identical to the three below
       if ((rc = cx_launch_gemv_glu(L.t_gate, L.gate, L.up, I, D, m->x, L.ffn_norm, c.eps,
                                    cx_sub(L.t_down), m->xq, m->xe, m->xs, s)))

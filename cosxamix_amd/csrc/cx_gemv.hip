@@ -854,6 +854,21 @@ TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
   return t;
 }
 
+// The plain (no prologue) launch's tile: the largest R <= 16 that leaves >= 2
+// tiles per CU (measured on MI355X at the 3B projection shapes)
+template <int T>
+TilePlan plain_plan(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_t* rows, int nseg) {
+  constexpr bool REG = T == CX_Q4_K || T == CX_Q5_K;  // weights straight into registers
+  TilePlan best{};
+  for (uint32_t R = 16; R >= 1; R >>= 1) {
+    TilePlan t = plan_tile(R, row_bytes, k, nsub, rows, nseg, false, REG);
+    if (t.lds > TILE_LDS_MAX) continue;
+    best = t;
+    if (t.tiles >= 512) break;
+  }
+  return best;
+}
+
 template <int T, bool NORM>
 int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   using Q = KQ<T>;
@@ -880,12 +895,7 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
       if (t.lds <= TILE_LDS_NORM_MAX) best = t;
     }
   } else {
-    for (uint32_t R = 16; R >= 1; R >>= 1) {
-      TilePlan t = plan_tile(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM, REG);
-      if (t.lds > TILE_LDS_MAX) continue;
-      best = t;
-      if (t.tiles >= 512) break;
-    }
+    best = plain_plan<T>(P.row_bytes, P.k, P.nsub, rows, P.nseg);
   }
   CX_REQUIRE(best.R, "gemv: a row of %u values does not fit in LDS", P.k);
   P.R = best.R;
@@ -1081,6 +1091,30 @@ int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t 
   }
   CX_HIP(hipGetLastError());
   return CX_OK;
+}
+
+// ------------------------------------------------------- L2 prefetch
+// The bytes workgroup t of a launch reads: tile t of the plain Q4_K/Q5_K
+// GEMV (R consecutive rows) or of the gate/up launch (GLU_ROWS rows of each
+// matrix). Workgroups go to XCDs by index, round robin, so a prefetch whose
+// workgroup t runs on XCD t % 8 leaves the tile in the L2 the GEMV's
+// workgroup t reads.
+bool cx_gemv_prefetch_plan(int type, const uint8_t* w, uint32_t n, uint32_t k, cx_l2_job* job) {
+  if ((type != CX_Q4_K && type != CX_Q5_K) || k % 256 || !n) return false;
+  const uint32_t rb = k / 256 * (uint32_t)cx_bpb(type), rows[1] = {n};
+  const TilePlan t = type == CX_Q4_K ? plain_plan<CX_Q4_K>(rb, k, k / 32, rows, 1)
+                                     : plain_plan<CX_Q5_K>(rb, k, k / 32, rows, 1);
+  if (!t.R) return false;
+  *job = cx_l2_job{w, nullptr, (size_t)n * rb, t.R * rb, t.tiles};
+  return true;
+}
+
+bool cx_glu_prefetch_plan(int type, const uint8_t* wg, const uint8_t* wu, uint32_t I, uint32_t k,
+                          cx_l2_job* job) {
+  if (!cx_glu_supported(type) || k % 256 || I % GLU_ROWS) return false;
+  const uint32_t rb = k / 256 * (uint32_t)cx_bpb(type);
+  *job = cx_l2_job{wg, wu, (size_t)I * rb, GLU_ROWS * rb, I / GLU_ROWS};
+  return true;
 }
 
 // ------------------------------------------------- activation kernels

@@ -7,6 +7,67 @@
 
 #include "cx_common.h"
 
+// An L2 prefetch run by extra workgroups of a launch that leaves most CUs
+// and most of HBM's bandwidth idle (the one-token attention). Job i reads
+// `tiles` tiles of `tile` bytes of p0 (and of p1 if set), tile t on XCD
+// t % 8, where the next launches' workgroup t reads it (workgroups go to
+// XCDs by index, round robin); a job with no tiles is skipped.
+struct cx_l2_job {
+  const uint8_t *p0, *p1;
+  size_t bytes;  // of each of p0, p1
+  uint32_t tile, tiles;
+};
+constexpr int CX_L2_JOBS = 2;
+struct cx_l2_prefetch {
+  cx_l2_job job[CX_L2_JOBS];
+};
+
+// Reads bytes [o, o + len) of base (clipped to total, 16-byte loads), eight
+// loads in flight per lane; the values feed an empty asm statement, which
+// keeps the loads and stores nothing.
+__device__ inline void cx_l2_touch(const uint8_t* base, size_t o, uint32_t len, size_t total) {
+  if (!base || o >= total) return;
+  const size_t end = (o + len < total ? o + len : total) & ~(size_t)15;
+  uint32_t acc = 0;
+  for (size_t i = o + 16 * threadIdx.x; i < end; i += 8 * 16 * blockDim.x) {
+    uint4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const size_t ij = i + (size_t)j * 16 * blockDim.x;
+      v[j] = ij < end ? *reinterpret_cast<const uint4*>(base + ij) : uint4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  asm volatile("" : : "v"(acc));
+}
+
+// Prefetch workgroup j of a launch whose first `first` workgroups (in
+// dispatch order) do other work: skips to the next multiple of 8 so that
+// tile t runs on XCD t % 8, then the jobs' tiles in order, each job from a
+// multiple of 8.
+__device__ inline void cx_l2_prefetch_run(const cx_l2_prefetch& pf, uint32_t j, uint32_t first) {
+  const uint32_t skip = (8 - first % 8) % 8;
+  if (j < skip) return;
+  uint32_t t = j - skip;
+  for (int i = 0; i < CX_L2_JOBS; i++) {
+    const cx_l2_job& b = pf.job[i];
+    if (t < b.tiles) {
+      cx_l2_touch(b.p0, (size_t)t * b.tile, b.tile, b.bytes);
+      cx_l2_touch(b.p1, (size_t)t * b.tile, b.tile, b.bytes);
+      return;
+    }
+    t -= (b.tiles + 7) / 8 * 8;
+  }
+}
+
+// The workgroups a prefetch adds to a launch of `first` workgroups
+inline uint32_t cx_l2_prefetch_groups(const cx_l2_prefetch& pf, uint32_t first) {
+  uint32_t n = 0;
+  for (int i = 0; i < CX_L2_JOBS; i++) n += (pf.job[i].tiles + 7) / 8 * 8;
+  return n ? (8 - first % 8) % 8 + n : 0;
+}
+
 // One matrix of a (possibly multi-matrix) GEMV launch. All segments of one
 // launch share the activation, the row width k and the weight type.
 struct cx_seg {
@@ -48,6 +109,13 @@ bool cx_glu_supported(int type);
 int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t I, uint32_t k,
                        const float* x, const float* w, float eps, int sub, int8_t* xq, float* xe,
                        float* xs, hipStream_t s);
+
+// A prefetch job of the tiles of the plain Q4_K/Q5_K GEMV of w (n x k) or
+// of the gate/up launch of wg and wu (I x k), each into the L2 it is read
+// from; false (and no job) where the launch has no such tiling.
+bool cx_gemv_prefetch_plan(int type, const uint8_t* w, uint32_t n, uint32_t k, cx_l2_job* job);
+bool cx_glu_prefetch_plan(int type, const uint8_t* wg, const uint8_t* wu, uint32_t I, uint32_t k,
+                          cx_l2_job* job);
 
 // Producers of the i8 activation, one value per lane:
 //   quantize   : rows x k values of x                           (ops.rs:178)

@@ -81,6 +81,7 @@ struct cx_attn_args {
   // one-token size; q already rotated and the caches already filled
   // (cos_t null), no quantized output.
   uint32_t tokens;
+  cx_l2_prefetch pf;           // optional (a and b0 null: none); one token only
 };
 int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s);
 int cx_launch_attn_exact(const cx_attn_args& a, float scale, hipStream_t s);

@@ -428,11 +428,18 @@ __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) 
 
 // 256 threads: every wave streams its share of the V ring (4x the loads in
 // flight of one wave); wave 0's lanes run the order-exact accumulation.
+// Rows of the grid past HD / PV_DS are prefetch workgroups (pf).
 template <int HD, int SUB, uint32_t PV_DS>
 __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
                                                   uint32_t heads, uint32_t kvh,
                                                   const cx_dstate* st, uint32_t cap, float* out,
-                                                  int8_t* xq, float* xe, float* xs) {
+                                                  int8_t* xq, float* xe, float* xs,
+                                                  cx_l2_prefetch pf) {
+  if (blockIdx.y >= HD / PV_DS) {
+    const uint32_t first = gridDim.x * (HD / PV_DS);
+    cx_l2_prefetch_run(pf, blockIdx.x + gridDim.x * blockIdx.y - first, first);
+    return;
+  }
   extern __shared__ __align__(16) float e[];  // sc_lds(cap) scores, then the V ring
   float* ring = e + sc_lds(cap);
   __shared__ uint64_t etab[32];  // exp's table in LDS: no global load after the prefetch
@@ -777,15 +784,16 @@ int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
   if (T > 1) {  // many query tokens: 64 dims a workgroup, f32 output only
     const dim3 grid(a.heads, HD / 64, T);
     hipLaunchKernelGGL((k_attn_seq<HD, 32, 64>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads,
-                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, cx_l2_prefetch{});
   } else {
-    const dim3 grid(a.heads, HD / 32, T);
+    const uint32_t rows = HD / 32, np = cx_l2_prefetch_groups(a.pf, a.heads * rows);
+    const dim3 grid(a.heads, rows + (np + a.heads - 1) / a.heads, T);
     if (a.sub == 16)
       hipLaunchKernelGGL((k_attn_seq<HD, 16, 32>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads,
-                         a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+                         a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
     else
       hipLaunchKernelGGL((k_attn_seq<HD, 32, 32>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads,
-                         a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs);
+                         a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   }
   CX_HIP(hipGetLastError());
   return CX_OK;
