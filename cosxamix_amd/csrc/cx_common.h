@@ -150,13 +150,15 @@ __device__ inline void cx_dma16_async(const void* g, void* l) {
       : "memory");
 }
 
-// Rust `f32 as i32` (saturating, NaN -> 0) then `as i8` (low 8 bits).
+// Rust `f32 as i32` (saturating, NaN -> 0) then `as i8` (low 8 bits),
+// without branches: r clamped to [-2^31, 2147483520] (the largest f32 below
+// 2^31) converts exactly as the in-range cast, then r >= 2^31 and NaN are
+// selected.
 __device__ inline int8_t cx_rust_i8(float r) {
-  int32_t v;
-  if (r != r) v = 0;
-  else if (r >= 2147483648.0f) v = 2147483647;
-  else if (r <= -2147483648.0f) v = (int32_t)0x80000000u;
-  else v = (int32_t)r;
+  const float c = fminf(fmaxf(r, -2147483648.0f), 2147483520.0f);
+  int32_t v = (int32_t)c;
+  v = r >= 2147483648.0f ? 2147483647 : v;
+  v = r != r ? 0 : v;
   return (int8_t)(uint8_t)(uint32_t)v;
 }
 

@@ -467,9 +467,12 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
     cx_barrier();  // every wave's share of x and w has landed
     const float* sw = sx + P.k;
     double sum = 0.0;
-    for (uint32_t i = 8 * tid; i < P.k; i += 2048)
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+      float a[8];
+      cx_load8(sx + i, a);  // two 16-byte LDS reads
 #pragma unroll
-      for (int j = 0; j < 8; j++) sum += (double)sx[i + j] * (double)sx[i + j];
+      for (int j = 0; j < 8; j++) sum += (double)a[j] * (double)a[j];
+    }
     sum = cx_wave_sum_d(sum);
     if (lane == 0) red[wave] = sum;
     cx_wait_lds();
@@ -477,9 +480,11 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
     const double tot = ((red[0] + red[1]) + red[2]) + red[3];
     const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
     for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
-      float v[8];
+      float v[8], a[8], b[8];
+      cx_load8(sx + i, a);
+      cx_load8(sw + i, b);
 #pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = (float)((double)sx[i + j] * scale) * sw[i + j];
+      for (int j = 0; j < 8; j++) v[j] = (float)((double)a[j] * scale) * b[j];
       cx_quant8_padded<Q::SUB>(v, i, sq, se, ss);
     }
   }
@@ -649,9 +654,12 @@ __global__ __launch_bounds__(256) void k_gemv_glu(GluParams P) {
   {
     const float* sw = sx + P.k;
     double sum = 0.0;
-    for (uint32_t i = 8 * tid; i < P.k; i += 2048)
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+      float a[8];
+      cx_load8(sx + i, a);  // two 16-byte LDS reads
 #pragma unroll
-      for (int j = 0; j < 8; j++) sum += (double)sx[i + j] * (double)sx[i + j];
+      for (int j = 0; j < 8; j++) sum += (double)a[j] * (double)a[j];
+    }
     sum = cx_wave_sum_d(sum);
     if (lane == 0) red[wave] = sum;
     cx_wait_lds();
@@ -659,9 +667,11 @@ __global__ __launch_bounds__(256) void k_gemv_glu(GluParams P) {
     const double tot = ((red[0] + red[1]) + red[2]) + red[3];
     const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
     for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
-      float v[8];
+      float v[8], a[8], b[8];
+      cx_load8(sx + i, a);
+      cx_load8(sw + i, b);
 #pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = (float)((double)sx[i + j] * scale) * sw[i + j];
+      for (int j = 0; j < 8; j++) v[j] = (float)((double)a[j] * scale) * b[j];
       cx_quant8_padded<Q::SUB>(v, i, sq, se, ss);
     }
   }
@@ -790,9 +800,12 @@ __global__ __launch_bounds__(256) void k_gemv32(GemvParams P) {
     cx_barrier();
     const float* sw = sx + P.k;
     double sum = 0.0;
-    for (uint32_t i = 8 * tid; i < P.k; i += 2048)
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+      float a[8];
+      cx_load8(sx + i, a);  // two 16-byte LDS reads
 #pragma unroll
-      for (int j = 0; j < 8; j++) sum += (double)sx[i + j] * (double)sx[i + j];
+      for (int j = 0; j < 8; j++) sum += (double)a[j] * (double)a[j];
+    }
     sum = cx_wave_sum_d(sum);
     if (lane == 0) red[wave] = sum;
     cx_wait_lds();
@@ -800,9 +813,11 @@ __global__ __launch_bounds__(256) void k_gemv32(GemvParams P) {
     const double tot = ((red[0] + red[1]) + red[2]) + red[3];
     const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
     for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
-      float v[8];
+      float v[8], a[8], b[8];
+      cx_load8(sx + i, a);
+      cx_load8(sw + i, b);
 #pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = (float)((double)sx[i + j] * scale) * sw[i + j];
+      for (int j = 0; j < 8; j++) v[j] = (float)((double)a[j] * scale) * b[j];
       cx_quant8<32>(v, i, sq, se, ss);
     }
   }
