@@ -71,6 +71,27 @@ __device__ inline void act8(const int8_t* x, int (&v)[8]) {
 // block's 256 activation bytes.
 template <int T> struct KQ;
 
+// The activation of one half super-block of a 32-value sub-block type
+// (Q4_K, Q5_K), in registers: the i8 values of pairs 2h and 2h + 1 (low
+// and high sub-block of each) and the four sub-blocks' xe and xs. A lane
+// whose items all fall on the same (block, half) reads it once.
+struct Pre4 {
+  int xa[2][8], xc[2][8];
+  float e[4], s[4];
+};
+__device__ inline void pre4(int h, const int8_t* xb, const float* xe, const float* xs, Pre4& a) {
+#pragma unroll
+  for (int pp = 0; pp < 2; pp++) {
+    act8(xb + 64 * (2 * h + pp), a.xa[pp]);
+    act8(xb + 64 * (2 * h + pp) + 32, a.xc[pp]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    a.e[j] = xe[4 * h + j];
+    a.s[j] = xs[4 * h + j];
+  }
+}
+
 // ------------------------------------------------------------------ Q4_K
 // 144 B: d(2) dmin(2) scales(12) qs(128). Pair p = 0..3: qs bytes
 // [32p, 32p+32) hold sub-block 2p (low nibbles) and 2p+1 (high nibbles),
@@ -94,12 +115,6 @@ template <> struct KQ<CX_Q4_K> {
       mn = ((c >> 4) & M4) | (((b >> 6) & top) << 4);
     }
   }
-  __device__ static void term(int j, int jj, int e, float d, float dm, uint32_t sc4, uint32_t mn4,
-                              const float* xe, const float* xs, int32_t* dbg, float* to) {
-    const uint32_t sc = (sc4 >> (8 * jj)) & 0xFF, mn = (mn4 >> (8 * jj)) & 0xFF;
-    if (dbg) dbg[j] = e;
-    to[j] = xe[j] * (d * (float)sc * (float)e - dm * (float)mn * xs[j]);
-  }
   // The bytes of half h: the 16-byte header and the qs of pairs 2h, 2h+1
   // (64 bytes at 16 + 64h), from LDS or straight from global memory.
   struct Regs {
@@ -118,29 +133,38 @@ template <> struct KQ<CX_Q4_K> {
     load(lds + off, h, r);
     half_regs(r, h, xb, xe, xs, dbg, to);
   }
-  __device__ static void half_regs(const Regs& r, int h, const int8_t* xb, const float* xe,
-                                   const float* xs, int32_t* dbg, float* to) {
+  // sub-block 4h + jj's term in the reference's order:
+  // xe * (d * sc * E - dmin * mn * xs)
+  __device__ static void term_pre(int jj, int e, float d, float dm, uint32_t sc4, uint32_t mn4,
+                                  const Pre4& a, int h, int32_t* dbg, float* to) {
+    const uint32_t sc = (sc4 >> (8 * jj)) & 0xFF, mn = (mn4 >> (8 * jj)) & 0xFF;
+    if (dbg) dbg[4 * h + jj] = e;
+    to[4 * h + jj] = a.e[jj] * (d * (float)sc * (float)e - dm * (float)mn * a.s[jj]);
+  }
+  __device__ static void half_pre(const Regs& r, int h, const Pre4& a, int32_t* dbg, float* to) {
     const uint4 hd = r.hd;
     const float d = cx_h2f(hd.x & 0xFFFF), dm = cx_h2f(hd.x >> 16);
     uint32_t sc4, mn4;
     scales_mins(h, hd.y, hd.z, hd.w, sc4, mn4);
 #pragma unroll
     for (int pp = 0; pp < 2; pp++) {
-      const int p = 2 * h + pp;
       const uint4 u0 = r.u[2 * pp], u1 = r.u[2 * pp + 1];
       const uint32_t q[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-      int xa[8], xc[8];
-      act8(xb + 64 * p, xa);
-      act8(xb + 64 * p + 32, xc);
       int e0 = 0, e1 = 0;
 #pragma unroll
       for (int w = 0; w < 8; w++) {
-        e0 = dot4(q[w] & M4, xa[w], e0);
-        e1 = dot4((q[w] >> 4) & M4, xc[w], e1);
+        e0 = dot4(q[w] & M4, a.xa[pp][w], e0);
+        e1 = dot4((q[w] >> 4) & M4, a.xc[pp][w], e1);
       }
-      term(2 * p, 2 * pp, e0, d, dm, sc4, mn4, xe, xs, dbg, to);
-      term(2 * p + 1, 2 * pp + 1, e1, d, dm, sc4, mn4, xe, xs, dbg, to);
+      term_pre(2 * pp, e0, d, dm, sc4, mn4, a, h, dbg, to);
+      term_pre(2 * pp + 1, e1, d, dm, sc4, mn4, a, h, dbg, to);
     }
+  }
+  __device__ static void half_regs(const Regs& r, int h, const int8_t* xb, const float* xe,
+                                   const float* xs, int32_t* dbg, float* to) {
+    Pre4 a;
+    pre4(h, xb, xe, xs, a);
+    half_pre(r, h, a, dbg, to);
   }
 };
 
@@ -169,8 +193,7 @@ template <> struct KQ<CX_Q5_K> {
     load(lds + off, h, r);
     half_regs(r, h, xb, xe, xs, dbg, to);
   }
-  __device__ static void half_regs(const Regs& r, int h, const int8_t* xb, const float* xe,
-                                   const float* xs, int32_t* dbg, float* to) {
+  __device__ static void half_pre(const Regs& r, int h, const Pre4& a, int32_t* dbg, float* to) {
     const uint4 hd = r.hd, h0 = r.h0, h1 = r.h1;
     const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
     const float d = cx_h2f(hd.x & 0xFFFF), dm = cx_h2f(hd.x >> 16);
@@ -181,20 +204,23 @@ template <> struct KQ<CX_Q5_K> {
       const int p = 2 * h + pp;
       const uint4 u0 = r.u[2 * pp], u1 = r.u[2 * pp + 1];
       const uint32_t q[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-      int xa[8], xc[8];
-      act8(xb + 64 * p, xa);
-      act8(xb + 64 * p + 32, xc);
       int e0 = 0, e1 = 0;
 #pragma unroll
       for (int w = 0; w < 8; w++) {
         const uint32_t lo = (q[w] & M4) | (((qh[w] >> (2 * p)) & M1) << 4);
         const uint32_t hi = ((q[w] >> 4) & M4) | (((qh[w] >> (2 * p + 1)) & M1) << 4);
-        e0 = dot4(lo, xa[w], e0);
-        e1 = dot4(hi, xc[w], e1);
+        e0 = dot4(lo, a.xa[pp][w], e0);
+        e1 = dot4(hi, a.xc[pp][w], e1);
       }
-      KQ<CX_Q4_K>::term(2 * p, 2 * pp, e0, d, dm, sc4, mn4, xe, xs, dbg, to);
-      KQ<CX_Q4_K>::term(2 * p + 1, 2 * pp + 1, e1, d, dm, sc4, mn4, xe, xs, dbg, to);
+      KQ<CX_Q4_K>::term_pre(2 * pp, e0, d, dm, sc4, mn4, a, h, dbg, to);
+      KQ<CX_Q4_K>::term_pre(2 * pp + 1, e1, d, dm, sc4, mn4, a, h, dbg, to);
     }
+  }
+  __device__ static void half_regs(const Regs& r, int h, const int8_t* xb, const float* xe,
+                                   const float* xs, int32_t* dbg, float* to) {
+    Pre4 a;
+    pre4(h, xb, xe, xs, a);
+    half_pre(r, h, a, dbg, to);
   }
 };
 
@@ -613,7 +639,9 @@ constexpr uint32_t GLU_ROWS = 32;
 // k = 2048 (4 items a thread), a ring refilled one item behind at larger k.
 constexpr int GLU_DEPTH = 4;
 
-template <int T, int SUB>
+// HOIST (nb divides 128): item it + 256 d has the (block, half) of item it,
+// so a lane reads its activation from LDS once, not once per item.
+template <int T, int SUB, bool HOIST>
 __global__ __launch_bounds__(256) void k_gemv_glu(GluParams P) {
   using Q = KQ<T>;
   constexpr int SPB = 256 / Q::SUB;
@@ -678,14 +706,22 @@ __global__ __launch_bounds__(256) void k_gemv_glu(GluParams P) {
   cx_wait_lds();
   cx_barrier();  // the activation is in LDS; x and w are read: the region becomes the terms
   // 3. the 64 rows' terms; slot d of the ring holds items d, d + DEPTH, ...
+  Pre4 pre;
+  if (HOIST) {
+    const uint32_t blk = (tid >> 1) % P.nb;
+    pre4(tid & 1, sq + blk * ACT_LDS_BLOCK, se + blk * SPB, ss + blk * SPB, pre);
+  }
   for (uint32_t base = tid; base < items; base += 256u * GLU_DEPTH) {
 #pragma unroll
     for (int d = 0; d < GLU_DEPTH; d++) {
       const uint32_t it = base + 256u * d;
       if (it < items) {
         const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
-        Q::half_regs(buf[d], (int)(it & 1), sq + blk * ACT_LDS_BLOCK, se + blk * SPB,
-                     ss + blk * SPB, nullptr, terms + r * P.tstride + blk * SPB);
+        if (HOIST)
+          Q::half_pre(buf[d], (int)(it & 1), pre, nullptr, terms + r * P.tstride + blk * SPB);
+        else
+          Q::half_regs(buf[d], (int)(it & 1), sq + blk * ACT_LDS_BLOCK, se + blk * SPB,
+                       ss + blk * SPB, nullptr, terms + r * P.tstride + blk * SPB);
         const uint32_t nx = it + 256u * GLU_DEPTH;
         if (nx < items) Q::load(block_of(nx), (int)(nx & 1), buf[d]);
       }
@@ -1097,12 +1133,23 @@ int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t 
   P.lds_gu = P.lds_terms + (terms > nin ? terms : nin);
   const uint32_t lds = P.lds_gu + 4 * 2 * GLU_ROWS;
   const dim3 grid(I / GLU_ROWS);
+  const bool hoist = 128 % P.nb == 0;
   if (type == CX_Q4_K) {
-    if (sub == 32) hipLaunchKernelGGL((k_gemv_glu<CX_Q4_K, 32>), grid, dim3(256), lds, s, P);
-    else hipLaunchKernelGGL((k_gemv_glu<CX_Q4_K, 16>), grid, dim3(256), lds, s, P);
+    if (sub == 32) {
+      if (hoist) hipLaunchKernelGGL((k_gemv_glu<CX_Q4_K, 32, true>), grid, dim3(256), lds, s, P);
+      else hipLaunchKernelGGL((k_gemv_glu<CX_Q4_K, 32, false>), grid, dim3(256), lds, s, P);
+    } else {
+      if (hoist) hipLaunchKernelGGL((k_gemv_glu<CX_Q4_K, 16, true>), grid, dim3(256), lds, s, P);
+      else hipLaunchKernelGGL((k_gemv_glu<CX_Q4_K, 16, false>), grid, dim3(256), lds, s, P);
+    }
   } else {
-    if (sub == 32) hipLaunchKernelGGL((k_gemv_glu<CX_Q5_K, 32>), grid, dim3(256), lds, s, P);
-    else hipLaunchKernelGGL((k_gemv_glu<CX_Q5_K, 16>), grid, dim3(256), lds, s, P);
+    if (sub == 32) {
+      if (hoist) hipLaunchKernelGGL((k_gemv_glu<CX_Q5_K, 32, true>), grid, dim3(256), lds, s, P);
+      else hipLaunchKernelGGL((k_gemv_glu<CX_Q5_K, 32, false>), grid, dim3(256), lds, s, P);
+    } else {
+      if (hoist) hipLaunchKernelGGL((k_gemv_glu<CX_Q5_K, 16, true>), grid, dim3(256), lds, s, P);
+      else hipLaunchKernelGGL((k_gemv_glu<CX_Q5_K, 16, false>), grid, dim3(256), lds, s, P);
+    }
   }
   CX_HIP(hipGetLastError());
   return CX_OK;
