@@ -417,25 +417,51 @@ __device__ inline void wait_all_but(uint32_t n) {
   else cx_wait_vm<0>();
 }
 
+// Row tid's epilogue operand: y (CX_EPI_ACCUM: y += acc), else the bias
+// (y = acc + bias) or 0. f32 addition is commutative, so acc + addend is
+// the reference's y + acc and acc + bias bit for bit.
+__device__ inline float epi_addend(const GemvParams& P, const cx_seg& S, uint32_t row0,
+                                   uint32_t rows, int tid) {
+  if ((uint32_t)tid >= rows) return 0.0f;
+  if (P.epi == CX_EPI_ACCUM) return S.y[row0 + tid];
+  return S.bias ? S.bias[row0 + tid] : 0.0f;
+}
+
 // total = 0; total += term_s for s = 0 .. n-1 (n % 4 == 0), in that order.
-// The terms are read eight float4s at a time before they are added, so the
-// LDS latency is paid once per 32 adds, not once per 4.
+// The terms are read eight float4s at a time, and the next 32 are read
+// while the current 32 are added: the adds are one dependent chain (~9
+// clocks each), and the LDS latency is paid once, not once per batch.
+__device__ inline void ld8(const float4* t, float4 (&v)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; i++) v[i] = t[i];
+}
+__device__ inline void add8(float& acc, const float4 (&v)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    acc += v[i].x;
+    acc += v[i].y;
+    acc += v[i].z;
+    acc += v[i].w;
+  }
+}
 __device__ inline float row_sum(const float* terms, uint32_t n) {
   const float4* t = reinterpret_cast<const float4*>(terms);
   const uint32_t n4 = n / 4;
   float acc = 0.0f;
   uint32_t s = 0;
-  for (; s + 8 <= n4; s += 8) {
-    float4 v[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = t[s + i];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      acc += v[i].x;
-      acc += v[i].y;
-      acc += v[i].z;
-      acc += v[i].w;
-    }
+  float4 a[8], b[8];
+  if (s + 8 <= n4) ld8(t + s, a);
+  while (s + 8 <= n4) {  // a holds batch s
+    const bool more = s + 16 <= n4;
+    if (more) ld8(t + s + 8, b);
+    add8(acc, a);
+    s += 8;
+    if (!more) break;  // b holds batch s
+    const bool more2 = s + 16 <= n4;
+    if (more2) ld8(t + s + 8, a);
+    add8(acc, b);
+    s += 8;
+    if (!more2) break;
   }
   for (; s < n4; s++) {
     const float4 v = t[s];
@@ -462,6 +488,9 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
   const cx_seg S = P.seg[sg];
   const uint32_t row0 = tile * P.R;
   const uint32_t rows = min(P.R, S.rows - row0);
+  // the epilogue's other operand (the residual, or the bias), loaded first:
+  // its latency passes under the tile's, not after the row sum
+  const float addend = epi_addend(P, S, row0, rows, tid);
   int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
   float* se = reinterpret_cast<float*>(lds + P.lds_scale);
   float* ss = se + P.nsub;
@@ -536,10 +565,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
   if ((uint32_t)tid < rows) {
     const float acc = row_sum(terms + tid * P.tstride, P.nsub);
     const uint32_t row = row0 + tid;
-    if (P.epi == CX_EPI_ACCUM)
-      S.y[row] += acc;
-    else
-      S.y[row] = S.bias ? acc + S.bias[row] : acc;
+    S.y[row] = (P.epi == CX_EPI_ACCUM || S.bias) ? acc + addend : acc;
   }
 }
 
@@ -564,6 +590,9 @@ __global__ __launch_bounds__(256) void k_gemv_reg(GemvParams P) {
   const cx_seg S = P.seg[sg];
   const uint32_t row0 = tile * P.R;
   const uint32_t rows = min(P.R, S.rows - row0);
+  // the epilogue's other operand (the residual, or the bias), loaded first:
+  // its latency passes under the tile's, not after the row sum
+  const float addend = epi_addend(P, S, row0, rows, tid);
   int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
   float* se = reinterpret_cast<float*>(lds + P.lds_scale);
   float* ss = se + P.nsub;
@@ -577,19 +606,32 @@ __global__ __launch_bounds__(256) void k_gemv_reg(GemvParams P) {
     const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
     return S.w + (size_t)(row0 + r) * P.row_bytes + (size_t)blk * Q::BPB;
   };
-  typename Q::Regs cur{}, nxt{};
-  uint32_t it = tid;
-  if (it < items) Q::load(block_of(it), (int)(it & 1), cur);
-  cx_wait_vm<Q::NLOAD>();  // the activation's direct loads (issued first) have landed
+  // a two-slot ring: the lane's first two items are loaded from the start
+  // (a wave's loads complete in order, so waiting for all but its weight
+  // loads waits for the activation); item j + 2 is loaded into item j's
+  // slot once j is computed
+  typename Q::Regs buf[2];
+  const uint32_t wave_first = tid & ~63u;  // wave-uniform count of item loads issued
+  const uint32_t issued = (wave_first < items) + (wave_first + 256 < items);
+  if (tid < items) Q::load(block_of(tid), (int)(tid & 1), buf[0]);
+  if (tid + 256 < items) Q::load(block_of(tid + 256), (int)((tid + 256) & 1), buf[1]);
+  if (issued == 2) cx_wait_vm<2 * Q::NLOAD>();
+  else if (issued == 1) cx_wait_vm<Q::NLOAD>();
+  else cx_wait_vm<0>();  // a wave with no items: its activation loads only
   cx_barrier();
-  for (; it < items; it += 256) {
-    const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
-    const int h = (int)(it & 1);
-    if (it + 256 < items) Q::load(block_of(it + 256), (int)((it + 256) & 1), nxt);
-    int32_t* dbg = P.dbg ? P.dbg + (size_t)(row0 + r) * P.nsub + blk * SPB : nullptr;
-    Q::half_regs(cur, h, sq + blk * ACT_LDS_BLOCK, se + blk * SPB, ss + blk * SPB, dbg,
-                 terms + r * P.tstride + blk * SPB);
-    cur = nxt;
+  for (uint32_t base = tid; base < items; base += 512) {
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+      const uint32_t it = base + 256u * d;
+      if (it < items) {
+        const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
+        int32_t* dbg = P.dbg ? P.dbg + (size_t)(row0 + r) * P.nsub + blk * SPB : nullptr;
+        Q::half_regs(buf[d], (int)(it & 1), sq + blk * ACT_LDS_BLOCK, se + blk * SPB,
+                     ss + blk * SPB, dbg, terms + r * P.tstride + blk * SPB);
+        const uint32_t nx = it + 512;
+        if (nx < items) Q::load(block_of(nx), (int)(nx & 1), buf[d]);
+      }
+    }
   }
   __syncthreads();
 
@@ -597,10 +639,7 @@ __global__ __launch_bounds__(256) void k_gemv_reg(GemvParams P) {
   if ((uint32_t)tid < rows) {
     const float acc = row_sum(terms + tid * P.tstride, P.nsub);
     const uint32_t row = row0 + tid;
-    if (P.epi == CX_EPI_ACCUM)
-      S.y[row] += acc;
-    else
-      S.y[row] = S.bias ? acc + S.bias[row] : acc;
+    S.y[row] = (P.epi == CX_EPI_ACCUM || S.bias) ? acc + addend : acc;
   }
 }
 
@@ -811,6 +850,9 @@ __global__ __launch_bounds__(256) void k_gemv32(GemvParams P) {
   const cx_seg S = P.seg[sg];
   const uint32_t row0 = tile * P.R;
   const uint32_t rows = min(P.R, S.rows - row0);
+  // the epilogue's other operand (the residual, or the bias), loaded first:
+  // its latency passes under the tile's, not after the row sum
+  const float addend = epi_addend(P, S, row0, rows, tid);
   int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
   float* se = reinterpret_cast<float*>(lds + P.lds_scale);
   float* ss = se + P.nsub;
@@ -877,10 +919,7 @@ __global__ __launch_bounds__(256) void k_gemv32(GemvParams P) {
   if ((uint32_t)tid < rows) {
     const float acc = row_sum_any(terms + tid * P.tstride, P.nsub);
     const uint32_t row = row0 + tid;
-    if (P.epi == CX_EPI_ACCUM)
-      S.y[row] += acc;
-    else
-      S.y[row] = S.bias ? acc + S.bias[row] : acc;
+    S.y[row] = (P.epi == CX_EPI_ACCUM || S.bias) ? acc + addend : acc;
   }
 }
 
