@@ -142,16 +142,7 @@ __global__ __launch_bounds__(256) void k_att_qk(const float* q, const float* kne
     float s = -INFINITY;
     if (p < np) {
       const float4* a4 = reinterpret_cast<const float4*>(qr + hl * HD);
-      float acc = 0.0f;
-#pragma unroll 8
-      for (int i = 0; i < HD / 4; i++) {
-        const float4 x = a4[i], y = b4[i];
-        acc += x.x * y.x;
-        acc += x.y * y.y;
-        acc += x.z * y.z;
-        acc += x.w * y.w;
-      }
-      s = acc * scale;
+      s = cx_dot_seq<HD / 4>(a4, b4) * scale;
       sc[(size_t)hl * stride + p0 + p] = s;
     }
     const float m = cx_wave_max(s);

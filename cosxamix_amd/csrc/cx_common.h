@@ -150,6 +150,34 @@ __device__ inline void cx_dma16_async(const void* g, void* l) {
       : "memory");
 }
 
+// s = 0; s += a[i] * b[i] for i = 0, 1, ... in order (the sequential f32
+// dot of src/kernels/scalar.rs:16-23) over N4 float4s. Eight products are
+// formed first and pinned by an empty asm that takes them as operands: left
+// to itself the compiler interleaves each multiply with its add, and the
+// chain then waits for a multiply and an add per term instead of one add.
+template <int N4>
+__device__ inline float cx_dot_seq(const float4* a, const float4* b) {
+  static_assert(N4 % 2 == 0, "pairs of float4");
+  float s = 0.0f;
+#pragma unroll 4
+  for (int i = 0; i < N4; i += 2) {
+    const float4 x = a[i], y = b[i], u = a[i + 1], v = b[i + 1];
+    float t0 = x.x * y.x, t1 = x.y * y.y, t2 = x.z * y.z, t3 = x.w * y.w;
+    float t4 = u.x * v.x, t5 = u.y * v.y, t6 = u.z * v.z, t7 = u.w * v.w;
+    asm volatile("" : "+v"(t0), "+v"(t1), "+v"(t2), "+v"(t3), "+v"(t4), "+v"(t5), "+v"(t6),
+                 "+v"(t7));
+    s += t0;
+    s += t1;
+    s += t2;
+    s += t3;
+    s += t4;
+    s += t5;
+    s += t6;
+    s += t7;
+  }
+  return s;
+}
+
 // Rust `f32 as i32` (saturating, NaN -> 0) then `as i8` (low 8 bits),
 // without branches: r clamped to [-2^31, 2147483520] (the largest f32 below
 // 2^31) converts exactly as the in-range cast, then r >= 2^31 and NaN are

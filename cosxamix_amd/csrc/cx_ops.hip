@@ -348,15 +348,7 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
   const uint32_t p = p0 + t;
   const float4* a4 = reinterpret_cast<const float4*>(qr);
   const float4* b4 = reinterpret_cast<const float4*>((has_new && p == pos) ? kr : kl + t * PADF);
-  float s = 0.0f;
-#pragma unroll 8
-  for (int i = 0; i < HD / 4; i++) {
-    const float4 a = a4[i], b = b4[i];
-    s += a.x * b.x;
-    s += a.y * b.y;
-    s += a.z * b.z;
-    s += a.w * b.w;
-  }
+  const float s = cx_dot_seq<HD / 4>(a4, b4);
   sc[(size_t)h * sc_stride(cap) + p] = s * scale;
 }
 
