@@ -262,9 +262,9 @@ constexpr uint32_t PV_STP = 128;  // positions per V stage
 // One query token (decode) takes 32 dims: twice the workgroups of 64, so the
 // shared softmax and chains run on more CUs at once; many query tokens
 // (prefill) take 64, which does that shared work half as often.
-template <uint32_t DS>
+template <uint32_t DS, uint32_t RING = 32768>
 struct PvShape {
-  static constexpr uint32_t NST = 32768 / (PV_STP * DS);
+  static constexpr uint32_t NST = RING / (PV_STP * DS);
   static constexpr uint32_t IPS = PV_STP * DS * 4 / 1024;  // 1 KiB loads per stage
   static constexpr uint32_t IPW = IPS / 4;                  // per wave
   static constexpr uint32_t LPP = DS / 4;                   // lanes per position in a load
@@ -418,10 +418,36 @@ __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) 
   o += t7;
 }
 
+// With helpers (HELP): the products p_j * v_j[d] of a stage are formed by
+// waves 1-3 one stage ahead, into a [dim][position] buffer (rows PV_PSTR
+// floats apart, so 16 lanes' 16-byte reads fall on distinct banks), and
+// wave 0's chain reads four positions' products per LDS read: an add and a
+// quarter of a read per position, where forming them itself costs a
+// multiply, an add and three quarters of a read. The V ring is then 96 KiB,
+// to leave room for the two product buffers.
+constexpr uint32_t PV_PSTR = PV_STP + 4;
+constexpr uint32_t PV_RING_HELP = 24576;
+__host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap, uint32_t ds, bool help) {
+  return sc_lds(cap) + (help ? PV_RING_HELP + 2 * ds * PV_PSTR : 32768u);
+}
+
+// Waits until at most `later` stages' loads (IPW each) of this wave are
+// outstanding, or fewer.
+template <uint32_t IPW, uint32_t MAXL>
+__device__ inline void wait_stages(uint32_t later) {
+  if constexpr (MAXL == 0) {
+    (void)later;
+    cx_wait_vm<0>();
+  } else {
+    if (later >= MAXL) cx_wait_vm<MAXL * IPW>();
+    else wait_stages<IPW, MAXL - 1>(later);
+  }
+}
+
 // 256 threads: every wave streams its share of the V ring (4x the loads in
 // flight of one wave); wave 0's lanes run the order-exact accumulation.
 // Rows of the grid past HD / PV_DS are prefetch workgroups (pf).
-template <int HD, int SUB, uint32_t PV_DS>
+template <int HD, int SUB, uint32_t PV_DS, bool HELP>
 __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
                                                   uint32_t heads, uint32_t kvh,
                                                   const cx_dstate* st, uint32_t cap, float* out,
@@ -438,7 +464,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   __shared__ float red[4];
   // query token z (blockIdx.z) sits at position st->pos + z
   const uint32_t z = blockIdx.z, total = st->pos + z + 1, h = blockIdx.x, g = h / (heads / kvh);
-  using PS = PvShape<PV_DS>;
+  using PS = PvShape<PV_DS, HELP ? PV_RING_HELP : 32768u>;
   constexpr uint32_t PV_NST = PS::NST, PV_IPW = PS::IPW, PV_LPP = PS::LPP;
   const uint32_t d0 = blockIdx.y * PV_DS, kvd = kvh * HD;
   sc_all += (size_t)z * heads * sc_stride(cap);
@@ -501,6 +527,66 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   }
   // 3. out[d0 + t] over the V ring, position order (wave 0)
   float o = 0.0f;
+  if constexpr (HELP) {
+    float* prod = ring + PV_NST * PV_STP * PV_DS;  // two buffers of PV_DS * PV_PSTR
+    // helper waves: stage s's products into buffer s % 2; task k is (dim
+    // k % PV_DS, positions 4 (k / PV_DS) .. +3)
+    auto make = [&](uint32_t s) {
+      const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS);
+      const float* ps = e + s * PV_STP;
+      float* pb = prod + (s & 1) * (PV_DS * PV_PSTR);
+      for (uint32_t k = tid - 64; k < PV_DS * (PV_STP / 4); k += 192) {
+        const uint32_t d = k % PV_DS, q = k / PV_DS;
+        const float4 p = *reinterpret_cast<const float4*>(ps + 4 * q);
+        float4 r;
+        r.x = p.x * vs[(4 * q + 0) * PV_DS + d];
+        r.y = p.y * vs[(4 * q + 1) * PV_DS + d];
+        r.z = p.z * vs[(4 * q + 2) * PV_DS + d];
+        r.w = p.w * vs[(4 * q + 3) * PV_DS + d];
+        *reinterpret_cast<float4*>(pb + d * PV_PSTR + 4 * q) = r;
+      }
+    };
+    // stages issued so far: [0, min(NST, nstage)); each iteration s issues
+    // stage s + NST into the slot of stage s, whose products are made
+    auto issued_end = [&](uint32_t s) { return min(s + PV_NST, nstage); };
+    wait_stages<PV_IPW, PV_NST - 1>(issued_end(0) - 1);  // stage 0 has landed
+    cx_barrier();
+    if (w != 0) make(0);
+    for (uint32_t s = 0; s < nstage; s++) {
+      if (s + 1 < nstage) wait_stages<PV_IPW, PV_NST - 1>(issued_end(s) - (s + 2));
+      cx_wait_lds();
+      cx_barrier();  // stage s's products are made; stage s + 1 has landed
+      if (s + PV_NST < nstage) issue(s + PV_NST);  // stage s's slot is no longer read
+      if (w == 0) {
+        if (t < (int)PV_DS) {
+          const float* pr = prod + (s & 1) * (PV_DS * PV_PSTR) + t * PV_PSTR;
+          if ((s + 1) * PV_STP <= total) {
+            // 32 positions a batch, the next batch's reads ahead of the adds
+            const float4* p4 = reinterpret_cast<const float4*>(pr);
+            float4 a[8], b[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) a[i] = p4[i];
+#pragma unroll
+            for (int i = 0; i < 8; i++) b[i] = p4[8 + i];
+            add32(o, a);
+#pragma unroll
+            for (int i = 0; i < 8; i++) a[i] = p4[16 + i];
+            add32(o, b);
+#pragma unroll
+            for (int i = 0; i < 8; i++) b[i] = p4[24 + i];
+            add32(o, a);
+            add32(o, b);
+          } else {
+            for (uint32_t j = 0; s * PV_STP + j < total; j++) o += pr[j];
+          }
+        }
+      } else if (s + 1 < nstage) {
+        make(s + 1);
+      }
+    }
+    cx_wait_lds();
+    cx_barrier();  // every read of the ring and the products is done
+  } else {
   for (uint32_t s = 0; s < nstage; s++) {
     if (s + PV_NST <= nstage)
       cx_wait_vm<(PV_NST - 1) * PV_IPW>();
@@ -544,6 +630,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     cx_wait_lds();
     cx_barrier();  // the slot is read: refill it
     if (s + PV_NST < nstage) issue(s + PV_NST);
+  }
   }
   if (w != 0 || t >= (int)PV_DS) return;
   out[h * HD + d0 + t] = o;
@@ -772,20 +859,21 @@ int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
                      sc_bytes, s, a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads,
                      a.kvh, a.st, scale, a.sc, a.cap);
   CX_HIP(hipGetLastError());
-  const size_t lds = (sc_lds(a.cap) + 32768) * sizeof(float);  // scores, then the V ring
   if (T > 1) {  // many query tokens: 64 dims a workgroup, f32 output only
+    const size_t lds = pv_lds_floats(a.cap, 64, false) * sizeof(float);
     const dim3 grid(a.heads, HD / 64, T);
-    hipLaunchKernelGGL((k_attn_seq<HD, 32, 64>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads,
-                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, cx_l2_prefetch{});
-  } else {
+    hipLaunchKernelGGL((k_attn_seq<HD, 32, 64, false>), grid, dim3(256), lds, s, a.vc, a.sc,
+                       a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, cx_l2_prefetch{});
+  } else {  // one token: 32 dims a workgroup, products made by helper waves
+    const size_t lds = pv_lds_floats(a.cap, 32, true) * sizeof(float);
     const uint32_t rows = HD / 32, np = cx_l2_prefetch_groups(a.pf, a.heads * rows);
     const dim3 grid(a.heads, rows + (np + a.heads - 1) / a.heads, T);
     if (a.sub == 16)
-      hipLaunchKernelGGL((k_attn_seq<HD, 16, 32>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads,
-                         a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+      hipLaunchKernelGGL((k_attn_seq<HD, 16, 32, true>), grid, dim3(256), lds, s, a.vc, a.sc,
+                         a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
     else
-      hipLaunchKernelGGL((k_attn_seq<HD, 32, 32>), grid, dim3(256), lds, s, a.vc, a.sc, a.heads,
-                         a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+      hipLaunchKernelGGL((k_attn_seq<HD, 32, 32, true>), grid, dim3(256), lds, s, a.vc, a.sc,
+                         a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   }
   CX_HIP(hipGetLastError());
   return CX_OK;
