@@ -556,7 +556,9 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
       if (s + 1 < nstage) wait_stages<PV_IPW, PV_NST - 1>(issued_end(s) - (s + 2));
       cx_wait_lds();
       cx_barrier();  // stage s's products are made; stage s + 1 has landed
-      if (s + PV_NST < nstage) issue(s + PV_NST);  // stage s's slot is no longer read
+      // stage s's slot is no longer read: refill it (wave 0 after its chain,
+      // which the barrier starts)
+      if (w != 0 && s + PV_NST < nstage) issue(s + PV_NST);
       if (w == 0) {
         if (t < (int)PV_DS) {
           const float* pr = prod + (s & 1) * (PV_DS * PV_PSTR) + t * PV_PSTR;
@@ -580,6 +582,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
             for (uint32_t j = 0; s * PV_STP + j < total; j++) o += pr[j];
           }
         }
+        if (s + PV_NST < nstage) issue(s + PV_NST);
       } else if (s + 1 < nstage) {
         make(s + 1);
       }
