@@ -489,7 +489,8 @@ def trace_summary(path):
 def token_summary(path, ntok=8):
     """Per decode token from a rocprofv3 kernel trace of a decode run: the
     kernels between consecutive lm_head launches (the largest GEMV grid),
-    averaged over the last `ntok` tokens."""
+    averaged over the last `ntok` tokens that ran no batched prefill kernel
+    (a run that also times the prompt's prefill ends with those)."""
     import collections
     import csv
     import re
@@ -502,9 +503,11 @@ def token_summary(path, ntok=8):
     rows.sort(key=lambda r: r[1])
     lm_grid = max(r[3] for r in rows if "k_gemv" in r[0])
     lm = [i for i, r in enumerate(rows) if r[3] == lm_grid and "k_gemv" in r[0]]
+    pairs = [(a, b) for a, b in zip(lm[:-1], lm[1:])
+             if not any("k_gemm" in r[0] or "k_quantize_gemm" in r[0] for r in rows[a + 1:b])]
     per = collections.defaultdict(list)
     spans = []
-    for a, b in zip(lm[-ntok - 1:-1], lm[-ntok:]):
+    for a, b in pairs[-ntok:]:
         seg = rows[a + 1:b + 1]
         spans.append(seg[-1][2] - rows[a][2])
         for r in seg:

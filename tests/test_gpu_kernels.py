@@ -292,7 +292,7 @@ def test_decode_attention_paths(cx, dev, heads, kvh, hd):
     oracle (src/ops.rs:1258-1325) at any length, for 1, 2, 4, 7, 8 and 16
     query heads per KV group; split-K mode within f32 rounding."""
     ops, _ = cx
-    for total in (1, 2, 37, 63, 64, 65, 100, 150, 255, 256, 257, 640, 1000, 4097, 8300):
+    for total in (1, 2, 37, 63, 64, 65, 100, 150, 255, 256, 257, 640, 1000, 2048, 4096, 4097, 8300):
         rng = np.random.default_rng(total + heads)
         q = rng.normal(0, 1, heads * hd).astype(np.float32)
         k = rng.normal(0, 1, total * kvh * hd).astype(np.float32)
