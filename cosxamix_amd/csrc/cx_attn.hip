@@ -100,9 +100,10 @@ __global__ __launch_bounds__(256) void k_att_qk(const float* q, const float* kne
     cx_dma16(reinterpret_cast<const uint8_t*>(kb + (size_t)r * kvd) + b, sm + ch * 1024);
   }
   // 2. rope while the rows arrive (src/ops.rs:1185-1188: a' = a*c - b*s,
-  //    b' = a*s + b*c, no FMA); the chunk holding st->pos appends the key
-  //    and value (src/forward.rs:454-455) and scores that position with the
-  //    rotated key from LDS, so no result depends on a row written here
+  //    b' = a*s + b*c, no FMA); the chunk holding st->pos scores that
+  //    position with the rotated key from LDS and appends the key and value
+  //    at the end (src/forward.rs:454-455), so no result depends on a row
+  //    written here
   const bool rot = cos_t != nullptr, has_new = rot && pos < p0 + QK_P;
   if (rot) {
     const float* cc = cos_t + (size_t)pos * half;
@@ -115,18 +116,11 @@ __global__ __launch_bounds__(256) void k_att_qk(const float* q, const float* kne
     }
     if (has_new) {
       const float* kn = knew + (size_t)z * kvd + g * HD;
-      const float* vn = vnew + (size_t)z * kvd + g * HD;
-      float* kd = kc + (size_t)pos * kvd + g * HD;
-      float* vd = vc + (size_t)pos * kvd + g * HD;
       for (uint32_t j = tid; j < half; j += 256) {
         const float k0 = kn[j], k1 = kn[j + half];
         const float a = k0 * cc[j] - k1 * ss[j], b = k0 * ss[j] + k1 * cc[j];
         kr[j] = a;
         kr[j + half] = b;
-        kd[j] = a;
-        kd[j + half] = b;
-        vd[j] = vn[j];
-        vd[j + half] = vn[j + half];
       }
     }
   } else {
@@ -147,6 +141,17 @@ __global__ __launch_bounds__(256) void k_att_qk(const float* q, const float* kne
     }
     const float m = cx_wave_max(s);
     if (lane == 0) cm[(size_t)hl * nck + c] = m;
+  }
+  // 4. the appended key (rotated, from LDS) and value: stored after the
+  //    dots, since a wave waits for its stores as for its loads
+  if (has_new) {
+    const float* vn = vnew + (size_t)z * kvd + g * HD;
+    float* kd = kc + (size_t)pos * kvd + g * HD;
+    float* vd = vc + (size_t)pos * kvd + g * HD;
+    for (uint32_t j = tid; j < (uint32_t)HD; j += 256) {
+      kd[j] = kr[j];
+      vd[j] = vn[j];
+    }
   }
 }
 

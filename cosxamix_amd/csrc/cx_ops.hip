@@ -328,14 +328,6 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
         const float a = k0 * c[j] - k1 * s[j], b = k0 * s[j] + k1 * c[j];
         kr[j] = a;
         kr[j + half] = b;
-        if (h % per == 0) {
-          float* kd = kc + (size_t)pos * kvd + g * HD;
-          float* vd = vc + (size_t)pos * kvd + g * HD;
-          kd[j] = a;
-          kd[j + half] = b;
-          vd[j] = vnew[g * HD + j];
-          vd[j + half] = vnew[g * HD + j + half];
-        }
       }
     }
   } else {
@@ -344,12 +336,25 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
   cx_wait_vm<0>();
   __syncthreads();
   // 3. lane t: position p0 + t
-  if ((uint32_t)t >= np) return;
-  const uint32_t p = p0 + t;
-  const float4* a4 = reinterpret_cast<const float4*>(qr);
-  const float4* b4 = reinterpret_cast<const float4*>((has_new && p == pos) ? kr : kl + t * PADF);
-  const float s = cx_dot_seq<HD / 4>(a4, b4);
-  sc[(size_t)h * sc_stride(cap) + p] = s * scale;
+  if ((uint32_t)t < np) {
+    const uint32_t p = p0 + t;
+    const float4* a4 = reinterpret_cast<const float4*>(qr);
+    const float4* b4 = reinterpret_cast<const float4*>((has_new && p == pos) ? kr : kl + t * PADF);
+    const float s = cx_dot_seq<HD / 4>(a4, b4);
+    sc[(size_t)h * sc_stride(cap) + p] = s * scale;
+  }
+  // 4. one workgroup of the KV group appends the rotated key (from LDS) and
+  //    the value at st->pos for later tokens (src/forward.rs:454-455):
+  //    stored after the dots, since a wave waits for its stores as for its
+  //    loads, and nothing here reads them
+  if (has_new && h % per == 0) {
+    float* kd = kc + (size_t)pos * kvd + g * HD;
+    float* vd = vc + (size_t)pos * kvd + g * HD;
+    for (uint32_t j = t; j < (uint32_t)HD; j += 64) {
+      kd[j] = kr[j];
+      vd[j] = vnew[g * HD + j];
+    }
+  }
 }
 
 // Sequential sum of x[0..n) from 0 (one lane). LDS reads run a batch of 32
