@@ -107,12 +107,45 @@ __device__ inline float cx_wave_sum(float v) {
   v += __shfl_xor(v, 32, CX_WAVE);
   return v;
 }
+// A lane's value from the lane a DPP control selects (every lane valid:
+// quad permutes and row mirrors)
+template <int CTRL>
+__device__ inline uint32_t cx_dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ inline double cx_dpp_d(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint64_t lo = cx_dpp<CTRL>((uint32_t)u), hi = cx_dpp<CTRL>((uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(lo | (hi << 32)));
+}
+constexpr int CX_DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int CX_DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int CX_DPP_HALF_MIRROR = 0x141;  // lane i of 8 <- 7 - i
+constexpr int CX_DPP_MIRROR = 0x140;       // lane i of 16 <- 15 - i
+
+// The xor butterfly v += v[lane ^ o], o = 1, 2, ..., 32: every lane ends
+// with the same tree's sum. Levels 4 and 8 read lane i ^ 7 and i ^ 15 (the
+// row mirrors), which after the levels before hold the same value as
+// i ^ 4 and i ^ 8; an f32/f64 add is commutative, so the result is the
+// butterfly's bit for bit. The first four levels are DPP moves, the last
+// two cross rows through the LDS crossbar.
 __device__ inline double cx_wave_sum_d(double v) {
-  for (int o = 1; o < CX_WAVE; o <<= 1) v += __shfl_xor(v, o, CX_WAVE);
+  v += cx_dpp_d<CX_DPP_XOR1>(v);
+  v += cx_dpp_d<CX_DPP_XOR2>(v);
+  v += cx_dpp_d<CX_DPP_HALF_MIRROR>(v);
+  v += cx_dpp_d<CX_DPP_MIRROR>(v);
+  v += __shfl_xor(v, 16, CX_WAVE);
+  v += __shfl_xor(v, 32, CX_WAVE);
   return v;
 }
 __device__ inline float cx_wave_max(float v) {
-  for (int o = 1; o < CX_WAVE; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, CX_WAVE));
+  v = fmaxf(v, __uint_as_float(cx_dpp<CX_DPP_XOR1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(cx_dpp<CX_DPP_XOR2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(cx_dpp<CX_DPP_HALF_MIRROR>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(cx_dpp<CX_DPP_MIRROR>(__float_as_uint(v))));
+  v = fmaxf(v, __shfl_xor(v, 16, CX_WAVE));
+  v = fmaxf(v, __shfl_xor(v, 32, CX_WAVE));
   return v;
 }
 
