@@ -55,6 +55,11 @@ def test_quantize_act_bit_exact(cx, dev, sub):
     x[1, 500] = 3e38
     x[2, 7], x[2, 300], x[2, 301] = np.nan, np.inf, -np.inf
     x[2, 1000:1032] = np.float32(2.5) * np.sign(rng.normal(size=32))  # exact .5 ties
+    # subnormal sub-blocks: 127 / amax overflows to inf, so v * inv is +-inf
+    # (Rust's `as i32` saturates, `as i8` keeps the low byte) or 0 * inf = NaN
+    x[0, 2048:2080] = np.float32(1e-40) * np.sign(rng.normal(size=32))
+    x[1, 4096:4128] = 0.0
+    x[1, 4097] = np.float32(-1e-42)
     xq, xe, xs = (a.cpu().numpy() for a in ops.cuantizar_i8_en(T(x, dev), sub))
     for r in range(3):
         q, e, s = O.quantize_act(x[r], sub)
