@@ -944,8 +944,9 @@ TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
   return t;
 }
 
-// The plain (no prologue) launch's tile: the largest R <= 16 that leaves >= 2
-// tiles per CU (measured on MI355X at the 3B projection shapes)
+// The plain (no prologue) launch's tile: the largest R <= 16 that leaves a
+// tile per CU (measured on MI355X in the 3B decode step: 2 tiles per CU
+// took 1.7% longer a token, 4 tiles per CU 8% longer)
 template <int T>
 TilePlan plain_plan(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_t* rows, int nseg) {
   constexpr bool REG = T == CX_Q4_K || T == CX_Q5_K;  // weights straight into registers
@@ -954,7 +955,7 @@ TilePlan plain_plan(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_
     TilePlan t = plan_tile(R, row_bytes, k, nsub, rows, nseg, false, REG);
     if (t.lds > TILE_LDS_MAX) continue;
     best = t;
-    if (t.tiles >= 512) break;
+    if (t.tiles >= 256) break;
   }
   return best;
 }
