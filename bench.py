@@ -544,6 +544,8 @@ def main():
     ap.add_argument("--config5-only", action="store_true",
                     help="only BASELINE config 5 (8B shape, 8K context)")
     ap.add_argument("--no-config5", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the config-1 GEMV roofline loop (e.g. under rocprofv3)")
     ap.add_argument("--small-only", action="store_true",
                     help="only the daiss-0.5b Q8_0 decode (the 32-value block GEMV)")
     a = ap.parse_args()
@@ -577,6 +579,14 @@ def main():
         return 0
     if a.small_only:
         print(json.dumps(small_model_bench(F, L, a.steps, a.warmup, a.prompt)), flush=True)
+        return 0
+    if a.roofline_only:
+        m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)
+        avg, gbps, ncopies = gemv_roofline(F, L, m)
+        print(json.dumps({"us_per_launch": round(avg * 1e6, 3), "GBps": round(gbps, 1),
+                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "rotating_matrices": ncopies}),
+              flush=True)
+        m.close()
         return 0
     if a.batched_only:
         m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)

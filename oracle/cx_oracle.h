@@ -17,10 +17,20 @@
  *   - f16<->f32: exhaustive over all 65536 halves vs the CPU's F16C;
  *   - activation quantizer: closed-form invariants of ops.rs:1431-1457;
  *   - unpack/dequant: exact-reconstruction identity (quant.rs:892-928);
- *   - quantizers: reference invariants (quant_kquants.rs:427-503) — the
- *     quantizers' exact bytes are "parity unpinned" (only a Rust build of
- *     the reference could pin them; GEMV parity does not depend on them);
- *   - Azar normals: integer xorshift exact; Box-Muller statistical only.
+ *     Q6_K: one-hot bytes against the reference's layout table
+ *     (kernels/scalar.rs:276-291) through dequant, unpack and the row dot;
+ *   - RoPE: one-hot rotations and the float64 rotation (direction pinned);
+ *     attention: the float64 softmax(q.k/sqrt(Dh)).v closed form (scale
+ *     pinned);
+ *   - seeds: FNV-1a published vectors; Azar normals: Box-Muller in float64
+ *     on the exact xorshift uniforms, to a few f32 ulps;
+ *   - quantizers Q2_K..Q5_K: byte for byte on exact-grid blocks whose bytes
+ *     follow from the format alone, plus the reference invariants
+ *     (quant_kquants.rs:427-503). On general inputs their exact bytes rest
+ *     on the line-by-line restatement (a Rust build of the reference would
+ *     pin them; GEMV parity does not depend on them: GPU and CPU read the
+ *     same bytes).
+ * tests/test_oracle_mutants.py shows each pin fails on a plausible slip.
  */
 #ifndef CX_ORACLE_H
 #define CX_ORACLE_H

@@ -14,7 +14,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# CX_ORACLE_LIB names another build of cx_oracle.c (tests/test_oracle_mutants.py
+# loads deliberately broken copies through it to show the pinning tests fail)
+LIB_PATH = os.environ.get("CX_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libcxref.so")
 
 F32, F16, Q5_0, Q8_0 = 0, 1, 6, 8
