@@ -41,6 +41,9 @@ class CxGgufTensor(C.Structure):
                 ("bytes", C.c_uint64)]
 
 
+# cx_token_fn: int (*)(uint32_t token, void *user)
+TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_uint32, C.c_void_p)
+
 # name -> (restype, argtypes); every symbol include/cosxamix_hip.h declares
 SIGNATURES = {
     "cx_last_error": (C.c_char_p, []),
@@ -100,11 +103,15 @@ SIGNATURES = {
     "cx_cache_truncate": (C.c_int, [_vp, _sz]),
     "cx_cache_clear": (None, [_vp]),
     "cx_cache_free": (None, [_vp]),
+    "cx_cache_bytes": (_sz, [_vp]),
+    "cx_cache_prefix": (C.c_int, [_vp, _sz, _sz, C.POINTER(_vp)]),
     "cx_forward": (C.c_int, [_vp, _vp, _u32p, _sz, _f32p, _u32p]),
     "cx_generate": (C.c_int, [_vp, _vp, _u32p, _sz, _sz, C.c_uint32, _u32p, C.POINTER(_sz),
                               _f32p]),
     "cx_generate_sampled": (C.c_int, [_vp, _vp, _u32p, _sz, _sz, C.c_uint32, C.c_uint64, C.c_float,
                                       C.c_float, _u32p, C.POINTER(_sz), _f32p]),
+    "cx_generate_stream": (C.c_int, [_vp, _vp, _u32p, _sz, _sz, _u32p, _sz, C.c_uint64, C.c_float,
+                                     C.c_float, TOKEN_FN, _vp, _u32p, C.POINTER(_sz)]),
     "cx_sample": (C.c_int, [_vp, _sz, C.c_float, C.c_float, C.POINTER(C.c_uint64),
                             C.POINTER(C.c_uint32), _vp]),
 }

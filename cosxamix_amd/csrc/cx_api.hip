@@ -5,6 +5,8 @@
 #include <string.h>
 #include <math.h>
 
+#include <functional>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -20,26 +22,54 @@ void cx_set_error(const char* fmt, ...) {
 }
 extern "C" const char* cx_last_error(void) { return g_err; }
 
-// ==================================================== library-wide state
+// ================================================================ state
+// The device of the calling thread's host-pointer entry points and models.
 static thread_local int g_device = 0;
-static cx_lib g_libs[64];
-static bool g_lib_ready[64];
+
+// Per-device pools of thread contexts. A thread takes a context at its first
+// call on a device and gives it back when it ends; a context is never freed,
+// so no thread can see its stream or scratch released under it. The pool
+// only grows to the largest number of threads that ran at once.
+static std::mutex g_pool_mu;
+static std::vector<cx_lib*> g_pool[64];
+
+namespace {
+struct ThreadContexts {
+  cx_lib* ctx[64] = {};
+  ~ThreadContexts() {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    for (int d = 0; d < 64; d++)
+      if (ctx[d]) g_pool[d].push_back(ctx[d]);
+  }
+};
+}  // namespace
+static thread_local ThreadContexts t_ctx;
 
 cx_lib* cx_lib_get() {
-  int dev = g_device;
+  const int dev = g_device;
   if (dev < 0 || dev >= 64) return nullptr;
-  if (!g_lib_ready[dev]) {
-    if (hipSetDevice(dev) != hipSuccess) return nullptr;
-    cx_lib& L = g_libs[dev];
-    L.device = dev;
-    if (hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    L.scratch = nullptr;
-    L.scratch_bytes = 0;
-    g_lib_ready[dev] = true;
+  if (cx_lib* L = t_ctx.ctx[dev]) return L;
+  cx_lib* L = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    if (!g_pool[dev].empty()) {
+      L = g_pool[dev].back();
+      g_pool[dev].pop_back();
+    }
   }
-  return &g_libs[g_device];
+  if (!L) {
+    if (hipSetDevice(dev) != hipSuccess) return nullptr;
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    L = new cx_lib{dev, s, nullptr, 0};
+  }
+  t_ctx.ctx[dev] = L;
+  return L;
 }
 
+// The calling thread's scratch of at least `bytes`. Growing it waits for the
+// device (the old buffer may still be read by this thread's earlier calls on
+// any stream) before the old buffer is freed.
 int cx_scratch_reserve(size_t bytes, void** out) {
   cx_lib* L = cx_lib_get();
   if (!L) {
@@ -47,7 +77,7 @@ int cx_scratch_reserve(size_t bytes, void** out) {
     return CX_EHIP;
   }
   if (L->scratch_bytes < bytes) {
-    // the old buffer may still be read by work on any stream of the device
+    CX_HIP(hipSetDevice(L->device));
     CX_HIP(hipDeviceSynchronize());
     if (L->scratch) CX_HIP(hipFree(L->scratch));
     L->scratch = nullptr;
@@ -450,7 +480,7 @@ extern "C" int cx_sample(const float* logits, size_t n, float temperature, float
   CX_HIP(hipMemcpyAsync(sd, &h, sizeof h, hipMemcpyHostToDevice, s));
   if ((rc = cx_launch_sample(logits, n, sd, (float*)(b + o_pb), (float*)(b + o_part),
                              (uint32_t*)(b + o_ord), (float*)(b + o_ordp), tok, nullptr, nullptr,
-                             s)))
+                             nullptr, s)))
     return rc;
   CX_HIP(hipMemcpyAsync(&h, sd, sizeof h, hipMemcpyDeviceToHost, s));
   CX_HIP(hipStreamSynchronize(s));
@@ -482,6 +512,11 @@ struct Layer {
 struct cx_model {
   cx_config cfg;
   int device;
+  // caches made from this model and not yet freed; a model freed while some
+  // remain is released by the last cx_cache_free (they use its stream and
+  // buffers)
+  int n_caches;
+  bool closed;
   int t_embd, t_out;
   bool tied;  // no output.weight: the lm_head is token_embd (src/forward.rs:218-227)
   hipStream_t stream;
@@ -517,6 +552,8 @@ struct cx_cache {
   size_t cap, len;
   float* kv;        // [layers][2][cap][kvd]
   uint32_t* hist;   // tokens by position, cap + 1
+  uint32_t* htok;   // the generated tokens by position, pinned host memory, cap + 1
+  uint32_t* htok_dev;  // its device address (written by the token loop's last kernel)
   cx_dstate* st;
   float *pm, *pl, *po;  // split-K partials
   float* sc;            // scores of the order-exact attention, heads x cap
@@ -535,8 +572,7 @@ struct cx_cache {
 
 static void* pool_at(cx_model* m, size_t off) { return m->pool + off; }
 
-extern "C" void cx_model_free(cx_model* m) {
-  if (!m) return;
+static void model_destroy(cx_model* m) {
   (void)hipSetDevice(m->device);
   (void)hipStreamSynchronize(m->stream);
   float* bufs[] = {m->x,      m->q,   m->k,     m->v,     m->att, m->g, m->u,
@@ -549,6 +585,12 @@ extern "C" void cx_model_free(cx_model* m) {
   if (m->pool) (void)hipFree(m->pool);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
+}
+
+extern "C" void cx_model_free(cx_model* m) {
+  if (!m) return;
+  m->closed = true;
+  if (m->n_caches == 0) model_destroy(m);
 }
 
 static cx_model* model_new(const cx_config& c) {
@@ -1017,8 +1059,10 @@ extern "C" int cx_cache_new(cx_model* m, size_t cap, cx_cache** out) {
   CX_HIP(hipSetDevice(m->device));
   const cx_config& c = m->cfg;
   const size_t kvd = (size_t)c.kv_heads * (c.dim / c.heads);
+  CX_REQUIRE(!m->closed, "cache: the model was freed");
   cx_cache* C = new cx_cache();
   C->m = m;
+  m->n_caches++;
   C->cap = cap;
   C->len = 0;
   const size_t ns = cx_attn_splits(cap);
@@ -1026,7 +1070,9 @@ extern "C" int cx_cache_new(cx_model* m, size_t cap, cx_cache** out) {
       hipMalloc(&C->st, sizeof(cx_dstate)) || hipMalloc(&C->pm, ns * c.heads * 4) ||
       hipMalloc(&C->pl, ns * c.heads * 4) || hipMalloc(&C->po, ns * c.heads * (c.dim / c.heads) * 4) ||
       hipMalloc(&C->sc, cx_attn_score_floats(c.heads, cap) * 4) ||
-      hipMalloc(&C->cm, cx_attn_chunk_floats(c.heads, cap) * 4)) {
+      hipMalloc(&C->cm, cx_attn_chunk_floats(c.heads, cap) * 4) ||
+      hipHostMalloc((void**)&C->htok, (cap + 1) * 4, hipHostMallocMapped) ||
+      hipHostGetDevicePointer((void**)&C->htok_dev, C->htok, 0)) {
     cx_cache_free(C);
     cx_set_error("cache: cannot allocate %zu tokens", cap);
     return CX_ENOMEM;
@@ -1044,6 +1090,50 @@ extern "C" int cx_cache_truncate(cx_cache* c, size_t n) {
 extern "C" void cx_cache_clear(cx_cache* c) {
   if (c) c->len = 0;
 }
+// Cache::bytes (src/forward.rs:130-136): the f32 K and V the cache holds,
+// len tokens of every layer
+extern "C" size_t cx_cache_bytes(const cx_cache* c) {
+  if (!c) return 0;
+  const cx_config& g = c->m->cfg;
+  return c->len * 2 * (size_t)g.layers * g.kv_heads * (g.dim / g.heads) * 4;
+}
+// Cache::prefijo (src/forward.rs:117-128): a new cache of `cap` tokens (0 =
+// the source's capacity) holding a copy of the source's first min(n, len)
+// tokens; stream-ordered after the source's work
+extern "C" int cx_cache_prefix(const cx_cache* src, size_t n, size_t cap, cx_cache** out) {
+  CX_REQUIRE(src && out, "cache prefix: null argument");
+  cx_model* m = src->m;
+  const size_t keep = n < src->len ? n : src->len;
+  if (!cap) cap = src->cap;
+  CX_REQUIRE(keep <= cap, "cache prefix: %zu tokens do not fit a cache of %zu", keep, cap);
+  cx_cache* C = nullptr;
+  int rc = cx_cache_new(m, cap, &C);
+  if (rc) return rc;
+  const cx_config& g = m->cfg;
+  const size_t kvd = (size_t)g.kv_heads * (g.dim / g.heads);
+  hipStream_t s = m->stream;
+  if (keep) {
+    for (uint32_t l = 0; l < g.layers; l++)
+      for (int kv = 0; kv < 2; kv++) {
+        const float* from = src->kv + ((size_t)l * 2 + kv) * src->cap * kvd;
+        float* to = C->kv + ((size_t)l * 2 + kv) * cap * kvd;
+        if (hipMemcpyAsync(to, from, keep * kvd * 4, hipMemcpyDeviceToDevice, s) != hipSuccess) {
+          cx_cache_free(C);
+          cx_set_error("cache prefix: copy failed");
+          return CX_EHIP;
+        }
+      }
+    if (hipMemcpyAsync(C->hist, src->hist, keep * 4, hipMemcpyDeviceToDevice, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+      cx_cache_free(C);
+      cx_set_error("cache prefix: copy failed");
+      return CX_EHIP;
+    }
+  }
+  C->len = keep;
+  *out = C;
+  return CX_OK;
+}
 extern "C" void cx_cache_free(cx_cache* c) {
   if (!c) return;
   (void)hipSetDevice(c->m->device);
@@ -1057,7 +1147,10 @@ extern "C" void cx_cache_free(cx_cache* c) {
                   P.scratch};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
+  if (c->htok) (void)hipHostFree(c->htok);
+  cx_model* m = c->m;
   delete c;
+  if (--m->n_caches == 0 && m->closed) model_destroy(m);
 }
 
 // ------------------------------------------------------- one decode step
@@ -1178,8 +1271,9 @@ static int enqueue_tail(cx_cache* C) {
   }
   if (C->sampling)
     return cx_launch_sample(m->logits, c.vocab, C->sd, C->spb, C->spart, C->sord, C->sordp,
-                            m->amax_out, C->st, C->hist, s);
-  return cx_launch_argmax(m->logits, c.vocab, m->apv, m->api, m->amax_out, C->st, C->hist, s);
+                            m->amax_out, C->st, C->hist, C->htok_dev, s);
+  return cx_launch_argmax(m->logits, c.vocab, m->apv, m->api, m->amax_out, C->st, C->hist,
+                          C->htok_dev, s);
 }
 
 // the step graph of the current tail (greedy or sampling), captured once
@@ -1408,47 +1502,100 @@ extern "C" int cx_forward(cx_model* m, cx_cache* C, const uint32_t* toks, size_t
   return CX_OK;
 }
 
+// Modelo::generar (src/forward.rs:533-559), and the token loop of
+// MotorPropio (src/engine_own.rs:257-282), on the device token loop:
+//   logits = forward(prompt);
+//   repeat up to max_new times: t = elegir(logits); stop at a stop token
+//   (not returned); push t; al_token(t) == false stops; stop when the cache
+//   holds the context; logits = forward([t]).
+// The step graph reads each token from device memory and writes the next
+// one (to hist and to the pinned host copy htok), so steps are launched up
+// to `ahead` tokens before the host has looked at them; the host then reads
+// token k once step k-1 has finished and applies the stopping rule. Steps
+// launched past the stop only write the cache beyond its length: the cache
+// keeps exactly the prompt and the forwarded tokens, as the reference's.
 static int generate(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n, size_t max_new,
-                    uint32_t eos, uint32_t* out, size_t* n_out, float* step_ms) {
+                    const uint32_t* stops, size_t n_stops, cx_token_fn fn, void* user,
+                    uint32_t* out, size_t* n_out, float* step_ms) {
   CX_REQUIRE(m && C && C->m == m && n_out, "generate: bad arguments");
   CX_REQUIRE(prompt && n > 0, "generate: empty prompt");
+  CX_REQUIRE(stops || !n_stops, "generate: null stop list");
   *n_out = 0;
-  const size_t start = C->len;
-  // forward(prompt) + one forward per generated token, the last included
-  // (src/forward.rs:544-557), bounded by the context.
-  size_t steps = n + max_new;
-  if (start + steps > m->cfg.ctx) steps = m->cfg.ctx - start;
-  CX_REQUIRE(start + steps <= C->cap, "generate: %zu tokens past the cache of %zu", start + steps,
-             C->cap);
-  CX_REQUIRE(steps >= n, "generate: the prompt does not fit the context");
+  const size_t start = C->len, ctx = m->cfg.ctx;
+  CX_REQUIRE(start + n <= C->cap, "generate: the prompt needs %zu tokens of a cache of %zu",
+             start + n, C->cap);
   for (size_t i = 0; i < n; i++)
     CX_REQUIRE(prompt[i] < m->cfg.vocab, "generate: token %u is not in the vocabulary", prompt[i]);
   CX_HIP(hipSetDevice(m->device));
   CX_HIP(hipMemcpyAsync(C->hist + start, prompt, n * 4, hipMemcpyHostToDevice, m->stream));
   int rc = n > 1 ? prefill(C, n) : run_steps(C, start + n, n, nullptr);
   if (rc) return rc;
-  rc = run_steps(C, start + n, steps - n, step_ms);
-  if (rc) return rc;
-  // generated token i sits at position start+n+i
-  const size_t made = steps - n + 1 > max_new ? max_new : steps - n + 1;
-  std::vector<uint32_t> toks(made);
-  CX_HIP(hipMemcpy(toks.data(), C->hist + start + n, made * 4, hipMemcpyDeviceToHost));
-  size_t k = 0;
-  for (; k < made; k++) {
-    if (toks[k] == eos) break;
-    if (out) out[k] = toks[k];
+  if (!max_new) return CX_OK;
+  // generated token k is at position pos0 + k; step k forwards it
+  const size_t pos0 = start + n;
+  size_t can = max_new < ctx - pos0 ? max_new : ctx - pos0;  // steps the reference may take
+  if (can > C->cap - pos0) can = C->cap - pos0;               // steps the cache holds
+  const size_t ahead = fn ? 2 : 8;
+  cx_dstate st{(uint32_t)pos0, (uint32_t)pos0, (uint32_t)C->cap, 0};
+  CX_HIP(hipMemcpyAsync(C->st, &st, sizeof st, hipMemcpyHostToDevice, m->stream));
+  if ((rc = ensure_graph(C))) return rc;
+  const hipGraphExec_t exec = C->sampling ? C->exec_s : C->exec;
+  // ev[i + 1] follows step i; ev[0] precedes step 0 (a ring when not timing)
+  const size_t nev = step_ms ? can + 1 : ahead + 2;
+  std::vector<hipEvent_t> ev(nev);
+  for (auto& e : ev) CX_HIP(hipEventCreate(&e));
+  auto event = [&](size_t i) { return ev[i % nev]; };
+  rc = CX_OK;
+  hipError_t he = hipEventRecord(event(0), m->stream);
+  size_t launched = 0, made = 0, forwarded = 0;
+  for (size_t k = 0; he == hipSuccess; k++) {
+    while (he == hipSuccess && launched < can && launched < k + ahead) {
+      he = hipGraphLaunch(exec, m->stream);
+      if (he == hipSuccess) he = hipEventRecord(event(launched + 1), m->stream);
+      launched++;
+    }
+    if (he != hipSuccess) break;
+    // token 0 came with the prompt's forward (synchronous); token k > 0 with step k - 1
+    if (k > 0 && (he = hipEventSynchronize(event(k))) != hipSuccess) break;
+    const uint32_t t = C->htok[pos0 + k];
+    bool stop = false;
+    for (size_t i = 0; i < n_stops; i++) stop |= t == stops[i];
+    if (stop) break;
+    if (out) out[made] = t;
+    made++;
+    if (fn && !fn(t, user)) break;
+    if (pos0 + k >= ctx) break;  // the cache holds the context: t is not forwarded
+    if (k >= can) {              // the reference forwards t; this cache has no room for it
+      cx_set_error("generate: the cache of %zu tokens is full before generation ends", C->cap);
+      rc = CX_ENOMEM;
+      break;
+    }
+    forwarded = k + 1;
+    if (made == max_new) break;
   }
-  *n_out = k;
-  // Modelo::generar forwards every pushed token, and stops at EOS without
-  // forwarding it: the cache holds the prompt plus the pushed tokens.
-  if (k < made) C->len = start + n + k;
-  return CX_OK;
+  const hipError_t se = hipStreamSynchronize(m->stream);  // steps launched past the stop
+  if (he == hipSuccess) he = se;
+  if (he == hipSuccess && step_ms)
+    for (size_t i = 0; i < launched && he == hipSuccess; i++)
+      he = hipEventElapsedTime(&step_ms[i], ev[i], ev[i + 1]);
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  CX_HIP(he);
+  C->len = pos0 + forwarded;
+  *n_out = made;
+  return rc;
+}
+
+static int generate_eos(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n,
+                        size_t max_new, uint32_t eos, uint32_t* out, size_t* n_out,
+                        float* step_ms) {
+  return generate(m, C, prompt, n, max_new, &eos, eos == UINT32_MAX ? 0 : 1, nullptr, nullptr,
+                  out, n_out, step_ms);
 }
 
 extern "C" int cx_generate(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n,
                            size_t max_new, uint32_t eos, uint32_t* out, size_t* n_out,
                            float* step_ms) {
-  return generate(m, C, prompt, n, max_new, eos, out, n_out, step_ms);
+  return generate_eos(m, C, prompt, n, max_new, eos, out, n_out, step_ms);
 }
 
 static int sampler_buffers(cx_cache* C) {
@@ -1465,11 +1612,12 @@ static int sampler_buffers(cx_cache* C) {
   return CX_OK;
 }
 
-extern "C" int cx_generate_sampled(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n,
-                                   size_t max_new, uint32_t eos, uint64_t seed, float temperature,
-                                   float top_p, uint32_t* out, size_t* n_out, float* step_ms) {
-  // src/sampler.rs:65-66: temperature <= 0 is greedy, with no draw
-  if (temperature <= 0.0f) return generate(m, C, prompt, n, max_new, eos, out, n_out, step_ms);
+// Muestreador::nuevo(seed, temperature, top_p) (src/sampler.rs:38-47) for
+// the generation that follows; temperature <= 0 is greedy, with no draw
+// (src/sampler.rs:65-66)
+static int sampled(cx_model* m, cx_cache* C, uint64_t seed, float temperature, float top_p,
+                   const std::function<int()>& run) {
+  if (temperature <= 0.0f) return run();
   CX_REQUIRE(m && C && C->m == m, "generate: bad arguments");
   CX_HIP(hipSetDevice(m->device));
   int rc = sampler_buffers(C);
@@ -1477,7 +1625,25 @@ extern "C" int cx_generate_sampled(cx_model* m, cx_cache* C, const uint32_t* pro
   const cx_samp_state h = sampler_state(seed, temperature, top_p);
   CX_HIP(hipMemcpyAsync(C->sd, &h, sizeof h, hipMemcpyHostToDevice, m->stream));
   C->sampling = true;
-  rc = generate(m, C, prompt, n, max_new, eos, out, n_out, step_ms);
+  rc = run();
   C->sampling = false;
   return rc;
 }
+
+extern "C" int cx_generate_sampled(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n,
+                                   size_t max_new, uint32_t eos, uint64_t seed, float temperature,
+                                   float top_p, uint32_t* out, size_t* n_out, float* step_ms) {
+  return sampled(m, C, seed, temperature, top_p, [&] {
+    return generate_eos(m, C, prompt, n, max_new, eos, out, n_out, step_ms);
+  });
+}
+
+extern "C" int cx_generate_stream(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n,
+                                  size_t max_new, const uint32_t* stops, size_t n_stops,
+                                  uint64_t seed, float temperature, float top_p, cx_token_fn fn,
+                                  void* user, uint32_t* out, size_t* n_out) {
+  return sampled(m, C, seed, temperature, top_p, [&] {
+    return generate(m, C, prompt, n, max_new, stops, n_stops, fn, user, out, n_out, nullptr);
+  });
+}
+

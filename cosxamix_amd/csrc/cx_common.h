@@ -223,12 +223,17 @@ __device__ inline int8_t cx_rust_i8(float r) {
   return (int8_t)(uint8_t)(uint32_t)v;
 }
 
-// ------------------------------------------------- library-wide state
+// ------------------------------------------------- library state
+// A host thread's context on one device: the stream of the host-pointer
+// entry points and the device scratch of the operators. Each host thread
+// holds its own (taken from a per-device pool at its first call, returned
+// when the thread ends), so calls from different threads never share a
+// stream or a scratch buffer.
 struct cx_lib {
   int device;
   hipStream_t stream;   // library stream for host-pointer entry points
-  void* scratch;        // device scratch for host-pointer entry points
+  void* scratch;        // device scratch of this thread's calls
   size_t scratch_bytes;
 };
-cx_lib* cx_lib_get();   // initialises lazily on device 0
+cx_lib* cx_lib_get();   // the calling thread's context on its current device
 int cx_scratch_reserve(size_t bytes, void** out);

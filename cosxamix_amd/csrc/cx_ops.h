@@ -29,10 +29,11 @@ size_t cx_sample_parts(size_t n);
 // One Muestreador::elegir with temperature on device logits[n]: pb (n
 // floats), part (cx_sample_parts(n) words), ord (n), ordp (n floats) are scratch;
 // the token goes to *out (device, optional) and, with st, to hist[pos + 1]
-// with the position advanced (the token loop's argmax step).
+// (and hist_host[pos + 1], pinned host memory, when given) with the position
+// advanced (the token loop's argmax step).
 int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb, float* part,
                      uint32_t* ord, float* ordp, uint32_t* out, cx_dstate* st, uint32_t* hist,
-                     hipStream_t s);
+                     uint32_t* hist_host, hipStream_t s);
 
 #define CX_ATT_MAX_TOTAL 16000  // general attention keeps scores in LDS
 // Decode attention holds a head's scores in LDS for caches up to this many
@@ -92,7 +93,7 @@ int cx_launch_softmax(float* x, size_t len, size_t width, hipStream_t s);
 int cx_launch_silu(float* out, const float* in, size_t n, hipStream_t s);
 size_t cx_argmax_parts(size_t n);
 int cx_launch_argmax(const float* v, size_t n, float* pv, uint32_t* pi, uint32_t* out,
-                     cx_dstate* st, uint32_t* hist, hipStream_t s);
+                     cx_dstate* st, uint32_t* hist, uint32_t* hist_host, hipStream_t s);
 
 int cx_launch_argmax_one(const float* v, size_t n, uint32_t* out, hipStream_t s);
 int cx_launch_rope(float* x, size_t tokens, size_t heads, size_t hd, const float* cos_t,

@@ -729,12 +729,12 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float* v, uint32_t n,
 }
 
 // Final reduction. With `st` (the model's token loop), also advances the
-// loop: hist[pos+1] = argmax when position pos+1 is past the prompt, then
-// pos += 1.
+// loop: hist[pos+1] = argmax when position pos+1 is past the prompt (and the
+// same slot of the pinned host copy hist_host, when given), then pos += 1.
 __global__ __launch_bounds__(256) void k_argmax_final(const float* v, const float* pv,
                                                       const uint32_t* pi, uint32_t nparts,
                                                       uint32_t* out, cx_dstate* st,
-                                                      uint32_t* hist) {
+                                                      uint32_t* hist, uint32_t* hist_host) {
   __shared__ VI red[4];
   VI best{-INFINITY, 0xFFFFFFFFu};
   for (uint32_t i = threadIdx.x; i < nparts; i += 256) best = vi_best(best, VI{pv[i], pi[i]});
@@ -749,7 +749,10 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float* v, const floa
     if (out) *out = tok;
     if (st) {
       const uint32_t nxt = st->pos + 1;
-      if (nxt >= st->prompt_end && nxt <= st->cap) hist[nxt] = tok;  // hist has cap+1 slots
+      if (nxt >= st->prompt_end && nxt <= st->cap) {  // hist has cap+1 slots
+        hist[nxt] = tok;
+        if (hist_host) hist_host[nxt] = tok;
+      }
       st->pos = nxt;
     }
   }
@@ -959,12 +962,13 @@ int cx_launch_silu(float* out, const float* in, size_t n, hipStream_t s) {
 size_t cx_argmax_parts(size_t n) { return (n + ARG_CHUNK - 1) / ARG_CHUNK; }
 
 int cx_launch_argmax(const float* v, size_t n, float* pv, uint32_t* pi, uint32_t* out,
-                     cx_dstate* st, uint32_t* hist, hipStream_t s) {
+                     cx_dstate* st, uint32_t* hist, uint32_t* hist_host, hipStream_t s) {
   CX_REQUIRE(n > 0 && n < 0xFFFFFFFFull, "argmax: length %zu", n);
   const uint32_t parts = (uint32_t)cx_argmax_parts(n);
   hipLaunchKernelGGL(k_argmax_part, dim3(parts), dim3(256), 0, s, v, (uint32_t)n, pv, pi);
   CX_HIP(hipGetLastError());
-  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, v, pv, pi, parts, out, st, hist);
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, v, pv, pi, parts, out, st, hist,
+                     hist_host);
   CX_HIP(hipGetLastError());
   return CX_OK;
 }

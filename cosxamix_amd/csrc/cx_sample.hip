@@ -438,7 +438,8 @@ __global__ __launch_bounds__(RS_T) void k_rs_scatter(const float* pb, const uint
 // argmax does.
 __global__ __launch_bounds__(CW) void k_samp_pick(const float* pb, uint32_t n, cx_samp_state* sd,
                                                   const uint32_t* ord, const float* ordp,
-                                                  uint32_t* out, cx_dstate* st, uint32_t* hist) {
+                                                  uint32_t* out, cx_dstate* st, uint32_t* hist,
+                                                  uint32_t* hist_host) {
   extern __shared__ __align__(16) float ring[];
   __shared__ float s_acc;
   const uint32_t tid = threadIdx.x;
@@ -476,7 +477,10 @@ __global__ __launch_bounds__(CW) void k_samp_pick(const float* pb, uint32_t n, c
     sd->token = tok;
     if (st) {
       const uint32_t nxt = st->pos + 1;
-      if (nxt >= st->prompt_end && nxt <= st->cap) hist[nxt] = tok;  // hist has cap+1 slots
+      if (nxt >= st->prompt_end && nxt <= st->cap) {  // hist has cap+1 slots
+        hist[nxt] = tok;
+        if (hist_host) hist_host[nxt] = tok;
+      }
       st->pos = nxt;
     }
   }
@@ -503,7 +507,7 @@ size_t cx_sample_parts(size_t n) { return sort_scratch(n).words(); }
 
 int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb, float* part,
                      uint32_t* ord, float* ordp, uint32_t* out, cx_dstate* st, uint32_t* hist,
-                     hipStream_t s) {
+                     uint32_t* hist_host, hipStream_t s) {
   CX_REQUIRE(logits && sd && pb && part && ord && ordp && n > 0 && n < (1u << 31),
              "sample: bad arguments (n=%zu)", n);
   CX_REQUIRE(((uintptr_t)pb & 15) == 0 && ((uintptr_t)ordp & 15) == 0,
@@ -546,7 +550,7 @@ int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb
       (rc = pass(k_rs_count<3>, k_rs_scatter<3>, kA, iA, nullptr, ord, ordp)))
     return rc;
   hipLaunchKernelGGL(k_samp_pick, dim3(1), dim3(CW), PICK_LDS, s, pb, N, sd, ord, ordp, out, st,
-                     hist);
+                     hist, hist_host);
   CX_HIP(hipGetLastError());
   return CX_OK;
 }

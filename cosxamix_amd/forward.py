@@ -148,11 +148,20 @@ class Modelo:
         return lg, am.value
 
     def generar(self, prompt, max_nuevos: int, cache: "Cache", fin: int | None = None,
-                tiempos: bool = False, muestreador=None):
+                tiempos: bool = False, muestreador=None, al_token=None, fines=None):
         """Modelo::generar (src/forward.rs:533-559): greedy, or with a
         ``sampler.Muestreador`` (its seed, temperature and top_p; the draws
         happen on the GPU). Returns the tokens, and the per-token decode times
-        in ms if `tiempos`."""
+        in ms if `tiempos`. ``al_token(t) -> bool`` is called with each token
+        as it is pushed (False stops at once, src/forward.rs:549-551);
+        ``fines`` is a list of stop tokens (MotorPropio stops at the end
+        token and the chat's end of turn, src/engine_own.rs:259-261)."""
+        if al_token is not None or fines is not None:
+            if tiempos:
+                raise ValueError("generar: tiempos with al_token/fines is not supported")
+            return self._generar_stream(prompt, max_nuevos, cache,
+                                        ([] if fin is None else [fin]) + list(fines or []),
+                                        muestreador, al_token)
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
         out = np.zeros(max(max_nuevos, 1), np.uint32)
         n = C.c_size_t()
@@ -181,6 +190,41 @@ class Modelo:
         toks = out[: n.value].copy()
         return (toks, ms) if tiempos else toks
 
+    def _generar_stream(self, prompt, max_nuevos, cache, fines, muestreador, al_token):
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(max_nuevos, 1), np.uint32)
+        stops = np.ascontiguousarray(fines, dtype=np.uint32)
+        n = C.c_size_t()
+        estado = {"error": None, "parado": False}
+
+        def cb(t, _user):
+            try:
+                sigue = bool(al_token(int(t)))
+            except BaseException as e:  # stops generation; raised once the call returns
+                estado["error"] = e
+                sigue = False
+            estado["parado"] = not sigue
+            return 1 if sigue else 0
+
+        fn = L.TOKEN_FN(cb) if al_token is not None else L.TOKEN_FN()
+        seed, temp, top_p = ((muestreador.estado, muestreador.temperatura, muestreador.top_p)
+                             if muestreador is not None else (0, 0.0, 1.0))
+        inicio = cache.largo()
+        rc = _lib.cx_generate_stream(self._h, cache._h, p.ctypes.data_as(L._u32p), p.size,
+                                     max_nuevos, stops.ctypes.data_as(L._u32p), stops.size,
+                                     seed, temp, top_p, fn, None, out.ctypes.data_as(L._u32p),
+                                     C.byref(n))
+        if estado["error"] is not None:
+            raise estado["error"]
+        L.check(rc, "generar")
+        if muestreador is not None and temp > 0.0:
+            # one draw per pushed token, and one more for a stop token: the
+            # loop stopped short of max_nuevos and of the context, not by al_token
+            hechos = min(max_nuevos, self.cfg.contexto - inicio - p.size + 1)
+            fin = n.value < hechos and not estado["parado"]
+            muestreador.avanzar(n.value + (1 if fin else 0))
+        return out[: n.value].copy()
+
 
 class Cache:
     """forward::Cache (src/forward.rs:62-137) with room for `capacidad` tokens."""
@@ -194,6 +238,22 @@ class Cache:
 
     def largo(self) -> int:
         return int(_lib.cx_cache_len(self._h))
+
+    def bytes(self) -> int:
+        """Cache::bytes (src/forward.rs:130-136): K and V bytes held."""
+        return int(_lib.cx_cache_bytes(self._h))
+
+    def prefijo(self, n: int, capacidad: int = 0) -> "Cache":
+        """Cache::prefijo (src/forward.rs:117-128): a new cache holding a copy
+        of the first min(n, largo) tokens (room for `capacidad`, 0 = this
+        cache's)."""
+        h = C.c_void_p()
+        L.check(_lib.cx_cache_prefix(self._h, n, capacidad, C.byref(h)), "prefijo")
+        c = Cache.__new__(Cache)
+        c.modelo = self.modelo
+        c._h = h
+        self.modelo._caches.add(c)
+        return c
 
     def truncar(self, n: int) -> None:
         L.check(_lib.cx_cache_truncate(self._h, n), "truncar")

@@ -22,8 +22,16 @@
  *     `stream` is a hipStream_t (NULL = the HIP null stream) and the call is
  *     asynchronous on it. Level-3 objects own their device memory.
  *   - Types are GGML type ids (src/gguf.rs:39-54).
- *   - A cx_model / cx_cache is not thread-safe; the reference serialises
- *     generation behind a Mutex (src/engine_own.rs:62,185).
+ *   - Threads. Level-1 functions are reentrant and thread-safe, like the
+ *     reference's pure `type Kernel` that rayon calls from many threads at
+ *     once (src/ops.rs:487-500): each host thread has its own stream and
+ *     device scratch. Level-2 functions may run on several threads at once
+ *     (each thread's scratch is its own); calls of ONE thread that use the
+ *     scratch (cx_matmul_auto, cx_matmul_multi_1row, cx_gemv_subsums,
+ *     cx_dequantize_rows, cx_attention_decode, cx_sample) on different
+ *     streams must be ordered by the caller. A cx_model and its caches are
+ *     used by one thread at a time; the reference serialises generation
+ *     behind a Mutex (src/engine_own.rs:62,185).
  */
 #ifndef COSXAMIX_HIP_H
 #define COSXAMIX_HIP_H
@@ -305,12 +313,23 @@ const void *cx_model_tensor_data(const cx_model *m, int idx);
  * row); the algorithmic traffic of one token without the KV reads. */
 size_t cx_model_weight_bytes(const cx_model *m);
 
-/* forward::Cache (src/forward.rs:62-137), with room for `cap` tokens. */
+/* forward::Cache (src/forward.rs:62-137), with room for `cap` tokens. A
+ * cache belongs to its model: cx_model_free on a model with live caches
+ * releases the model when its last cache is freed (caches can be freed
+ * before or after their model). */
 int cx_cache_new(cx_model *m, size_t cap, cx_cache **out);
 size_t cx_cache_len(const cx_cache *c);
 int cx_cache_truncate(cx_cache *c, size_t n);
 void cx_cache_clear(cx_cache *c);
 void cx_cache_free(cx_cache *c);
+/* Cache::bytes (src/forward.rs:130-136): bytes of K and V the cache holds
+ * (len tokens x layers x 2 x kv_heads*head_dim f32), not its capacity. */
+size_t cx_cache_bytes(const cx_cache *c);
+/* Cache::prefijo (src/forward.rs:117-128): a new cache of the same model
+ * with room for `cap` tokens (0 = the source's capacity) holding a copy of
+ * the source's first min(n, len) tokens, as MotorPropio borrows another
+ * session's prefix (src/engine_own.rs:227-245). */
+int cx_cache_prefix(const cx_cache *src, size_t n, size_t cap, cx_cache **out);
 
 /* Modelo::forward (src/forward.rs:375-505): appends `t` tokens to the cache
  * and gives the logits of the last one (HOST buffer of vocab floats, may be
@@ -320,9 +339,14 @@ int cx_forward(cx_model *m, cx_cache *c, const uint32_t *toks, size_t t,
 
 /* Modelo::generar (src/forward.rs:533-559) with a greedy sampler
  * (src/sampler.rs:65-66): prefill `prompt`, then up to max_new tokens.
- * `eos` stops generation like Modelo::fin (pass UINT32_MAX for none).
- * out[] gets the tokens, *n_out how many. If step_ms is not NULL it gets
- * max_new per-token decode times (ms, measured with HIP events). */
+ * `eos` stops generation like Modelo::fin (pass UINT32_MAX for none): the
+ * stop token is not returned or forwarded, and the device stops within a
+ * few steps of it. out[] gets the tokens, *n_out how many; the cache then
+ * holds the prompt and the forwarded tokens, as the reference's. The cache
+ * needs room for the positions generation reaches (CX_ENOMEM, with the
+ * tokens made so far in out/n_out, when it fills first). If step_ms is not
+ * NULL it gets one decode time per step run (ms, HIP events; max_new of
+ * them when generation runs to max_new). */
 int cx_generate(cx_model *m, cx_cache *c, const uint32_t *prompt, size_t n,
                 size_t max_new, uint32_t eos, uint32_t *out, size_t *n_out,
                 float *step_ms);
@@ -333,6 +357,23 @@ int cx_generate_sampled(cx_model *m, cx_cache *c, const uint32_t *prompt,
                         size_t n, size_t max_new, uint32_t eos, uint64_t seed,
                         float temperature, float top_p, uint32_t *out,
                         size_t *n_out, float *step_ms);
+
+/* The `al_token` of Modelo::generar (src/forward.rs:538-553): called on the
+ * calling thread with each token as it is pushed; returning 0 stops
+ * generation at once (that token is returned, not forwarded). */
+typedef int (*cx_token_fn)(uint32_t token, void *user);
+/* Modelo::generar with its per-token callback, and MotorPropio's token loop
+ * (src/engine_own.rs:257-282): any of the n_stops tokens in `stops` ends
+ * generation unreturned (the reference stops at Modelo::fin and at the
+ * chat's end-of-turn token); temperature <= 0 is greedy, otherwise
+ * Muestreador::nuevo(seed, temperature, top_p) draws on the GPU. The
+ * callback sees each token while the next steps already run on the device;
+ * otherwise as cx_generate. `fn` may be NULL. */
+int cx_generate_stream(cx_model *m, cx_cache *c, const uint32_t *prompt,
+                       size_t n, size_t max_new, const uint32_t *stops,
+                       size_t n_stops, uint64_t seed, float temperature,
+                       float top_p, cx_token_fn fn, void *user, uint32_t *out,
+                       size_t *n_out);
 
 #ifdef __cplusplus
 }
