@@ -63,6 +63,7 @@ SIGNATURES = {
     "cx_dequantize_rows": (C.c_int, [C.c_int, _vp, _sz, _sz, C.POINTER(_sz), _sz, _vp, _vp]),
     "cx_unpack_i8": (C.c_int, [C.c_int, _vp, _sz, _vp, _vp, _vp, C.POINTER(C.c_int), _vp]),
     "cx_matmul_auto": (C.c_int, [_sz, _sz, _sz, _vp, _vp, C.c_int, _vp, _vp]),
+    "cx_matmul_auto_noalloc": (C.c_int, [_sz, _sz, _sz, _vp, _vp, C.c_int, _vp, _vp]),
     "cx_matmul_multi_1row": (C.c_int, [_vp, _sz, _sz, C.POINTER(_vp), C.POINTER(C.c_int),
                                        C.POINTER(_sz), C.POINTER(_vp), _vp]),
     "cx_rmsnorm": (C.c_int, [_vp, _vp, _vp, _sz, _sz, C.c_float, _vp]),

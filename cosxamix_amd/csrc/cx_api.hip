@@ -89,12 +89,17 @@ int cx_scratch_reserve(size_t bytes, void** out) {
   return CX_OK;
 }
 
+static int noalloc_scratch(int dev, void** out);
+
 extern "C" int cx_init(int device) {
   int n = 0;
   CX_HIP(hipGetDeviceCount(&n));
   CX_REQUIRE(device >= 0 && device < n && device < 64, "cx_init: device %d of %d", device, n);
   g_device = device;
   CX_HIP(hipSetDevice(device));
+  void* sp = nullptr;
+  int rc = noalloc_scratch(device, &sp);
+  if (rc) return rc;
   return cx_lib_get() ? CX_OK : CX_EHIP;
 }
 
@@ -263,12 +268,24 @@ extern "C" int cx_unpack_i8(int type, const uint8_t* bytes, size_t n, int8_t* q,
   return rc;
 }
 
-extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, const uint8_t* w,
-                              int type, float* dst, void* stream) {
+// Scratch bytes cx_matmul_auto needs for m rows of k values of `type`: the
+// MFMA contraction's padded rows for m > 1, the rows' i8 quantization for
+// the row-by-row GEMV, nothing for F32/F16.
+static size_t matmul_auto_scratch(size_t m, size_t k, int type) {
+  if (type == CX_F32 || type == CX_F16 || !m) return 0;
+  if (m > 1 && cx_gemm_supported(type)) return cx_gemm_scratch_bytes(m, k);
+  auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+  return up(m * k) + 2 * up(m * (k / cx_sub(type)) * 4);
+}
+
+// cx_matmul_auto on a given scratch (at least matmul_auto_scratch bytes,
+// 256-byte aligned); `reserve` when the thread's own scratch is to be used
+static int matmul_auto_on(size_t m, size_t k, size_t n, const float* lhs, const uint8_t* w,
+                          int type, float* dst, void* scratch, bool reserve, hipStream_t s) {
   // src/ops.rs:1064-1071: the unquantized formats take the f32 path
   if (type == CX_F32 || type == CX_F16) {
     CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
-    return cx_launch_matmul_f(type, w, n, k, lhs, m, dst, STREAM(stream));
+    return cx_launch_matmul_f(type, w, n, k, lhs, m, dst, s);
   }
   CX_REQUIRE(cx_has_gemv(type), "matmul_auto: type %d has no quantized path here", type);
   CX_REQUIRE(k % (size_t)cx_vpb(type) == 0, "matmul_auto: a row of %zu is not a multiple of the block of %d",
@@ -276,29 +293,84 @@ extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, co
   CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
   CX_REQUIRE(n < (1u << 31) && k < (1u << 31), "matmul_auto: shape too large");
   if (!m || !n) return CX_OK;
-  // Several rows of a Q4_K/Q5_K matrix: all at once on int8 MFMA, each
-  // output bit-identical to the row-by-row GEMV below.
-  if (m > 1 && cx_gemm_supported(type)) {
-    void* sp = nullptr;
-    int rc = cx_scratch_reserve(cx_gemm_scratch_bytes(m, k), &sp);
+  if (reserve) {
+    int rc = cx_scratch_reserve(matmul_auto_scratch(m, k, type), &scratch);
     if (rc) return rc;
-    return cx_launch_gemm(type, w, n, k, lhs, m, dst, sp, STREAM(stream));
   }
+  // Several rows: all at once on int8 MFMA, each output bit-identical to the
+  // row-by-row GEMV below.
+  if (m > 1 && cx_gemm_supported(type))
+    return cx_launch_gemm(type, w, n, k, lhs, m, dst, scratch, s);
   // Every input row is quantized once (ops.rs:469-483), then each output row
   // is the fused GEMV of its own input row: row by row is exactly the
   // reference's "one row equals a batch" (ops.rs:1364-1393).
-  QuantScratch q;
+  auto up = [](size_t b) { return (b + 255) / 256 * 256; };
   const int sub = cx_sub(type);
-  int rc = quant_scratch(m, k, sub == 16 ? &q : nullptr, sub == 32 ? &q : nullptr);
-  if (!rc) rc = cx_launch_quantize(lhs, m, k, sub, q.xq, q.xe, q.xs, STREAM(stream));
+  uint8_t* p = (uint8_t*)scratch;
+  QuantScratch q;
+  q.xq = (int8_t*)p;
+  q.xe = (float*)(p + up(m * k));
+  q.xs = (float*)(p + up(m * k) + up(m * (k / sub) * 4));
+  int rc = cx_launch_quantize(lhs, m, k, sub, q.xq, q.xe, q.xs, s);
   if (rc) return rc;
   for (size_t f = 0; f < m; f++) {
     cx_seg seg{w, dst + f * n, nullptr, (uint32_t)n};
-    rc = cx_launch_gemv(type, &seg, 1, (uint32_t)k, q.row(f, k, cx_sub(type)), CX_EPI_STORE,
-                        nullptr, STREAM(stream));
+    rc = cx_launch_gemv(type, &seg, 1, (uint32_t)k, q.row(f, k, sub), CX_EPI_STORE, nullptr, s);
     if (rc) return rc;
   }
   return CX_OK;
+}
+
+extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, const uint8_t* w,
+                              int type, float* dst, void* stream) {
+  return matmul_auto_on(m, k, n, lhs, w, type, dst, nullptr, true, STREAM(stream));
+}
+
+// ------------------------------------------- the allocation-free variant
+// cx_matmul_auto for callers that cannot allocate: its scratch is this
+// fixed array, one copy per GPU, held until the process ends. Every call on
+// a GPU shares that GPU's copy, so calls that overlap on one GPU (from any
+// thread or stream) race; nothing in it needs to start at zero (the
+// quantization writes every byte the contraction reads).
+static __device__ __align__(256) uint8_t scratch[CX_NOALLOC_SCRATCH_BYTES];
+
+// The array's device address on each GPU, found once per device with that
+// device current (the host-side name is not a device address).
+static void* g_scratch_ptr[64];
+static hipError_t g_scratch_err[64];
+static std::once_flag g_scratch_once[64];
+
+static int noalloc_scratch(int dev, void** out) {
+  CX_REQUIRE(dev >= 0 && dev < 64, "no HIP device %d", dev);
+  std::call_once(g_scratch_once[dev], [dev] {
+    int prev = 0;
+    hipError_t e = hipGetDevice(&prev);
+    if (e == hipSuccess) e = hipSetDevice(dev);
+    if (e == hipSuccess) e = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
+    if (e == hipSuccess) e = hipSetDevice(prev);
+    g_scratch_err[dev] = e;
+  });
+  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev]) {
+    cx_set_error("matmul_auto_noalloc: the scratch of device %d has no address: %s", dev,
+                 hipGetErrorString(g_scratch_err[dev]));
+    return CX_EHIP;
+  }
+  *out = g_scratch_ptr[dev];
+  return CX_OK;
+}
+
+extern "C" int cx_matmul_auto_noalloc(size_t m, size_t k, size_t n, const float* lhs,
+                                      const uint8_t* w, int type, float* dst, void* stream) {
+  const size_t need = matmul_auto_scratch(m, k, type);
+  CX_REQUIRE(need <= CX_NOALLOC_SCRATCH_BYTES,
+             "matmul_auto_noalloc: %zu x %zu rows need %zu bytes of scratch, past its %d", m, k,
+             need, CX_NOALLOC_SCRATCH_BYTES);
+  int dev = 0;
+  CX_HIP(hipGetDevice(&dev));
+  void* sp = nullptr;
+  int rc = noalloc_scratch(dev, &sp);
+  if (rc) return rc;
+  return matmul_auto_on(m, k, n, lhs, w, type, dst, sp, false, STREAM(stream));
 }
 
 extern "C" int cx_matmul_multi_1row(const float* x, size_t k, size_t count,

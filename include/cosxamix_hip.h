@@ -157,6 +157,20 @@ int cx_unpack_i8(int type, const uint8_t *bytes, size_t n, int8_t *q,
 int cx_matmul_auto(size_t m, size_t k, size_t n, const float *lhs,
                    const uint8_t *w, int type, float *dst, void *stream);
 
+/* cx_matmul_auto without allocating: no counterpart in the reference. For
+ * callers that cannot call hipMalloc (code under HIP graph capture, serving
+ * loops, harnesses that forbid allocation). Same arguments and results as
+ * cx_matmul_auto (bit-identical), but its scratch is a fixed device array of
+ * CX_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends: a call
+ * needing more (about m * k bytes plus m * k / 2 for m > 1, m * k * 1.5 for
+ * m = 1) fails with CX_EINVAL. Every call on a GPU shares that array, so
+ * calls that overlap on one GPU (any thread, any stream) race: order them.
+ * The first call on a device (or cx_init) looks the array's address up. */
+#define CX_NOALLOC_SCRATCH_BYTES (32 << 20)
+int cx_matmul_auto_noalloc(size_t m, size_t k, size_t n, const float *lhs,
+                           const uint8_t *w, int type, float *dst,
+                           void *stream);
+
 /* ops::matmul_varias_una_fila (src/ops.rs:895-1009): dsts[i] = x . W_i^T for
  * `count` matrices sharing one activation vector of length k; one
  * quantization per sub size and one launch per type. Bit-identical to
