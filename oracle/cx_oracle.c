@@ -14,6 +14,7 @@
  */
 #include "cx_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -1165,33 +1166,97 @@ int orc_softmax(float *x, size_t len, size_t width) {
   }
   return 0;
 }
-/* src/ops.rs:1258-1325 — causal GQA; head h reads kv group h/(H/Hkv) */
+/* src/ops.rs:1258-1325 — causal GQA; head h reads kv group h/(H/Hkv).
+ * Each score is kernels::dot's sequential sum from 0 times the scale, and
+ * each output value the sum of prob*v in position order from 0. For many
+ * query rows the keys are first copied to a [group dim][position] layout so
+ * that sixteen positions' sums advance together in AVX lanes, each lane in
+ * its own order; the output's dims advance together the same way. */
+static void scores16(const float *qh, const float *kg, size_t total, size_t hd, size_t p,
+                     float scale, float *pts) {
+  __m256 s0 = _mm256_setzero_ps(), s1 = _mm256_setzero_ps();
+  for (size_t d = 0; d < hd; d++) {
+    const __m256 qd = _mm256_set1_ps(qh[d]);
+    const float *kd = kg + d * total + p;
+    s0 = _mm256_add_ps(s0, _mm256_mul_ps(qd, _mm256_loadu_ps(kd)));
+    s1 = _mm256_add_ps(s1, _mm256_mul_ps(qd, _mm256_loadu_ps(kd + 8)));
+  }
+  const __m256 sc = _mm256_set1_ps(scale);
+  _mm256_storeu_ps(pts + p, _mm256_mul_ps(s0, sc));
+  _mm256_storeu_ps(pts + p + 8, _mm256_mul_ps(s1, sc));
+}
+
+/* out[d] = sum_p prob[p] * v[p][d] in position order, 64 dims at a time */
+static void weighted_sum(const float *pts, const float *v, size_t wkv, size_t vis, size_t hd,
+                         float *dst) {
+  size_t d0 = 0;
+  for (; d0 + 64 <= hd; d0 += 64) {
+    __m256 a[8];
+    for (int i = 0; i < 8; i++) a[i] = _mm256_setzero_ps();
+    for (size_t p = 0; p < vis; p++) {
+      const __m256 w = _mm256_set1_ps(pts[p]);
+      const float *vp = v + p * wkv + d0;
+      for (int i = 0; i < 8; i++) a[i] = _mm256_add_ps(a[i], _mm256_mul_ps(w, _mm256_loadu_ps(vp + 8 * i)));
+    }
+    for (int i = 0; i < 8; i++) _mm256_storeu_ps(dst + d0 + 8 * i, a[i]);
+  }
+  for (; d0 < hd; d0++) {
+    float acc = 0.0f;
+    for (size_t p = 0; p < vis; p++) acc += pts[p] * v[p * wkv + d0];
+    dst[d0] = acc;
+  }
+}
+
 int orc_attention(const float *q, const float *k, const float *v, size_t tokens,
                   size_t total, size_t heads, size_t kvh, size_t hd, float *out) {
   if (!kvh || heads % kvh) { set_err("attention: groups"); return -1; }
   if (tokens > total) { set_err("attention: tokens > total"); return -1; }
   size_t wq = heads * hd, wkv = kvh * hd, per = heads / kvh, off = total - tokens;
   float scale = 1.0f / sqrtf((float)hd);
+  /* the transposed keys pay off when many query rows read them */
+  float *kt = tokens * per >= 32 ? (float *)malloc(total * wkv * sizeof(float)) : NULL;
+  if (kt) {
+#pragma omp parallel for schedule(static)
+    for (size_t c0 = 0; c0 < wkv; c0 += 64)
+      for (size_t p0 = 0; p0 < total; p0 += 64)
+        for (size_t p = p0; p < p0 + 64 && p < total; p++)
+          for (size_t c = c0; c < c0 + 64 && c < wkv; c++) kt[c * total + p] = k[p * wkv + c];
+  }
   int err = 0;
 #pragma omp parallel for schedule(dynamic)
-  for (size_t t = 0; t < tokens; t++) {
+  for (size_t th = 0; th < tokens * heads; th++) {
+    const size_t t = th / heads, h = th % heads;
     size_t vis = off + t + 1;
-    float *pts = (float *)malloc(vis * sizeof(float));
+    float *pts = (float *)malloc((vis + 16) * sizeof(float));
     if (!pts) { err = 1; continue; }
-    for (size_t h = 0; h < heads; h++) {
+    {
       const float *qh = q + t * wq + h * hd;
       size_t base = (h / per) * hd;
-      for (size_t p = 0; p < vis; p++) pts[p] = orc_dot_f32(qh, k + p * wkv + base, hd) * scale;
-      orc_softmax(pts, vis, vis);
-      float *dst = out + t * wq + h * hd;
-      for (size_t d = 0; d < hd; d++) dst[d] = 0.0f;
-      for (size_t p = 0; p < vis; p++) {
-        const float *vh = v + p * wkv + base;
-        for (size_t d = 0; d < hd; d++) dst[d] += pts[p] * vh[d];
+      size_t p = 0;
+      if (kt) {
+        const float *kg = kt + base * total;
+        for (; p + 16 <= vis; p += 16) scores16(qh, kg, total, hd, p, scale, pts);
+        for (; p < vis; p++) {
+          float s = 0.0f;
+          for (size_t d = 0; d < hd; d++) s += qh[d] * kg[d * total + p];
+          pts[p] = s * scale;
+        }
+      } else {
+        for (; p + 8 <= vis; p += 8) {
+          float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+          const float *kp = k + p * wkv + base;
+          for (size_t d = 0; d < hd; d++)
+            for (int j = 0; j < 8; j++) s[j] += qh[d] * kp[(size_t)j * wkv + d];
+          for (int j = 0; j < 8; j++) pts[p + (size_t)j] = s[j] * scale;
+        }
+        for (; p < vis; p++) pts[p] = orc_dot_f32(qh, k + p * wkv + base, hd) * scale;
       }
+      orc_softmax(pts, vis, vis);
+      weighted_sum(pts, v + base, wkv, vis, hd, out + t * wq + h * hd);
     }
     free(pts);
   }
+  free(kt);
   if (err) { set_err("attention: alloc"); return -1; }
   return 0;
 }
@@ -1209,6 +1274,177 @@ static int act_alloc(act_buf *a, size_t m, size_t k, int sub) {
 }
 static void act_free(act_buf *a) { free(a->q); free(a->e); free(a->s); }
 
+/* The scalar row kernels above (src/kernels/scalar.rs:132-324,
+ * src/kernels/q2k.rs:41-69) restructured for speed, bit for bit:
+ * a weight row is unpacked once into its levels (the integers each kernel
+ * multiplies the activation by) and two f32 coefficients per sub-block (the
+ * same products the kernel forms: d*sc and dmin*mn, or d*scale); then its
+ * dots with four activation rows run as four independent chains, each
+ * adding its sub-block terms in the kernel's order from 0. The integer
+ * sub-block sums are exact in any order. tests/test_oracle_ops.py checks
+ * this against the per-row kernels for every type. */
+enum { TERM_MIN, TERM_OFF4, TERM_OFF32 };
+
+static int prep_row(int type, const uint8_t *row, size_t nb, uint8_t *q, float *A, float *B) {
+  for (size_t bl = 0; bl < nb; bl++) {
+    uint8_t *qb = q + bl * 256;
+    switch (type) {
+    case ORC_Q4_K: case ORC_Q5_K: {
+      const size_t bpb = type == ORC_Q4_K ? 144 : 176;
+      const uint8_t *o = row + bl * bpb, *esc = o + 4, *qh = o + 16;
+      const uint8_t *qs = o + (type == ORC_Q4_K ? 16 : 48);
+      const float d = rd_f16(o), dmin = rd_f16(o + 2);
+      for (int j = 0; j < 8; j++) {
+        uint8_t sc, mn;
+        orc_scale_min_k4(j, esc, &sc, &mn);
+        A[bl * 8 + j] = d * (float)sc;
+        B[bl * 8 + j] = dmin * (float)mn;
+        const int pr = j / 2, h = j % 2;
+        for (int i = 0; i < 32; i++) {
+          int v = h == 0 ? (qs[pr * 32 + i] & 0x0F) : (qs[pr * 32 + i] >> 4);
+          if (type == ORC_Q5_K && (qh[i] & (1 << j))) v += 16;
+          qb[j * 32 + i] = (uint8_t)v;
+        }
+      }
+      break;
+    }
+    case ORC_Q3_K: {
+      const uint8_t *o = row + bl * 110, *hm = o, *qs = o + 32;
+      const float d = rd_f16(o + 108);
+      int8_t esc[16];
+      orc_scales_q3k(o, esc);
+      for (int g = 0; g < 8; g++) {
+        const uint8_t *qsg = qs + (g / 4) * 32;
+        const int sh = 2 * (g % 4);
+        const uint8_t m = (uint8_t)(1u << g);
+        for (int half = 0; half < 2; half++) A[bl * 16 + g * 2 + half] = d * ((float)esc[g * 2 + half] - 32.0f);
+        for (int idx = 0; idx < 32; idx++)
+          qb[g * 32 + idx] = (uint8_t)(((qsg[idx] >> sh) & 3) + ((hm[idx] & m) ? 4 : 0));
+      }
+      break;
+    }
+    case ORC_Q2_K: {
+      const uint8_t *o = row + bl * 84, *esc = o, *qs = o + 16;
+      const float d = rd_f16(o + 80), dm = rd_f16(o + 82);
+      for (int s = 0; s < 16; s++) {
+        A[bl * 16 + s] = d * (float)(esc[s] & 0xF);
+        B[bl * 16 + s] = dm * (float)(esc[s] >> 4);
+      }
+      for (int g = 0; g < 8; g++)
+        for (int idx = 0; idx < 32; idx++)
+          qb[g * 32 + idx] = (uint8_t)((qs[(g / 4) * 32 + idx] >> (2 * (g % 4))) & 3);
+      break;
+    }
+    case ORC_Q6_K: {
+      const uint8_t *o = row + bl * 210, *esc = o + 192;
+      const float d = rd_f16(o + 208);
+      for (int s = 0; s < 16; s++) A[bl * 16 + s] = d * (float)(int8_t)esc[s];
+      for (int g = 0; g < 8; g++) {
+        const int half = g / 4, gi = g % 4;
+        const uint8_t *ql = o + 64 * half + 32 * (gi % 2), *qh = o + 128 + 32 * half;
+        for (int i = 0; i < 32; i++) {
+          const int nib = gi < 2 ? (ql[i] & 0x0F) : (ql[i] >> 4);
+          qb[g * 32 + i] = (uint8_t)(nib | (((qh[i] >> (2 * gi)) & 3) << 4));
+        }
+      }
+      break;
+    }
+    default:
+      return -1;
+    }
+  }
+  return 0;
+}
+
+/* Up to four activation rows against one prepared weight row: SUB values
+ * per sub-block, TERM the kernel's term:
+ *   TERM_MIN   xe * (A*E - B*xs)     (Q4_K, Q5_K, Q2_K)
+ *   TERM_OFF4  (xe*A) * (E - 4*xs)   (Q3_K)
+ *   TERM_OFF32 (xe*A) * (E - 32*xs)  (Q6_K) */
+/* the exact integer sum of one sub-block: levels (0..63) times i8 values,
+ * pairwise in 16 bits (at most 2 * 63 * 128, no saturation), then 32 bits */
+static inline int32_t isum32(const uint8_t *q, const int8_t *x) {
+  const __m256i p = _mm256_maddubs_epi16(_mm256_loadu_si256((const __m256i *)q),
+                                         _mm256_loadu_si256((const __m256i *)x));
+  const __m256i w = _mm256_madd_epi16(p, _mm256_set1_epi16(1));
+  __m128i v = _mm_add_epi32(_mm256_castsi256_si128(w), _mm256_extracti128_si256(w, 1));
+  v = _mm_add_epi32(v, _mm_shuffle_epi32(v, 0x4E));
+  v = _mm_add_epi32(v, _mm_shuffle_epi32(v, 0xB1));
+  return _mm_cvtsi128_si32(v);
+}
+static inline int32_t isum16(const uint8_t *q, const int8_t *x) {
+  const __m128i p = _mm_maddubs_epi16(_mm_loadu_si128((const __m128i *)q),
+                                      _mm_loadu_si128((const __m128i *)x));
+  __m128i v = _mm_madd_epi16(p, _mm_set1_epi16(1));
+  v = _mm_add_epi32(v, _mm_shuffle_epi32(v, 0x4E));
+  v = _mm_add_epi32(v, _mm_shuffle_epi32(v, 0xB1));
+  return _mm_cvtsi128_si32(v);
+}
+
+#define DOT_ROWS(NAME, SUB, TERM)                                                              \
+  static void NAME(size_t ns, const uint8_t *q, const float *A, const float *B,              \
+                   const int8_t *const *x, const float *const *xe, const float *const *xs,   \
+                   int nr, float *out) {                                                      \
+    float t0 = 0.0f, t1 = 0.0f, t2 = 0.0f, t3 = 0.0f;                                         \
+    for (size_t s = 0; s < ns; s++) {                                                         \
+      const uint8_t *qs = q + s * SUB;                                                        \
+      float tm[4];                                                                            \
+      for (int r = 0; r < 4; r++) {                                                           \
+        const int8_t *xr = x[r < nr ? r : 0] + s * SUB;                                       \
+        const int32_t e = SUB == 32 ? isum32(qs, xr) : isum16(qs, xr);                        \
+        const float E = (float)e, ve = xe[r < nr ? r : 0][s], vs = xs[r < nr ? r : 0][s];     \
+        if (TERM == TERM_MIN) tm[r] = ve * (A[s] * E - B[s] * vs);                            \
+        else if (TERM == TERM_OFF4) tm[r] = ve * A[s] * (E - 4.0f * vs);                      \
+        else tm[r] = ve * A[s] * (E - 32.0f * vs);                                            \
+      }                                                                                       \
+      t0 += tm[0];                                                                            \
+      t1 += tm[1];                                                                            \
+      t2 += tm[2];                                                                            \
+      t3 += tm[3];                                                                            \
+    }                                                                                         \
+    const float t[4] = {t0, t1, t2, t3};                                                      \
+    for (int r = 0; r < nr; r++) out[r] = t[r];                                               \
+  }
+DOT_ROWS(dot_rows_min32, 32, TERM_MIN)
+DOT_ROWS(dot_rows_min16, 16, TERM_MIN)
+DOT_ROWS(dot_rows_off4, 16, TERM_OFF4)
+DOT_ROWS(dot_rows_off32, 16, TERM_OFF32)
+
+/* one activation row (decode): a single chain */
+#define DOT_ROW(NAME, SUB, TERM)                                                               \
+  static float NAME(size_t ns, const uint8_t *q, const float *A, const float *B,             \
+                    const int8_t *x, const float *xe, const float *xs) {                      \
+    float t = 0.0f;                                                                           \
+    for (size_t s = 0; s < ns; s++) {                                                         \
+      const int32_t e = SUB == 32 ? isum32(q + s * SUB, x + s * SUB)                          \
+                                  : isum16(q + s * SUB, x + s * SUB);                         \
+      const float E = (float)e;                                                               \
+      if (TERM == TERM_MIN) t += xe[s] * (A[s] * E - B[s] * xs[s]);                           \
+      else if (TERM == TERM_OFF4) t += xe[s] * A[s] * (E - 4.0f * xs[s]);                     \
+      else t += xe[s] * A[s] * (E - 32.0f * xs[s]);                                           \
+    }                                                                                         \
+    return t;                                                                                 \
+  }
+DOT_ROW(dot_row_min32, 32, TERM_MIN)
+DOT_ROW(dot_row_min16, 16, TERM_MIN)
+DOT_ROW(dot_row_off4, 16, TERM_OFF4)
+DOT_ROW(dot_row_off32, 16, TERM_OFF32)
+
+typedef void (*dot_rows_fn)(size_t, const uint8_t *, const float *, const float *,
+                            const int8_t *const *, const float *const *, const float *const *,
+                            int, float *);
+typedef float (*dot_row_fn)(size_t, const uint8_t *, const float *, const float *,
+                            const int8_t *, const float *, const float *);
+static dot_rows_fn dot_rows_for(int type, dot_row_fn *one) {
+  switch (type) {
+  case ORC_Q4_K: case ORC_Q5_K: *one = dot_row_min32; return dot_rows_min32;
+  case ORC_Q2_K: *one = dot_row_min16; return dot_rows_min16;
+  case ORC_Q3_K: *one = dot_row_off4; return dot_rows_off4;
+  case ORC_Q6_K: *one = dot_row_off32; return dot_rows_off32;
+  default: return NULL;
+  }
+}
+
 /* src/ops.rs:435-522 (matmul_i8_fusionado) */
 int orc_matmul_fused(size_t m, size_t k, size_t n, const float *lhs,
                      const uint8_t *w, int type, float *dst, orc_row_kernel kern,
@@ -1224,10 +1460,49 @@ int orc_matmul_fused(size_t m, size_t k, size_t n, const float *lhs,
     orc_quantize_act(lhs + f * k, k, sub, a.q + f * k, a.e + f * nsub, a.s + f * nsub);
   size_t tasks = (n + ROWS_PER_TASK - 1) / ROWS_PER_TASK;
   if (threads < 1) threads = 1;
+  /* the oracle's own kernel: the restructured form (same bits) */
+  dot_row_fn row1 = NULL;
+  dot_rows_fn rows4 = kern == orc_row_kernel_for(type) ? dot_rows_for(type, &row1) : NULL;
+  int err = 0;
 #pragma omp parallel for schedule(dynamic) num_threads(threads)
   for (size_t t = 0; t < tasks; t++) {
     size_t r0 = t * ROWS_PER_TASK, r1 = r0 + ROWS_PER_TASK;
     if (r1 > n) r1 = n;
+    if (rows4) {
+      /* the task's rows prepared once; each group of four activation rows
+       * then meets all of them while it sits in cache */
+      const size_t nr_w = r1 - r0;
+      uint8_t *q = (uint8_t *)malloc(nr_w * k);
+      float *A = (float *)malloc(nr_w * nsub * 4), *B = (float *)malloc(nr_w * nsub * 4);
+      if (!q || !A || !B) {
+        err = 1;
+      } else {
+        for (size_t r = 0; r < nr_w && !err; r++)
+          if (prep_row(type, w + (r0 + r) * rowb, nb, q + r * k, A + r * nsub, B + r * nsub)) err = 1;
+        for (size_t f = 0; f < m && !err; f += 4) {
+          const int nr = m - f < 4 ? (int)(m - f) : 4;
+          const int8_t *xr[4];
+          const float *er[4], *sr[4];
+          for (int i = 0; i < 4; i++) {
+            const size_t g = f + (size_t)(i < nr ? i : 0);
+            xr[i] = a.q + g * k;
+            er[i] = a.e + g * nsub;
+            sr[i] = a.s + g * nsub;
+          }
+          for (size_t r = 0; r < nr_w; r++) {
+            if (nr == 1) {
+              dst[f * n + r0 + r] = row1(nsub, q + r * k, A + r * nsub, B + r * nsub, xr[0], er[0], sr[0]);
+              continue;
+            }
+            float out[4];
+            rows4(nsub, q + r * k, A + r * nsub, B + r * nsub, xr, er, sr, nr, out);
+            for (int i = 0; i < nr; i++) dst[(f + (size_t)i) * n + r0 + r] = out[i];
+          }
+        }
+      }
+      free(q); free(A); free(B);
+      continue;
+    }
     for (size_t r = r0; r < r1; r++) {
       const uint8_t *row = w + r * rowb;
       if (prefetch > 0 && r + (size_t)prefetch < r1) {
@@ -1239,6 +1514,7 @@ int orc_matmul_fused(size_t m, size_t k, size_t n, const float *lhs,
     }
   }
   act_free(&a);
+  if (err) { set_err("matmul_fused: alloc"); return -1; }
   return 0;
 }
 
@@ -1444,24 +1720,30 @@ int orc_forward(const orc_model *M, const uint32_t *toks, size_t t, orc_cache *c
   }
   for (size_t li = 0; li < g->layers; li++) {
     const orc_layer *L = &M->layers[li];
+    /* Past the last layer's K and V only the last token's row reaches the
+     * logits (and every step is a function of its own row), so that layer
+     * computes the rest for the last token alone: the same values the
+     * reference computes for it. */
+    const size_t r0 = li + 1 == g->layers ? t - 1 : 0, tr = t - r0;
+    float *xr = x + r0 * D, *xnr = xn + r0 * D, *qr = q + r0 * D;
     for (size_t r = 0; r < t; r++) orc_rmsnorm(xn + r * D, x + r * D, L->attn_norm, D, g->eps);
-    if (proj(M, xn, t, D, D, L->q, L->t_q, L->q_bias, q)) goto done;
+    if (proj(M, xnr, tr, D, D, L->q, L->t_q, L->q_bias, qr)) goto done;
     if (proj(M, xn, t, D, kvd, L->k, L->t_k, L->k_bias, kk)) goto done;
     if (proj(M, xn, t, D, kvd, L->v, L->t_v, L->v_bias, vv)) goto done;
-    if (orc_rope(q, t, g->heads, hd, M->cos_t, M->sin_t, g->ctx, c->len)) goto done;
+    if (orc_rope(qr, tr, g->heads, hd, M->cos_t, M->sin_t, g->ctx, c->len + r0)) goto done;
     if (orc_rope(kk, t, g->kv_heads, hd, M->cos_t, M->sin_t, g->ctx, c->len)) goto done;
     memcpy(c->k[li] + c->len * kvd, kk, t * kvd * 4);
     memcpy(c->v[li] + c->len * kvd, vv, t * kvd * 4);
-    if (orc_attention(q, c->k[li], c->v[li], t, total, g->heads, g->kv_heads, hd, att)) goto done;
-    if (proj(M, att, t, D, D, L->o, L->t_o, NULL, pr)) goto done;
-    for (size_t i = 0; i < t * D; i++) x[i] += pr[i];
-    for (size_t r = 0; r < t; r++) orc_rmsnorm(xn + r * D, x + r * D, L->ffn_norm, D, g->eps);
-    if (proj(M, xn, t, D, I, L->gate, L->t_gate, NULL, ga)) goto done;
-    if (proj(M, xn, t, D, I, L->up, L->t_up, NULL, up)) goto done;
-    orc_silu(ga, ga, t * I);
-    for (size_t i = 0; i < t * I; i++) ga[i] *= up[i];
-    if (proj(M, ga, t, I, D, L->down, L->t_down, NULL, pr)) goto done;
-    for (size_t i = 0; i < t * D; i++) x[i] += pr[i];
+    if (orc_attention(qr, c->k[li], c->v[li], tr, total, g->heads, g->kv_heads, hd, att)) goto done;
+    if (proj(M, att, tr, D, D, L->o, L->t_o, NULL, pr)) goto done;
+    for (size_t i = 0; i < tr * D; i++) xr[i] += pr[i];
+    for (size_t r = 0; r < tr; r++) orc_rmsnorm(xnr + r * D, xr + r * D, L->ffn_norm, D, g->eps);
+    if (proj(M, xnr, tr, D, I, L->gate, L->t_gate, NULL, ga)) goto done;
+    if (proj(M, xnr, tr, D, I, L->up, L->t_up, NULL, up)) goto done;
+    orc_silu(ga, ga, tr * I);
+    for (size_t i = 0; i < tr * I; i++) ga[i] *= up[i];
+    if (proj(M, ga, tr, I, D, L->down, L->t_down, NULL, pr)) goto done;
+    for (size_t i = 0; i < tr * D; i++) xr[i] += pr[i];
   }
   orc_rmsnorm(xn, x + (t - 1) * D, M->out_norm, D, g->eps);
   if (proj(M, xn, 1, D, g->vocab, M->out, M->t_out, NULL, logits)) goto done;

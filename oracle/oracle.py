@@ -362,6 +362,14 @@ class Model:
         except Exception:
             pass
 
+    def set_q4k_kernel(self, ref_q4k=None):
+        """The Q4_K row kernel of later forwards: a reference _ref kernel, or
+        None for the oracle's own (scalar order)."""
+        self.m.kern_override = C.cast(ref_q4k, C.c_void_p) if ref_q4k is not None else None
+
+    def set_threads(self, n: int):
+        self.m.threads = max(1, int(n))
+
     def new_cache(self, cap: int) -> "Cache":
         return Cache(self, cap)
 

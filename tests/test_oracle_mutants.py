@@ -89,8 +89,9 @@ def _run_pins(name, src, tests, workdir):
     with open(c_path, "w") as f:
         f.write(src)
     shutil.copy(os.path.join(ROOT, "oracle", "cx_oracle.h"), os.path.join(workdir, "cx_oracle.h"))
-    subprocess.run(["gcc", "-std=c11", "-O2", "-fPIC", "-ffp-contract=off", "-fno-fast-math",
-                    "-fopenmp", "-shared", "-o", so_path, c_path, "-lm"], check=True)
+    subprocess.run(["gcc", "-std=c11", "-O3", "-mavx2", "-fPIC", "-ffp-contract=off",
+                    "-fno-fast-math", "-fopenmp", "-shared", "-o", so_path, c_path, "-lm"],
+                   check=True)  # oracle/Makefile's flags
     args = [sys.executable, "-m", "pytest", "-q", "-p", "no:cacheprovider", PINS]
     if tests:
         args += ["-k", " or ".join(tests)]

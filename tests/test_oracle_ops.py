@@ -148,5 +148,36 @@ def test_tiny_model_is_deterministic_and_cache_consistent():
     m.forward(p[:4], c)
     b = m.forward(p[4:], c)
     assert np.allclose(a, b, atol=1e-6)
+    # token by token gives the same bits (every step is a function of its
+    # own row; the last layer's shortcut for the last row changes nothing)
+    c = m.new_cache(32)
+    for tok in p:
+        one = m.forward(np.array([tok], np.uint32), c)
+    assert np.array_equal(a.view(np.uint32), one.view(np.uint32))
     toks = m.generate(p, 5, m.new_cache(32))
     assert len(toks) == 5 and (toks < 300).all()
+
+
+F16_AT = {O.Q2_K: (80, 82), O.Q3_K: (108,), O.Q4_K: (0, 2), O.Q5_K: (0, 2), O.Q6_K: (208,)}
+
+
+@pytest.mark.parametrize("t", [O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K])
+def test_fused_matmul_equals_the_per_row_kernels(t):
+    """orc_matmul_fused runs the scalar kernels restructured (rows prepared
+    once, four activation rows as four chains): bit-identical to the
+    per-row kernel for every (row, activation) pair, at any row count."""
+    rng = np.random.default_rng(t)
+    for k, n in ((256, 33), (2048, 40), (4352, 9)):
+        bpb = O.BYTES_PER_BLOCK[t]
+        w = rng.integers(0, 256, (n, k // 256 * bpb), dtype=np.uint8)
+        for b in range(k // 256):
+            for off in F16_AT[t]:
+                h = rng.integers(0x1000, 0x3000, n)
+                w[:, b * bpb + off], w[:, b * bpb + off + 1] = h & 0xFF, h >> 8
+        for m in (1, 3, 4, 9):
+            lhs = rng.normal(0, 1, (m, k)).astype(np.float32)
+            got = O.matmul_fused(t, lhs, w, n, threads=3)
+            for f in range(m):
+                xq, xe, xs = O.quantize_act(lhs[f], O.SUB[t])
+                want = np.array([O.dot_row(t, w[r], xq, xe, xs) for r in range(n)], np.float32)
+                assert np.array_equal(got[f].view(np.uint32), want.view(np.uint32)), (k, m, f)
