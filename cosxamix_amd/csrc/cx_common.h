@@ -183,30 +183,62 @@ __device__ inline void cx_dma16_async(const void* g, void* l) {
       : "memory");
 }
 
+// The same for 4 bytes a lane: LDS `l` + 4 * lane.
+__device__ inline void cx_dma4_async(const void* g, void* l) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(cx_lds_ptr)l);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+      "global_load_lds_dword %2, off\n\ts_nop 0\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(la), "v"(g)
+      : "memory");
+}
+
 // s = 0; s += a[i] * b[i] for i = 0, 1, ... in order (the sequential f32
-// dot of src/kernels/scalar.rs:16-23) over N4 float4s. Eight products are
-// formed first and pinned by an empty asm that takes them as operands: left
-// to itself the compiler interleaves each multiply with its add, and the
-// chain then waits for a multiply and an add per term instead of one add.
+// dot of src/kernels/scalar.rs:16-23) over N4 float4s (LDS or global). The
+// operands stream in batches of 16 values, two batches ahead of the adds;
+// a batch's 16 products are formed first and pinned by empty asms that take
+// them as operands: left to itself the compiler interleaves each multiply
+// with its add, and the chain then waits for a multiply and an add per term
+// instead of one add.
 template <int N4>
 __device__ inline float cx_dot_seq(const float4* a, const float4* b) {
-  static_assert(N4 % 2 == 0, "pairs of float4");
+  static_assert(N4 % 4 == 0, "batches of four float4");
+  constexpr int NB = N4 / 4;
+  float4 x[2][4], y[2][4];
+#pragma unroll
+  for (int k = 0; k < 2 && k < NB; k++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      x[k][j] = a[4 * k + j];
+      y[k][j] = b[4 * k + j];
+    }
   float s = 0.0f;
-#pragma unroll 4
-  for (int i = 0; i < N4; i += 2) {
-    const float4 x = a[i], y = b[i], u = a[i + 1], v = b[i + 1];
-    float t0 = x.x * y.x, t1 = x.y * y.y, t2 = x.z * y.z, t3 = x.w * y.w;
-    float t4 = u.x * v.x, t5 = u.y * v.y, t6 = u.z * v.z, t7 = u.w * v.w;
-    asm volatile("" : "+v"(t0), "+v"(t1), "+v"(t2), "+v"(t3), "+v"(t4), "+v"(t5), "+v"(t6),
-                 "+v"(t7));
-    s += t0;
-    s += t1;
-    s += t2;
-    s += t3;
-    s += t4;
-    s += t5;
-    s += t6;
-    s += t7;
+#pragma unroll
+  for (int i = 0; i < NB; i++) {
+    const int k = i & 1;
+    float t[16];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      t[4 * j] = x[k][j].x * y[k][j].x;
+      t[4 * j + 1] = x[k][j].y * y[k][j].y;
+      t[4 * j + 2] = x[k][j].z * y[k][j].z;
+      t[4 * j + 3] = x[k][j].w * y[k][j].w;
+    }
+    asm volatile("" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]),
+                 "+v"(t[6]), "+v"(t[7]));
+    asm volatile("" : "+v"(t[8]), "+v"(t[9]), "+v"(t[10]), "+v"(t[11]), "+v"(t[12]),
+                 "+v"(t[13]), "+v"(t[14]), "+v"(t[15]));
+    if (i + 2 < NB)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        x[k][j] = a[4 * (i + 2) + j];
+        y[k][j] = b[4 * (i + 2) + j];
+      }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 16; j++) s += t[j];
   }
   return s;
 }

@@ -237,8 +237,8 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 // with direct-to-LDS loads, so a wave keeps up to 63 KiB of the cache in
 // flight instead of waiting on one row at a time.
 //
-// k_attn_scores, one wave per (64 positions, head h): the 64 K rows of the
-// head's group are copied into LDS (rows padded by 16 bytes against bank
+// k_attn_scores, one workgroup per (64 positions, head h): the 64 K rows of
+// the head's group are copied into LDS by its four waves (rows padded by 16 bytes against bank
 // conflicts), then lane p forms the sequential dot of
 // src/kernels/scalar.rs:16-23 times 1/sqrt(hd) and writes sc[h][p]. With
 // rope tables it first rotates q and this step's key (src/ops.rs:1185-1188:
@@ -280,12 +280,12 @@ __host__ __device__ constexpr uint32_t sc_stride(uint32_t cap) { return (cap + 3
 __host__ __device__ constexpr uint32_t sc_lds(uint32_t cap) { return (cap + 255) / 256 * 256; }
 
 template <int HD>
-__global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float* knew,
+__global__ __launch_bounds__(256) void k_attn_scores(const float* q, const float* knew,
                                                     const float* vnew, float* kc, float* vc,
                                                     const float* cos_t, const float* sin_t,
                                                     uint32_t heads, uint32_t kvh,
                                                     const cx_dstate* st, float scale,
-                                                    float* sc, uint32_t cap) {
+                                                    float* sc, float* cm, uint32_t cap) {
   constexpr uint32_t ROWB = HD * 4, PADB = ROWB + 16, PADF = PADB / 4;
   constexpr uint32_t NCH = (SC_P * PADB + 1023) / 1024;
   extern __shared__ __align__(16) uint8_t sm[];
@@ -294,8 +294,9 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
   float* kr = qr + HD;
   constexpr uint32_t half = HD / 2;
   // query token z (blockIdx.z) sits at position st->pos + z
+  const uint32_t chunk = blockIdx.x, h = blockIdx.y;
   const uint32_t z = blockIdx.z, pos = st->pos + z, total = pos + 1;
-  const uint32_t p0 = blockIdx.x * SC_P, h = blockIdx.y, per = heads / kvh, g = h / per;
+  const uint32_t p0 = chunk * SC_P, per = heads / kvh, g = h / per;
   if (p0 >= total) return;
   const uint32_t np = min(SC_P, total - p0), kvd = kvh * HD;
   q += (size_t)z * heads * HD;
@@ -304,11 +305,18 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
     vnew += (size_t)z * kvd;
   }
   sc += (size_t)z * heads * sc_stride(cap);
-  const int t = threadIdx.x;
-  // 1. the K rows [p0, p0 + np) into LDS; pad bytes and rows past the end
-  //    load a valid dummy that is never read
+  const uint32_t nck = (cap + SC_P - 1) / SC_P;
+  cm += (size_t)z * heads * nck;
+  const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
+  // the scale is read here, with the other arguments: read where it is
+  // used, its scalar load would make the dots' LDS reads wait for it
+  asm volatile("" ::"s"(scale));
+  // 1. the K rows [p0, p0 + np) into LDS, a quarter of the loads by each
+  //    wave (a wave issues such loads at a bounded rate: four issue them in
+  //    a quarter of the time); pad bytes and rows past the end load a valid
+  //    dummy that is never read
   const float* kb = kc + (size_t)p0 * kvd + g * HD;
-  for (uint32_t c = 0; c < NCH; c++) {
+  for (uint32_t c = w; c < NCH; c += 4) {
     const uint32_t o = c * 1024 + 16 * t;
     uint32_t r = o / PADB, b = o % PADB;
     if (r >= np || b >= ROWB) r = 0, b = 0;
@@ -319,7 +327,7 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
   if (rot) {
     const float* c = cos_t + (size_t)pos * half;
     const float* s = sin_t + (size_t)pos * half;
-    for (uint32_t j = t; j < half; j += 64) {
+    for (uint32_t j = tid; j < half; j += 256) {
       const float x0 = q[h * HD + j], x1 = q[h * HD + j + half];
       qr[j] = x0 * c[j] - x1 * s[j];
       qr[j + half] = x0 * s[j] + x1 * c[j];
@@ -331,18 +339,24 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* q, const float*
       }
     }
   } else {
-    for (uint32_t j = t; j < HD; j += 64) qr[j] = q[h * HD + j];
+    for (uint32_t j = tid; j < HD; j += 256) qr[j] = q[h * HD + j];
   }
   cx_wait_vm<0>();
   __syncthreads();
-  // 3. lane t: position p0 + t
+  if (w != 0) return;
+  // 3. wave 0, lane t: position p0 + t; the chunk's maximum (fmaxf: a NaN score
+  //    is passed over, as in the softmax's own maximum)
+  float v = -INFINITY;
   if ((uint32_t)t < np) {
     const uint32_t p = p0 + t;
     const float4* a4 = reinterpret_cast<const float4*>(qr);
     const float4* b4 = reinterpret_cast<const float4*>((has_new && p == pos) ? kr : kl + t * PADF);
     const float s = cx_dot_seq<HD / 4>(a4, b4);
-    sc[(size_t)h * sc_stride(cap) + p] = s * scale;
+    v = s * scale;
+    sc[(size_t)h * sc_stride(cap) + p] = v;
   }
+  v = cx_wave_max(v);
+  if (t == 0) cm[(size_t)h * nck + chunk] = v;
   // 4. one workgroup of the KV group appends the rotated key (from LDS) and
   //    the value at st->pos for later tokens (src/forward.rs:454-455):
   //    stored after the dots, since a wave waits for its stores as for its
@@ -368,10 +382,13 @@ __device__ inline void add32(float& tot, const float4 (&a)[8]) {
     tot += a[i].w;
   }
 }
-__device__ inline float seq_sum_lds(const float* x, uint32_t n) {
+// (The scheduling barriers keep each batch's reads issued ahead of the
+// previous batch's adds: left to itself the scheduler sinks them next to
+// their first use, and the chain then waits out an LDS latency every few
+// adds.)
+__device__ inline float seq_sum_lds(const float* x, uint32_t n, float tot = 0.0f) {
   const float4* x4 = reinterpret_cast<const float4*>(x);
   const uint32_t n4 = n / 4;
-  float tot = 0.0f;
   float4 A[8], B[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) A[i] = x4[i];  // may read past n: never used
@@ -380,6 +397,7 @@ __device__ inline float seq_sum_lds(const float* x, uint32_t n) {
     if (b + 8 > n4) break;
 #pragma unroll
     for (int i = 0; i < 8; i++) B[i] = x4[b + 8 + i];
+    __builtin_amdgcn_sched_barrier(0);
     add32(tot, A);
     b += 8;
     if (b + 8 > n4) {
@@ -389,6 +407,7 @@ __device__ inline float seq_sum_lds(const float* x, uint32_t n) {
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) A[i] = x4[b + 8 + i];
+    __builtin_amdgcn_sched_barrier(0);
     add32(tot, B);
     b += 8;
   }
@@ -401,6 +420,69 @@ __device__ inline float seq_sum_lds(const float* x, uint32_t n) {
       tot += A[i].w;
     }
   for (uint32_t p = n4 * 4; p < n; p++) tot += x[p];
+  return tot;
+}
+
+// Sequential sum of x[0..n) from tot, with no LDS read on the chain: lanes
+// 0-15 of a wave (exactly those active) read 64 positions a batch, lane l
+// the four at 64 b + 4 l, and lane 15 adds lane l's values in position order
+// through DPP (row_shr:15-l): one v_add a position, as from registers.
+// Batches are read whole, four ahead of the adds (reads past the last batch
+// read the last batch again, so that every read is counted): x must hold
+// +0.0 from n to the next multiple of 64 (adding +0.0 changes no sum of
+// exps, which is never -0.0). The sum is valid in lane 15.
+template <int S>
+__device__ inline void dpp_add(float& tot, float v) {
+  if constexpr (S == 0)
+    asm volatile("v_add_f32_e32 %0, %1, %0" : "+v"(tot) : "v"(v));
+  else
+    asm volatile("v_add_f32_dpp %0, %1, %0 row_shr:%2 row_mask:0xf bank_mask:0xf"
+                 : "+v"(tot)
+                 : "v"(v), "n"(S));
+}
+template <int L>
+__device__ inline void dpp_add4(float& tot, const float4& a) {
+  dpp_add<15 - L>(tot, a.x);
+  dpp_add<15 - L>(tot, a.y);
+  dpp_add<15 - L>(tot, a.z);
+  dpp_add<15 - L>(tot, a.w);
+}
+// one batch: `left` positions remain from its first (16 at a time)
+__device__ __forceinline__ void dpp_add64(float& tot, const float4& a, uint32_t left) {
+  // a DPP read waits 2 cycles after a VALU write of its source (copies the
+  // compiler may place between the read and the adds)
+  asm volatile("s_nop 1");
+  dpp_add4<0>(tot, a); dpp_add4<1>(tot, a); dpp_add4<2>(tot, a); dpp_add4<3>(tot, a);
+  if (left <= 16) return;
+  dpp_add4<4>(tot, a); dpp_add4<5>(tot, a); dpp_add4<6>(tot, a); dpp_add4<7>(tot, a);
+  if (left <= 32) return;
+  dpp_add4<8>(tot, a); dpp_add4<9>(tot, a); dpp_add4<10>(tot, a); dpp_add4<11>(tot, a);
+  if (left <= 48) return;
+  dpp_add4<12>(tot, a); dpp_add4<13>(tot, a); dpp_add4<14>(tot, a); dpp_add4<15>(tot, a);
+}
+__device__ __forceinline__ float seq_sum_dpp(const float* x, uint32_t n, float tot) {
+  const float4* x4 = reinterpret_cast<const float4*>(x) + (threadIdx.x & 15);
+  const uint32_t nb = (n + 63) / 64;
+  asm volatile("s_nop 4");  // a DPP read waits 5 cycles after the exec write that enabled it
+  float4 A[4], B[4];
+#pragma unroll
+  for (uint32_t i = 0; i < 4; i++) A[i] = x4[16 * min(i, nb - 1)];
+  for (uint32_t b = 0;; b += 8) {
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) B[i] = x4[16 * min(b + 4 + i, nb - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++)
+      if (b + i < nb) dpp_add64(tot, A[i], n - 64 * (b + i));
+    if (b + 4 >= nb) break;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) A[i] = x4[16 * min(b + 8 + i, nb - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++)
+      if (b + 4 + i < nb) dpp_add64(tot, B[i], n - 64 * (b + 4 + i));
+    if (b + 8 >= nb) break;
+  }
   return tot;
 }
 
@@ -454,9 +536,9 @@ __device__ inline void wait_stages(uint32_t later) {
 // Rows of the grid past HD / PV_DS are prefetch workgroups (pf).
 template <int HD, int SUB, uint32_t PV_DS, bool HELP>
 __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
-                                                  uint32_t heads, uint32_t kvh,
-                                                  const cx_dstate* st, uint32_t cap, float* out,
-                                                  int8_t* xq, float* xe, float* xs,
+                                                  const float* cm_all, uint32_t heads,
+                                                  uint32_t kvh, const cx_dstate* st, uint32_t cap,
+                                                  float* out, int8_t* xq, float* xe, float* xs,
                                                   cx_l2_prefetch pf) {
   if (blockIdx.y >= HD / PV_DS) {
     const uint32_t first = gridDim.x * (HD / PV_DS);
@@ -467,26 +549,48 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   float* ring = e + sc_lds(cap);
   __shared__ uint64_t etab[32];  // exp's table in LDS: no global load after the prefetch
   __shared__ float red[4];
+  __shared__ __align__(16) float cml[64];  // the head's chunk maxima (one token)
   // query token z (blockIdx.z) sits at position st->pos + z
-  const uint32_t z = blockIdx.z, total = st->pos + z + 1, h = blockIdx.x, g = h / (heads / kvh);
+  // With one query token the workgroups of a (KV group, dims slice) pair
+  // take linear ids i, i + 8, i + 16, ...: workgroups are dispatched to the
+  // 8 XCDs round-robin, so the heads of a group that read the same V slice
+  // share one XCD's L2, and each V line is fetched from memory once.
+  uint32_t h = blockIdx.x, y = blockIdx.y;
+  if (HELP) {
+    constexpr uint32_t NY = HD / PV_DS;
+    const uint32_t n = heads * NY, per = heads / kvh;
+    if (n % 8 == 0) {
+      const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y, J = (L % 8) * (n / 8) + L / 8;
+      y = J / per % NY;
+      h = J / per / NY * per + J % per;
+    }
+  }
+  const uint32_t z = blockIdx.z, total = st->pos + z + 1, g = h / (heads / kvh);
   using PS = PvShape<PV_DS, HELP ? PV_RING_HELP : 32768u>;
   constexpr uint32_t PV_NST = PS::NST, PV_IPW = PS::IPW, PV_LPP = PS::LPP;
-  const uint32_t d0 = blockIdx.y * PV_DS, kvd = kvh * HD;
+  const uint32_t d0 = y * PV_DS, kvd = kvh * HD;
   sc_all += (size_t)z * heads * sc_stride(cap);
   out += (size_t)z * heads * HD;
   const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
-  if (tid == 0) {  // uniform indices: scalar loads, which leave vmcnt alone
-    const uint64_t tab[32] = CX_EXP2_TAB;
-    for (int i = 0; i < 32; i++) etab[i] = tab[i];
-  }
   // 1. the head's scores, then the first V stages, as untracked
   //    direct-to-LDS loads; a wave's loads complete in issue order, so
-  //    waiting for all but its V loads waits for its scores only
+  //    waiting for all but its V loads waits for its scores only. With one
+  //    query token, wave 0 first fetches the chunk maxima the scores kernel
+  //    wrote (64 positions a chunk, at most 64 chunks).
+  const uint32_t nck = (total + SC_P - 1) / SC_P;
+  if (HELP && w == 0) {  // lane t: chunk t (lanes past the chunks read chunk 0)
+    const float* crow = cm_all + (size_t)h * ((cap + SC_P - 1) / SC_P);
+    cx_dma4_async(crow + ((uint32_t)t < nck ? t : 0), cml);
+  }
   const float* srow = sc_all + (size_t)h * sc_stride(cap);
   const uint32_t nsc = (total + 255) / 256;  // 1 KiB per load
   for (uint32_t c = w; c < nsc; c += 4) {
     const uint32_t i = c * 256 + 4 * t;
     cx_dma16_async(srow + (i < total ? i : 0), e + c * 256);
+  }
+  if (tid == 0) {  // while the scores arrive; uniform indices: scalar loads
+    const uint64_t tab[32] = CX_EXP2_TAB;
+    for (int i = 0; i < 32; i++) etab[i] = tab[i];
   }
   const uint32_t nstage = (total + PV_STP - 1) / PV_STP;
   const float* vb = vc + g * HD + d0;
@@ -500,14 +604,157 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
                      dst + i * 256);
     }
   };
-  for (uint32_t s = 0; s + 1 < PV_NST && s < nstage; s++) issue(s);
-  if (nstage >= PV_NST - 1)
-    cx_wait_vm<(PV_NST - 1) * PV_IPW>();
-  else
-    cx_wait_vm<0>();
-  if (PV_NST - 1 < nstage) issue(PV_NST - 1);
+  // The V loads are issued once the scores have landed: issued together,
+  // every workgroup's V burst would queue ahead of the scores that the
+  // softmax needs first (V is read only after the sum). With one query token
+  // and a V slice that fits the ring whole (early), waves 1-3 issue all of
+  // it later, while wave 0 adds the exps, so no load issue delays the
+  // softmax.
+  const bool early = HELP && nstage <= PV_NST;
+  cx_wait_vm<0>();
+  if (!early)
+    for (uint32_t s = 0; s < PV_NST && s < nstage; s++) issue(s);
   cx_wait_lds();
-  cx_barrier();  // every wave's scores and the exp table are in LDS
+  cx_barrier();  // every wave's scores (and chunk maxima) and the exp table are in LDS
+  float o = 0.0f;
+  if constexpr (HELP) {
+    // 2. softmax over positions [0, total): the maximum of the chunk maxima
+    //    (the same in every wave), e = exp(s - max) of the first 256
+    //    positions by every thread, then of the rest by waves 1-3 while
+    //    lane 0 of wave 0 adds the first ones: the sum runs in position
+    //    order from 0 either way (src/ops.rs:1211-1229). The division by the
+    //    sum is folded into the products below.
+    float mx = (uint32_t)t < nck ? cml[t] : -INFINITY;
+    mx = cx_wave_max(mx);
+    const bool uniform = !isfinite(mx);  // all -inf, or a NaN (src/ops.rs:1214-1219)
+    const float pu = 1.0f / (float)total;
+    const uint32_t r64 = (total + 63) / 64 * 64;  // +0.0 from total to r64 (seq_sum_dpp)
+    if ((uint32_t)tid < total)
+      e[tid] = uniform ? pu : cx_expf_tab(e[tid] - mx, etab);
+    else if ((uint32_t)tid < r64)
+      e[tid] = 0.0f;
+    cx_wait_lds();
+    cx_barrier();
+    // early: the whole V slice, stage s into slot s, load i of a stage by
+    // wave 1 + i % 3
+    static_assert((PV_NST * PS::IPS + 2) / 3 <= 63, "a helper wave's share of the slice");
+    auto issue_all = [&]() {
+      for (uint32_t l = w - 1; l < nstage * PS::IPS; l += 3) {
+        const uint32_t s = l / PS::IPS, i = l % PS::IPS;
+        uint32_t p = s * PV_STP + i * (64 / PV_LPP) + t / PV_LPP;
+        if (p >= total) p = 0;
+        cx_dma16_async(reinterpret_cast<const uint8_t*>(vb + (size_t)p * kvd) + (t % PV_LPP) * 16,
+                       ring + s * (PV_STP * PV_DS) + i * 256);
+      }
+    };
+    float tot = 0.0f;
+    if (w != 0) {
+      for (uint32_t p = 256 + tid - 64; p < r64; p += 192)
+        e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
+      if (early && total <= 256) issue_all();
+    } else if (t < 16 && !uniform) {
+      tot = seq_sum_dpp(e, min(total, 256u), 0.0f);
+    }
+    if (total > 256) {
+      cx_wait_lds();
+      cx_barrier();  // the rest of the exps are in LDS
+      if (w != 0 && early) issue_all();
+      if (w == 0 && t < 16 && !uniform) tot = seq_sum_dpp(e + 256, total - 256, tot);
+    }
+    if (tid == 15) red[0] = 1.0f / tot;
+    cx_wait_lds();
+    cx_barrier();
+    const float inv = red[0];
+    // 3. out[d0 + t] over the V ring, position order (wave 0)
+    float* prod = ring + PV_NST * PV_STP * PV_DS;  // two buffers of PV_DS * PV_PSTR
+    // helper waves: stage s's products p_j * v_j[d], p_j = e_j * (1/sum) (or
+    // 1/total when uniform), into buffer s % 2, [dim][position]; task k is
+    // dims 4 (k % DQ) .. +3 and positions 8 (k / DQ) .. +7
+    auto make = [&](uint32_t s) {
+      constexpr uint32_t DQ = PV_DS / 4, NT = DQ * (PV_STP / 8);
+      const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS);
+      const float* ps = e + s * PV_STP;
+      float* pb = prod + (s & 1) * (PV_DS * PV_PSTR);
+      for (uint32_t k = tid - 64; k < NT; k += 192) {
+        const uint32_t dq = k % DQ, pq = k / DQ;
+        const float4 e0 = *reinterpret_cast<const float4*>(ps + 8 * pq);
+        const float4 e1 = *reinterpret_cast<const float4*>(ps + 8 * pq + 4);
+        float4 vv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+          vv[i] = *reinterpret_cast<const float4*>(vs + (8 * pq + i) * PV_DS + 4 * dq);
+        __builtin_amdgcn_sched_barrier(0);  // every read in flight before the first use
+        float pp[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+        if (!uniform)
+#pragma unroll
+          for (int i = 0; i < 8; i++) pp[i] = pp[i] * inv;
+        float r[4][8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float4 v = vv[i];
+          r[0][i] = pp[i] * v.x;
+          r[1][i] = pp[i] * v.y;
+          r[2][i] = pp[i] * v.z;
+          r[3][i] = pp[i] * v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          float* row = pb + (4 * dq + j) * PV_PSTR + 8 * pq;
+          *reinterpret_cast<float4*>(row) = make_float4(r[j][0], r[j][1], r[j][2], r[j][3]);
+          *reinterpret_cast<float4*>(row + 4) = make_float4(r[j][4], r[j][5], r[j][6], r[j][7]);
+        }
+      }
+    };
+    // stages issued so far: [0, min(NST, nstage)); each iteration s issues
+    // stage s + NST into the slot of stage s, whose products are made
+    auto issued_end = [&](uint32_t s) { return min(s + PV_NST, nstage); };
+    if (early)
+      cx_wait_vm<0>();  // the whole slice has landed (wave 0 issued none)
+    else
+      wait_stages<PV_IPW, PV_NST - 1>(issued_end(0) - 1);  // stage 0 has landed
+    cx_barrier();
+    if (w != 0) make(0);
+    for (uint32_t s = 0; s < nstage; s++) {
+      if (!early && s + 1 < nstage) wait_stages<PV_IPW, PV_NST - 1>(issued_end(s) - (s + 2));
+      cx_wait_lds();
+      cx_barrier();  // stage s's products are made; stage s + 1 has landed
+      // stage s's slot is no longer read: refill it (wave 0 after its chain,
+      // which the barrier starts)
+      if (w != 0 && s + PV_NST < nstage) issue(s + PV_NST);
+      if (w == 0) {
+        if (t < (int)PV_DS) {
+          const float* pr = prod + (s & 1) * (PV_DS * PV_PSTR) + t * PV_PSTR;
+          if ((s + 1) * PV_STP <= total) {
+            // 32 positions a batch, the next batch's reads ahead of the adds
+            const float4* p4 = reinterpret_cast<const float4*>(pr);
+            float4 a[8], b[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) a[i] = p4[i];
+#pragma unroll
+            for (int i = 0; i < 8; i++) b[i] = p4[8 + i];
+            __builtin_amdgcn_sched_barrier(0);
+            add32(o, a);
+#pragma unroll
+            for (int i = 0; i < 8; i++) a[i] = p4[16 + i];
+            __builtin_amdgcn_sched_barrier(0);
+            add32(o, b);
+#pragma unroll
+            for (int i = 0; i < 8; i++) b[i] = p4[24 + i];
+            __builtin_amdgcn_sched_barrier(0);
+            add32(o, a);
+            add32(o, b);
+          } else {
+            for (uint32_t j = 0; s * PV_STP + j < total; j++) o += pr[j];
+          }
+        }
+        if (s + PV_NST < nstage) issue(s + PV_NST);
+      } else if (s + 1 < nstage) {
+        make(s + 1);
+      }
+    }
+    cx_wait_lds();
+    cx_barrier();  // every read of the ring and the products is done
+  } else {
   // 2. softmax over positions [0, total)
   float mx = -INFINITY;
   for (uint32_t p = tid; p < total; p += 256) mx = fmaxf(mx, e[p]);
@@ -531,70 +778,6 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     cx_barrier();
   }
   // 3. out[d0 + t] over the V ring, position order (wave 0)
-  float o = 0.0f;
-  if constexpr (HELP) {
-    float* prod = ring + PV_NST * PV_STP * PV_DS;  // two buffers of PV_DS * PV_PSTR
-    // helper waves: stage s's products into buffer s % 2; task k is (dim
-    // k % PV_DS, positions 4 (k / PV_DS) .. +3)
-    auto make = [&](uint32_t s) {
-      const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS);
-      const float* ps = e + s * PV_STP;
-      float* pb = prod + (s & 1) * (PV_DS * PV_PSTR);
-      for (uint32_t k = tid - 64; k < PV_DS * (PV_STP / 4); k += 192) {
-        const uint32_t d = k % PV_DS, q = k / PV_DS;
-        const float4 p = *reinterpret_cast<const float4*>(ps + 4 * q);
-        float4 r;
-        r.x = p.x * vs[(4 * q + 0) * PV_DS + d];
-        r.y = p.y * vs[(4 * q + 1) * PV_DS + d];
-        r.z = p.z * vs[(4 * q + 2) * PV_DS + d];
-        r.w = p.w * vs[(4 * q + 3) * PV_DS + d];
-        *reinterpret_cast<float4*>(pb + d * PV_PSTR + 4 * q) = r;
-      }
-    };
-    // stages issued so far: [0, min(NST, nstage)); each iteration s issues
-    // stage s + NST into the slot of stage s, whose products are made
-    auto issued_end = [&](uint32_t s) { return min(s + PV_NST, nstage); };
-    wait_stages<PV_IPW, PV_NST - 1>(issued_end(0) - 1);  // stage 0 has landed
-    cx_barrier();
-    if (w != 0) make(0);
-    for (uint32_t s = 0; s < nstage; s++) {
-      if (s + 1 < nstage) wait_stages<PV_IPW, PV_NST - 1>(issued_end(s) - (s + 2));
-      cx_wait_lds();
-      cx_barrier();  // stage s's products are made; stage s + 1 has landed
-      // stage s's slot is no longer read: refill it (wave 0 after its chain,
-      // which the barrier starts)
-      if (w != 0 && s + PV_NST < nstage) issue(s + PV_NST);
-      if (w == 0) {
-        if (t < (int)PV_DS) {
-          const float* pr = prod + (s & 1) * (PV_DS * PV_PSTR) + t * PV_PSTR;
-          if ((s + 1) * PV_STP <= total) {
-            // 32 positions a batch, the next batch's reads ahead of the adds
-            const float4* p4 = reinterpret_cast<const float4*>(pr);
-            float4 a[8], b[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) a[i] = p4[i];
-#pragma unroll
-            for (int i = 0; i < 8; i++) b[i] = p4[8 + i];
-            add32(o, a);
-#pragma unroll
-            for (int i = 0; i < 8; i++) a[i] = p4[16 + i];
-            add32(o, b);
-#pragma unroll
-            for (int i = 0; i < 8; i++) b[i] = p4[24 + i];
-            add32(o, a);
-            add32(o, b);
-          } else {
-            for (uint32_t j = 0; s * PV_STP + j < total; j++) o += pr[j];
-          }
-        }
-        if (s + PV_NST < nstage) issue(s + PV_NST);
-      } else if (s + 1 < nstage) {
-        make(s + 1);
-      }
-    }
-    cx_wait_lds();
-    cx_barrier();  // every read of the ring and the products is done
-  } else {
   for (uint32_t s = 0; s < nstage; s++) {
     if (s + PV_NST <= nstage)
       cx_wait_vm<(PV_NST - 1) * PV_IPW>();
@@ -866,25 +1049,26 @@ template <int HD>
 int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
   constexpr size_t sc_bytes = (SC_P * (HD * 4 + 16) + 1023) / 1024 * 1024 + 2 * HD * 4;
   const uint32_t T = a.tokens ? a.tokens : 1;
-  hipLaunchKernelGGL(k_attn_scores<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads, T), dim3(64),
+  CX_REQUIRE(a.cm, "attention: the chunk maxima buffer");
+  hipLaunchKernelGGL(k_attn_scores<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads, T), dim3(256),
                      sc_bytes, s, a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads,
-                     a.kvh, a.st, scale, a.sc, a.cap);
+                     a.kvh, a.st, scale, a.sc, a.cm, a.cap);
   CX_HIP(hipGetLastError());
   if (T > 1) {  // many query tokens: 64 dims a workgroup, f32 output only
     const size_t lds = pv_lds_floats(a.cap, 64, false) * sizeof(float);
     const dim3 grid(a.heads, HD / 64, T);
     hipLaunchKernelGGL((k_attn_seq<HD, 32, 64, false>), grid, dim3(256), lds, s, a.vc, a.sc,
-                       a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, cx_l2_prefetch{});
+                       a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, cx_l2_prefetch{});
   } else {  // one token: 32 dims a workgroup, products made by helper waves
     const size_t lds = pv_lds_floats(a.cap, 32, true) * sizeof(float);
     const uint32_t rows = HD / 32, np = cx_l2_prefetch_groups(a.pf, a.heads * rows);
     const dim3 grid(a.heads, rows + (np + a.heads - 1) / a.heads, T);
     if (a.sub == 16)
       hipLaunchKernelGGL((k_attn_seq<HD, 16, 32, true>), grid, dim3(256), lds, s, a.vc, a.sc,
-                         a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+                         a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
     else
       hipLaunchKernelGGL((k_attn_seq<HD, 32, 32, true>), grid, dim3(256), lds, s, a.vc, a.sc,
-                         a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+                         a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   }
   CX_HIP(hipGetLastError());
   return CX_OK;
