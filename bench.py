@@ -67,20 +67,39 @@ def prompt_tokens(n: int, vocab: int, seed: int = 1234):
 
 
 def cpu_info():
-    name, cores = "unknown", os.cpu_count() or 1
+    """The host CPU as the reference sizes its pool (num_cpus::get_physical,
+    src/main.rs:578-595): (model name, ISA flags that matter to the
+    reference's kernels, logical CPUs this process may use, physical cores
+    among them)."""
+    name, flags, cpus = "unknown", [], {}
+    cur = {}
     try:
         with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    name = line.split(":", 1)[1].strip()
-                    break
+            for line in list(f) + [""]:
+                if not line.strip():
+                    if "processor" in cur:
+                        cpus[int(cur["processor"])] = cur
+                    cur = {}
+                    continue
+                k, _, v = line.partition(":")
+                cur[k.strip()] = v.strip()
     except OSError:
         pass
     try:
-        cores = len(os.sched_getaffinity(0))
+        allowed = sorted(os.sched_getaffinity(0))
     except AttributeError:
-        pass
-    return name, cores
+        allowed = sorted(cpus) or list(range(os.cpu_count() or 1))
+    if cpus:
+        first = cpus.get(allowed[0], next(iter(cpus.values())))
+        name = first.get("model name", name)
+        have = set(first.get("flags", "").split())
+        flags = [f for f in ("avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl",
+                             "avx512_vnni", "avx_vnni") if f in have]
+        cores = {(cpus[c].get("physical id"), cpus[c].get("core id")) for c in allowed if c in cpus}
+        physical = len(cores) if all(k != (None, None) for k in cores) else len(allowed)
+    else:
+        physical = len(allowed)
+    return name, flags, len(allowed), physical
 
 
 def decode_bench(F, L, steps, warmup, prompt_len):
@@ -132,12 +151,39 @@ def config5_bench(F, L, steps=256, warmup=8, prefix=8192):
            "median_us_per_token": round(statistics.median(timed) * 1000, 2),
            "weight_bytes_per_token": w, "kv_bytes_per_token_mid": kv,
            "effective_GBps": round((w + kv) / (total / steps) / 1e9, 1),
+           "hbm_frac": round((w + kv) / (total / steps) / 1e9 / HBM_PEAK_GBPS, 4),
            "prefill_s": round(prefill_s, 3), "prefill_tok_per_s": round(prefix / prefill_s, 1),
            "model_generation_s": round(gen_s, 2)}
     log(f"[bench] config 5: prefill {prefix} tokens {prefill_s:.2f}s; {steps} tokens at "
         f"{out['tok_per_s']} tok/s ({out['median_us_per_token']} us median), "
         f"{out['effective_GBps']} GB/s effective")
     m.close()
+    return out
+
+
+def attention_bench(calls):
+    """cx_attention_decode (the model's order-exact decode kernels) on seeded
+    q, K and V: the 3B shape at 548 cached positions and config 5's at 8448.
+    Wall time a call (the operator synchronizes: the position state lives in
+    shared scratch); kernel times come from a profiler's trace."""
+    import torch
+    from cosxamix_amd import ops
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(3)
+    for name, total, heads, kvh, hd in (("3b", 548, 16, 2, 128), ("config5", 8448, 32, 8, 128)):
+        q = torch.randn(heads * hd, device="cuda", generator=g)
+        k = torch.randn(total * kvh * hd, device="cuda", generator=g)
+        v = torch.randn(total * kvh * hd, device="cuda", generator=g)
+        o = torch.empty(heads * hd, device="cuda")
+        for _ in range(3):
+            ops.atencion_decode(q, k, v, (total, heads, kvh, hd), o)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            ops.atencion_decode(q, k, v, (total, heads, kvh, hd), o)
+        torch.cuda.synchronize()
+        out[name] = {"positions": total, "heads": heads, "kv_heads": kvh, "head_dim": hd,
+                     "us_per_call": round((time.perf_counter() - t0) / calls * 1e6, 2)}
     return out
 
 
@@ -344,13 +390,25 @@ def gemv_traffic():
                      "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}
 
 
-def cpu_baseline(F, L, m, prompt, decode_tokens=6):
+# the GPU box's CPU share: pools are sized to it whatever the host reports
+BOX_CPU_SHARE = 16
+
+
+def cpu_baseline(F, L, m, prompt, decode_tokens=16, decode_tokens_1t=4):
+    """The reference's CPU decode of the same model: the 3B weights copied to
+    the host; the prompt prefilled by the oracle (not timed); then decode
+    tokens timed with the Q4_K row kernel the reference runs on x86 (its own
+    compiled cosxamix_q4k_completo, oracle/_ref) over all physical cores, as
+    the reference's pool is sized (src/main.rs:578-595), and again on one
+    thread. The per-token ops around the row kernel (rmsnorm, rope,
+    attention, SwiGLU, argmax, the 32-row task loop) are the oracle's C
+    restatement of the reference's."""
     import numpy as np
     from oracle import oracle as O
     ref = O.load_ref()
     kind = "reference" if ref is not None else "port"
-    name, cores = cpu_info()
-    threads = max(1, min(cores, 16))
+    name, flags, logical, physical = cpu_info()
+    threads = max(1, min(physical, BOX_CPU_SHARE))
     t0 = time.perf_counter()
     tensors, types = {}, {}
     for i, (nm, t, _, _) in enumerate(m.tensores()):
@@ -359,29 +417,44 @@ def cpu_baseline(F, L, m, prompt, decode_tokens=6):
     c = m.cfg
     cfg = dict(layers=c.capas, dim=c.dim, heads=c.cabezas, kv_heads=c.cabezas_kv, ffn=c.ffn,
                vocab=c.vocab, ctx=c.contexto, eps=c.eps, rope_base=c.rope)
-    model = O.Model(cfg, tensors, types, threads=threads,
-                    ref_q4k=O.ref_row_kernel(ref, O.Q4_K) if ref is not None else None)
-    log(f"[bench] cpu baseline: weights on host in {time.perf_counter() - t0:.1f}s; "
-        f"{threads} threads on {name}; row kernel: {'cosxamix_q4k_completo' if ref else 'oracle scalar'}")
-    cache = model.new_cache(len(prompt) + decode_tokens + 1)
+    model = O.Model(cfg, tensors, types, threads=threads)
+    kern = O.ref_row_kernel(ref, O.Q4_K) if ref is not None else None
+    log(f"[bench] cpu baseline: weights on host in {time.perf_counter() - t0:.1f}s; {name}, "
+        f"{physical} physical cores of {logical} CPUs, {threads} threads; flags {flags}; row "
+        f"kernel {'cosxamix_q4k_completo' if ref else 'oracle scalar'}")
+    cache = model.new_cache(len(prompt) + decode_tokens + decode_tokens_1t + 1)
     t0 = time.perf_counter()
     lg = model.forward(prompt, cache)
     pre = time.perf_counter() - t0
+    model.set_q4k_kernel(kern)
     tok = O.argmax(lg)
-    per = []
-    for _ in range(decode_tokens):
-        t0 = time.perf_counter()
-        lg = model.forward(np.array([tok], np.uint32), cache)
-        per.append(time.perf_counter() - t0)
-        tok = O.argmax(lg)
-    med = statistics.median(per)
-    log(f"[bench] cpu baseline: prefill {len(prompt)} tokens {pre:.1f}s; decode median "
-        f"{med * 1e3:.1f} ms/token ({1 / med:.2f} tok/s)")
+
+    def decode(n):
+        per = []
+        nonlocal tok
+        for _ in range(n):
+            t1 = time.perf_counter()
+            lg = model.forward(np.array([tok], np.uint32), cache)
+            per.append(time.perf_counter() - t1)
+            tok = O.argmax(lg)
+        return statistics.median(per)
+
+    med = decode(decode_tokens)
+    model.set_threads(1)
+    med1 = decode(decode_tokens_1t)
+    log(f"[bench] cpu baseline: prefill {len(prompt)} tokens {pre:.1f}s (oracle kernels); decode "
+        f"median {med * 1e3:.1f} ms/token on {threads} threads ({1 / med:.2f} tok/s), "
+        f"{med1 * 1e3:.1f} ms/token on 1 ({1 / med1:.2f} tok/s)")
     return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads, "kind": kind,
-            "sample": (f"same 3B Q4_K weights on the host: {len(prompt)}-token prefill then "
-                       f"{decode_tokens} decode tokens (median), reference Q4_K row kernel "
-                       f"cosxamix_q4k_completo + oracle per-token ops, 32-row tasks over "
-                       f"{threads} threads; CPU: {name}")}
+            "value_1_thread": round(1.0 / med1, 3), "cpu": name, "isa_flags": flags,
+            "physical_cores": physical, "logical_cpus": logical,
+            "sample": (f"same 3B Q4_K weights on the host; {len(prompt)}-token prompt prefilled "
+                       f"(untimed), then the median of {decode_tokens} decode tokens on {threads} "
+                       f"threads (all physical cores, at most the box's share of "
+                       f"{BOX_CPU_SHARE}) and of {decode_tokens_1t} on 1 thread. Row kernel: the "
+                       f"reference's compiled cosxamix_q4k_completo (AVX2 asm); the per-token ops "
+                       f"(rmsnorm, rope, attention, SwiGLU, argmax) are the oracle's C "
+                       f"restatement of the reference's, in 32-row tasks as src/ops.rs")}
 
 
 CONFIG4_MS = (8, 32, 512)
@@ -407,8 +480,7 @@ def batched_bench(L, m, with_cpu, calls=20, reps=5):
         assert t == L.Q4_K
         mats.append((suffix, i, n, k))
     ref = O.load_ref() if with_cpu else None
-    _, cores = cpu_info()
-    threads = max(1, min(cores, 16))
+    threads = max(1, min(cpu_info()[3], BOX_CPU_SHARE))
     stream = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)
     cases = []
     for name, i, n, k in mats:
@@ -544,6 +616,9 @@ def main():
     ap.add_argument("--config5-only", action="store_true",
                     help="only BASELINE config 5 (8B shape, 8K context)")
     ap.add_argument("--no-config5", action="store_true")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="the decode attention operator alone at the 3B shape (548 positions) "
+                         "and config 5's (8448 positions, 32/8 heads): for kernel profiles")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the config-1 GEMV roofline loop (e.g. under rocprofv3)")
     ap.add_argument("--small-only", action="store_true",
@@ -568,8 +643,12 @@ def main():
     from cosxamix_amd import _lib as L
     from cosxamix_amd import forward as F
 
-    if a.config5_only:
-        print(json.dumps(config5_bench(F, L)), flush=True)
+    if a.attention_only:
+        print(json.dumps(attention_bench(a.steps)), flush=True)
+        return 0
+    if a.config5_only:  # --steps above 128 (the default) up to 256, the full run's count
+        print(json.dumps(config5_bench(F, L, steps=min(a.steps, 256), warmup=a.warmup)),
+              flush=True)
         return 0
     if a.sampled_only:
         m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)
@@ -639,6 +718,9 @@ def main():
         "decode": {"median_us_per_token": round(statistics.median(timed) * 1000, 2),
                    "weight_bytes_per_token": per_tok_bytes,
                    "effective_GBps": round((per_tok_bytes + kv_bytes) / (total_ms * 1e-3 / a.steps) / 1e9, 1),
+                   # the whole step's bytes (weights + KV read) over its time, against 8 TB/s
+                   "hbm_frac": round((per_tok_bytes + kv_bytes) / (total_ms * 1e-3 / a.steps) / 1e9
+                                     / HBM_PEAK_GBPS, 4),
                    "first_tokens": [int(t) for t in toks[:8]]},
         "batched": batched,
         "prefill": prefill,

@@ -484,7 +484,7 @@ __global__ __launch_bounds__(768) void k_att_sv(const float* vc, const float* sc
 
 size_t cx_attn_chunk_floats(size_t heads, size_t cap) { return heads * att_chunks((uint32_t)cap); }
 
-int cx_launch_attn_exact(const cx_attn_args& a, float scale, hipStream_t s) {
+int cx_launch_att_scores(const cx_attn_args& a, float scale, hipStream_t s) {
   const uint32_t per = a.heads / a.kvh, T = a.tokens ? a.tokens : 1;
   CX_REQUIRE(per >= 1 && per <= MAXG, "attention: %u query heads per KV group (at most %u)", per,
              MAXG);  // k_att_qk keeps a group's queries in LDS
@@ -500,6 +500,13 @@ int cx_launch_attn_exact(const cx_attn_args& a, float scale, hipStream_t s) {
     hipLaunchKernelGGL(k_att_qk<128>, qk_grid, dim3(256), qk_lds, s, a.q, a.knew, a.vnew, a.kc,
                        a.vc, a.cos_t, a.sin_t, a.kvh, per, a.st, scale, a.sc, a.cm, a.cap);
   CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_launch_attn_exact(const cx_attn_args& a, float scale, hipStream_t s) {
+  const uint32_t per = a.heads / a.kvh, T = a.tokens ? a.tokens : 1;
+  int rc = cx_launch_att_scores(a, scale, s);
+  if (rc) return rc;
   const uint32_t nhb = (per + HB - 1) / HB, nh = per < HB ? per : HB;
   const SvLayout LY = sv_layout(nh);  // the largest workgroup's
   CX_REQUIRE(LY.nstp >= 3 && LY.bytes <= LDS_BUDGET,

@@ -944,9 +944,14 @@ TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
   return t;
 }
 
-// The plain (no prologue) launch's tile: the largest R <= 16 that leaves a
-// tile per CU (measured on MI355X in the 3B decode step: 2 tiles per CU
-// took 1.7% longer a token, 4 tiles per CU 8% longer)
+// Tiles of a launch without the rmsnorm prologue: one per CU (measured on
+// MI355X: in the 3B decode step 2 tiles per CU took 1.7% longer a token and
+// 4 tiles 8% longer; in the daiss-0.5b Q8_0 step 2 tiles per CU took 1.8%
+// longer)
+constexpr uint32_t PLAIN_TILES = 256;
+
+// The plain (no prologue) launch's tile: the largest R <= 16 that leaves
+// PLAIN_TILES tiles
 template <int T>
 TilePlan plain_plan(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_t* rows, int nseg) {
   constexpr bool REG = T == CX_Q4_K || T == CX_Q5_K;  // weights straight into registers
@@ -955,7 +960,7 @@ TilePlan plain_plan(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_
     TilePlan t = plan_tile(R, row_bytes, k, nsub, rows, nseg, false, REG);
     if (t.lds > TILE_LDS_MAX) continue;
     best = t;
-    if (t.tiles >= 256) break;
+    if (t.tiles >= PLAIN_TILES) break;
   }
   return best;
 }
@@ -974,7 +979,8 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   //  - with the rmsnorm prologue every workgroup repeats the activation
   //    work, so take one tile per CU (R = rows/256) when it fits in LDS, else
   //    two tiles per CU;
-  //  - otherwise the largest R <= 16 that leaves >= 2 tiles per CU.
+  //  - otherwise plain_plan's: the largest R <= 16 that leaves a tile per
+  //    CU (256 tiles).
   uint32_t total_rows = 0;
   for (int i = 0; i < P.nseg; i++) total_rows += rows[i];
   TilePlan best{};
@@ -1029,7 +1035,7 @@ int launch_b32(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   uint32_t total_rows = 0;
   for (int i = 0; i < P.nseg; i++) total_rows += rows[i];
   // the k-quant GEMV's tile choice: with the prologue one or two tiles per
-  // CU, otherwise the largest R <= 16 that leaves >= 2 tiles per CU
+  // CU, otherwise the largest R <= 16 that leaves a tile per CU
   TilePlan best{};
   if (NORM) {
     for (uint32_t per_cu = 1; per_cu <= 8 && !best.R; per_cu *= 2) {
@@ -1043,7 +1049,7 @@ int launch_b32(GemvParams& P, const uint32_t* rows, hipStream_t s) {
       TilePlan t = plan_tile32(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM);
       if (t.lds > TILE_LDS_MAX) continue;
       best = t;
-      if (t.tiles >= 512) break;
+      if (t.tiles >= PLAIN_TILES) break;
     }
   }
   CX_REQUIRE(best.R, "gemv: a row of %u values does not fit in LDS", P.k);

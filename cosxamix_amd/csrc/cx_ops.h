@@ -40,6 +40,10 @@ int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb
 // tokens (cx_ops.hip) and streams them above it (cx_attn.hip); both paths
 // are order-exact.
 #define CX_ATT_LDS_MAX 4096
+// one query token: the same softmax-V kernel up to this many cached
+// positions (a smaller V ring leaves LDS for the scores), with k_att_qk's
+// scores; k_att_sv above
+#define CX_ATT_LONG_MAX 11520
 
 // x[r] = row hist[st->pos + r] of the embedding table (GGUF bytes of
 // `type`), dequantized, for r < rows
@@ -86,6 +90,10 @@ struct cx_attn_args {
 };
 int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s);
 int cx_launch_attn_exact(const cx_attn_args& a, float scale, hipStream_t s);
+// k_att_qk alone: the scores sc[h][p] (times the scale) and the chunk maxima
+// cm[h][chunk] of every head, any cache length (rope and the KV append
+// as k_attn_scores)
+int cx_launch_att_scores(const cx_attn_args& a, float scale, hipStream_t s);
 int cx_launch_attention(const float* q, const float* k, const float* v, size_t tokens,
                         size_t total, size_t heads, size_t kvh, size_t hd, float* out,
                         hipStream_t s);

@@ -514,8 +514,14 @@ __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) 
 // to leave room for the two product buffers.
 constexpr uint32_t PV_PSTR = PV_STP + 4;
 constexpr uint32_t PV_RING_HELP = 24576;
-__host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap, uint32_t ds, bool help) {
-  return sc_lds(cap) + (help ? PV_RING_HELP + 2 * ds * PV_PSTR : 32768u);
+// Above CX_ATT_LDS_MAX (the model's longer caches, scores from k_att_qk) the
+// ring is 80 KiB (5 stages), which leaves room for the scores of up to
+// CX_ATT_LONG_MAX positions.
+constexpr uint32_t PV_RING_LONG = 20480;
+constexpr uint32_t CML_MAX = 256;  // chunk maxima of one head: 16384 positions
+__host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap, uint32_t ds, bool help,
+                                                     uint32_t ring) {
+  return sc_lds(cap) + ring + (help ? 2 * ds * PV_PSTR : 0u);
 }
 
 // Waits until at most `later` stages' loads (IPW each) of this wave are
@@ -534,7 +540,7 @@ __device__ inline void wait_stages(uint32_t later) {
 // 256 threads: every wave streams its share of the V ring (4x the loads in
 // flight of one wave); wave 0's lanes run the order-exact accumulation.
 // Rows of the grid past HD / PV_DS are prefetch workgroups (pf).
-template <int HD, int SUB, uint32_t PV_DS, bool HELP>
+template <int HD, int SUB, uint32_t PV_DS, bool HELP, uint32_t RING>
 __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
                                                   const float* cm_all, uint32_t heads,
                                                   uint32_t kvh, const cx_dstate* st, uint32_t cap,
@@ -549,7 +555,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   float* ring = e + sc_lds(cap);
   __shared__ uint64_t etab[32];  // exp's table in LDS: no global load after the prefetch
   __shared__ float red[4];
-  __shared__ __align__(16) float cml[64];  // the head's chunk maxima (one token)
+  __shared__ __align__(16) float cml[CML_MAX];  // the head's chunk maxima (one token)
   // query token z (blockIdx.z) sits at position st->pos + z
   // With one query token the workgroups of a (KV group, dims slice) pair
   // take linear ids i, i + 8, i + 16, ...: workgroups are dispatched to the
@@ -566,7 +572,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     }
   }
   const uint32_t z = blockIdx.z, total = st->pos + z + 1, g = h / (heads / kvh);
-  using PS = PvShape<PV_DS, HELP ? PV_RING_HELP : 32768u>;
+  using PS = PvShape<PV_DS, RING>;
   constexpr uint32_t PV_NST = PS::NST, PV_IPW = PS::IPW, PV_LPP = PS::LPP;
   const uint32_t d0 = y * PV_DS, kvd = kvh * HD;
   sc_all += (size_t)z * heads * sc_stride(cap);
@@ -576,11 +582,12 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   //    direct-to-LDS loads; a wave's loads complete in issue order, so
   //    waiting for all but its V loads waits for its scores only. With one
   //    query token, wave 0 first fetches the chunk maxima the scores kernel
-  //    wrote (64 positions a chunk, at most 64 chunks).
+  //    wrote (64 positions a chunk, at most CML_MAX chunks).
   const uint32_t nck = (total + SC_P - 1) / SC_P;
-  if (HELP && w == 0) {  // lane t: chunk t (lanes past the chunks read chunk 0)
+  if (HELP && w == 0) {  // lane t: chunks t, t + 64, ... (past the chunks: chunk 0)
     const float* crow = cm_all + (size_t)h * ((cap + SC_P - 1) / SC_P);
-    cx_dma4_async(crow + ((uint32_t)t < nck ? t : 0), cml);
+    for (uint32_t i = 0; 64 * i < nck; i++)
+      cx_dma4_async(crow + (64 * i + t < nck ? 64 * i + t : 0), cml + 64 * i);
   }
   const float* srow = sc_all + (size_t)h * sc_stride(cap);
   const uint32_t nsc = (total + 255) / 256;  // 1 KiB per load
@@ -621,10 +628,13 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     // 2. softmax over positions [0, total): the maximum of the chunk maxima
     //    (the same in every wave), e = exp(s - max) of the first 256
     //    positions by every thread, then of the rest by waves 1-3 while
-    //    lane 0 of wave 0 adds the first ones: the sum runs in position
-    //    order from 0 either way (src/ops.rs:1211-1229). The division by the
-    //    sum is folded into the products below.
-    float mx = (uint32_t)t < nck ? cml[t] : -INFINITY;
+    //    lanes 0-15 of wave 0 add the ones formed: the sum runs in position
+    //    order from 0 (src/ops.rs:1211-1229). The division by the sum is
+    //    folded into the products below.
+    float mx = -INFINITY;
+#pragma unroll
+    for (uint32_t i = 0; i < CML_MAX / 64; i++)
+      if (64 * i + t < nck) mx = fmaxf(mx, cml[64 * i + t]);
     mx = cx_wave_max(mx);
     const bool uniform = !isfinite(mx);  // all -inf, or a NaN (src/ops.rs:1214-1219)
     const float pu = 1.0f / (float)total;
@@ -648,18 +658,40 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
       }
     };
     float tot = 0.0f;
-    if (w != 0) {
-      for (uint32_t p = 256 + tid - 64; p < r64; p += 192)
-        e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
-      if (early && total <= 256) issue_all();
-    } else if (t < 16 && !uniform) {
-      tot = seq_sum_dpp(e, min(total, 256u), 0.0f);
-    }
-    if (total > 256) {
-      cx_wait_lds();
-      cx_barrier();  // the rest of the exps are in LDS
-      if (w != 0 && early) issue_all();
-      if (w == 0 && t < 16 && !uniform) tot = seq_sum_dpp(e + 256, total - 256, tot);
+    if (early) {
+      // the V slice fits the ring: waves 1-3 form every other exp at once
+      // while wave 0 adds the first 256, then issue all of V while it adds
+      // the rest
+      if (w != 0) {
+        for (uint32_t p = 256 + tid - 64; p < r64; p += 192)
+          e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
+        if (total <= 256) issue_all();
+      } else if (t < 16 && !uniform) {
+        tot = seq_sum_dpp(e, min(total, 256u), 0.0f);
+      }
+      if (total > 256) {
+        cx_wait_lds();
+        cx_barrier();  // the rest of the exps are in LDS
+        if (w != 0) issue_all();
+        if (w == 0 && t < 16 && !uniform) tot = seq_sum_dpp(e + 256, total - 256, tot);
+      }
+    } else {
+      // a longer cache (V streams through the ring later): stage by stage,
+      // waves 1-3 form stage s + 1's exps while wave 0 adds stage s's
+      const uint32_t nss = (total + 255) / 256;
+      for (uint32_t s = 0; s < nss; s++) {
+        if (w != 0) {
+          const uint32_t b = 256 * (s + 1), end = min(b + 256, r64);
+          for (uint32_t p = b + tid - 64; p < end; p += 192)
+            e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
+        } else if (t < 16 && !uniform) {
+          tot = seq_sum_dpp(e + 256 * s, min(256u, total - 256 * s), tot);
+        }
+        if (s + 1 < nss) {
+          cx_wait_lds();
+          cx_barrier();  // stage s + 1's exps are in LDS
+        }
+      }
     }
     if (tid == 15) red[0] = 1.0f / tot;
     cx_wait_lds();
@@ -1045,6 +1077,25 @@ size_t cx_attn_splits(size_t cap) { return (cap + ATT_P - 1) / ATT_P; }
 
 
 namespace {
+// One query token: the softmax-V kernel with helper-made products, 32 dims
+// a workgroup (a ring of RING floats), plus rows of prefetch workgroups.
+template <int HD, uint32_t RING>
+int launch_seq_one(const cx_attn_args& a, hipStream_t s) {
+  const size_t lds = pv_lds_floats(a.cap, 32, true, RING) * sizeof(float);
+  CX_REQUIRE(lds <= 158 * 1024 && (a.cap + SC_P - 1) / SC_P <= CML_MAX,
+             "attention: %u cached positions need %zu bytes of LDS", a.cap, lds);
+  const uint32_t rows = HD / 32, np = cx_l2_prefetch_groups(a.pf, a.heads * rows);
+  const dim3 grid(a.heads, rows + (np + a.heads - 1) / a.heads, 1);
+  if (a.sub == 16)
+    hipLaunchKernelGGL((k_attn_seq<HD, 16, 32, true, RING>), grid, dim3(256), lds, s, a.vc, a.sc,
+                       a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+  else
+    hipLaunchKernelGGL((k_attn_seq<HD, 32, 32, true, RING>), grid, dim3(256), lds, s, a.vc, a.sc,
+                       a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
 template <int HD>
 int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
   constexpr size_t sc_bytes = (SC_P * (HD * 4 + 16) + 1023) / 1024 * 1024 + 2 * HD * 4;
@@ -1055,23 +1106,26 @@ int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
                      a.kvh, a.st, scale, a.sc, a.cm, a.cap);
   CX_HIP(hipGetLastError());
   if (T > 1) {  // many query tokens: 64 dims a workgroup, f32 output only
-    const size_t lds = pv_lds_floats(a.cap, 64, false) * sizeof(float);
+    const size_t lds = pv_lds_floats(a.cap, 64, false, 32768) * sizeof(float);
     const dim3 grid(a.heads, HD / 64, T);
-    hipLaunchKernelGGL((k_attn_seq<HD, 32, 64, false>), grid, dim3(256), lds, s, a.vc, a.sc,
-                       a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, cx_l2_prefetch{});
-  } else {  // one token: 32 dims a workgroup, products made by helper waves
-    const size_t lds = pv_lds_floats(a.cap, 32, true) * sizeof(float);
-    const uint32_t rows = HD / 32, np = cx_l2_prefetch_groups(a.pf, a.heads * rows);
-    const dim3 grid(a.heads, rows + (np + a.heads - 1) / a.heads, T);
-    if (a.sub == 16)
-      hipLaunchKernelGGL((k_attn_seq<HD, 16, 32, true>), grid, dim3(256), lds, s, a.vc, a.sc,
-                         a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
-    else
-      hipLaunchKernelGGL((k_attn_seq<HD, 32, 32, true>), grid, dim3(256), lds, s, a.vc, a.sc,
-                         a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+    hipLaunchKernelGGL((k_attn_seq<HD, 32, 64, false, 32768>), grid, dim3(256), lds, s, a.vc,
+                       a.sc, a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs,
+                       cx_l2_prefetch{});
+    CX_HIP(hipGetLastError());
+    return CX_OK;
   }
-  CX_HIP(hipGetLastError());
-  return CX_OK;
+  return launch_seq_one<HD, PV_RING_HELP>(a, s);  // one token: 32 dims a workgroup
+}
+
+// One query token over a longer cache: the scores of all heads of a KV group
+// from one kernel (cx_attn.hip's k_att_qk, the same sc/cm layout), then the
+// same softmax-V kernel with a smaller V ring.
+template <int HD>
+int launch_long(const cx_attn_args& a, float scale, hipStream_t s) {
+  CX_REQUIRE(a.cm, "attention: the chunk maxima buffer");
+  int rc = cx_launch_att_scores(a, scale, s);
+  if (rc) return rc;
+  return launch_seq_one<HD, PV_RING_LONG>(a, s);
 }
 }  // namespace
 
@@ -1094,6 +1148,8 @@ int cx_launch_attn_decode(const cx_attn_args& a, hipStream_t s) {
     // caches: fewer, lighter stages), or streamed (any length)
     if (a.cap <= CX_ATT_LDS_MAX && heads / kvh <= ATT_MAXG)
       return hd == 64 ? launch_exact<64>(a, scale, s) : launch_exact<128>(a, scale, s);
+    if (T == 1 && a.cap <= CX_ATT_LONG_MAX && heads / kvh <= ATT_MAXG)
+      return hd == 64 ? launch_long<64>(a, scale, s) : launch_long<128>(a, scale, s);
     return cx_launch_attn_exact(a, scale, s);
   }
   int rc;
