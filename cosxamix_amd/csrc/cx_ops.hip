@@ -582,19 +582,22 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   //    direct-to-LDS loads; a wave's loads complete in issue order, so
   //    waiting for all but its V loads waits for its scores only. With one
   //    query token, wave 0 first fetches the chunk maxima the scores kernel
-  //    wrote (64 positions a chunk, at most CML_MAX chunks).
-  const uint32_t nck = (total + SC_P - 1) / SC_P;
+  //    wrote (64 positions a chunk, at most CML_MAX chunks). Both cover the
+  //    whole cache (positions past the token's are loaded and never used),
+  //    so that they are issued before the position state arrives.
+  const uint32_t nckc = (cap + SC_P - 1) / SC_P;
   if (HELP && w == 0) {  // lane t: chunks t, t + 64, ... (past the chunks: chunk 0)
-    const float* crow = cm_all + (size_t)h * ((cap + SC_P - 1) / SC_P);
-    for (uint32_t i = 0; 64 * i < nck; i++)
-      cx_dma4_async(crow + (64 * i + t < nck ? 64 * i + t : 0), cml + 64 * i);
+    const float* crow = cm_all + (size_t)h * nckc;
+    for (uint32_t i = 0; 64 * i < nckc; i++)
+      cx_dma4_async(crow + (64 * i + t < nckc ? 64 * i + t : 0), cml + 64 * i);
   }
   const float* srow = sc_all + (size_t)h * sc_stride(cap);
-  const uint32_t nsc = (total + 255) / 256;  // 1 KiB per load
+  const uint32_t nsc = (cap + 255) / 256;  // 1 KiB per load
   for (uint32_t c = w; c < nsc; c += 4) {
     const uint32_t i = c * 256 + 4 * t;
-    cx_dma16_async(srow + (i < total ? i : 0), e + c * 256);
+    cx_dma16_async(srow + (i < cap ? i : 0), e + c * 256);
   }
+  const uint32_t nck = (total + SC_P - 1) / SC_P;
   if (tid == 0) {  // while the scores arrive; uniform indices: scalar loads
     const uint64_t tab[32] = CX_EXP2_TAB;
     for (int i = 0; i < 32; i++) etab[i] = tab[i];
