@@ -22,22 +22,28 @@ struct cx_l2_prefetch {
   cx_l2_job job[CX_L2_JOBS];
 };
 
-// Reads bytes [o, o + len) of base (clipped to total, 16-byte loads), eight
-// loads in flight per lane; the values feed an empty asm statement, which
-// keeps the loads and stores nothing.
-__device__ inline void cx_l2_touch(const uint8_t* base, size_t o, uint32_t len, size_t total) {
-  if (!base || o >= total) return;
-  const size_t end = (o + len < total ? o + len : total) & ~(size_t)15;
+// Reads bytes [o, o + len) of p0 and of p1 (either may be null; clipped to
+// total), 16-byte loads, sixteen in flight per lane over both ranges (a
+// gate/up tile's two halves are one round trip); the values feed an empty
+// asm statement, which keeps the loads and stores nothing.
+__device__ inline void cx_l2_touch(const uint8_t* p0, const uint8_t* p1, size_t o, uint32_t len,
+                                   size_t total) {
+  if (o >= total) return;
+  const uint32_t n = (uint32_t)(((o + len < total ? o + len : total) - o) / 16);  // chunks per range
+  const uint32_t n0 = p0 ? n : 0, nt = n0 + (p1 ? n : 0);
   uint32_t acc = 0;
-  for (size_t i = o + 16 * threadIdx.x; i < end; i += 8 * 16 * blockDim.x) {
-    uint4 v[8];
+  for (uint32_t c0 = threadIdx.x; c0 < nt; c0 += 16 * blockDim.x) {
+    uint4 v[16];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const size_t ij = i + (size_t)j * 16 * blockDim.x;
-      v[j] = ij < end ? *reinterpret_cast<const uint4*>(base + ij) : uint4{0, 0, 0, 0};
+    for (int j = 0; j < 16; j++) {
+      const uint32_t c = c0 + (uint32_t)j * blockDim.x;
+      v[j] = uint4{0, 0, 0, 0};
+      if (c < nt)
+        v[j] = *reinterpret_cast<const uint4*>((c < n0 ? p0 + o + 16 * (size_t)c
+                                                        : p1 + o + 16 * (size_t)(c - n0)));
     }
 #pragma unroll
-    for (int j = 0; j < 8; j++) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    for (int j = 0; j < 16; j++) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
   }
   asm volatile("" : : "v"(acc));
 }
@@ -53,8 +59,7 @@ __device__ inline void cx_l2_prefetch_run(const cx_l2_prefetch& pf, uint32_t j, 
   for (int i = 0; i < CX_L2_JOBS; i++) {
     const cx_l2_job& b = pf.job[i];
     if (t < b.tiles) {
-      cx_l2_touch(b.p0, (size_t)t * b.tile, b.tile, b.bytes);
-      cx_l2_touch(b.p1, (size_t)t * b.tile, b.tile, b.bytes);
+      cx_l2_touch(b.p0, b.p1, (size_t)t * b.tile, b.tile, b.bytes);
       return;
     }
     t -= (b.tiles + 7) / 8 * 8;
