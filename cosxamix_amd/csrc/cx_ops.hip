@@ -486,6 +486,147 @@ __device__ __forceinline__ float seq_sum_dpp(const float* x, uint32_t n, float t
   return tot;
 }
 
+// Inclusive prefix sum over the wave's 64 lanes (rows of 16 by shifts of
+// 1, 2, 4 and 8, then row 0's and row 2's sums into rows 1 and 3, then
+// lanes 0-31's sum into rows 2 and 3). Exact for non-negative integers
+// whose total is below 2^24; above, every sum that reaches 2^24 stays at
+// or above it (rounding is monotone).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_shifted(float v) {  // 0 where no source lane
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ float wave_scan_incl(float v) {
+  v += dpp_shifted<0x111, 0xF>(v);  // row_shr:1
+  v += dpp_shifted<0x112, 0xF>(v);  // row_shr:2
+  v += dpp_shifted<0x114, 0xF>(v);  // row_shr:4
+  v += dpp_shifted<0x118, 0xF>(v);  // row_shr:8
+  v += dpp_shifted<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  v += dpp_shifted<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+// The binade of s >= 0: E with s in [2^E, 2^(E+1)), and E = -126 for s
+// below 2^-125 (zero, subnormals and the first normal binade share the
+// spacing 2^-149).
+__device__ __forceinline__ int binade_of(float s) {
+  return max((int)((__float_as_uint(s) >> 23) & 0xFF), 1) - 127;
+}
+
+__device__ __forceinline__ uint32_t first_lane(uint64_t m) {
+  return m ? (uint32_t)__builtin_ctzll(m) : 64u;
+}
+
+// tot + x[0] + x[1] + ... + x[n-1], added in position order with IEEE f32
+// rounding after every add (the reference's `tot += e` loop), by the whole
+// wave and without one dependent add per position. x[j] >= 0 (or NaN).
+//
+// While the running sum s stays in one binade [2^E, 2^(E+1)), every float
+// there is a multiple of u = 2^(E-23), and fl(s + x) is the multiple of u
+// nearest s + x: s + u * rne(x / u), since s is a multiple of u. So in
+// units of u the adds are integer adds of r = rne(x / u), which a prefix
+// scan forms in any order, exactly. Two kinds of position end such a run
+// and are added as one f32 add instead (an event): the one whose add
+// reaches 2^(E+1) (the unit doubles), and one whose x / u lies exactly
+// halfway between integers (the rounding then goes to the even sum, which
+// depends on s). A window is 256 positions, four a lane; after an event the
+// next window starts at the position after it, in the new binade. A sum
+// from 0 changes binade every time it doubles, so with `head` the first
+// SCAN_HEAD positions are added one by one (lanes 0-15, seq_sum_dpp). A
+// NaN term is an event, and the rest is then added one by one.
+//
+// Reads x up to n + 511 (values past n are never used: the LDS there must
+// exist) and, for the head, needs +0.0 from n to the next multiple of 16
+// as seq_sum_dpp does. The result is valid in every lane.
+constexpr uint32_t SCAN_HEAD = 256;
+constexpr uint32_t SCAN_STAGE = 2048;  // positions a stage of the long softmax
+__device__ __forceinline__ float seq_sum_scan(const float* x, uint32_t n, float tot, bool head) {
+  const uint32_t l = threadIdx.x & 63;
+  uint32_t p = 0;
+  if (head && n) {
+    p = min(n, SCAN_HEAD);
+    if (l < 16) tot = seq_sum_dpp(x, p, tot);
+    tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 15));
+  }
+  if (p >= n) return tot;
+  int E = binade_of(tot);
+  float A = ldexpf(tot, 23 - E);  // s / u, an integer below 2^24
+  // volatile LDS reads: kept where they are written (the next window's are
+  // issued after this window's arithmetic and waited for a window later)
+  typedef __attribute__((address_space(3))) volatile float lds_vf;
+  lds_vf* xl = (lds_vf*)(x + 4 * l);
+  float v0 = xl[p], v1 = xl[p + 1], v2 = xl[p + 2], v3 = xl[p + 3];
+  for (;;) {
+    const int k = 23 - E;
+    float r0, c1, c2, c3, P, H;
+    uint64_t t0, t1, t2, t3;
+    // the window at p in (a0..a3), lane l's positions p + 4 l .. + 3; the
+    // next window's values read into (b0..b3). True: no event, p advanced.
+    auto step = [&](float& a0, float& a1, float& a2, float& a3, float& b0, float& b1, float& b2,
+                    float& b3) -> bool {
+      const float q0 = ldexpf(a0, k), q1 = ldexpf(a1, k), q2 = ldexpf(a2, k), q3 = ldexpf(a3, k);
+      r0 = rintf(q0);  // x / u is exact (inf past 2^128: an event)
+      const float r1 = rintf(q1), r2 = rintf(q2), r3 = rintf(q3);
+      t0 = __builtin_amdgcn_ballot_w64(!(fabsf(q0 - r0) < 0.5f));  // a tie, or not finite
+      t1 = __builtin_amdgcn_ballot_w64(!(fabsf(q1 - r1) < 0.5f));
+      t2 = __builtin_amdgcn_ballot_w64(!(fabsf(q2 - r2) < 0.5f));
+      t3 = __builtin_amdgcn_ballot_w64(!(fabsf(q3 - r3) < 0.5f));
+      c1 = r0 + r1;
+      c2 = c1 + r2;
+      c3 = c2 + r3;
+      __builtin_amdgcn_sched_barrier(0);
+      b0 = xl[p + 256];
+      b1 = xl[p + 257];
+      b2 = xl[p + 258];
+      b3 = xl[p + 259];
+      __builtin_amdgcn_sched_barrier(0);
+      P = wave_scan_incl(c3);  // the window's sum through this lane's last
+      H = 16777216.0f - A;     // the binade's room: 2^24 - s / u
+      const uint64_t ev = t0 | t1 | t2 | t3 | __builtin_amdgcn_ballot_w64(P >= H);
+      if (ev || n - p <= 256) return false;
+      A += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(P), 63));
+      p += 256;
+      return true;
+    };
+    float w0, w1, w2, w3;
+    for (;;) {
+      if (!step(v0, v1, v2, v3, w0, w1, w2, w3)) break;
+      if (!step(w0, w1, w2, w3, v0, v1, v2, v3)) break;
+    }
+    // the window's first event (positions 4 l + i, from ballots) or its
+    // end; X, the sum before the lane, is exact up to the first lane with
+    // an event, as every sum before it is below H <= 2^24
+    const float X = dpp_shifted<0x138, 0xF>(P);  // wave_shr:1
+    const uint64_t e0 = t0 | __builtin_amdgcn_ballot_w64(X + r0 >= H);
+    const uint64_t e1 = t1 | __builtin_amdgcn_ballot_w64(X + c1 >= H);
+    const uint64_t e2 = t2 | __builtin_amdgcn_ballot_w64(X + c2 >= H);
+    const uint64_t e3 = t3 | __builtin_amdgcn_ballot_w64(X + c3 >= H);
+    const uint32_t at = min(min(4 * first_lane(e0), 4 * first_lane(e1) + 1),
+                            min(4 * first_lane(e2) + 2, 4 * first_lane(e3) + 3));
+    const uint32_t room = n - p, stop = min(at, room);
+    if (stop) {  // the window's positions before the event (or all it has)
+      const uint32_t j = stop - 1, lj = j / 4, ij = j % 4;
+      const float s = X + (ij == 0 ? r0 : ij == 1 ? c1 : ij == 2 ? c2 : c3);
+      A += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), (int)lj));
+    }
+    if (at >= room) return ldexpf(A, E - 23);
+    const float s = ldexpf(A, E - 23) + x[p + at];  // the event's add
+    p += at + 1;
+    if (!(s < INFINITY)) {  // NaN: one by one from here
+      float t = s;
+      for (; p < n; p++) t += x[p];
+      return t;
+    }
+    if (p >= n) return s;
+    const float su = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s)));
+    E = binade_of(su);
+    A = ldexpf(su, 23 - E);
+    v0 = xl[p];
+    v1 = xl[p + 1];
+    v2 = xl[p + 2];
+    v3 = xl[p + 3];
+  }
+}
+
 // o += p[j] * v[j] for 8 positions in order. The 8 products are formed
 // first, pinned there by an empty asm that takes them as operands: left to
 // itself the compiler interleaves each multiply with its add, and the chain
@@ -631,9 +772,10 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     // 2. softmax over positions [0, total): the maximum of the chunk maxima
     //    (the same in every wave), e = exp(s - max) of the first 256
     //    positions by every thread, then of the rest by waves 1-3 while
-    //    lanes 0-15 of wave 0 add the ones formed: the sum runs in position
-    //    order from 0 (src/ops.rs:1211-1229). The division by the sum is
-    //    folded into the products below.
+    //    wave 0 adds the ones formed: the sum is the f32 sum in position
+    //    order from 0 (src/ops.rs:1211-1229), its first 256 adds one by one
+    //    and the rest by seq_sum_scan. The division by the sum is folded
+    //    into the products below.
     float mx = -INFINITY;
 #pragma unroll
     for (uint32_t i = 0; i < CML_MAX / 64; i++)
@@ -669,26 +811,31 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
         for (uint32_t p = 256 + tid - 64; p < r64; p += 192)
           e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
         if (total <= 256) issue_all();
-      } else if (t < 16 && !uniform) {
-        tot = seq_sum_dpp(e, min(total, 256u), 0.0f);
+      } else if (!uniform) {
+        tot = seq_sum_scan(e, min(total, 256u), 0.0f, true);
       }
       if (total > 256) {
         cx_wait_lds();
         cx_barrier();  // the rest of the exps are in LDS
         if (w != 0) issue_all();
-        if (w == 0 && t < 16 && !uniform) tot = seq_sum_dpp(e + 256, total - 256, tot);
+        if (w == 0 && !uniform) tot = seq_sum_scan(e + 256, total - 256, tot, false);
       }
     } else {
-      // a longer cache (V streams through the ring later): stage by stage,
-      // waves 1-3 form stage s + 1's exps while wave 0 adds stage s's
-      const uint32_t nss = (total + 255) / 256;
+      // a longer cache (V streams through the ring later): stages of
+      // SCAN_STAGE positions, the first stage's exps by every thread, then
+      // waves 1-3 forming stage s + 1's while wave 0 adds stage s's
+      for (uint32_t p = 256 + tid; p < min(SCAN_STAGE, r64); p += 256)
+        e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
+      cx_wait_lds();
+      cx_barrier();
+      const uint32_t nss = (total + SCAN_STAGE - 1) / SCAN_STAGE;
       for (uint32_t s = 0; s < nss; s++) {
         if (w != 0) {
-          const uint32_t b = 256 * (s + 1), end = min(b + 256, r64);
+          const uint32_t b = SCAN_STAGE * (s + 1), end = min(b + SCAN_STAGE, r64);
           for (uint32_t p = b + tid - 64; p < end; p += 192)
             e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
-        } else if (t < 16 && !uniform) {
-          tot = seq_sum_dpp(e + 256 * s, min(256u, total - 256 * s), tot);
+        } else if (!uniform) {
+          tot = seq_sum_scan(e + SCAN_STAGE * s, min(SCAN_STAGE, total - SCAN_STAGE * s), tot, s == 0);
         }
         if (s + 1 < nss) {
           cx_wait_lds();

@@ -314,6 +314,41 @@ def test_decode_attention_paths(cx, dev, heads, kvh, hd):
                     total, float(np.max(np.abs(got - want))))
 
 
+@pytest.mark.parametrize("heads,kvh", [(16, 2), (32, 8)])
+def test_decode_attention_sum_edge_cases(cx, dev, heads, kvh):
+    """Order-exact decode attention on scores that stress the sum of exps:
+    a wide spread (most exps subnormal or zero, the sum starting far below
+    1 and jumping binades), equal keys (every exp 1, the sum landing on
+    each power of two exactly), a peaked first position, and a NaN key row
+    (that KV group's outputs NaN, the others bit-identical)."""
+    ops, _ = cx
+    hd = 128
+    for total in (1, 63, 64, 65, 300, 548, 2047, 8300):
+        rng = np.random.default_rng(7 * total + heads)
+        base_q = rng.normal(0, 1, heads * hd).astype(np.float32)
+        k = rng.normal(0, 1, total * kvh * hd).astype(np.float32)
+        v = rng.normal(0, 1, total * kvh * hd).astype(np.float32)
+        cases = {"spread": (base_q * 40, k), "equal": (base_q, np.tile(k[:kvh * hd], total)),
+                 "peak": (base_q, k.copy())}
+        cases["peak"][1][:kvh * hd] = np.repeat(base_q.reshape(kvh, -1, hd)[:, 0], 1, 0).ravel() * 6
+        if total > 2:
+            kn = k.copy()
+            kn[(total // 2) * kvh * hd] = np.nan  # KV group 0 at the middle position
+            cases["nan"] = (base_q, kn)
+        for name, (q, kk) in cases.items():
+            q = np.ascontiguousarray(q, np.float32)
+            kk = np.ascontiguousarray(kk, np.float32)
+            want = O.attention(q, kk, v, 1, total, heads, kvh, hd)
+            out = torch.empty(heads * hd, dtype=torch.float32, device=dev)
+            ops.atencion_decode(T(q, dev), T(kk, dev), T(v, dev), (total, heads, kvh, hd), out, 1)
+            got = out.cpu().numpy()
+            nan = np.isnan(want)
+            assert np.array_equal(np.isnan(got), nan), (total, name)
+            if name == "nan":
+                assert nan[: heads // kvh * hd].all() and not nan[heads // kvh * hd:].any()
+            assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), (total, name)
+
+
 def test_attention_matches_oracle_and_properties(cx, dev):
     ops, _ = cx
     heads, kvh, hd = 16, 2, 128
