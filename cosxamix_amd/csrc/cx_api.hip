@@ -1292,7 +1292,7 @@ static int enqueue_step(cx_cache* C) {
     a.xe = m->xe;
     a.xs = m->xs;
     a.sub = cx_sub(L.t_o);
-    const bool glu = L.t_gate == L.t_up && cx_glu_supported(L.t_gate) && I % 32 == 0 && D <= 8192;
+    const bool glu = L.t_gate == L.t_up && cx_glu_fits(L.t_gate, D) && I % 32 == 0;
     // the attention's spare CUs pull the o-proj's and gate/up's weights into L2
     (void)cx_gemv_prefetch_plan(L.t_o, L.o, D, D, &a.pf.job[0]);
     if (glu) (void)cx_glu_prefetch_plan(L.t_gate, L.gate, L.up, I, D, &a.pf.job[1]);

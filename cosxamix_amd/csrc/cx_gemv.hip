@@ -923,6 +923,126 @@ __global__ __launch_bounds__(256) void k_gemv32(GemvParams P) {
   }
 }
 
+// Gate and up of one 32-value-block type (Q8_0, Q5_0) and SwiGLU in one
+// launch, as k_gemv_glu for the k-quants: tile t holds gate rows [32t,
+// 32t+32) and the same rows of up, both in LDS (each at its own skew); every
+// workgroup makes the rmsnorm + quantization of x (k_gemv32's prologue), forms
+// the 64 rows' terms and block-order row sums (k_gemv32's steps 2 and 3),
+// then act[i] = silu(gate[i]) * up[i] for its 32 values and their i8
+// quantization in sub-blocks of SUB (the down projection's) — the bytes
+// k_gemv32<T, true> over gate and up and k_swiglu_quant would write.
+struct Glu32Params {
+  const uint8_t* wg;
+  const uint8_t* wu;
+  const float* nx;
+  const float* nw;
+  float eps;
+  uint32_t k, nsub, row_bytes, tstride;
+  uint32_t lds_up, lds_act, lds_scale, lds_terms, lds_gu;  // byte offsets
+  int8_t* xq;  // the down projection's activation
+  float* xe;
+  float* xs;
+};
+
+template <int T, int SUB>
+__global__ __launch_bounds__(256) void k_gemv32_glu(Glu32Params P) {
+  using Q = B32<T>;
+  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ double red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t row0 = blockIdx.x * GLU_ROWS;
+  int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
+  float* se = reinterpret_cast<float*>(lds + P.lds_scale);
+  float* ss = se + P.nsub;
+  float* sx = reinterpret_cast<float*>(lds + P.lds_terms);  // the norm input, then the terms
+  float* terms = sx;
+  float* gu = reinterpret_cast<float*>(lds + P.lds_gu);
+
+  // 1. x and the norm weight, then the gate tile and the up tile, by
+  //    direct loads
+  copy_to_lds(P.nx, sx, P.k / 4, wave, lane);
+  copy_to_lds(P.nw, sx + P.k, P.k / 4, wave, lane);
+  const uint8_t* src_g = P.wg + (size_t)row0 * P.row_bytes;
+  const uint8_t* src_u = P.wu + (size_t)row0 * P.row_bytes;
+  const uint32_t skg = (uint32_t)((uintptr_t)src_g & 15u), sku = (uint32_t)((uintptr_t)src_u & 15u);
+  uint32_t ntile = copy_to_lds(src_g - skg, lds, (skg + GLU_ROWS * P.row_bytes + 15) >> 4, wave, lane);
+  ntile += copy_to_lds(src_u - sku, lds + P.lds_up, (sku + GLU_ROWS * P.row_bytes + 15) >> 4, wave,
+                       lane);
+  // 2. rmsnorm then quantization, as k_gemv32's prologue (the same f64 tree)
+  wait_all_but(ntile);
+  cx_barrier();
+  {
+    const float* sw = sx + P.k;
+    double sum = 0.0;
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+      float a[8];
+      cx_load8(sx + i, a);
+#pragma unroll
+      for (int j = 0; j < 8; j++) sum += (double)a[j] * (double)a[j];
+    }
+    sum = cx_wave_sum_d(sum);
+    if (lane == 0) red[wave] = sum;
+    cx_wait_lds();
+    cx_barrier();
+    const double tot = ((red[0] + red[1]) + red[2]) + red[3];
+    const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
+    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+      float v[8], a[8], b[8];
+      cx_load8(sx + i, a);
+      cx_load8(sw + i, b);
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = (float)((double)a[j] * scale) * b[j];
+      cx_quant8<32>(v, i, sq, se, ss);
+    }
+  }
+  cx_wait_vm<0>();
+  cx_wait_lds();
+  __syncthreads();  // x and w are read: the region becomes the terms
+  // 3. one (row, block) a lane: rows 0-31 are gate's, 32-63 up's
+  const uint32_t items = 2 * GLU_ROWS * P.nsub;
+  for (uint32_t it = tid; it < items; it += 256) {
+    const uint32_t r = it / P.nsub, b = it - r * P.nsub;
+    const uint32_t off = r < GLU_ROWS ? skg + r * P.row_bytes + b * Q::BPB
+                                      : P.lds_up + sku + (r - GLU_ROWS) * P.row_bytes + b * Q::BPB;
+    int e;
+    const float d = Q::dot(lds, off, sq + 32 * b, e);
+    terms[r * P.tstride + b] = d * se[b] * (float)e;
+  }
+  __syncthreads();
+  // 4. row sums in block order from 0; SwiGLU one value a lane; then the
+  //    quantization, 8 values a lane
+  if ((uint32_t)tid < 2 * GLU_ROWS) gu[tid] = row_sum_any(terms + tid * P.tstride, P.nsub);
+  __syncthreads();
+  if (tid < (int)GLU_ROWS) gu[tid] = cx_swiglu(gu[tid], gu[GLU_ROWS + tid]);
+  __syncthreads();
+  if (tid < (int)(GLU_ROWS / 8)) {
+    float a[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) a[j] = gu[8 * tid + j];
+    cx_quant8<SUB>(a, row0 + 8 * tid, P.xq, P.xe, P.xs);
+  }
+}
+
+// LDS of the block-32 gate/up launch: [gate tile][up tile] (16 skew + 32
+// rows + 16 pad each) [xq, k bytes][xe, xs][norm input (2k floats), then
+// the terms (64 x (nsub + 4))][64 row sums]
+Glu32Params plan_glu32(int type, uint32_t k, uint32_t* lds) {
+  Glu32Params P{};
+  P.k = k;
+  P.nsub = k / 32;
+  P.row_bytes = P.nsub * (uint32_t)cx_bpb(type);
+  P.tstride = P.nsub + 4;
+  const uint32_t tile = (16 + GLU_ROWS * P.row_bytes + 16 + 15) / 16 * 16;
+  P.lds_up = tile;
+  P.lds_act = 2 * tile;
+  P.lds_scale = P.lds_act + (k + 15) / 16 * 16;
+  P.lds_terms = P.lds_scale + (8 * P.nsub + 15) / 16 * 16;
+  const uint32_t terms = 4 * 2 * GLU_ROWS * P.tstride, nin = 8 * k;
+  P.lds_gu = P.lds_terms + (terms > nin ? terms : nin);
+  *lds = P.lds_gu + 4 * 2 * GLU_ROWS;
+  return P;
+}
+
 struct TilePlan {
   uint32_t R, tiles, lds, lds_act, lds_scale, lds_terms, lds_norm;
 };
@@ -1146,11 +1266,47 @@ int cx_launch_gemv_norm(int type, const cx_seg* segs, int nseg, uint32_t k, cons
 
 bool cx_glu_supported(int type) { return type == CX_Q4_K || type == CX_Q5_K; }
 
+bool cx_glu_fits(int type, uint32_t k) {
+  if (cx_glu_supported(type)) return k > 0 && k % 256 == 0 && k <= 8192;
+  if (type != CX_Q8_0 && type != CX_Q5_0) return false;
+  if (!k || k % 32 || k > 8192) return false;
+  uint32_t lds = 0;
+  (void)plan_glu32(type, k, &lds);
+  return lds <= TILE_LDS_NORM_MAX;
+}
+
 int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t I, uint32_t k,
                        const float* x, const float* w, float eps, int sub, int8_t* xq, float* xe,
                        float* xs, hipStream_t s) {
-  CX_REQUIRE(cx_glu_supported(type), "gemv glu: type %d (Q4_K or Q5_K)", type);
+  CX_REQUIRE(cx_glu_fits(type, k), "gemv glu: type %d at k=%u (Q4_K or Q5_K with k a multiple "
+             "of 256; Q8_0 or Q5_0 whose two tiles fit in LDS)", type, k);
   CX_REQUIRE(sub == 16 || sub == 32, "gemv glu: sub-blocks of 16 or 32, not %d", sub);
+  if (type == CX_Q8_0 || type == CX_Q5_0) {
+    CX_REQUIRE(I > 0 && I % GLU_ROWS == 0, "gemv glu: %u rows are not tiles of %u", I, GLU_ROWS);
+    CX_REQUIRE(wg && wu && x && w && xq && xe && xs, "gemv glu: null pointer");
+    CX_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)xq & 7) == 0,
+               "gemv glu: x and w 16-byte aligned, xq 8-byte");
+    uint32_t lds = 0;
+    Glu32Params Q = plan_glu32(type, k, &lds);
+    Q.wg = wg;
+    Q.wu = wu;
+    Q.nx = x;
+    Q.nw = w;
+    Q.eps = eps;
+    Q.xq = xq;
+    Q.xe = xe;
+    Q.xs = xs;
+    const dim3 grid(I / GLU_ROWS);
+    if (type == CX_Q8_0) {
+      if (sub == 32) hipLaunchKernelGGL((k_gemv32_glu<CX_Q8_0, 32>), grid, dim3(256), lds, s, Q);
+      else hipLaunchKernelGGL((k_gemv32_glu<CX_Q8_0, 16>), grid, dim3(256), lds, s, Q);
+    } else {
+      if (sub == 32) hipLaunchKernelGGL((k_gemv32_glu<CX_Q5_0, 32>), grid, dim3(256), lds, s, Q);
+      else hipLaunchKernelGGL((k_gemv32_glu<CX_Q5_0, 16>), grid, dim3(256), lds, s, Q);
+    }
+    CX_HIP(hipGetLastError());
+    return CX_OK;
+  }
   CX_REQUIRE(k > 0 && k % 256 == 0 && k <= 8192, "gemv glu: k=%u (a multiple of 256, at most 8192)", k);
   CX_REQUIRE(I > 0 && I % GLU_ROWS == 0, "gemv glu: %u rows are not tiles of %u", I, GLU_ROWS);
   CX_REQUIRE(wg && wu && x && w && xq && xe && xs, "gemv glu: null pointer");
@@ -1219,8 +1375,8 @@ bool cx_gemv_prefetch_plan(int type, const uint8_t* w, uint32_t n, uint32_t k, c
 
 bool cx_glu_prefetch_plan(int type, const uint8_t* wg, const uint8_t* wu, uint32_t I, uint32_t k,
                           cx_l2_job* job) {
-  if (!cx_glu_supported(type) || k % 256 || I % GLU_ROWS) return false;
-  const uint32_t rb = k / 256 * (uint32_t)cx_bpb(type);
+  if (!cx_glu_fits(type, k) || I % GLU_ROWS) return false;
+  const uint32_t rb = (cx_glu_supported(type) ? k / 256 : k / 32) * (uint32_t)cx_bpb(type);
   *job = cx_l2_job{wg, wu, (size_t)I * rb, GLU_ROWS * rb, I / GLU_ROWS};
   return true;
 }

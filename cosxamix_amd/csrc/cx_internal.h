@@ -105,12 +105,16 @@ int cx_launch_gemv_norm(int type, const cx_seg* segs, int nseg, uint32_t k, cons
                         const float* w, float eps, int epi, hipStream_t s);
 
 // The decode step's gate/up projections and SwiGLU in one launch
-// (src/forward.rs:472-487) for gate and up of one type (cx_glu_supported):
-// rmsnorm(x, w) quantized per workgroup, gate and up rows [32t, 32t+32) in
-// workgroup t, then silu(gate) * up quantized in sub-blocks of `sub` (the
-// down projection's) into xq/xe/xs. Bit-identical to cx_launch_gemv_norm over
-// gate and up followed by cx_launch_swiglu_quant. I % 32 == 0.
+// (src/forward.rs:472-487) for gate and up of one type at row width k
+// (cx_glu_fits): rmsnorm(x, w) quantized per workgroup, gate and up rows
+// [32t, 32t+32) in workgroup t, then silu(gate) * up quantized in sub-blocks
+// of `sub` (the down projection's) into xq/xe/xs. Bit-identical to
+// cx_launch_gemv_norm over gate and up followed by cx_launch_swiglu_quant.
+// I % 32 == 0. cx_glu_supported: the k-quant types (Q4_K, Q5_K), whose
+// tiles the attention's L2 prefetch also knows; cx_glu_fits adds Q8_0 and
+// Q5_0 where both 32-row tiles fit in LDS.
 bool cx_glu_supported(int type);
+bool cx_glu_fits(int type, uint32_t k);
 int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t I, uint32_t k,
                        const float* x, const float* w, float eps, int sub, int8_t* xq, float* xe,
                        float* xs, hipStream_t s);
