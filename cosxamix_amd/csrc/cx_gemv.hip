@@ -1150,6 +1150,20 @@ TilePlan plan_tile32(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
   return t;
 }
 
+// The plain block-32 launch's tile: the largest R <= 16 that leaves
+// PLAIN_TILES tiles
+TilePlan plain_plan32(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_t* rows,
+                      int nseg) {
+  TilePlan best{};
+  for (uint32_t R = 16; R >= 1; R >>= 1) {
+    TilePlan t = plan_tile32(R, row_bytes, k, nsub, rows, nseg, false);
+    if (t.lds > TILE_LDS_MAX) continue;
+    best = t;
+    if (t.tiles >= PLAIN_TILES) break;
+  }
+  return best;
+}
+
 template <int T, bool NORM>
 int launch_b32(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   uint32_t total_rows = 0;
@@ -1165,12 +1179,7 @@ int launch_b32(GemvParams& P, const uint32_t* rows, hipStream_t s) {
       if (t.lds <= TILE_LDS_NORM_MAX) best = t;
     }
   } else {
-    for (uint32_t R = 16; R >= 1; R >>= 1) {
-      TilePlan t = plan_tile32(R, P.row_bytes, P.k, P.nsub, rows, P.nseg, NORM);
-      if (t.lds > TILE_LDS_MAX) continue;
-      best = t;
-      if (t.tiles >= PLAIN_TILES) break;
-    }
+    best = plain_plan32(P.row_bytes, P.k, P.nsub, rows, P.nseg);
   }
   CX_REQUIRE(best.R, "gemv: a row of %u values does not fit in LDS", P.k);
   P.R = best.R;
@@ -1364,6 +1373,13 @@ int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t 
 // workgroup t runs on XCD t % 8 leaves the tile in the L2 the GEMV's
 // workgroup t reads.
 bool cx_gemv_prefetch_plan(int type, const uint8_t* w, uint32_t n, uint32_t k, cx_l2_job* job) {
+  if ((type == CX_Q8_0 || type == CX_Q5_0) && k % 32 == 0 && n) {
+    const uint32_t rb = k / 32 * (uint32_t)cx_bpb(type), rows[1] = {n};
+    const TilePlan t = plain_plan32(rb, k, k / 32, rows, 1);
+    if (!t.R) return false;
+    *job = cx_l2_job{w, nullptr, (size_t)n * rb, t.R * rb, t.tiles};
+    return true;
+  }
   if ((type != CX_Q4_K && type != CX_Q5_K) || k % 256 || !n) return false;
   const uint32_t rb = k / 256 * (uint32_t)cx_bpb(type), rows[1] = {n};
   const TilePlan t = type == CX_Q4_K ? plain_plan<CX_Q4_K>(rb, k, k / 32, rows, 1)

@@ -119,9 +119,10 @@ int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t 
                        const float* x, const float* w, float eps, int sub, int8_t* xq, float* xe,
                        float* xs, hipStream_t s);
 
-// A prefetch job of the tiles of the plain Q4_K/Q5_K GEMV of w (n x k) or
-// of the gate/up launch of wg and wu (I x k), each into the L2 it is read
-// from; false (and no job) where the launch has no such tiling.
+// A prefetch job of the tiles of the plain GEMV of w (n x k; Q4_K, Q5_K,
+// Q8_0, Q5_0) or of the gate/up launch of wg and wu (I x k), each into the
+// L2 it is read from; false (and no job) where the launch has no such
+// tiling.
 bool cx_gemv_prefetch_plan(int type, const uint8_t* w, uint32_t n, uint32_t k, cx_l2_job* job);
 bool cx_glu_prefetch_plan(int type, const uint8_t* wg, const uint8_t* wu, uint32_t I, uint32_t k,
                           cx_l2_job* job);
