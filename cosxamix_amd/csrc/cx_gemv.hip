@@ -1064,14 +1064,16 @@ TilePlan plan_tile(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
   return t;
 }
 
-// Tiles of a launch without the rmsnorm prologue: one per CU (measured on
-// MI355X: in the 3B decode step 2 tiles per CU took 1.7% longer a token and
-// 4 tiles 8% longer; in the daiss-0.5b Q8_0 step 2 tiles per CU took 1.8%
-// longer)
+// Tiles of a launch without the rmsnorm prologue: about one per CU, the
+// largest tile height that leaves at least 7/8 of PLAIN_TILES tiles
+// (measured on MI355X: in the 3B decode step 2 tiles per CU took 1.7%
+// longer a token and 4 tiles 8% longer; in the daiss-0.5b Q8_0 step 2
+// tiles per CU took 1.8% longer, and its 896-row matrices in 224 tiles of
+// 4 rows rather than 448 of 2 made the token 0.4% shorter)
 constexpr uint32_t PLAIN_TILES = 256;
 
 // The plain (no prologue) launch's tile: the largest R <= 16 that leaves
-// PLAIN_TILES tiles
+// 7/8 of PLAIN_TILES tiles
 template <int T>
 TilePlan plain_plan(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_t* rows, int nseg) {
   constexpr bool REG = T == CX_Q4_K || T == CX_Q5_K;  // weights straight into registers
@@ -1080,7 +1082,7 @@ TilePlan plain_plan(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_
     TilePlan t = plan_tile(R, row_bytes, k, nsub, rows, nseg, false, REG);
     if (t.lds > TILE_LDS_MAX) continue;
     best = t;
-    if (t.tiles >= PLAIN_TILES) break;
+    if (t.tiles >= PLAIN_TILES * 7 / 8) break;
   }
   return best;
 }
@@ -1099,8 +1101,8 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   //  - with the rmsnorm prologue every workgroup repeats the activation
   //    work, so take one tile per CU (R = rows/256) when it fits in LDS, else
   //    two tiles per CU;
-  //  - otherwise plain_plan's: the largest R <= 16 that leaves a tile per
-  //    CU (256 tiles).
+  //  - otherwise plain_plan's: the largest R <= 16 that leaves about a
+  //    tile per CU (at least 224 tiles).
   uint32_t total_rows = 0;
   for (int i = 0; i < P.nseg; i++) total_rows += rows[i];
   TilePlan best{};
@@ -1150,7 +1152,7 @@ TilePlan plan_tile32(uint32_t R, uint32_t row_bytes, uint32_t k, uint32_t nsub,
   return t;
 }
 
-// The plain block-32 launch's tile: the largest R <= 16 that leaves
+// The plain block-32 launch's tile: the largest R <= 16 that leaves 7/8 of
 // PLAIN_TILES tiles
 TilePlan plain_plan32(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_t* rows,
                       int nseg) {
@@ -1159,7 +1161,7 @@ TilePlan plain_plan32(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint3
     TilePlan t = plan_tile32(R, row_bytes, k, nsub, rows, nseg, false);
     if (t.lds > TILE_LDS_MAX) continue;
     best = t;
-    if (t.tiles >= PLAIN_TILES) break;
+    if (t.tiles >= PLAIN_TILES * 7 / 8) break;
   }
   return best;
 }
@@ -1169,7 +1171,7 @@ int launch_b32(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   uint32_t total_rows = 0;
   for (int i = 0; i < P.nseg; i++) total_rows += rows[i];
   // the k-quant GEMV's tile choice: with the prologue one or two tiles per
-  // CU, otherwise the largest R <= 16 that leaves a tile per CU
+  // CU, otherwise the largest R <= 16 that leaves about a tile per CU
   TilePlan best{};
   if (NORM) {
     for (uint32_t per_cu = 1; per_cu <= 8 && !best.R; per_cu *= 2) {
