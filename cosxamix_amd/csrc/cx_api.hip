@@ -1294,8 +1294,15 @@ static int enqueue_step(cx_cache* C) {
     a.sub = cx_sub(L.t_o);
     const bool glu = L.t_gate == L.t_up && cx_glu_fits(L.t_gate, D) && I % 32 == 0;
     // the attention's spare CUs pull the o-proj's and gate/up's weights into L2
+    // (all of them: past L2's 4 MB an XCD the Infinity Cache still holds
+    // them; trimming config 5's 75 MB to 28 MB made its token 0.8% slower)
     (void)cx_gemv_prefetch_plan(L.t_o, L.o, D, D, &a.pf.job[0]);
     if (glu) (void)cx_glu_prefetch_plan(L.t_gate, L.gate, L.up, I, D, &a.pf.job[1]);
+    // With a cache past the short path (the attention then runs for tens of
+    // µs), the down projection's weights too: beyond L2's capacity, they are
+    // read back from the Infinity Cache (config 5: +0.6% a token; the next
+    // layer's q/k/v as well gave nothing more)
+    if (a.cap > CX_ATT_LDS_MAX) (void)cx_gemv_prefetch_plan(L.t_down, L.down, D, I, &a.pf.job[2]);
     if ((rc = cx_launch_attn_decode(a, s))) return rc;
     // src/forward.rs:466-469: output projection added to the residual
     cx_seg o{L.o, m->x, nullptr, D};
