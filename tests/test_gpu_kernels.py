@@ -167,7 +167,8 @@ def test_matmul_auto_rows_equal_single_rows(cx, dev):  # src/ops.rs:1364-1393
 @pytest.mark.parametrize("t,n,k,ms", [
     (O.Q4_K, 11008, 2048, (8, 32, 40, 70, 512)),  # BASELINE config 4, first matrix
     (O.Q4_K, 2048, 11008, (8, 32, 512)),           # config 4, second matrix (43 blocks)
-    (O.Q5_K, 1000, 4096, (3, 17, 64, 100, 200)),   # ragged n, partial tiles
+    (O.Q5_K, 1000, 4096, (3, 16, 17, 64, 100, 200)),  # ragged n, partial tiles
+    (O.Q4_K, 2048, 2048, (2, 12, 16)),             # few rows: one 16-row tile, mostly padding
     # the 16-value sub-block formats (two masked MFMAs a 32-value group)
     (O.Q6_K, 2048, 11008, (2, 17, 64)),             # Q*_K_M down projections
     (O.Q6_K, 1000, 2048, (5, 130)),
