@@ -316,6 +316,26 @@ def test_decode_attention_paths(cx, dev, heads, kvh, hd):
 
 
 @pytest.mark.parametrize("heads,kvh", [(16, 2), (32, 8)])
+def test_decode_attention_long_path_limits(cx, dev, heads, kvh):
+    """Order-exact decode attention on either side of the long one-token
+    path's limits: 4096/4097 (the scores from k_att_qk and an 80 KiB V ring
+    from 4097 on), 6145 (three stages of the softmax sum's 2048 positions and
+    one more), 11520/11521 (the last cache the long path holds in LDS, then
+    k_att_sv); bit-identical to the oracle."""
+    ops, _ = cx
+    hd = 128
+    for total in (4096, 4097, 6145, 11520, 11521):
+        rng = np.random.default_rng(total + 3 * heads)
+        q = rng.normal(0, 1, heads * hd).astype(np.float32)
+        k = rng.normal(0, 1, total * kvh * hd).astype(np.float32)
+        v = rng.normal(0, 1, total * kvh * hd).astype(np.float32)
+        want = O.attention(q, k, v, 1, total, heads, kvh, hd)
+        out = torch.empty(heads * hd, dtype=torch.float32, device=dev)
+        ops.atencion_decode(T(q, dev), T(k, dev), T(v, dev), (total, heads, kvh, hd), out, 1)
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32)), total
+
+
+@pytest.mark.parametrize("heads,kvh", [(16, 2), (32, 8)])
 def test_decode_attention_sum_edge_cases(cx, dev, heads, kvh):
     """Order-exact decode attention on scores that stress the sum of exps:
     a wide spread (most exps subnormal or zero, the sum starting far below
