@@ -31,10 +31,12 @@
 //                of p (8-bit digits, least significant first); they return
 //                at once when top_p >= 1 (no order needed)
 //   k_samp_pick  the token                                      (1 workgroup)
-// The sequential sums (S, the running sums) are single-lane chains fed from
-// LDS stages that the other waves fill with direct-to-LDS loads.
+// The sequential sums (S, the running sums) are ordered f32 sums that one
+// wave forms by binade scans (cx_scan.h), fed from LDS stages that the other
+// waves fill with direct-to-LDS loads.
 #include "cx_ops.h"
 #include "cx_act.h"
+#include "cx_scan.h"
 
 namespace {
 
@@ -48,7 +50,8 @@ constexpr uint32_t RS_T = 256;       // threads of a radix-sort workgroup
 constexpr uint32_t RS_R = 8;         // rounds of RS_T elements a tile
 constexpr uint32_t RS_TILE = RS_T * RS_R;
 
-constexpr size_t PICK_LDS = NST * SEG * sizeof(float);  // the chains' ring
+// the chains' ring, and the 511 floats past its last stage that a scan reads
+constexpr size_t RING_LDS = (NST * SEG + 512) * sizeof(float);
 
 // total-order key of a probability (f32::total_cmp): larger key, larger value
 __device__ inline uint32_t pkey(float p) {
@@ -111,10 +114,10 @@ __global__ __launch_bounds__(ZB) void k_samp_p(float* pb, uint32_t n, const cx_s
   }
 }
 
-// ------------------------------------------------------ single-lane chains
+// ---------------------------------------------------------- ordered sums
 // A ring of NST stages of SEG floats: loader waves 1..8 each load one KiB of
-// every stage; stage s sits in slot s % NST. The chain (thread 0) walks the
-// stages in order; after each stage every wave learns whether it stopped.
+// every stage; stage s sits in slot s % NST. Wave 0 walks the stages in
+// order; after each stage every wave learns whether it stopped.
 struct Ring {
   float* lds;
   const float* src;
@@ -143,9 +146,10 @@ struct Ring {
   }
 };
 
-// Walks x[0..n) in order through the ring: `stage(v, m, base)` runs on
-// thread 0 for each stage (m values at LDS v, indices base..) and returns
-// true to stop. Every wave leaves with every load landed.
+// Walks x[0..n) in order through the ring: `stage(v, m, base)` runs on wave
+// 0 for each stage (m values at LDS v, indices base..; +0.0 from m to the
+// next multiple of 16) and returns true, the same in every lane, to stop.
+// Every wave leaves with every load landed.
 template <class F>
 __device__ inline void chain_walk(const float* x, uint32_t n, float* lds, F stage) {
   __shared__ uint32_t stop;
@@ -159,7 +163,12 @@ __device__ inline void chain_walk(const float* x, uint32_t n, float* lds, F stag
     cx_wait_lds();
     cx_barrier();  // stage s landed; `stop` from the last stage is visible
     if (stop) break;
-    if (tid == 0 && stage(lds + (s % NST) * SEG, min(SEG, n - s * SEG), s * SEG)) stop = 1;
+    if (R.wave == 0) {
+      float* v = lds + (s % NST) * SEG;
+      const uint32_t m = min(SEG, n - s * SEG);
+      if (R.lane < (16 - m % 16) % 16) v[m + R.lane] = 0.0f;  // the loads past n hold x[0..]
+      if (stage(v, m, s * SEG) && R.lane == 0) stop = 1;
+    }
     cx_wait_lds();
     cx_barrier();  // slot s read
     if (s + NST < R.nstage) R.issue(s + NST);
@@ -169,118 +178,22 @@ __device__ inline void chain_walk(const float* x, uint32_t n, float* lds, F stag
   __syncthreads();
 }
 
-// tot += v[0] + ... + v[m) in order; 32 values a batch, two register
-// buffers taking turns: a batch is read while the one before it is added
-// (v holds whole batches: reads past m stay in the stage)
-__device__ inline void add32v(float& tot, const float4 (&a)[8]) {
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    tot += a[i].x;
-    tot += a[i].y;
-    tot += a[i].z;
-    tot += a[i].w;
-  }
-}
-__device__ inline void load32v(float4 (&a)[8], const float4* v4, uint32_t j) {
-#pragma unroll
-  for (int i = 0; i < 8; i++) a[i] = v4[j / 4 + i];
-}
-__device__ inline void stage_sum(float& tot, const float* v, uint32_t m) {
-  const float4* v4 = reinterpret_cast<const float4*>(v);
-  float4 A[8], B[8];
-  const uint32_t mb = m / 32 * 32;  // whole batches
-  uint32_t j = 0;
-  if (mb) load32v(A, v4, 0);
-  while (j < mb) {
-    if (j + 32 < mb) load32v(B, v4, j + 32);
-    add32v(tot, A);
-    j += 32;
-    if (j >= mb) break;
-    if (j + 32 < mb) load32v(A, v4, j + 32);
-    add32v(tot, B);
-    j += 32;
-  }
-  for (; j < m; j++) tot += v[j];
-}
-
-// The running sum acc += v[j] in order, stopping at the first j with
-// acc > target (GE: acc >= target; returns j, or m). The sums of a batch of
-// 32 are formed first and checked once: acc never decreases (v >= 0), so the
-// batch crosses iff its last sum does; a NaN sum takes the one-by-one check.
-template <bool GE>
-__device__ inline bool passes(float a, float target) { return GE ? a >= target : a > target; }
-
-// one batch of 32: true (and acc = the crossing sum, *at = its offset) if it
-// crosses, else acc = the batch's last sum
-template <bool GE>
-__device__ inline bool cross32(float& acc, const float4 (&A)[8], float target, uint32_t* at) {
-  float r[32];
-  float a = acc;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    a += A[i].x;
-    r[4 * i] = a;
-    a += A[i].y;
-    r[4 * i + 1] = a;
-    a += A[i].z;
-    r[4 * i + 2] = a;
-    a += A[i].w;
-    r[4 * i + 3] = a;
-  }
-  if (passes<GE>(a, target) || a != a) {
-#pragma unroll
-    for (int k = 0; k < 32; k++)
-      if (passes<GE>(r[k], target)) {
-        acc = r[k];
-        *at = (uint32_t)k;
-        return true;
-      }
-  }
-  acc = a;
-  return false;
-}
-
-template <bool GE = false>
-__device__ inline uint32_t stage_cross(float& acc, const float* v, uint32_t m, float target) {
-  const float4* v4 = reinterpret_cast<const float4*>(v);
-  float4 A[8], B[8];
-  const uint32_t mb = m / 32 * 32;
-  uint32_t j = 0, k = 0;
-  if (mb) load32v(A, v4, 0);
-  while (j < mb) {
-    if (j + 32 < mb) load32v(B, v4, j + 32);
-    if (cross32<GE>(acc, A, target, &k)) return j + k;
-    j += 32;
-    if (j >= mb) break;
-    if (j + 32 < mb) load32v(A, v4, j + 32);
-    if (cross32<GE>(acc, B, target, &k)) return j + k;
-    j += 32;
-  }
-  for (; j < m; j++) {
-    acc += v[j];
-    if (passes<GE>(acc, target)) return j;
-  }
-  return m;
-}
-
 // The running sum of x[0..n) continued from *acc: the first index where it
-// exceeds target (GE: reaches it), or n; *acc (thread 0) ends as the sum
-// through that index, or through x[n - 1]
+// exceeds target (M = SCAN_EXCEED) or reaches it (SCAN_REACH), or n; *acc
+// ends as the sum through that index, or through x[n - 1]. x >= 0 (or NaN).
 // (*acc in shared memory; every thread sees the result and *acc on return)
-template <bool GE = false>
+template <int M>
 __device__ inline uint32_t chain_find(const float* x, uint32_t n, float* lds, float target,
                                       float* acc) {
   __shared__ uint32_t s_at;
   __syncthreads();  // every read of the last call's s_at and *acc is done
-  float a = 0.0f;
-  if (threadIdx.x == 0) {
-    a = *acc;
-    s_at = n;
-  }
+  float a = *acc;
+  if (threadIdx.x == 0) s_at = n;
   chain_walk(x, n, lds, [&](const float* v, uint32_t m, uint32_t base) {
-    const uint32_t k = stage_cross<GE>(a, v, m, target);
+    uint32_t k;
+    a = seq_scan<M>(v, m, a, base == 0, target, &k);
     if (k < m) {
-      s_at = base + k;
+      if ((threadIdx.x & 63) == 0) s_at = base + k;
       return true;
     }
     return false;
@@ -295,7 +208,7 @@ __device__ inline uint32_t chain_cross(const float* x, uint32_t n, float* lds, f
   __shared__ float acc;
   __syncthreads();  // no thread still reads the last call's acc
   if (threadIdx.x == 0) acc = 0.0f;
-  return chain_find<false>(x, n, lds, target, &acc);
+  return chain_find<SCAN_EXCEED>(x, n, lds, target, &acc);
 }
 
 // S = e_0 + e_1 + ... sequentially from 0, then 1/S; and the draw of u
@@ -311,8 +224,8 @@ __global__ __launch_bounds__(CW) void k_samp_sum(const float* pb, uint32_t n, cx
   }
   if (sd->uniform) return;
   float tot = 0.0f;
-  chain_walk(pb, n, ring, [&](const float* v, uint32_t m, uint32_t) {
-    stage_sum(tot, v, m);
+  chain_walk(pb, n, ring, [&](const float* v, uint32_t m, uint32_t base) {
+    tot = seq_sum_scan(v, m, tot, base == 0);
     return false;
   });
   if (threadIdx.x == 0) sd->inv_s = 1.0f / tot;
@@ -453,13 +366,13 @@ __global__ __launch_bounds__(CW) void k_samp_pick(const float* pb, uint32_t n, c
     const uint32_t k = min(CAND, n);
     if (tid == 0) s_acc = 0.0f;
     __syncthreads();
-    uint32_t at = chain_find<true>(ordp, k, ring, top_p, &s_acc);
+    uint32_t at = chain_find<SCAN_REACH>(ordp, k, ring, top_p, &s_acc);
     uint32_t cut;
     if (at < k) {
       cut = at + 1;
     } else if (s_acc < top_p && k < n) {
       // their mass falls short: the nucleus comes from every token's order
-      at = chain_find<true>(ordp + k, n - k, ring, top_p, &s_acc);
+      at = chain_find<SCAN_REACH>(ordp + k, n - k, ring, top_p, &s_acc);
       cut = at < n - k ? k + at + 1 : n;
     } else {
       cut = k;  // a NaN top_p: the candidates, whole
@@ -519,12 +432,11 @@ int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb
   uint32_t* iA = kA + S.n4;
   uint32_t* kB = iA + S.n4;
   uint32_t* cnt = kB + S.n4;
-  const size_t ring = (size_t)NST * SEG * sizeof(float);
   hipLaunchKernelGGL(k_samp_z, dim3(g), dim3(ZB), 0, s, logits, N, sd, pb, part);
   CX_HIP(hipGetLastError());
   hipLaunchKernelGGL(k_samp_e, dim3(g), dim3(ZB), 0, s, pb, N, part, g, sd);
   CX_HIP(hipGetLastError());
-  hipLaunchKernelGGL(k_samp_sum, dim3(1), dim3(CW), ring, s, pb, N, sd);
+  hipLaunchKernelGGL(k_samp_sum, dim3(1), dim3(CW), RING_LDS, s, pb, N, sd);
   CX_HIP(hipGetLastError());
   hipLaunchKernelGGL(k_samp_p, dim3(g), dim3(ZB), 0, s, pb, N, sd);
   CX_HIP(hipGetLastError());
@@ -549,7 +461,7 @@ int cx_launch_sample(const float* logits, size_t n, cx_samp_state* sd, float* pb
       (rc = pass(k_rs_count<2>, k_rs_scatter<2>, kB, ord, kA, iA, nullptr)) ||
       (rc = pass(k_rs_count<3>, k_rs_scatter<3>, kA, iA, nullptr, ord, ordp)))
     return rc;
-  hipLaunchKernelGGL(k_samp_pick, dim3(1), dim3(CW), PICK_LDS, s, pb, N, sd, ord, ordp, out, st,
+  hipLaunchKernelGGL(k_samp_pick, dim3(1), dim3(CW), RING_LDS, s, pb, N, sd, ord, ordp, out, st,
                      hist, hist_host);
   CX_HIP(hipGetLastError());
   return CX_OK;

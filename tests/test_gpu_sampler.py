@@ -120,3 +120,78 @@ def test_generate_with_sampler_stops_at_the_end_token(S, dev):
     want = O.generate_sampled(ref, prompt, 30, o, ref.new_cache(256), eos=eos)
     assert np.array_equal(got, want) and len(got) == first
     assert g.estado == o.state  # the end token's draw counted
+
+
+def first_u(seed):
+    """u of the sampler's first draw (Azar::siguiente, src/daiss.rs:330-337;
+    uniforme, src/sampler.rs:55-58)."""
+    M = 2**64 - 1
+    x = (seed & M) or 0x9E3779B97F4A7C15
+    x ^= x >> 12
+    x ^= (x << 25) & M
+    x ^= x >> 27
+    return np.float32(((x * 0x2545F4914F6CDD1D) & M) >> 40) / np.float32(16777216.0)
+
+
+def test_targets_on_exact_running_sums(S, dev):
+    """The three running-sum searches with targets equal to a running sum,
+    past the first 256 positions and the first 2048-position stage of the
+    GPU's sums: the draw over the index order (the first sum > u), the
+    nucleus cut (the first sum >= top_p enters) and the draw inside the
+    nucleus (the first sum > u * total). Each case is chosen so that a search
+    stopping one position early or late, or using the other inequality,
+    returns another token; the expected tokens come from the running sums
+    here and are checked against the oracle too."""
+    n = 151936
+    lg = logits_of("soft", n, 5)
+    p = O.softmax(lg, n)  # temperature 1: z = logit
+    run = np.cumsum(p, dtype=np.float32)  # in order, one f32 add a position
+    order = np.lexsort((np.arange(n), -p))  # descending, ties by index
+    rund = np.cumsum(p[order], dtype=np.float32)
+    d = torch.from_numpy(lg).to(dev)
+    us = [(s, first_u(s)) for s in range(1, 60000)]
+
+    def first_above(r, t, last):
+        i = int(np.searchsorted(r[:last + 1], t, side="right"))
+        return min(i, last)
+
+    def check(seed, top_p, want):
+        assert O.Sampler(seed, 1.0, top_p).choose(lg) == want, (seed, top_p)
+        assert S.Muestreador(seed, 1.0, top_p).elegir(d) == want, (seed, top_p)
+
+    # 1. top_p = 1: u equals run[i]; the token is i + 1 (i with >=)
+    hits = [(s, int(np.searchsorted(run, u))) for s, u in us]
+    hits = [(s, i) for s, i in hits if 2048 < i < n - 1 and run[i] == us[s - 1][1]]
+    assert len(hits) >= 2
+    for s, i in hits[:3]:
+        assert run[i + 1] > run[i]
+        check(s, 1.0, i + 1)
+    # 2. top_p = rund[j]: the nucleus is order[0..j] (j in the candidates, and
+    # past them); u close enough to 1 that the draw takes its last token, and
+    # would take order[j + 1] from a nucleus one longer
+    for j in (700, 1500, 5000):
+        top_p = float(rund[j])
+        found = 0
+        for s, u in us:
+            want = first_above(rund, np.float32(u * rund[j]), j)
+            late = first_above(rund, np.float32(u * rund[j + 1]), j + 1)
+            if want == j and late == j + 1:
+                check(s, top_p, int(order[j]))
+                found += 1
+                if found == 2:
+                    break
+        assert found == 2, j
+    # 3. the draw inside a nucleus of 100,001 tokens: u * total equals rund[i]
+    J = 100000
+    top_p = float(rund[J])
+    found = 0
+    for s, u in us:
+        t = np.float32(u * rund[J])
+        i = int(np.searchsorted(rund[:J + 1], t))
+        if 2048 < i < J and rund[i] == t:
+            assert rund[i + 1] > t
+            check(s, top_p, int(order[i + 1]))
+            found += 1
+            if found == 3:
+                break
+    assert found == 3

@@ -24,14 +24,45 @@ def _binade(s):
     return max(e, 1) - 127
 
 
-def scan_sum(x, tot=0.0, head=256):
+def _passes(a, target, mode):
+    return a >= target if mode == "reach" else a > target
+
+
+def scan(x, tot=0.0, head=256, mode="sum", target=0.0):
+    """The kernel's seq_scan: (sum, at). mode "sum" (at = n), or "exceed" /
+    "reach": at = the first position whose running sum is > / >= target and
+    the sum ends there, else at = n and the sum is the whole one (a NaN sum
+    ends a search at once)."""
     x = np.asarray(x, F)
-    n, tot = len(x), F(tot)
-    p = min(n, head)
-    for i in range(p):
-        tot = F(tot + x[i])
+    n, tot, target = len(x), F(tot), F(target)
+    find = mode != "sum"
+
+    def serial(t, p):
+        for i in range(p, n):
+            if find and np.isnan(t):
+                break
+            t = F(t + x[i])
+            if find and _passes(t, target, mode):
+                return t, i
+        return t, n
+
+    p = 0
+    if head and n:
+        p = min(n, head)
+        t0 = tot
+        for i in range(p):
+            tot = F(tot + x[i])
+        if find and (_passes(tot, target, mode) or np.isnan(tot)):
+            t = t0
+            for j in range(p):
+                t = F(t + x[j])
+                if _passes(t, target, mode):
+                    return t, j
+            return t, n
     if p >= n:
-        return tot
+        return tot, n
+    if not tot < np.inf:
+        return serial(tot, p)
     E = _binade(tot)
     A = F(np.ldexp(tot, 23 - E))
     while True:
@@ -40,26 +71,36 @@ def scan_sum(x, tot=0.0, head=256):
             q = np.ldexp(w, 23 - E).astype(F)
             r = np.rint(q)
             half = ~(np.abs(q - r) < 0.5)
-        P = np.cumsum(r, dtype=F)
-        H = F(F(16777216.0) - A)
-        ev = np.nonzero(half | (P >= H))[0]
-        at = int(ev[0]) if len(ev) else 256
-        room = n - p
-        stop = min(at, room)
+            P = np.cumsum(r, dtype=F)
+            H = F(F(16777216.0) - A)
+            ev = np.nonzero(half | (P >= H))[0]
+            at = int(ev[0]) if len(ev) else 256
+            room = n - p
+            stop = min(at, room)
+            if find:  # the running sums before the first event, exact
+                sums = np.ldexp(F(A) + P, E - 23).astype(F)
+                g = np.nonzero(_passes(sums, target, mode))[0]
+                pa = int(g[0]) if len(g) else 256
+                if pa < stop:
+                    return F(sums[pa]), p + pa
         if stop:
             A = F(A + P[stop - 1])
         if at >= room:
-            return F(np.ldexp(A, E - 23))
+            return F(np.ldexp(A, E - 23)), n
         s = F(F(np.ldexp(A, E - 23)) + x[p + at])
+        if find and _passes(s, target, mode):
+            return s, p + at
         p += at + 1
-        if not np.isfinite(s):
-            for i in range(p, n):
-                s = F(s + x[i])
-            return s
+        if not s < np.inf:
+            return serial(s, p)
         if p >= n:
-            return s
+            return s, n
         E = _binade(s)
         A = F(np.ldexp(s, 23 - E))
+
+
+def scan_sum(x, tot=0.0, head=256):
+    return scan(x, tot, head)[0]
 
 
 def seq_sum(x, tot=0.0):
@@ -67,6 +108,16 @@ def seq_sum(x, tot=0.0):
     for v in np.asarray(x, F):
         tot = F(tot + v)
     return tot
+
+
+def seq_find(x, tot, target, mode):
+    """The reference's running-sum search: the first i whose sum passes."""
+    tot, target = F(tot), F(target)
+    for i, v in enumerate(np.asarray(x, F)):
+        tot = F(tot + v)
+        if _passes(tot, target, mode):
+            return tot, i
+    return tot, len(x)
 
 
 def _exps(rng, n, mode):
@@ -123,3 +174,70 @@ def test_scan_sum_binade_edges_and_nan():
     x = np.ones(900, F)
     x[700] = np.nan
     assert np.isnan(scan_sum(x, 0.0, 0)) and np.isnan(seq_sum(x))
+
+
+def _probs(rng, n, mode):
+    e = _exps(rng, n, mode)
+    return (e * F(F(1.0) / seq_sum(e))).astype(F)
+
+
+@pytest.mark.parametrize("mode", ["normal", "sink", "bimodal", "ties", "tiny", "wide"])
+@pytest.mark.parametrize("search", ["exceed", "reach"])
+def test_scan_search_equals_sequential_search(mode, search):
+    # the sampler's running sums: probabilities in index order (the draw
+    # with top_p >= 1) and in descending order (the nucleus cut and the
+    # draw inside it), against targets between, on and past the sums
+    rng = np.random.default_rng(10 + ["normal", "sink", "bimodal", "ties", "tiny", "wide"].index(mode))
+    for n in (1, 7, 255, 256, 257, 700, 2048, 5000):
+        for order in ("index", "descending"):
+            x = _probs(rng, n, mode)
+            if order == "descending":
+                x = -np.sort(-x)
+            run = np.cumsum(x, dtype=F)  # numpy's float32 cumsum adds in order
+            targets = [F(rng.random()), F(0.9), F(0.0), F(-1.0), F(2.0), run[n // 2], run[-1],
+                       run[min(n - 1, 300)], np.nextafter(run[n // 3], F(0)), F(np.inf), F(np.nan)]
+            for target in targets:
+                for head in (256, 0):
+                    got = scan(x, 0.0, head, search, target)
+                    want = seq_find(x, 0.0, target, search)
+                    assert got[1] == want[1] and _same(got[0], want[0]), (mode, n, order, target,
+                                                                          head, got, want)
+            # continued from a partial sum, as the nucleus's second search is
+            k = n // 4
+            t0 = seq_sum(x[:k])
+            for target in (F(0.9), run[-1], F(rng.random())):
+                got = scan(x[k:], t0, 256, search, target)
+                want = seq_find(x[k:], t0, target, search)
+                assert got[1] == want[1] and _same(got[0], want[0]), (mode, n, target, "cont")
+
+
+def test_scan_search_on_the_sums_and_nan():
+    # a target equal to a running sum: "reach" stops there, "exceed" at the
+    # first larger sum; equal terms make long runs of distinct sums
+    x = np.full(3000, F(1.0 / 3000), F)
+    run = np.cumsum(x, dtype=F)
+    for j in (0, 1, 255, 256, 257, 1000, 2047, 2999):
+        for head in (256, 0):
+            assert scan(x, 0.0, head, "reach", run[j])[1] == seq_find(x, 0.0, run[j], "reach")[1] == j
+            want = seq_find(x, 0.0, run[j], "exceed")
+            assert scan(x, 0.0, head, "exceed", run[j]) [1] == want[1] > j
+    # zero terms: sums that repeat
+    x = np.zeros(1000, F)
+    x[::7] = F(1e-3)
+    for target in (F(0.0), F(1e-3), F(0.05)):
+        for search in ("exceed", "reach"):
+            for head in (256, 0):
+                got, want = scan(x, 0.0, head, search, target), seq_find(x, 0.0, target, search)
+                assert got[1] == want[1] and _same(got[0], want[0]), (target, search, head)
+    # a NaN term: a crossing before it is found, none after it
+    x = np.full(900, F(1e-3), F)
+    x[600] = np.nan
+    for head in (256, 0):
+        assert scan(x, 0.0, head, "exceed", F(0.3))[1] == seq_find(x, 0.0, F(0.3), "exceed")[1]
+        got = scan(x, 0.0, head, "exceed", F(0.7))
+        assert got[1] == 900 and np.isnan(got[0])
+    x[100] = np.nan  # inside the head
+    got = scan(x, 0.0, 256, "reach", F(0.05))
+    assert got == seq_find(x, 0.0, F(0.05), "reach")
+    got = scan(x, 0.0, 256, "reach", F(0.5))
+    assert got[1] == 900 and np.isnan(got[0])
