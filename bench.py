@@ -621,6 +621,8 @@ def main():
                          "and config 5's (8448 positions, 32/8 heads): for kernel profiles")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the config-1 GEMV roofline loop (e.g. under rocprofv3)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the 3B model's batched prefill of --prompt tokens")
     ap.add_argument("--small-only", action="store_true",
                     help="only the daiss-0.5b Q8_0 decode (the 32-value block GEMV)")
     a = ap.parse_args()
@@ -658,6 +660,11 @@ def main():
         return 0
     if a.small_only:
         print(json.dumps(small_model_bench(F, L, a.steps, a.warmup, a.prompt)), flush=True)
+        return 0
+    if a.prefill_only:
+        m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)
+        print(json.dumps(prefill_bench(m, prompt_tokens(a.prompt, F.DAISS_3B.vocab))), flush=True)
+        m.close()
         return 0
     if a.roofline_only:
         m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)

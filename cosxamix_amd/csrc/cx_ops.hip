@@ -248,21 +248,22 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 // (src/forward.rs:454-455). The score at st->pos uses the rotated key from
 // LDS, so no result depends on a cache row written in the same launch.
 //
-// k_attn_seq, one wave per (head, 64 head dims): the head's scores are
-// copied in, then the softmax in the reference's order: exact max,
-// e = exp(s - max) (glibc's expf), the sum accumulated sequentially from 0,
-// p = e * (1/sum) (src/ops.rs:1211-1229). Meanwhile the V slice streams
-// through a ring of LDS stages; lane d accumulates out[d] = sum over p of
-// prob_p * v_p[d] in position order (src/ops.rs:1316-1321). The output is
-// then quantized for the output projection (64 values are whole
-// sub-blocks). Bit-identical to the scalar reference.
+// k_attn_seq, one workgroup per (head, 32 head dims): the head's scores are
+// copied in, then the softmax in the reference's order: exact max (from the
+// scores kernel's chunk maxima), e = exp(s - max) (glibc's expf), the sum in
+// position order from 0 (its first 256 adds one by one, the rest by binade
+// scan), p = e * (1/sum) (src/ops.rs:1211-1229). Meanwhile the V slice
+// streams through a ring of LDS stages; waves 1-3 form each stage's
+// products p * v[d] and wave 0's lane d adds them into out[d] in position
+// order (src/ops.rs:1316-1321). The output is then quantized for the
+// output projection (32 values are whole sub-blocks). Bit-identical to the
+// scalar reference.
 constexpr uint32_t SC_P = 64;     // positions per scores wave
 constexpr uint32_t PV_STP = 128;  // positions per V stage
 // The softmax-V kernel's shape: DS head dims per workgroup (wave 0's lanes),
-// NST V stages of PV_STP positions in the LDS ring (128 KiB either way).
-// One query token (decode) takes 32 dims: twice the workgroups of 64, so the
-// shared softmax and chains run on more CUs at once; many query tokens
-// (prefill) take 64, which does that shared work half as often.
+// NST V stages of PV_STP positions in a ring of RING floats. 32 dims give
+// twice the workgroups of 64, so the softmax and chains, done once per
+// workgroup, run on more CUs at once.
 template <uint32_t DS, uint32_t RING = 32768>
 struct PvShape {
   static constexpr uint32_t NST = RING / (PV_STP * DS);
@@ -294,20 +295,12 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* q, const float
   float* qr = reinterpret_cast<float*>(sm + NCH * 1024);
   float* kr = qr + HD;
   constexpr uint32_t half = HD / 2;
-  // query token z (blockIdx.z) sits at position st->pos + z
   const uint32_t chunk = blockIdx.x, h = blockIdx.y;
-  const uint32_t z = blockIdx.z, pos = st->pos + z, total = pos + 1;
+  const uint32_t pos = st->pos, total = pos + 1;
   const uint32_t p0 = chunk * SC_P, per = heads / kvh, g = h / per;
   if (p0 >= total) return;
   const uint32_t np = min(SC_P, total - p0), kvd = kvh * HD;
-  q += (size_t)z * heads * HD;
-  if (cos_t) {
-    knew += (size_t)z * kvd;
-    vnew += (size_t)z * kvd;
-  }
-  sc += (size_t)z * heads * sc_stride(cap);
   const uint32_t nck = (cap + SC_P - 1) / SC_P;
-  cm += (size_t)z * heads * nck;
   const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
   // the scale is read here, with the other arguments: read where it is
   // used, its scalar load would make the dots' LDS reads wait for it
@@ -372,8 +365,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* q, const float
   }
 }
 
-// Sequential sum of x[0..n) from 0 (one lane). LDS reads run a batch of 32
-// values ahead, alternating between two register buffers.
+// tot += the 32 values of a, in order
 __device__ inline void add32(float& tot, const float4 (&a)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; i++) {
@@ -382,46 +374,6 @@ __device__ inline void add32(float& tot, const float4 (&a)[8]) {
     tot += a[i].z;
     tot += a[i].w;
   }
-}
-// (The scheduling barriers keep each batch's reads issued ahead of the
-// previous batch's adds: left to itself the scheduler sinks them next to
-// their first use, and the chain then waits out an LDS latency every few
-// adds.)
-__device__ inline float seq_sum_lds(const float* x, uint32_t n, float tot = 0.0f) {
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  const uint32_t n4 = n / 4;
-  float4 A[8], B[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) A[i] = x4[i];  // may read past n: never used
-  uint32_t b = 0;
-  for (;;) {
-    if (b + 8 > n4) break;
-#pragma unroll
-    for (int i = 0; i < 8; i++) B[i] = x4[b + 8 + i];
-    __builtin_amdgcn_sched_barrier(0);
-    add32(tot, A);
-    b += 8;
-    if (b + 8 > n4) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) A[i] = B[i];
-      break;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) A[i] = x4[b + 8 + i];
-    __builtin_amdgcn_sched_barrier(0);
-    add32(tot, B);
-    b += 8;
-  }
-#pragma unroll
-  for (int i = 0; i < 8; i++)
-    if (b + i < n4) {
-      tot += A[i].x;
-      tot += A[i].y;
-      tot += A[i].z;
-      tot += A[i].w;
-    }
-  for (uint32_t p = n4 * 4; p < n; p++) tot += x[p];
-  return tot;
 }
 
 constexpr uint32_t SCAN_STAGE = 2048;  // positions a stage of the long softmax
@@ -445,7 +397,7 @@ __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) 
   o += t7;
 }
 
-// With helpers (HELP): the products p_j * v_j[d] of a stage are formed by
+// The products p_j * v_j[d] of a stage are formed by
 // waves 1-3 one stage ahead, into a [dim][position] buffer (rows PV_PSTR
 // floats apart, so 16 lanes' 16-byte reads fall on distinct banks), and
 // wave 0's chain reads four positions' products per LDS read: an add and a
@@ -453,15 +405,14 @@ __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) 
 // multiply, an add and three quarters of a read. The V ring is then 96 KiB,
 // to leave room for the two product buffers.
 constexpr uint32_t PV_PSTR = PV_STP + 4;
-constexpr uint32_t PV_RING_HELP = 24576;
+constexpr uint32_t PV_RING_SHORT = 24576;
 // Above CX_ATT_LDS_MAX (the model's longer caches, scores from k_att_qk) the
 // ring is 80 KiB (5 stages), which leaves room for the scores of up to
 // CX_ATT_LONG_MAX positions.
 constexpr uint32_t PV_RING_LONG = 20480;
 constexpr uint32_t CML_MAX = 256;  // chunk maxima of one head: 16384 positions
-__host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap, uint32_t ds, bool help,
-                                                     uint32_t ring) {
-  return sc_lds(cap) + ring + (help ? 2 * ds * PV_PSTR : 0u);
+__host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap, uint32_t ds, uint32_t ring) {
+  return sc_lds(cap) + ring + 2 * ds * PV_PSTR;
 }
 
 // Waits until at most `later` stages' loads (IPW each) of this wave are
@@ -480,7 +431,7 @@ __device__ inline void wait_stages(uint32_t later) {
 // 256 threads: every wave streams its share of the V ring (4x the loads in
 // flight of one wave); wave 0's lanes run the order-exact accumulation.
 // Rows of the grid past HD / PV_DS are prefetch workgroups (pf).
-template <int HD, int SUB, uint32_t PV_DS, bool HELP, uint32_t RING>
+template <int HD, int SUB, uint32_t PV_DS, uint32_t RING>
 __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
                                                   const float* cm_all, uint32_t heads,
                                                   uint32_t kvh, const cx_dstate* st, uint32_t cap,
@@ -495,14 +446,13 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   float* ring = e + sc_lds(cap);
   __shared__ uint64_t etab[32];  // exp's table in LDS: no global load after the prefetch
   __shared__ float red[4];
-  __shared__ __align__(16) float cml[CML_MAX];  // the head's chunk maxima (one token)
-  // query token z (blockIdx.z) sits at position st->pos + z
-  // With one query token the workgroups of a (KV group, dims slice) pair
+  __shared__ __align__(16) float cml[CML_MAX];  // the head's chunk maxima
+  // The workgroups of a (KV group, dims slice) pair
   // take linear ids i, i + 8, i + 16, ...: workgroups are dispatched to the
   // 8 XCDs round-robin, so the heads of a group that read the same V slice
   // share one XCD's L2, and each V line is fetched from memory once.
   uint32_t h = blockIdx.x, y = blockIdx.y;
-  if (HELP) {
+  {
     constexpr uint32_t NY = HD / PV_DS;
     const uint32_t n = heads * NY, per = heads / kvh;
     if (n % 8 == 0) {
@@ -511,12 +461,10 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
       h = J / per / NY * per + J % per;
     }
   }
-  const uint32_t z = blockIdx.z, total = st->pos + z + 1, g = h / (heads / kvh);
+  const uint32_t total = st->pos + 1, g = h / (heads / kvh);
   using PS = PvShape<PV_DS, RING>;
   constexpr uint32_t PV_NST = PS::NST, PV_IPW = PS::IPW, PV_LPP = PS::LPP;
   const uint32_t d0 = y * PV_DS, kvd = kvh * HD;
-  sc_all += (size_t)z * heads * sc_stride(cap);
-  out += (size_t)z * heads * HD;
   const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
   // 1. the head's scores, then the first V stages, as untracked
   //    direct-to-LDS loads; a wave's loads complete in issue order, so
@@ -526,7 +474,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   //    whole cache (positions past the token's are loaded and never used),
   //    so that they are issued before the position state arrives.
   const uint32_t nckc = (cap + SC_P - 1) / SC_P;
-  if (HELP && w == 0) {  // lane t: chunks t, t + 64, ... (past the chunks: chunk 0)
+  if (w == 0) {  // lane t: chunks t, t + 64, ... (past the chunks: chunk 0)
     const float* crow = cm_all + (size_t)h * nckc;
     for (uint32_t i = 0; 64 * i < nckc; i++)
       cx_dma4_async(crow + (64 * i + t < nckc ? 64 * i + t : 0), cml + 64 * i);
@@ -560,250 +508,180 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   // and a V slice that fits the ring whole (early), waves 1-3 issue all of
   // it later, while wave 0 adds the exps, so no load issue delays the
   // softmax.
-  const bool early = HELP && nstage <= PV_NST;
+  const bool early = nstage <= PV_NST;
   cx_wait_vm<0>();
   if (!early)
     for (uint32_t s = 0; s < PV_NST && s < nstage; s++) issue(s);
   cx_wait_lds();
   cx_barrier();  // every wave's scores (and chunk maxima) and the exp table are in LDS
   float o = 0.0f;
-  if constexpr (HELP) {
-    // 2. softmax over positions [0, total): the maximum of the chunk maxima
-    //    (the same in every wave), e = exp(s - max) of the first 256
-    //    positions by every thread, then of the rest by waves 1-3 while
-    //    wave 0 adds the ones formed: the sum is the f32 sum in position
-    //    order from 0 (src/ops.rs:1211-1229), its first 256 adds one by one
-    //    and the rest by seq_sum_scan. The division by the sum is folded
-    //    into the products below.
-    float mx = -INFINITY;
-#pragma unroll
-    for (uint32_t i = 0; i < CML_MAX / 64; i++)
-      if (64 * i + t < nck) mx = fmaxf(mx, cml[64 * i + t]);
-    mx = cx_wave_max(mx);
-    const bool uniform = !isfinite(mx);  // all -inf, or a NaN (src/ops.rs:1214-1219)
-    const float pu = 1.0f / (float)total;
-    const uint32_t r64 = (total + 63) / 64 * 64;  // +0.0 from total to r64 (seq_sum_dpp)
-    if ((uint32_t)tid < total)
-      e[tid] = uniform ? pu : cx_expf_tab(e[tid] - mx, etab);
-    else if ((uint32_t)tid < r64)
-      e[tid] = 0.0f;
-    cx_wait_lds();
-    cx_barrier();
-    // early: the whole V slice, stage s into slot s, load i of a stage by
-    // wave 1 + i % 3
-    static_assert((PV_NST * PS::IPS + 2) / 3 <= 63, "a helper wave's share of the slice");
-    auto issue_all = [&]() {
-      for (uint32_t l = w - 1; l < nstage * PS::IPS; l += 3) {
-        const uint32_t s = l / PS::IPS, i = l % PS::IPS;
-        uint32_t p = s * PV_STP + i * (64 / PV_LPP) + t / PV_LPP;
-        if (p >= total) p = 0;
-        cx_dma16_async(reinterpret_cast<const uint8_t*>(vb + (size_t)p * kvd) + (t % PV_LPP) * 16,
-                       ring + s * (PV_STP * PV_DS) + i * 256);
-      }
-    };
-    float tot = 0.0f;
-    if (early) {
-      // the V slice fits the ring: waves 1-3 form every other exp at once
-      // while wave 0 adds the first 256, then issue all of V while it adds
-      // the rest
-      if (w != 0) {
-        for (uint32_t p = 256 + tid - 64; p < r64; p += 192)
-          e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
-        if (total <= 256) issue_all();
-      } else if (!uniform) {
-        tot = seq_sum_scan(e, min(total, 256u), 0.0f, true);
-      }
-      if (total > 256) {
-        cx_wait_lds();
-        cx_barrier();  // the rest of the exps are in LDS
-        if (w != 0) issue_all();
-        if (w == 0 && !uniform) tot = seq_sum_scan(e + 256, total - 256, tot, false);
-      }
-    } else {
-      // a longer cache (V streams through the ring later): stages of
-      // SCAN_STAGE positions, the first stage's exps by every thread, then
-      // waves 1-3 forming stage s + 1's while wave 0 adds stage s's
-      for (uint32_t p = 256 + tid; p < min(SCAN_STAGE, r64); p += 256)
-        e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
-      cx_wait_lds();
-      cx_barrier();
-      const uint32_t nss = (total + SCAN_STAGE - 1) / SCAN_STAGE;
-      for (uint32_t s = 0; s < nss; s++) {
-        if (w != 0) {
-          const uint32_t b = SCAN_STAGE * (s + 1), end = min(b + SCAN_STAGE, r64);
-          for (uint32_t p = b + tid - 64; p < end; p += 192)
-            e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
-        } else if (!uniform) {
-          tot = seq_sum_scan(e + SCAN_STAGE * s, min(SCAN_STAGE, total - SCAN_STAGE * s), tot, s == 0);
-        }
-        if (s + 1 < nss) {
-          cx_wait_lds();
-          cx_barrier();  // stage s + 1's exps are in LDS
-        }
-      }
-    }
-    if (tid == 15) red[0] = 1.0f / tot;
-    cx_wait_lds();
-    cx_barrier();
-    const float inv = red[0];
-    // 3. out[d0 + t] over the V ring, position order (wave 0)
-    float* prod = ring + PV_NST * PV_STP * PV_DS;  // two buffers of PV_DS * PV_PSTR
-    // helper waves: stage s's products p_j * v_j[d], p_j = e_j * (1/sum) (or
-    // 1/total when uniform), into buffer s % 2, [dim][position]; task k is
-    // dims 4 (k % DQ) .. +3 and positions 8 (k / DQ) .. +7
-    auto make = [&](uint32_t s) {
-      constexpr uint32_t DQ = PV_DS / 4, NT = DQ * (PV_STP / 8);
-      const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS);
-      const float* ps = e + s * PV_STP;
-      float* pb = prod + (s & 1) * (PV_DS * PV_PSTR);
-      for (uint32_t k = tid - 64; k < NT; k += 192) {
-        const uint32_t dq = k % DQ, pq = k / DQ;
-        const float4 e0 = *reinterpret_cast<const float4*>(ps + 8 * pq);
-        const float4 e1 = *reinterpret_cast<const float4*>(ps + 8 * pq + 4);
-        float4 vv[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-          vv[i] = *reinterpret_cast<const float4*>(vs + (8 * pq + i) * PV_DS + 4 * dq);
-        __builtin_amdgcn_sched_barrier(0);  // every read in flight before the first use
-        float pp[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-        if (!uniform)
-#pragma unroll
-          for (int i = 0; i < 8; i++) pp[i] = pp[i] * inv;
-        float r[4][8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float4 v = vv[i];
-          r[0][i] = pp[i] * v.x;
-          r[1][i] = pp[i] * v.y;
-          r[2][i] = pp[i] * v.z;
-          r[3][i] = pp[i] * v.w;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          float* row = pb + (4 * dq + j) * PV_PSTR + 8 * pq;
-          *reinterpret_cast<float4*>(row) = make_float4(r[j][0], r[j][1], r[j][2], r[j][3]);
-          *reinterpret_cast<float4*>(row + 4) = make_float4(r[j][4], r[j][5], r[j][6], r[j][7]);
-        }
-      }
-    };
-    // stages issued so far: [0, min(NST, nstage)); each iteration s issues
-    // stage s + NST into the slot of stage s, whose products are made
-    auto issued_end = [&](uint32_t s) { return min(s + PV_NST, nstage); };
-    if (early)
-      cx_wait_vm<0>();  // the whole slice has landed (wave 0 issued none)
-    else
-      wait_stages<PV_IPW, PV_NST - 1>(issued_end(0) - 1);  // stage 0 has landed
-    cx_barrier();
-    if (w != 0) make(0);
-    for (uint32_t s = 0; s < nstage; s++) {
-      if (!early && s + 1 < nstage) wait_stages<PV_IPW, PV_NST - 1>(issued_end(s) - (s + 2));
-      cx_wait_lds();
-      cx_barrier();  // stage s's products are made; stage s + 1 has landed
-      // stage s's slot is no longer read: refill it (wave 0 after its chain,
-      // which the barrier starts)
-      if (w != 0 && s + PV_NST < nstage) issue(s + PV_NST);
-      if (w == 0) {
-        if (t < (int)PV_DS) {
-          const float* pr = prod + (s & 1) * (PV_DS * PV_PSTR) + t * PV_PSTR;
-          if ((s + 1) * PV_STP <= total) {
-            // 32 positions a batch, the next batch's reads ahead of the adds
-            const float4* p4 = reinterpret_cast<const float4*>(pr);
-            float4 a[8], b[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) a[i] = p4[i];
-#pragma unroll
-            for (int i = 0; i < 8; i++) b[i] = p4[8 + i];
-            __builtin_amdgcn_sched_barrier(0);
-            add32(o, a);
-#pragma unroll
-            for (int i = 0; i < 8; i++) a[i] = p4[16 + i];
-            __builtin_amdgcn_sched_barrier(0);
-            add32(o, b);
-#pragma unroll
-            for (int i = 0; i < 8; i++) b[i] = p4[24 + i];
-            __builtin_amdgcn_sched_barrier(0);
-            add32(o, a);
-            add32(o, b);
-          } else {
-            for (uint32_t j = 0; s * PV_STP + j < total; j++) o += pr[j];
-          }
-        }
-        if (s + PV_NST < nstage) issue(s + PV_NST);
-      } else if (s + 1 < nstage) {
-        make(s + 1);
-      }
-    }
-    cx_wait_lds();
-    cx_barrier();  // every read of the ring and the products is done
-  } else {
-  // 2. softmax over positions [0, total)
+  // 2. softmax over positions [0, total): the maximum of the chunk maxima
+  //    (the same in every wave), e = exp(s - max) of the first 256
+  //    positions by every thread, then of the rest by waves 1-3 while
+  //    wave 0 adds the ones formed: the sum is the f32 sum in position
+  //    order from 0 (src/ops.rs:1211-1229), its first 256 adds one by one
+  //    and the rest by seq_sum_scan. The division by the sum is folded
+  //    into the products below.
   float mx = -INFINITY;
-  for (uint32_t p = tid; p < total; p += 256) mx = fmaxf(mx, e[p]);
+#pragma unroll
+  for (uint32_t i = 0; i < CML_MAX / 64; i++)
+    if (64 * i + t < nck) mx = fmaxf(mx, cml[64 * i + t]);
   mx = cx_wave_max(mx);
-  if (t == 0) red[w] = mx;
-  cx_wait_lds();
-  cx_barrier();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const bool uniform = !isfinite(mx);  // all -inf, or a NaN (src/ops.rs:1214-1219)
-  for (uint32_t p = tid; p < total; p += 256)
-    e[p] = uniform ? 1.0f / (float)total : cx_expf_tab(e[p] - mx, etab);
+  const float pu = 1.0f / (float)total;
+  const uint32_t r64 = (total + 63) / 64 * 64;  // +0.0 from total to r64 (seq_sum_dpp)
+  if ((uint32_t)tid < total)
+    e[tid] = uniform ? pu : cx_expf_tab(e[tid] - mx, etab);
+  else if ((uint32_t)tid < r64)
+    e[tid] = 0.0f;
   cx_wait_lds();
   cx_barrier();
-  if (!uniform) {
-    if (tid == 0) red[0] = 1.0f / seq_sum_lds(e, total);
+  // early: the whole V slice, stage s into slot s, load i of a stage by
+  // wave 1 + i % 3
+  static_assert((PV_NST * PS::IPS + 2) / 3 <= 63, "a helper wave's share of the slice");
+  auto issue_all = [&]() {
+    for (uint32_t l = w - 1; l < nstage * PS::IPS; l += 3) {
+      const uint32_t s = l / PS::IPS, i = l % PS::IPS;
+      uint32_t p = s * PV_STP + i * (64 / PV_LPP) + t / PV_LPP;
+      if (p >= total) p = 0;
+      cx_dma16_async(reinterpret_cast<const uint8_t*>(vb + (size_t)p * kvd) + (t % PV_LPP) * 16,
+                     ring + s * (PV_STP * PV_DS) + i * 256);
+    }
+  };
+  float tot = 0.0f;
+  if (early) {
+    // the V slice fits the ring: waves 1-3 form every other exp at once
+    // while wave 0 adds the first 256, then issue all of V while it adds
+    // the rest
+    if (w != 0) {
+      for (uint32_t p = 256 + tid - 64; p < r64; p += 192)
+        e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
+      if (total <= 256) issue_all();
+    } else if (!uniform) {
+      tot = seq_sum_scan(e, min(total, 256u), 0.0f, true);
+    }
+    if (total > 256) {
+      cx_wait_lds();
+      cx_barrier();  // the rest of the exps are in LDS
+      if (w != 0) issue_all();
+      if (w == 0 && !uniform) tot = seq_sum_scan(e + 256, total - 256, tot, false);
+    }
+  } else {
+    // a longer cache (V streams through the ring later): stages of
+    // SCAN_STAGE positions, the first stage's exps by every thread, then
+    // waves 1-3 forming stage s + 1's while wave 0 adds stage s's
+    for (uint32_t p = 256 + tid; p < min(SCAN_STAGE, r64); p += 256)
+      e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
     cx_wait_lds();
     cx_barrier();
-    const float inv = red[0];
-    for (uint32_t p = tid; p < total; p += 256) e[p] = e[p] * inv;
-    cx_wait_lds();
-    cx_barrier();
-  }
-  // 3. out[d0 + t] over the V ring, position order (wave 0)
-  for (uint32_t s = 0; s < nstage; s++) {
-    if (s + PV_NST <= nstage)
-      cx_wait_vm<(PV_NST - 1) * PV_IPW>();
-    else
-      cx_wait_vm<0>();
-    cx_barrier();  // stage s has landed, from every wave
-    if (w == 0 && t < (int)PV_DS) {
-      const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS) + t;
-      const float* ps = e + s * PV_STP;
-      if ((s + 1) * PV_STP <= total) {
-        // batches of 32 positions, two register buffers: a batch's LDS
-        // reads are issued before the previous batch's arithmetic, so their
-        // latency hides behind 32 adds
-        const float4* p4 = reinterpret_cast<const float4*>(ps);
-        float va[32], vb[32];
-        float4 pa[8], pb[8];
-        auto fetch = [&](float (&v)[32], float4 (&pp)[8], int b) {
-#pragma unroll
-          for (int j = 0; j < 32; j++) v[j] = vs[(32 * b + j) * PV_DS];
-#pragma unroll
-          for (int i = 0; i < 8; i++) pp[i] = p4[8 * b + i];
-        };
-        auto apply = [&](const float (&v)[32], const float4 (&pp)[8]) {
-#pragma unroll
-          for (int q = 0; q < 4; q++) pv8(o, *reinterpret_cast<const float4(*)[2]>(pp + 2 * q),
-                                          *reinterpret_cast<const float(*)[8]>(v + 8 * q));
-        };
-        static_assert(PV_STP == 128, "four batches of 32 a stage");
-        fetch(va, pa, 0);
-        fetch(vb, pb, 1);
-        apply(va, pa);
-        fetch(va, pa, 2);
-        apply(vb, pb);
-        fetch(vb, pb, 3);
-        apply(va, pa);
-        apply(vb, pb);
-      } else {
-        for (uint32_t j = 0; s * PV_STP + j < total; j++) o += ps[j] * vs[j * PV_DS];
+    const uint32_t nss = (total + SCAN_STAGE - 1) / SCAN_STAGE;
+    for (uint32_t s = 0; s < nss; s++) {
+      if (w != 0) {
+        const uint32_t b = SCAN_STAGE * (s + 1), end = min(b + SCAN_STAGE, r64);
+        for (uint32_t p = b + tid - 64; p < end; p += 192)
+          e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
+      } else if (!uniform) {
+        tot = seq_sum_scan(e + SCAN_STAGE * s, min(SCAN_STAGE, total - SCAN_STAGE * s), tot, s == 0);
+      }
+      if (s + 1 < nss) {
+        cx_wait_lds();
+        cx_barrier();  // stage s + 1's exps are in LDS
       }
     }
+  }
+  if (tid == 15) red[0] = 1.0f / tot;
+  cx_wait_lds();
+  cx_barrier();
+  const float inv = red[0];
+  // 3. out[d0 + t] over the V ring, position order (wave 0)
+  float* prod = ring + PV_NST * PV_STP * PV_DS;  // two buffers of PV_DS * PV_PSTR
+  // helper waves: stage s's products p_j * v_j[d], p_j = e_j * (1/sum) (or
+  // 1/total when uniform), into buffer s % 2, [dim][position]; task k is
+  // dims 4 (k % DQ) .. +3 and positions 8 (k / DQ) .. +7
+  auto make = [&](uint32_t s) {
+    constexpr uint32_t DQ = PV_DS / 4, NT = DQ * (PV_STP / 8);
+    const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS);
+    const float* ps = e + s * PV_STP;
+    float* pb = prod + (s & 1) * (PV_DS * PV_PSTR);
+    for (uint32_t k = tid - 64; k < NT; k += 192) {
+      const uint32_t dq = k % DQ, pq = k / DQ;
+      const float4 e0 = *reinterpret_cast<const float4*>(ps + 8 * pq);
+      const float4 e1 = *reinterpret_cast<const float4*>(ps + 8 * pq + 4);
+      float4 vv[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        vv[i] = *reinterpret_cast<const float4*>(vs + (8 * pq + i) * PV_DS + 4 * dq);
+      __builtin_amdgcn_sched_barrier(0);  // every read in flight before the first use
+      float pp[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+      if (!uniform)
+#pragma unroll
+        for (int i = 0; i < 8; i++) pp[i] = pp[i] * inv;
+      float r[4][8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float4 v = vv[i];
+        r[0][i] = pp[i] * v.x;
+        r[1][i] = pp[i] * v.y;
+        r[2][i] = pp[i] * v.z;
+        r[3][i] = pp[i] * v.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float* row = pb + (4 * dq + j) * PV_PSTR + 8 * pq;
+        *reinterpret_cast<float4*>(row) = make_float4(r[j][0], r[j][1], r[j][2], r[j][3]);
+        *reinterpret_cast<float4*>(row + 4) = make_float4(r[j][4], r[j][5], r[j][6], r[j][7]);
+      }
+    }
+  };
+  // stages issued so far: [0, min(NST, nstage)); each iteration s issues
+  // stage s + NST into the slot of stage s, whose products are made
+  auto issued_end = [&](uint32_t s) { return min(s + PV_NST, nstage); };
+  if (early)
+    cx_wait_vm<0>();  // the whole slice has landed (wave 0 issued none)
+  else
+    wait_stages<PV_IPW, PV_NST - 1>(issued_end(0) - 1);  // stage 0 has landed
+  cx_barrier();
+  if (w != 0) make(0);
+  for (uint32_t s = 0; s < nstage; s++) {
+    if (!early && s + 1 < nstage) wait_stages<PV_IPW, PV_NST - 1>(issued_end(s) - (s + 2));
     cx_wait_lds();
-    cx_barrier();  // the slot is read: refill it
-    if (s + PV_NST < nstage) issue(s + PV_NST);
+    cx_barrier();  // stage s's products are made; stage s + 1 has landed
+    // stage s's slot is no longer read: refill it (wave 0 after its chain,
+    // which the barrier starts)
+    if (w != 0 && s + PV_NST < nstage) issue(s + PV_NST);
+    if (w == 0) {
+      if (t < (int)PV_DS) {
+        const float* pr = prod + (s & 1) * (PV_DS * PV_PSTR) + t * PV_PSTR;
+        if ((s + 1) * PV_STP <= total) {
+          // 32 positions a batch, the next batch's reads ahead of the adds
+          const float4* p4 = reinterpret_cast<const float4*>(pr);
+          float4 a[8], b[8];
+#pragma unroll
+          for (int i = 0; i < 8; i++) a[i] = p4[i];
+#pragma unroll
+          for (int i = 0; i < 8; i++) b[i] = p4[8 + i];
+          __builtin_amdgcn_sched_barrier(0);
+          add32(o, a);
+#pragma unroll
+          for (int i = 0; i < 8; i++) a[i] = p4[16 + i];
+          __builtin_amdgcn_sched_barrier(0);
+          add32(o, b);
+#pragma unroll
+          for (int i = 0; i < 8; i++) b[i] = p4[24 + i];
+          __builtin_amdgcn_sched_barrier(0);
+          add32(o, a);
+          add32(o, b);
+        } else {
+          for (uint32_t j = 0; s * PV_STP + j < total; j++) o += pr[j];
+        }
+      }
+      if (s + PV_NST < nstage) issue(s + PV_NST);
+    } else if (s + 1 < nstage) {
+      make(s + 1);
+    }
   }
-  }
+  cx_wait_lds();
+  cx_barrier();  // every read of the ring and the products is done
   if (w != 0 || t >= (int)PV_DS) return;
   out[h * HD + d0 + t] = o;
   if (!xq) return;
@@ -816,6 +694,184 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     for (int j = 0; j < 8; j++) v[j] = os[8 * t + j];
     cx_quant8<SUB>(v, (size_t)h * HD + d0 + 8 * t, xq, xe, xs);
   }
+}
+
+// ------------------------------------ order-exact attention, many queries
+// The batched prefill's attention (several query tokens; q rotated and the
+// caches filled by the chunk's rope/KV launch) in the reference's order:
+// every query token's scores, softmax and P·V exactly as k_attn_scores and
+// k_attn_seq form them for one, but MT_Q tokens a workgroup, one a wave.
+// The K chunk (scores) or the V stages (softmax-V) are loaded once for the
+// MT_Q tokens, and their chains run at once, one per SIMD.
+constexpr uint32_t MT_Q = 4;
+
+// k_attn_scores_mt, one workgroup per (64 positions, head h, MT_Q tokens):
+// the chunk's K rows into LDS (rows padded by 16 bytes against bank
+// conflicts) and the tokens' q rows; wave w's lane t forms token
+// (MT_Q zg + w)'s score at position p0 + t, the sequential dot of
+// src/kernels/scalar.rs:16-23 times 1/sqrt(hd), where the token sees it.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_scores_mt(const float* q, const float* kc,
+                                                       uint32_t heads, uint32_t kvh,
+                                                       const cx_dstate* st, float scale, float* sc,
+                                                       uint32_t cap, uint32_t T) {
+  constexpr uint32_t ROWB = HD * 4, PADB = ROWB + 16, PADF = PADB / 4;
+  constexpr uint32_t NCH = (SC_P * PADB + 1023) / 1024;
+  extern __shared__ __align__(16) uint8_t sm[];
+  const float* kl = reinterpret_cast<const float*>(sm);
+  float* qs = reinterpret_cast<float*>(sm + NCH * 1024);  // MT_Q rows of HD
+  const uint32_t chunk = blockIdx.x, h = blockIdx.y, z0 = blockIdx.z * MT_Q;
+  const uint32_t pos = st->pos, p0 = chunk * SC_P, zn = min(MT_Q, T - z0);
+  const uint32_t tmax = pos + z0 + zn;  // the largest count of positions a token sees
+  if (p0 >= tmax) return;
+  const uint32_t np = min(SC_P, tmax - p0), g = h / (heads / kvh), kvd = kvh * HD;
+  const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
+  asm volatile("" ::"s"(scale));  // read with the arguments, not by the dots
+  const float* kb = kc + (size_t)p0 * kvd + g * HD;
+  for (uint32_t c = w; c < NCH; c += 4) {
+    const uint32_t o = c * 1024 + 16 * t;
+    uint32_t r = o / PADB, b = o % PADB;
+    if (r >= np || b >= ROWB) r = 0, b = 0;  // a valid dummy, never read
+    cx_dma16(reinterpret_cast<const uint8_t*>(kb + (size_t)r * kvd) + b, sm + c * 1024);
+  }
+  for (uint32_t j = tid; j < zn * HD; j += 256)
+    qs[j] = q[((size_t)(z0 + j / HD) * heads + h) * HD + j % HD];
+  cx_wait_vm<0>();
+  __syncthreads();
+  if ((uint32_t)w >= zn) return;
+  const uint32_t z = z0 + w, total = pos + z + 1;
+  if (p0 + t < total && (uint32_t)t < np) {
+    const float s = cx_dot_seq<HD / 4>(reinterpret_cast<const float4*>(qs + w * HD),
+                                       reinterpret_cast<const float4*>(kl + t * PADF));
+    sc[((size_t)z * heads + h) * sc_stride(cap) + p0 + t] = s * scale;
+  }
+}
+
+// k_attn_seq_mt, one workgroup per (head h, MT_DS head dims, MT_Q tokens):
+// wave w takes token z = MT_Q zg + w and its total = pos + z + 1 positions.
+// Its scores row into LDS; the softmax in the reference's order (exact
+// max; e = exp(s - max), glibc's expf; the sum in position order from 0,
+// its first 256 adds one by one and the rest by binade scan; p = e * (1/sum);
+// a max that is not finite gives 1/total: src/ops.rs:1211-1229); then lane
+// t accumulates out[d0 + t] = sum over positions of p * v[d0 + t] in
+// position order (src/ops.rs:1316-1321). The V slice streams through a ring
+// of MT_NST stages of MT_STP positions, each loaded a quarter by each wave
+// and read by every wave's chain.
+constexpr uint32_t MT_DS = 64, MT_STP = 64, MT_NST = 4;  // a 64 KiB ring
+constexpr uint32_t MT_SLOT = MT_STP * MT_DS;             // floats a stage
+__host__ __device__ constexpr uint32_t mt_lds_floats(uint32_t cap) {
+  return MT_Q * sc_lds(cap) + MT_NST * MT_SLOT;
+}
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_seq_mt(const float* vc, const float* sc_all,
+                                                    uint32_t heads, uint32_t kvh,
+                                                    const cx_dstate* st, uint32_t cap, uint32_t T,
+                                                    float* out) {
+  constexpr uint32_t IPW = MT_SLOT * 4 / 1024 / 4;  // 1 KiB loads a stage, per wave
+  constexpr uint32_t LPP = MT_DS / 4;                // lanes per position in a load
+  static_assert(IPW >= 1 && 4 + MT_NST * IPW <= 63, "loads a wave keeps in flight");
+  extern __shared__ __align__(16) float e[];  // MT_Q scores rows of sc_lds(cap), then the ring
+  __shared__ uint64_t etab[32];
+  const uint32_t scl = sc_lds(cap);
+  float* ring = e + MT_Q * scl;
+  const uint32_t h = blockIdx.x, d0 = blockIdx.y * MT_DS, z0 = blockIdx.z * MT_Q;
+  const uint32_t zn = min(MT_Q, T - z0), pos = st->pos, tmax = pos + z0 + zn;
+  const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
+  const uint32_t g = h / (heads / kvh), kvd = kvh * HD;
+  const bool mine = (uint32_t)w < zn;  // this wave has a token
+  const uint32_t z = z0 + w, total = pos + z + 1;
+  float* ew = e + w * scl;
+  // 1. the token's scores (whole 1 KiB loads over the cache), then the
+  //    first MT_NST stages of V (positions past tmax load position 0 and
+  //    are never read): a wave's loads complete in issue order, so waiting
+  //    for all but its V loads waits for its scores
+  if (mine) {
+    const float* srow = sc_all + ((size_t)z * heads + h) * sc_stride(cap);
+    for (uint32_t c = 0; c * 256 < cap; c++) {
+      const uint32_t i = c * 256 + 4 * t;
+      cx_dma16_async(srow + (i < cap ? i : 0), ew + c * 256);
+    }
+  }
+  const float* vb = vc + g * HD + d0;
+  auto issue = [&](uint32_t s) {  // wave w's loads of stage s: 4 positions each
+    float* dst = ring + (s % MT_NST) * MT_SLOT;
+    for (uint32_t j = 0; j < IPW; j++) {
+      const uint32_t i = w + 4 * j;
+      uint32_t p = s * MT_STP + i * (64 / LPP) + t / LPP;
+      if (p >= tmax) p = 0;
+      cx_dma16_async(reinterpret_cast<const uint8_t*>(vb + (size_t)p * kvd) + (t % LPP) * 16,
+                     dst + i * 256);
+    }
+  };
+  for (uint32_t s = 0; s < MT_NST; s++) issue(s);
+  if (tid == 0) {
+    const uint64_t tab[32] = CX_EXP2_TAB;
+    for (int i = 0; i < 32; i++) etab[i] = tab[i];
+  }
+  cx_wait_vm<MT_NST * IPW>();
+  cx_wait_lds();
+  cx_barrier();  // the scores and the exp table are in LDS
+  float o = 0.0f;
+  if (mine) {
+    // 2. the softmax of this token's row (one wave; its LDS accesses are in order)
+    float mx = -INFINITY;
+    for (uint32_t p = t; p < total; p += 64) mx = fmaxf(mx, ew[p]);
+    mx = cx_wave_max(mx);
+    const bool uniform = !isfinite(mx);  // all -inf, or a NaN (src/ops.rs:1214-1219)
+    const float pu = 1.0f / (float)total;
+    const uint32_t r64 = (total + 63) / 64 * 64;  // +0.0 from total to r64 (the scan's head)
+    for (uint32_t p = t; p < r64; p += 64)
+      ew[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(ew[p] - mx, etab);
+    if (!uniform) {
+      const float inv = 1.0f / seq_sum_scan(ew, total, 0.0f, true);
+      for (uint32_t p = t; p < total; p += 64) ew[p] = ew[p] * inv;
+    }
+  }
+  // 3. P·V, stage s in slot s % MT_NST; MT_NST stages were issued, and
+  //    stage s + MT_NST is issued once stage s is read
+  const uint32_t nstage = (tmax + MT_STP - 1) / MT_STP;
+  const uint32_t refills = nstage > MT_NST ? nstage - MT_NST : 0u;
+  for (uint32_t s = 0; s < nstage; s++) {
+    const uint32_t issued = MT_NST + min(s, refills);
+    wait_stages<IPW, MT_NST - 1>(issued - s - 1);
+    cx_wait_lds();
+    cx_barrier();  // stage s has landed, from every wave
+    if (mine && s * MT_STP < total) {
+      const float* vs = ring + (s % MT_NST) * MT_SLOT + t;
+      const float* ps = ew + s * MT_STP;
+      if ((s + 1) * MT_STP <= total) {
+        // two batches of 32 positions: the second's reads are issued before
+        // the first's arithmetic
+        const float4* p4 = reinterpret_cast<const float4*>(ps);
+        float va[32], vb2[32];
+        float4 pa[8], pb[8];
+#pragma unroll
+        for (int j = 0; j < 32; j++) va[j] = vs[j * MT_DS];
+#pragma unroll
+        for (int i = 0; i < 8; i++) pa[i] = p4[i];
+#pragma unroll
+        for (int j = 0; j < 32; j++) vb2[j] = vs[(32 + j) * MT_DS];
+#pragma unroll
+        for (int i = 0; i < 8; i++) pb[i] = p4[8 + i];
+        static_assert(MT_STP == 64, "two batches of 32 a stage");
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          pv8(o, *reinterpret_cast<const float4(*)[2]>(pa + 2 * k),
+              *reinterpret_cast<const float(*)[8]>(va + 8 * k));
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          pv8(o, *reinterpret_cast<const float4(*)[2]>(pb + 2 * k),
+              *reinterpret_cast<const float(*)[8]>(vb2 + 8 * k));
+      } else {
+        for (uint32_t j = 0; s * MT_STP + j < total; j++) o += ps[j] * vs[j * MT_DS];
+      }
+    }
+    cx_wait_lds();
+    cx_barrier();  // every chain has read the slot: refill it
+    if (s + MT_NST < nstage) issue(s + MT_NST);
+  }
+  cx_wait_vm<0>();  // the loads of stages past the last one have landed
+  if (mine) out[((size_t)z * heads + h) * HD + d0 + t] = o;
 }
 
 // -------------------------------------------------------------- softmax
@@ -1030,16 +1086,16 @@ namespace {
 // a workgroup (a ring of RING floats), plus rows of prefetch workgroups.
 template <int HD, uint32_t RING>
 int launch_seq_one(const cx_attn_args& a, hipStream_t s) {
-  const size_t lds = pv_lds_floats(a.cap, 32, true, RING) * sizeof(float);
+  const size_t lds = pv_lds_floats(a.cap, 32, RING) * sizeof(float);
   CX_REQUIRE(lds <= 158 * 1024 && (a.cap + SC_P - 1) / SC_P <= CML_MAX,
              "attention: %u cached positions need %zu bytes of LDS", a.cap, lds);
   const uint32_t rows = HD / 32, np = cx_l2_prefetch_groups(a.pf, a.heads * rows);
   const dim3 grid(a.heads, rows + (np + a.heads - 1) / a.heads, 1);
   if (a.sub == 16)
-    hipLaunchKernelGGL((k_attn_seq<HD, 16, 32, true, RING>), grid, dim3(256), lds, s, a.vc, a.sc,
+    hipLaunchKernelGGL((k_attn_seq<HD, 16, 32, RING>), grid, dim3(256), lds, s, a.vc, a.sc,
                        a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   else
-    hipLaunchKernelGGL((k_attn_seq<HD, 32, 32, true, RING>), grid, dim3(256), lds, s, a.vc, a.sc,
+    hipLaunchKernelGGL((k_attn_seq<HD, 32, 32, RING>), grid, dim3(256), lds, s, a.vc, a.sc,
                        a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   CX_HIP(hipGetLastError());
   return CX_OK;
@@ -1049,21 +1105,26 @@ template <int HD>
 int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
   constexpr size_t sc_bytes = (SC_P * (HD * 4 + 16) + 1023) / 1024 * 1024 + 2 * HD * 4;
   const uint32_t T = a.tokens ? a.tokens : 1;
-  CX_REQUIRE(a.cm, "attention: the chunk maxima buffer");
-  hipLaunchKernelGGL(k_attn_scores<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads, T), dim3(256),
-                     sc_bytes, s, a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads,
-                     a.kvh, a.st, scale, a.sc, a.cm, a.cap);
-  CX_HIP(hipGetLastError());
-  if (T > 1) {  // many query tokens: 64 dims a workgroup, f32 output only
-    const size_t lds = pv_lds_floats(a.cap, 64, false, 32768) * sizeof(float);
-    const dim3 grid(a.heads, HD / 64, T);
-    hipLaunchKernelGGL((k_attn_seq<HD, 32, 64, false, 32768>), grid, dim3(256), lds, s, a.vc,
-                       a.sc, a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs,
-                       cx_l2_prefetch{});
+  if (T > 1) {  // many query tokens: MT_Q a workgroup, f32 output only
+    const uint32_t G = (T + MT_Q - 1) / MT_Q;
+    constexpr size_t sc_mt = (SC_P * (HD * 4 + 16) + 1023) / 1024 * 1024 + MT_Q * HD * 4;
+    hipLaunchKernelGGL(k_attn_scores_mt<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads, G),
+                       dim3(256), sc_mt, s, a.q, a.kc, a.heads, a.kvh, a.st, scale, a.sc, a.cap, T);
+    CX_HIP(hipGetLastError());
+    const size_t lds = mt_lds_floats(a.cap) * sizeof(float);
+    CX_REQUIRE(lds <= 158 * 1024, "attention: %u cached positions need %zu bytes of LDS", a.cap,
+               lds);
+    hipLaunchKernelGGL(k_attn_seq_mt<HD>, dim3(a.heads, HD / MT_DS, G), dim3(256), lds, s, a.vc,
+                       a.sc, a.heads, a.kvh, a.st, a.cap, T, a.out);
     CX_HIP(hipGetLastError());
     return CX_OK;
   }
-  return launch_seq_one<HD, PV_RING_HELP>(a, s);  // one token: 32 dims a workgroup
+  CX_REQUIRE(a.cm, "attention: the chunk maxima buffer");
+  hipLaunchKernelGGL(k_attn_scores<HD>, dim3((a.cap + SC_P - 1) / SC_P, a.heads), dim3(256),
+                     sc_bytes, s, a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads,
+                     a.kvh, a.st, scale, a.sc, a.cm, a.cap);
+  CX_HIP(hipGetLastError());
+  return launch_seq_one<HD, PV_RING_SHORT>(a, s);  // one token: 32 dims a workgroup
 }
 
 // One query token over a longer cache: the scores of all heads of a KV group
