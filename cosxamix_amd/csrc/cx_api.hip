@@ -1479,6 +1479,26 @@ static int prefill_matmul(cx_cache* C, int type, const uint8_t* w, uint32_t n, u
   return CX_OK;
 }
 
+// prefill_matmul of `count` matrices over one input (q/k/v, gate/up): on the
+// MFMA contraction one launch for all of them when their types agree
+static int prefill_matmuls(cx_cache* C, const int* type, const uint8_t* const* w,
+                           const uint32_t* n, uint32_t count, uint32_t k, const float* in,
+                           uint32_t rows, float* const* out, int* quantized) {
+  bool same = true;
+  for (uint32_t i = 1; i < count; i++) same = same && type[i] == type[0];
+  if (same && cx_gemm_supported(type[0])) {
+    const int sub = cx_sub(type[0]);
+    int rc;
+    if (*quantized != sub && (rc = cx_gemm_quantize(in, rows, k, sub, C->pf.scratch, C->m->stream)))
+      return rc;
+    *quantized = sub;
+    return cx_gemm_apply_multi(type[0], w, n, count, k, rows, out, C->pf.scratch, C->m->stream);
+  }
+  for (uint32_t i = 0; i < count; i++)
+    if (int rc = prefill_matmul(C, type[i], w[i], n[i], k, in, rows, out[i], quantized)) return rc;
+  return CX_OK;
+}
+
 // tokens at positions [st->pos, st->pos + nt), already in hist: the layers
 static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
   cx_model* m = C->m;
@@ -1494,11 +1514,15 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
     float* vc = kc + C->cap * kvd;
     // src/forward.rs:422-464
     int qd = 0;
-    if ((rc = cx_launch_norm_rows(P.x, L.attn_norm, nt, D, c.eps, P.nrm, s)) ||
-        (rc = prefill_matmul(C, L.t_q, L.q, D, D, P.nrm, nt, P.q, &qd)) ||
-        (rc = prefill_matmul(C, L.t_k, L.k, kvd, D, P.nrm, nt, P.k, &qd)) ||
-        (rc = prefill_matmul(C, L.t_v, L.v, kvd, D, P.nrm, nt, P.v, &qd)))
-      return rc;
+    {
+      const int t[3] = {L.t_q, L.t_k, L.t_v};
+      const uint8_t* w[3] = {L.q, L.k, L.v};
+      const uint32_t n[3] = {D, kvd, kvd};
+      float* o[3] = {P.q, P.k, P.v};
+      if ((rc = cx_launch_norm_rows(P.x, L.attn_norm, nt, D, c.eps, P.nrm, s)) ||
+          (rc = prefill_matmuls(C, t, w, n, 3, D, P.nrm, nt, o, &qd)))
+        return rc;
+    }
     if ((L.q_bias && (rc = cx_launch_add_rows(P.q, L.q_bias, nt, D, 1, s))) ||
         (L.k_bias && (rc = cx_launch_add_rows(P.k, L.k_bias, nt, kvd, 1, s))) ||
         (L.v_bias && (rc = cx_launch_add_rows(P.v, L.v_bias, nt, kvd, 1, s))))
@@ -1527,10 +1551,15 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
         (rc = cx_launch_norm_rows(P.x, L.ffn_norm, nt, D, c.eps, P.nrm, s)))
       return rc;
     qd = 0;
-    if ((rc = prefill_matmul(C, L.t_gate, L.gate, I, D, P.nrm, nt, P.g, &qd)) ||
-        (rc = prefill_matmul(C, L.t_up, L.up, I, D, P.nrm, nt, P.u, &qd)) ||
-        (rc = cx_launch_swiglu_rows(P.g, P.u, (size_t)nt * I, P.nrm, s)))
-      return rc;
+    {
+      const int t[2] = {L.t_gate, L.t_up};
+      const uint8_t* w[2] = {L.gate, L.up};
+      const uint32_t n[2] = {I, I};
+      float* o[2] = {P.g, P.u};
+      if ((rc = prefill_matmuls(C, t, w, n, 2, D, P.nrm, nt, o, &qd)) ||
+          (rc = cx_launch_swiglu_rows(P.g, P.u, (size_t)nt * I, P.nrm, s)))
+        return rc;
+    }
     qd = 0;
     if ((rc = prefill_matmul(C, L.t_down, L.down, D, I, P.nrm, nt, P.tmp, &qd)) ||
         (rc = cx_launch_add_rows(P.x, P.tmp, nt, D, nt, s)))

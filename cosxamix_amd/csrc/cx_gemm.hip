@@ -103,6 +103,13 @@ struct GemmParams {
   uint32_t n, k, m, m_pad, nb, row_bytes, row_tiles, act_tiles;
   const float* lhs;     // m x k f32: the quantizer's input (not read by k_gemm)
   uint8_t* scratch;     // where xq and xexs are carved (not read by k_gemm)
+  // k_gemm only: with nseg > 1 the n rows are nseg matrices of one type and
+  // width, rows [sr[i], sr[i + 1]) matrix i with weights sw[i] and its own
+  // output sd[i] (m x (sr[i + 1] - sr[i])); every sr[i] is a multiple of
+  // the tile's rows, so a tile lies in one matrix
+  uint32_t nseg, sr[CX_GEMM_SEGS + 1];
+  const uint8_t* sw[CX_GEMM_SEGS];
+  float* sd[CX_GEMM_SEGS];
 };
 
 template <int T, int RW, int AW, int WA, int KS, int NSB>
@@ -159,7 +166,19 @@ __global__ __launch_bounds__(64 * RW * AW * KS) void k_gemm(GemmParams P) {
   const uint32_t b = blockIdx.x, A = P.act_tiles;
   const uint32_t rt = b / (8 * A) * 8 + b % 8, at = b / 8 % A;
   if (rt >= P.row_tiles) return;  // whole workgroup, before any load or barrier
-  const uint32_t r0 = rt * TW, a0 = at * MT;
+  const uint32_t a0 = at * MT;
+  // the tile's matrix: its weights W, rows N, output DST; r0 its first row there
+  const uint8_t* W = P.w;
+  float* DST = P.dst;
+  uint32_t N = P.n, r0 = rt * TW;
+  if (P.nseg > 1) {
+    uint32_t i = 0;
+    while (i + 1 < P.nseg && r0 >= P.sr[i + 1]) i++;
+    W = P.sw[i];
+    DST = P.sd[i];
+    N = P.sr[i + 1] - P.sr[i];
+    r0 -= P.sr[i];
+  }
 
   // this lane's load sources: slot s carries chunk NW*64 s + 64 wave + lane
   // of a stage, i.e. LDS bytes [16 c, 16 c + 16) of the stage; the chunk
@@ -171,13 +190,13 @@ __global__ __launch_bounds__(64 * RW * AW * KS) void k_gemm(GemmParams P) {
 #pragma unroll
   for (int s = 0; s < D; s++) {
     const uint32_t c = NW * 64 * s + 64 * wave + lane;
-    src[s] = P.w;
+    src[s] = W;
     inc[s] = 0;
     bis[s] = 0;
     if (c < (uint32_t)SH::WCH) {
       const uint32_t r = c / (RB / 16), part = c % (RB / 16);
-      const uint32_t row = r0 + r < P.n ? r0 + r : P.n - 1;  // past the end: a valid row
-      src[s] = P.w + (size_t)row * P.row_bytes + 16 * part;
+      const uint32_t row = r0 + r < N ? r0 + r : N - 1;  // past the end: a valid row
+      src[s] = W + (size_t)row * P.row_bytes + 16 * part;
       inc[s] = RB;
       bis[s] = part / (BPB / 16);
     } else if (c < (uint32_t)(SH::WCH + SH::XCH)) {
@@ -202,7 +221,7 @@ __global__ __launch_bounds__(64 * RW * AW * KS) void k_gemm(GemmParams P) {
     uint8_t* base = lds + (sb % S) * SH::STAGE + 1024 * wave;
 #pragma unroll
     for (int s = 0; s < D; s++) {
-      const uint8_t* p = sb * NSB + bis[s] < nb ? src[s] + (size_t)sb * inc[s] : P.w;
+      const uint8_t* p = sb * NSB + bis[s] < nb ? src[s] + (size_t)sb * inc[s] : W;
       cx_dma16_async(p, base + SH::SLOT * s);
     }
   };
@@ -319,18 +338,18 @@ __global__ __launch_bounds__(64 * RW * AW * KS) void k_gemm(GemmParams P) {
     for (int i = 0; i < PP; i++) {
       const int q = tid + 64 * NW * i;
       const uint32_t a = a0 + q % MT, r = r0 + q / MT;
-      if (q < NQ && a < P.m && r < P.n) P.dst[(size_t)a * P.n + r] = cacc[i];
+      if (q < NQ && a < P.m && r < N) DST[(size_t)a * N + r] = cacc[i];
     }
   } else {
     // lane: weight row r, activation rows 4g .. 4g+3 of each MFMA tile
     const uint32_t r = r0 + 16 * rw + c16;
-    if (r < P.n) {
+    if (r < N) {
 #pragma unroll
       for (int t = 0; t < WA; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const uint32_t a = a0 + 16 * (aw * WA + t) + 4 * g + i;
-          if (a < P.m) P.dst[(size_t)a * P.n + r] = acc[t][i];
+          if (a < P.m) DST[(size_t)a * N + r] = acc[t][i];
         }
     }
   }
@@ -853,5 +872,48 @@ int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, floa
   P.nb = (uint32_t)(k / vpb);
   P.row_bytes = P.nb * cx_bpb(type);
   if (direct_type(type)) return contract_direct(type, P, s);
+  return type == CX_Q4_K ? contract<CX_Q4_K>(P, s) : contract<CX_Q5_K>(P, s);
+}
+
+int cx_gemm_apply_multi(int type, const uint8_t* const* w, const uint32_t* n, uint32_t count,
+                        size_t k, size_t m, float* const* dst, const void* scratch,
+                        hipStream_t s) {
+  CX_REQUIRE(w && n && dst && count >= 1 && count <= CX_GEMM_SEGS,
+             "gemm: %u matrices (1 to %d)", count, CX_GEMM_SEGS);
+  uint32_t total = 0;
+  for (uint32_t i = 0; i < count; i++) total += n[i];
+  auto each = [&]() -> int {
+    for (uint32_t i = 0; i < count; i++)
+      if (int rc = cx_gemm_apply(type, w[i], n[i], k, m, dst[i], scratch, s)) return rc;
+    return CX_OK;
+  };
+  if (count == 1 || !m || !cx_gemm_supported(type) || direct_type(type)) return each();
+  gemm_kernel kern = nullptr;
+  const Config c = type == CX_Q4_K ? config<CX_Q4_K>(choose(total, (uint32_t)m), &kern)
+                                   : config<CX_Q5_K>(choose(total, (uint32_t)m), &kern);
+  for (uint32_t i = 0; i < count; i++)
+    if (n[i] % c.tw != 0) return each();  // a tile would straddle two matrices
+  const size_t vpb = (size_t)cx_vpb(type);
+  CX_REQUIRE(k % vpb == 0 && k > 0 && m < (1u << 24) && k < (1u << 24),
+             "gemm: k=%zu, m=%zu", k, m);
+  CX_REQUIRE(((uintptr_t)scratch & 255) == 0, "gemm: scratch misaligned");
+  GemmParams P{};
+  P.scratch = const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(scratch));
+  P.nseg = count;
+  for (uint32_t i = 0; i < count; i++) {
+    CX_REQUIRE(w[i] && dst[i] && ((uintptr_t)w[i] & 15) == 0,
+               "gemm: matrix %u: null or misaligned (16-byte) pointer", i);
+    P.sw[i] = w[i];
+    P.sd[i] = dst[i];
+    P.sr[i + 1] = P.sr[i] + n[i];
+  }
+  P.w = w[0];
+  P.dst = dst[0];
+  P.n = total;
+  P.k = (uint32_t)k;
+  P.m = (uint32_t)m;
+  P.m_pad = pad64(m);
+  P.nb = (uint32_t)(k / vpb);
+  P.row_bytes = P.nb * cx_bpb(type);
   return type == CX_Q4_K ? contract<CX_Q4_K>(P, s) : contract<CX_Q5_K>(P, s);
 }
