@@ -1479,23 +1479,34 @@ static int prefill_matmul(cx_cache* C, int type, const uint8_t* w, uint32_t n, u
   return CX_OK;
 }
 
-// prefill_matmul of `count` matrices over one input (q/k/v, gate/up): on the
-// MFMA contraction one launch for all of them when their types agree
-static int prefill_matmuls(cx_cache* C, const int* type, const uint8_t* const* w,
-                           const uint32_t* n, uint32_t count, uint32_t k, const float* in,
-                           uint32_t rows, float* const* out, int* quantized) {
+// out[i] = in . w[i]^T (+ bias[i]) for `count` matrices over one input
+// (q/k/v, gate/up), or with accum (one matrix) out[0] += in . w[0]^T: on the
+// MFMA contraction in one launch with the adds in its epilogue when the
+// matrices fit one (cx_gemm_multi_fits), else a launch a matrix and the
+// adds as row kernels. The same f32 adds either way: acc + bias, then
+// out + that.
+static int prefill_linear(cx_cache* C, const int* type, const uint8_t* const* w,
+                          const uint32_t* n, uint32_t count, uint32_t k, const float* in,
+                          uint32_t rows, float* const* out, const float* const* bias, bool accum,
+                          int* quantized) {
+  CX_REQUIRE(!accum || count == 1, "prefill: an accumulating product takes one matrix");
+  hipStream_t s = C->m->stream;
   bool same = true;
   for (uint32_t i = 1; i < count; i++) same = same && type[i] == type[0];
-  if (same && cx_gemm_supported(type[0])) {
+  int rc;
+  if (same && cx_gemm_multi_fits(type[0], n, count, rows)) {
     const int sub = cx_sub(type[0]);
-    int rc;
-    if (*quantized != sub && (rc = cx_gemm_quantize(in, rows, k, sub, C->pf.scratch, C->m->stream)))
-      return rc;
+    if (*quantized != sub && (rc = cx_gemm_quantize(in, rows, k, sub, C->pf.scratch, s))) return rc;
     *quantized = sub;
-    return cx_gemm_apply_multi(type[0], w, n, count, k, rows, out, C->pf.scratch, C->m->stream);
+    return cx_gemm_apply_multi(type[0], w, n, count, k, rows, out, bias, accum, C->pf.scratch, s);
   }
-  for (uint32_t i = 0; i < count; i++)
-    if (int rc = prefill_matmul(C, type[i], w[i], n[i], k, in, rows, out[i], quantized)) return rc;
+  for (uint32_t i = 0; i < count; i++) {
+    float* dst = accum ? C->pf.tmp : out[i];
+    if ((rc = prefill_matmul(C, type[i], w[i], n[i], k, in, rows, dst, quantized)) ||
+        (bias && bias[i] && (rc = cx_launch_add_rows(dst, bias[i], rows, n[i], 1, s))) ||
+        (accum && (rc = cx_launch_add_rows(out[i], dst, rows, n[i], rows, s))))
+      return rc;
+  }
   return CX_OK;
 }
 
@@ -1519,14 +1530,11 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
       const uint8_t* w[3] = {L.q, L.k, L.v};
       const uint32_t n[3] = {D, kvd, kvd};
       float* o[3] = {P.q, P.k, P.v};
+      const float* b[3] = {L.q_bias, L.k_bias, L.v_bias};
       if ((rc = cx_launch_norm_rows(P.x, L.attn_norm, nt, D, c.eps, P.nrm, s)) ||
-          (rc = prefill_matmuls(C, t, w, n, 3, D, P.nrm, nt, o, &qd)))
+          (rc = prefill_linear(C, t, w, n, 3, D, P.nrm, nt, o, b, false, &qd)))
         return rc;
     }
-    if ((L.q_bias && (rc = cx_launch_add_rows(P.q, L.q_bias, nt, D, 1, s))) ||
-        (L.k_bias && (rc = cx_launch_add_rows(P.k, L.k_bias, nt, kvd, 1, s))) ||
-        (L.v_bias && (rc = cx_launch_add_rows(P.v, L.v_bias, nt, kvd, 1, s))))
-      return rc;
     if ((rc = cx_launch_rope_kv(P.q, P.k, P.v, kc, vc, m->cos_t, m->sin_t, c.heads, c.kv_heads,
                                 hd, C->st, nt, s)))
       return rc;
@@ -1546,24 +1554,33 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
     if ((rc = cx_launch_attn_decode(a, s))) return rc;
     // src/forward.rs:466-491
     qd = 0;
-    if ((rc = prefill_matmul(C, L.t_o, L.o, D, D, P.att, nt, P.tmp, &qd)) ||
-        (rc = cx_launch_add_rows(P.x, P.tmp, nt, D, nt, s)) ||
-        (rc = cx_launch_norm_rows(P.x, L.ffn_norm, nt, D, c.eps, P.nrm, s)))
-      return rc;
+    {  // x += att . o^T
+      const int t[1] = {L.t_o};
+      const uint8_t* w[1] = {L.o};
+      const uint32_t n[1] = {D};
+      float* o[1] = {P.x};
+      if ((rc = prefill_linear(C, t, w, n, 1, D, P.att, nt, o, nullptr, true, &qd)) ||
+          (rc = cx_launch_norm_rows(P.x, L.ffn_norm, nt, D, c.eps, P.nrm, s)))
+        return rc;
+    }
     qd = 0;
     {
       const int t[2] = {L.t_gate, L.t_up};
       const uint8_t* w[2] = {L.gate, L.up};
       const uint32_t n[2] = {I, I};
       float* o[2] = {P.g, P.u};
-      if ((rc = prefill_matmuls(C, t, w, n, 2, D, P.nrm, nt, o, &qd)) ||
+      if ((rc = prefill_linear(C, t, w, n, 2, D, P.nrm, nt, o, nullptr, false, &qd)) ||
           (rc = cx_launch_swiglu_rows(P.g, P.u, (size_t)nt * I, P.nrm, s)))
         return rc;
     }
     qd = 0;
-    if ((rc = prefill_matmul(C, L.t_down, L.down, D, I, P.nrm, nt, P.tmp, &qd)) ||
-        (rc = cx_launch_add_rows(P.x, P.tmp, nt, D, nt, s)))
-      return rc;
+    {  // x += swiglu . down^T
+      const int t[1] = {L.t_down};
+      const uint8_t* w[1] = {L.down};
+      const uint32_t n[1] = {D};
+      float* o[1] = {P.x};
+      if ((rc = prefill_linear(C, t, w, n, 1, I, P.nrm, nt, o, nullptr, true, &qd))) return rc;
+    }
   }
   return CX_OK;
 }

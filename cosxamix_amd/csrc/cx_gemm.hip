@@ -110,6 +110,11 @@ struct GemmParams {
   uint32_t nseg, sr[CX_GEMM_SEGS + 1];
   const uint8_t* sw[CX_GEMM_SEGS];
   float* sd[CX_GEMM_SEGS];
+  // k_gemm only, per matrix (index 0 without segments): a bias added to
+  // every output row (dst = acc + bias[r]), and with accum the output added
+  // to what dst holds (dst = dst + (acc [+ bias])), f32 adds as written
+  const float* sbias[CX_GEMM_SEGS];
+  uint32_t accum;
 };
 
 template <int T, int RW, int AW, int WA, int KS, int NSB>
@@ -170,15 +175,23 @@ __global__ __launch_bounds__(64 * RW * AW * KS) void k_gemm(GemmParams P) {
   // the tile's matrix: its weights W, rows N, output DST; r0 its first row there
   const uint8_t* W = P.w;
   float* DST = P.dst;
+  const float* BIAS = P.sbias[0];
   uint32_t N = P.n, r0 = rt * TW;
   if (P.nseg > 1) {
     uint32_t i = 0;
     while (i + 1 < P.nseg && r0 >= P.sr[i + 1]) i++;
     W = P.sw[i];
     DST = P.sd[i];
+    BIAS = P.sbias[i];
     N = P.sr[i + 1] - P.sr[i];
     r0 -= P.sr[i];
   }
+  auto put = [&](uint32_t a, uint32_t r, float v) {  // output (a, r) of the tile's matrix
+    float* d = DST + (size_t)a * N + r;
+    if (BIAS) v = v + BIAS[r];
+    if (P.accum) v = *d + v;
+    *d = v;
+  };
 
   // this lane's load sources: slot s carries chunk NW*64 s + 64 wave + lane
   // of a stage, i.e. LDS bytes [16 c, 16 c + 16) of the stage; the chunk
@@ -338,7 +351,7 @@ __global__ __launch_bounds__(64 * RW * AW * KS) void k_gemm(GemmParams P) {
     for (int i = 0; i < PP; i++) {
       const int q = tid + 64 * NW * i;
       const uint32_t a = a0 + q % MT, r = r0 + q / MT;
-      if (q < NQ && a < P.m && r < N) DST[(size_t)a * N + r] = cacc[i];
+      if (q < NQ && a < P.m && r < N) put(a, r, cacc[i]);
     }
   } else {
     // lane: weight row r, activation rows 4g .. 4g+3 of each MFMA tile
@@ -349,7 +362,7 @@ __global__ __launch_bounds__(64 * RW * AW * KS) void k_gemm(GemmParams P) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const uint32_t a = a0 + 16 * (aw * WA + t) + 4 * g + i;
-          if (a < P.m) DST[(size_t)a * N + r] = acc[t][i];
+          if (a < P.m) put(a, r, acc[t][i]);
         }
     }
   }
@@ -875,27 +888,28 @@ int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, floa
   return type == CX_Q4_K ? contract<CX_Q4_K>(P, s) : contract<CX_Q5_K>(P, s);
 }
 
-int cx_gemm_apply_multi(int type, const uint8_t* const* w, const uint32_t* n, uint32_t count,
-                        size_t k, size_t m, float* const* dst, const void* scratch,
-                        hipStream_t s) {
-  CX_REQUIRE(w && n && dst && count >= 1 && count <= CX_GEMM_SEGS,
-             "gemm: %u matrices (1 to %d)", count, CX_GEMM_SEGS);
+bool cx_gemm_multi_fits(int type, const uint32_t* n, uint32_t count, size_t m) {
+  if (!n || count < 1 || count > CX_GEMM_SEGS || !m || m >= (1u << 24) ||
+      !cx_gemm_supported(type) || direct_type(type))
+    return false;
   uint32_t total = 0;
   for (uint32_t i = 0; i < count; i++) total += n[i];
-  auto each = [&]() -> int {
-    for (uint32_t i = 0; i < count; i++)
-      if (int rc = cx_gemm_apply(type, w[i], n[i], k, m, dst[i], scratch, s)) return rc;
-    return CX_OK;
-  };
-  if (count == 1 || !m || !cx_gemm_supported(type) || direct_type(type)) return each();
+  if (!total) return false;
   gemm_kernel kern = nullptr;
   const Config c = type == CX_Q4_K ? config<CX_Q4_K>(choose(total, (uint32_t)m), &kern)
                                    : config<CX_Q5_K>(choose(total, (uint32_t)m), &kern);
-  for (uint32_t i = 0; i < count; i++)
-    if (n[i] % c.tw != 0) return each();  // a tile would straddle two matrices
+  for (uint32_t i = 0; count > 1 && i < count; i++)
+    if (n[i] % c.tw != 0) return false;  // a tile would straddle two matrices
+  return true;
+}
+
+int cx_gemm_apply_multi(int type, const uint8_t* const* w, const uint32_t* n, uint32_t count,
+                        size_t k, size_t m, float* const* dst, const float* const* bias, int accum,
+                        const void* scratch, hipStream_t s) {
+  CX_REQUIRE(w && dst && cx_gemm_multi_fits(type, n, count, m),
+             "gemm: %u matrices of type %d over %zu rows do not fit one launch", count, type, m);
   const size_t vpb = (size_t)cx_vpb(type);
-  CX_REQUIRE(k % vpb == 0 && k > 0 && m < (1u << 24) && k < (1u << 24),
-             "gemm: k=%zu, m=%zu", k, m);
+  CX_REQUIRE(k % vpb == 0 && k > 0 && k < (1u << 24), "gemm: k=%zu", k);
   CX_REQUIRE(((uintptr_t)scratch & 255) == 0, "gemm: scratch misaligned");
   GemmParams P{};
   P.scratch = const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(scratch));
@@ -905,11 +919,13 @@ int cx_gemm_apply_multi(int type, const uint8_t* const* w, const uint32_t* n, ui
                "gemm: matrix %u: null or misaligned (16-byte) pointer", i);
     P.sw[i] = w[i];
     P.sd[i] = dst[i];
+    P.sbias[i] = bias ? bias[i] : nullptr;
     P.sr[i + 1] = P.sr[i] + n[i];
   }
+  P.accum = accum ? 1u : 0u;
   P.w = w[0];
   P.dst = dst[0];
-  P.n = total;
+  P.n = P.sr[count];
   P.k = (uint32_t)k;
   P.m = (uint32_t)m;
   P.m_pad = pad64(m);

@@ -163,13 +163,17 @@ int cx_gemm_quantize(const float* lhs, size_t m, size_t k, int sub, void* scratc
 int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, float* dst,
                   const void* scratch, hipStream_t s);
 // cx_gemm_apply of `count` matrices of one type and width k (up to
-// CX_GEMM_SEGS: q/k/v, gate/up), matrix i (n[i] rows, weights w[i]) into
-// dst[i] (m x n[i]): one launch when every n[i] is a multiple of the tile's
-// rows, else one a matrix; every value as cx_gemm_apply gives it.
+// CX_GEMM_SEGS: q/k/v, gate/up) in one launch, matrix i (n[i] rows, weights
+// w[i]) into dst[i] (m x n[i]), with optional per-matrix biases (dst =
+// acc + bias[r]) and, with accum, added into dst (dst = dst + ...); every
+// value as cx_gemm_apply (and the separate adds) give it. Only where
+// cx_gemm_multi_fits: Q4_K/Q5_K, and with several matrices every n[i] a
+// multiple of the tile's rows.
 #define CX_GEMM_SEGS 3
+bool cx_gemm_multi_fits(int type, const uint32_t* n, uint32_t count, size_t m);
 int cx_gemm_apply_multi(int type, const uint8_t* const* w, const uint32_t* n, uint32_t count,
-                        size_t k, size_t m, float* const* dst, const void* scratch,
-                        hipStream_t s);
+                        size_t k, size_t m, float* const* dst, const float* const* bias, int accum,
+                        const void* scratch, hipStream_t s);
 
 // Format conversion (cx_quant.hip): bit-identical to quant::descuantizar,
 // descuantizar_filas and desempaquetar_i8; rows[] are device indices.
