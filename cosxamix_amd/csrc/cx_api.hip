@@ -1485,16 +1485,35 @@ static int prefill_matmul(cx_cache* C, int type, const uint8_t* w, uint32_t n, u
 // matrices fit one (cx_gemm_multi_fits), else a launch a matrix and the
 // adds as row kernels. The same f32 adds either way: acc + bias, then
 // out + that.
+// the matrices take one contraction launch (one type, cx_gemm_multi_fits)
+static bool prefill_fits(const int* type, const uint32_t* n, uint32_t count, uint32_t rows) {
+  for (uint32_t i = 1; i < count; i++)
+    if (type[i] != type[0]) return false;
+  return cx_gemm_multi_fits(type[0], n, count, rows);
+}
+
+// rmsnorm of the residual rows into the input of the matrices that follow:
+// straight into their quantized rows when they take one contraction launch
+// (*quantized is then their sub-block size), else into P.nrm
+static int prefill_norm(cx_cache* C, const float* nw, const int* type, const uint32_t* n,
+                        uint32_t count, uint32_t rows, int* quantized) {
+  cx_prefill& P = C->pf;
+  const cx_config& c = C->m->cfg;
+  if (prefill_fits(type, n, count, rows)) {
+    *quantized = cx_sub(type[0]);
+    return cx_gemm_norm_quantize(P.x, nw, rows, c.dim, c.eps, *quantized, P.scratch, C->m->stream);
+  }
+  return cx_launch_norm_rows(P.x, nw, rows, c.dim, c.eps, P.nrm, C->m->stream);
+}
+
 static int prefill_linear(cx_cache* C, const int* type, const uint8_t* const* w,
                           const uint32_t* n, uint32_t count, uint32_t k, const float* in,
                           uint32_t rows, float* const* out, const float* const* bias, bool accum,
                           int* quantized) {
   CX_REQUIRE(!accum || count == 1, "prefill: an accumulating product takes one matrix");
   hipStream_t s = C->m->stream;
-  bool same = true;
-  for (uint32_t i = 1; i < count; i++) same = same && type[i] == type[0];
   int rc;
-  if (same && cx_gemm_multi_fits(type[0], n, count, rows)) {
+  if (prefill_fits(type, n, count, rows)) {
     const int sub = cx_sub(type[0]);
     if (*quantized != sub && (rc = cx_gemm_quantize(in, rows, k, sub, C->pf.scratch, s))) return rc;
     *quantized = sub;
@@ -1531,7 +1550,7 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
       const uint32_t n[3] = {D, kvd, kvd};
       float* o[3] = {P.q, P.k, P.v};
       const float* b[3] = {L.q_bias, L.k_bias, L.v_bias};
-      if ((rc = cx_launch_norm_rows(P.x, L.attn_norm, nt, D, c.eps, P.nrm, s)) ||
+      if ((rc = prefill_norm(C, L.attn_norm, t, n, 3, nt, &qd)) ||
           (rc = prefill_linear(C, t, w, n, 3, D, P.nrm, nt, o, b, false, &qd)))
         return rc;
     }
@@ -1559,9 +1578,7 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
       const uint8_t* w[1] = {L.o};
       const uint32_t n[1] = {D};
       float* o[1] = {P.x};
-      if ((rc = prefill_linear(C, t, w, n, 1, D, P.att, nt, o, nullptr, true, &qd)) ||
-          (rc = cx_launch_norm_rows(P.x, L.ffn_norm, nt, D, c.eps, P.nrm, s)))
-        return rc;
+      if ((rc = prefill_linear(C, t, w, n, 1, D, P.att, nt, o, nullptr, true, &qd))) return rc;
     }
     qd = 0;
     {
@@ -1569,8 +1586,8 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
       const uint8_t* w[2] = {L.gate, L.up};
       const uint32_t n[2] = {I, I};
       float* o[2] = {P.g, P.u};
-      if ((rc = prefill_linear(C, t, w, n, 2, D, P.nrm, nt, o, nullptr, false, &qd)) ||
-          (rc = cx_launch_swiglu_rows(P.g, P.u, (size_t)nt * I, P.nrm, s)))
+      if ((rc = prefill_norm(C, L.ffn_norm, t, n, 2, nt, &qd)) ||
+          (rc = prefill_linear(C, t, w, n, 2, D, P.nrm, nt, o, nullptr, false, &qd)))
         return rc;
     }
     qd = 0;
@@ -1579,6 +1596,12 @@ static int enqueue_prefill_chunk(cx_cache* C, uint32_t nt) {
       const uint8_t* w[1] = {L.down};
       const uint32_t n[1] = {D};
       float* o[1] = {P.x};
+      if (prefill_fits(t, n, 1, nt)) {  // silu(g) * u straight into the quantized rows
+        if ((rc = cx_gemm_swiglu_quantize(P.g, P.u, nt, I, cx_sub(t[0]), P.scratch, s))) return rc;
+        qd = cx_sub(t[0]);
+      } else if ((rc = cx_launch_swiglu_rows(P.g, P.u, (size_t)nt * I, P.nrm, s))) {
+        return rc;
+      }
       if ((rc = prefill_linear(C, t, w, n, 1, I, P.nrm, nt, o, nullptr, true, &qd))) return rc;
     }
   }

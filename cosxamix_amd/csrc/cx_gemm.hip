@@ -691,6 +691,84 @@ __global__ __launch_bounds__(256) void k_quantize_gemm(const float* x, uint32_t 
   }
 }
 
+// The prefill's row ops straight into that layout, for the contraction that
+// reads them: rmsnorm (k_norm_rows' arithmetic: the f64 sum of squares in
+// the same tree, then (float)(x * scale) * w; src/kernels/scalar.rs:36-54),
+// one workgroup a row; and silu(g) * u (src/forward.rs:483-487); each
+// value is what the row kernel writes, then quantized as k_quantize_gemm
+// quantizes it. Rows [m, m_pad) are zero.
+template <int SUB>
+__global__ __launch_bounds__(256) void k_norm_quant_gemm(const float* x, const float* w,
+                                                         uint32_t m, uint32_t k, float eps,
+                                                         uint32_t m_pad, int8_t* xq, float* xexs) {
+  __shared__ double red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t a = blockIdx.x;
+  const float* xr = x + (size_t)a * k;
+  double scale = 0.0;
+  if (a < m) {
+    double sum = 0.0;
+    for (uint32_t i = 8 * tid; i < k; i += 2048) {
+      float v[8];
+      cx_load8(xr + i, v);
+#pragma unroll
+      for (int j = 0; j < 8; j++) sum += (double)v[j] * (double)v[j];
+    }
+    sum = cx_wave_sum_d(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    const double tot = ((red[0] + red[1]) + red[2]) + red[3];
+    scale = 1.0 / sqrt(tot / (double)k + (double)eps);
+  }
+  for (uint32_t i = 8 * tid; i < k; i += 2048) {  // whole quads of lanes (k % 32 == 0)
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (a < m) {
+      float nw[8];
+      cx_load8(xr + i, v);
+      cx_load8(w + i, nw);
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = (float)((double)v[j] * scale) * nw[j];
+    }
+    uint32_t lo, hi;
+    float d;
+    int32_t s;
+    cx_quant8_vals<SUB>(v, lo, hi, d, s);
+    *reinterpret_cast<uint2*>(xq + (size_t)a * k + i) = make_uint2(lo, hi);
+    if ((i & (SUB - 1)) == 0) {
+      float* e = xexs + (size_t)(i / SUB) * 2 * m_pad + a;
+      e[0] = d;
+      e[m_pad] = (float)s;
+    }
+  }
+}
+
+template <int SUB>
+__global__ __launch_bounds__(256) void k_swiglu_quant_gemm(const float* g, const float* u,
+                                                           uint32_t m, uint32_t k, uint32_t m_pad,
+                                                           int8_t* xq, float* xexs) {
+  const size_t i = 8 * (blockIdx.x * 256ull + threadIdx.x);
+  if (i >= (size_t)m_pad * k) return;
+  const uint32_t a = (uint32_t)(i / k), col = (uint32_t)(i % k);
+  float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (a < m) {
+    float b[8];
+    cx_load8(g + i, v);
+    cx_load8(u + i, b);
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = cx_swiglu(v[j], b[j]);
+  }
+  uint32_t lo, hi;
+  float d;
+  int32_t s;
+  cx_quant8_vals<SUB>(v, lo, hi, d, s);
+  *reinterpret_cast<uint2*>(xq + i) = make_uint2(lo, hi);
+  if ((col & (SUB - 1)) == 0) {
+    float* e = xexs + (size_t)(col / SUB) * 2 * m_pad + a;
+    e[0] = d;
+    e[m_pad] = (float)s;
+  }
+}
+
 struct Config {
   int tw, mt, threads;
   size_t lds;
@@ -862,6 +940,50 @@ int cx_gemm_quantize(const float* lhs, size_t m, size_t k, int sub, void* scratc
   if (!m) return CX_OK;
   return quantize(lhs, (uint32_t)m, (uint32_t)k, pad64(m), sub, reinterpret_cast<uint8_t*>(scratch),
                   s);
+}
+
+int cx_gemm_norm_quantize(const float* x, const float* w, size_t m, size_t k, float eps, int sub,
+                          void* scratch, hipStream_t s) {
+  CX_REQUIRE(x && w && scratch, "gemm: null pointer");
+  CX_REQUIRE(sub == 16 || sub == 32, "gemm: sub-blocks of 16 or 32, not %d", sub);
+  CX_REQUIRE(k % 32 == 0 && k > 0 && k < (1u << 24) && m < (1u << 24), "gemm: %zu x %zu", m, k);
+  CX_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+                 ((uintptr_t)scratch & 255) == 0,
+             "gemm: rows and weights must be 16-byte and scratch 256-byte aligned");
+  if (!m) return CX_OK;
+  const uint32_t mp = pad64(m);
+  uint8_t* sc = reinterpret_cast<uint8_t*>(scratch);
+  if (sub == 16)
+    hipLaunchKernelGGL(k_norm_quant_gemm<16>, dim3(mp), dim3(256), 0, s, x, w, (uint32_t)m,
+                       (uint32_t)k, eps, mp, scratch_xq(sc), scratch_xexs(sc, mp, k));
+  else
+    hipLaunchKernelGGL(k_norm_quant_gemm<32>, dim3(mp), dim3(256), 0, s, x, w, (uint32_t)m,
+                       (uint32_t)k, eps, mp, scratch_xq(sc), scratch_xexs(sc, mp, k));
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
+int cx_gemm_swiglu_quantize(const float* g, const float* u, size_t m, size_t k, int sub,
+                            void* scratch, hipStream_t s) {
+  CX_REQUIRE(g && u && scratch, "gemm: null pointer");
+  CX_REQUIRE(sub == 16 || sub == 32, "gemm: sub-blocks of 16 or 32, not %d", sub);
+  CX_REQUIRE(k % 32 == 0 && k > 0 && k < (1u << 24) && m < (1u << 24), "gemm: %zu x %zu", m, k);
+  CX_REQUIRE(((uintptr_t)g & 15) == 0 && ((uintptr_t)u & 15) == 0 &&
+                 ((uintptr_t)scratch & 255) == 0,
+             "gemm: rows must be 16-byte and scratch 256-byte aligned");
+  if (!m) return CX_OK;
+  const uint32_t mp = pad64(m);
+  uint8_t* sc = reinterpret_cast<uint8_t*>(scratch);
+  const size_t grid = ((size_t)mp * k / 8 + 255) / 256;
+  CX_REQUIRE(grid < (1ull << 31), "gemm: %zu activation values is too many", (size_t)mp * k);
+  if (sub == 16)
+    hipLaunchKernelGGL(k_swiglu_quant_gemm<16>, dim3((unsigned)grid), dim3(256), 0, s, g, u,
+                       (uint32_t)m, (uint32_t)k, mp, scratch_xq(sc), scratch_xexs(sc, mp, k));
+  else
+    hipLaunchKernelGGL(k_swiglu_quant_gemm<32>, dim3((unsigned)grid), dim3(256), 0, s, g, u,
+                       (uint32_t)m, (uint32_t)k, mp, scratch_xq(sc), scratch_xexs(sc, mp, k));
+  CX_HIP(hipGetLastError());
+  return CX_OK;
 }
 
 int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, float* dst,

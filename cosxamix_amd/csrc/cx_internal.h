@@ -160,6 +160,12 @@ int cx_launch_gemm(int type, const uint8_t* w, size_t n, size_t k, const float* 
 // then contract any number of matrices of width k and that sub-block size
 // against it (scratch of cx_gemm_scratch_bytes(m, k)).
 int cx_gemm_quantize(const float* lhs, size_t m, size_t k, int sub, void* scratch, hipStream_t s);
+// cx_gemm_quantize of rmsnorm(x) * w (cx_launch_norm_rows' values), and of
+// silu(g) * u (cx_launch_swiglu_rows'), without the f32 rows in between
+int cx_gemm_norm_quantize(const float* x, const float* w, size_t m, size_t k, float eps, int sub,
+                          void* scratch, hipStream_t s);
+int cx_gemm_swiglu_quantize(const float* g, const float* u, size_t m, size_t k, int sub,
+                            void* scratch, hipStream_t s);
 int cx_gemm_apply(int type, const uint8_t* w, size_t n, size_t k, size_t m, float* dst,
                   const void* scratch, hipStream_t s);
 // cx_gemm_apply of `count` matrices of one type and width k (up to
