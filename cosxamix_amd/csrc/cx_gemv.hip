@@ -166,6 +166,37 @@ template <> struct KQ<CX_Q4_K> {
     pre4(h, xb, xe, xs, a);
     half_pre(r, h, a, dbg, to);
   }
+  // half_pre's four terms into registers: t[jj] is sub-block 4h + jj's term;
+  // the lane's h selects its scales with selects, not branches
+  __device__ static void half_t4(const Regs& r, int h, const Pre4& a, int32_t* dbg,
+                                 float (&t)[4]) {
+    const uint4 hd = r.hd;
+    const float d = cx_h2f(hd.x & 0xFFFF), dm = cx_h2f(hd.x >> 16);
+    uint32_t sc0, mn0, sc1, mn1;
+    scales_mins(0, hd.y, hd.z, hd.w, sc0, mn0);
+    scales_mins(1, hd.y, hd.z, hd.w, sc1, mn1);
+    const uint32_t sc4 = h ? sc1 : sc0, mn4 = h ? mn1 : mn0;
+#pragma unroll
+    for (int pp = 0; pp < 2; pp++) {
+      const uint4 u0 = r.u[2 * pp], u1 = r.u[2 * pp + 1];
+      const uint32_t q[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+      int e0 = 0, e1 = 0;
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        e0 = dot4(q[w] & M4, a.xa[pp][w], e0);
+        e1 = dot4((q[w] >> 4) & M4, a.xc[pp][w], e1);
+      }
+      t[2 * pp] = term_val(2 * pp, e0, d, dm, sc4, mn4, a, h, dbg);
+      t[2 * pp + 1] = term_val(2 * pp + 1, e1, d, dm, sc4, mn4, a, h, dbg);
+    }
+  }
+  // term_pre's value, returned
+  __device__ static float term_val(int jj, int e, float d, float dm, uint32_t sc4, uint32_t mn4,
+                                   const Pre4& a, int h, int32_t* dbg) {
+    const uint32_t sc = (sc4 >> (8 * jj)) & 0xFF, mn = (mn4 >> (8 * jj)) & 0xFF;
+    if (dbg) dbg[4 * h + jj] = e;
+    return a.e[jj] * (d * (float)sc * (float)e - dm * (float)mn * a.s[jj]);
+  }
 };
 
 // ------------------------------------------------------------------ Q5_K
@@ -221,6 +252,33 @@ template <> struct KQ<CX_Q5_K> {
     Pre4 a;
     pre4(h, xb, xe, xs, a);
     half_pre(r, h, a, dbg, to);
+  }
+  // half_pre's four terms into registers (as KQ<CX_Q4_K>::half_t4)
+  __device__ static void half_t4(const Regs& r, int h, const Pre4& a, int32_t* dbg,
+                                 float (&t)[4]) {
+    const uint4 hd = r.hd, h0 = r.h0, h1 = r.h1;
+    const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    const float d = cx_h2f(hd.x & 0xFFFF), dm = cx_h2f(hd.x >> 16);
+    uint32_t sc0, mn0, sc1, mn1;
+    KQ<CX_Q4_K>::scales_mins(0, hd.y, hd.z, hd.w, sc0, mn0);
+    KQ<CX_Q4_K>::scales_mins(1, hd.y, hd.z, hd.w, sc1, mn1);
+    const uint32_t sc4 = h ? sc1 : sc0, mn4 = h ? mn1 : mn0;
+#pragma unroll
+    for (int pp = 0; pp < 2; pp++) {
+      const uint4 u0 = r.u[2 * pp], u1 = r.u[2 * pp + 1];
+      const uint32_t q[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+      const uint32_t p2 = 2 * (2 * (uint32_t)h + pp);  // pair p = 2h + pp: bits 2p, 2p + 1
+      int e0 = 0, e1 = 0;
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        const uint32_t lo = (q[w] & M4) | (((qh[w] >> p2) & M1) << 4);
+        const uint32_t hi = ((q[w] >> 4) & M4) | (((qh[w] >> (p2 + 1)) & M1) << 4);
+        e0 = dot4(lo, a.xa[pp][w], e0);
+        e1 = dot4(hi, a.xc[pp][w], e1);
+      }
+      t[2 * pp] = KQ<CX_Q4_K>::term_val(2 * pp, e0, d, dm, sc4, mn4, a, h, dbg);
+      t[2 * pp + 1] = KQ<CX_Q4_K>::term_val(2 * pp + 1, e1, d, dm, sc4, mn4, a, h, dbg);
+    }
   }
 };
 
@@ -641,6 +699,135 @@ __global__ __launch_bounds__(256) void k_gemv_reg(GemvParams P) {
     const uint32_t row = row0 + tid;
     S.y[row] = (P.epi == CX_EPI_ACCUM || S.bias) ? acc + addend : acc;
   }
+}
+
+// The plain Q4_K/Q5_K GEMV for rows of NB = 8 or 16 super-blocks (k = 2048
+// or 4096), one (row, super-block, half) item a lane: the row's 2*NB lanes
+// are consecutive lanes of one wave, lane 2b + h holding half h of
+// super-block b, so its four terms are terms 8b + 4h .. 8b + 4h + 3 of the
+// row. The scalar spec's sum (total = 0; total += term_s in order,
+// src/kernels/scalar.rs:141-167) then runs along the lanes: at step s every
+// lane takes its left neighbour's running sum (DPP wave_shr:1, lane 0 reads
+// +0.0) and adds its four terms in order, so after 2*NB steps the row's last
+// lane holds the row total, rounded add by add as the reference rounds it.
+// Every lane starts at +0.0, so the first lane of each row also reads +0.0
+// at step 0, and at step s lane 2*NB*r + s reads lane 2*NB*r + s - 1 of the
+// same row. No workgroup barrier follows the loads: the activation (k bytes
+// + 2k/32 floats) is the only data shared across waves, and it arrives from
+// L2 long before the weights, which go straight from HBM into registers, a
+// lane's 80 (Q4_K) or 112 (Q5_K) bytes issued at the start.
+// Chunk c of the activation of a row-kernel launch, 16 bytes: xq's NB*16
+// chunks, then xe's NB*2 and xs's NB*2 (c past the end: the last one). The
+// address is picked with masks, not branches: a load behind branches is
+// issued late.
+template <int NB>
+__device__ inline int4 row_act_load(uint64_t xq, uint64_t xe, uint64_t xs, int c) {
+  constexpr int NX = NB * 16, NE = NB * 2;
+  c = min(c, NX + 2 * NE - 1);
+  const uint64_t me = 0 - (uint64_t)(c >= NX), ms = 0 - (uint64_t)(c >= NX + NE);
+  uint64_t a = xq + 16 * (uint64_t)c;
+  a = (a & ~me) | ((xe + 16 * (uint64_t)(c - NX)) & me);
+  a = (a & ~ms) | ((xs + 16 * (uint64_t)(c - NX - NE)) & ms);
+  return *(const int4*)reinterpret_cast<const __attribute__((address_space(1))) int4*>(a);
+}
+// ... and its place in LDS (xq blocks ACT_LDS_BLOCK bytes apart)
+template <int NB>
+__device__ inline void row_act_store(int8_t* sq, float* se, float* ss, int c, const int4& v) {
+  constexpr int NX = NB * 16, NE = NB * 2;
+  if (c >= NX + 2 * NE) return;
+  int4* p = c < NX ? reinterpret_cast<int4*>(sq + (c >> 4) * ACT_LDS_BLOCK + 16 * (c & 15))
+            : c < NX + NE ? reinterpret_cast<int4*>(se) + (c - NX)
+                          : reinterpret_cast<int4*>(ss) + (c - NX - NE);
+  *p = v;
+}
+template <int T, int NB, bool MULTI, bool DBG>
+__global__ __launch_bounds__(1024) void k_gemv_row(GemvParams P) {
+  using Q = KQ<T>;
+  constexpr int AP = (NB * 20 + 63) / 64;  // activation chunks a lane of wave 0 loads
+  constexpr int LPR = 2 * NB;     // lanes per row
+  constexpr int RPW = 64 / LPR;   // rows per wave
+  __shared__ __align__(16) int8_t sq[NB * ACT_LDS_BLOCK];
+  __shared__ __align__(16) float se[8 * NB], ss[8 * NB];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the kernel arguments the loads need, read up front in one batch of
+  // scalar loads (the empty asms hold them in SGPRs here; left alone, the
+  // compiler reads each one where it is first used, a round trip each)
+  uint64_t xq = (uint64_t)P.act.xq, xe = (uint64_t)P.act.xe, xs = (uint64_t)P.act.xs;
+  uint32_t tile = blockIdx.x;
+  int sg = 0;
+  if constexpr (MULTI) {
+    while (tile >= P.tile_end[sg]) sg++;
+    if (sg) tile -= P.tile_end[sg - 1];
+  }
+  const cx_seg S = P.seg[sg];
+  uint64_t wbase = (uint64_t)S.w;
+  uint32_t R = P.R, rb = P.row_bytes, srows = S.rows;
+  asm volatile("" : "+s"(xq), "+s"(xe), "+s"(xs), "+s"(wbase), "+s"(R), "+s"(rb), "+s"(srows));
+  const uint32_t row0 = tile * R;
+  const uint32_t rows = min(R, srows - row0);
+  const uint32_t lr = (uint32_t)(wave * RPW + lane / LPR);  // the lane's row in the tile
+  const int b = (lane % LPR) >> 1, h = lane & 1;
+  const bool owner = lr < rows && lane % LPR == LPR - 1;     // stores the row
+
+  // 1. wave 0 loads the activation's 16-byte chunks into registers (L2
+  //    hits; a lane past the last chunk reloads it), every wave its weights.
+  //    Named registers, not an array: an array here ends up in memory.
+  //    (Activation loads spread over every wave measured 0.3 us slower at
+  //    config 1: each wave's weight loads then queue behind its share.)
+  int4 av0{}, av1{}, av2{}, av3{}, av4{};
+  if (wave == 0) {
+    av0 = row_act_load<NB>(xq, xe, xs, lane);
+    av1 = row_act_load<NB>(xq, xe, xs, lane + 64);
+    av2 = row_act_load<NB>(xq, xe, xs, lane + 128);
+    if constexpr (AP > 3) av3 = row_act_load<NB>(xq, xe, xs, lane + 192);
+    if constexpr (AP > 4) av4 = row_act_load<NB>(xq, xe, xs, lane + 256);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  typename Q::Regs r;
+  const uint32_t row = row0 + (lr < rows ? lr : rows - 1);
+  // (an address formed from an integer is generic; cast through the global
+  // address space, the loads are global loads)
+  Q::load((const uint8_t*)reinterpret_cast<const __attribute__((address_space(1))) uint8_t*>(wbase) +
+              (size_t)row * rb + (size_t)b * Q::BPB, h, r);
+  const bool add = P.epi == CX_EPI_ACCUM || S.bias;
+  const float* addp = P.epi == CX_EPI_ACCUM ? S.y : S.bias;
+  const float addend = add ? addp[row] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
+  if (wave == 0) {
+    row_act_store<NB>(sq, se, ss, lane, av0);
+    row_act_store<NB>(sq, se, ss, lane + 64, av1);
+    row_act_store<NB>(sq, se, ss, lane + 128, av2);
+    if constexpr (AP > 3) row_act_store<NB>(sq, se, ss, lane + 192, av3);
+    if constexpr (AP > 4) row_act_store<NB>(sq, se, ss, lane + 256, av4);
+  }
+  // a plain barrier (__syncthreads() would also wait for the weights), and
+  // nothing that needs the weights moved above it
+  __builtin_amdgcn_sched_barrier(0);
+  cx_wait_lds();
+  cx_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. the lane's four terms
+  Pre4 a;
+  pre4(h, sq + b * ACT_LDS_BLOCK, se + 8 * b, ss + 8 * b, a);
+  int32_t* dbg = DBG ? P.dbg + (size_t)row * P.nsub + 8 * b : nullptr;
+  float t[4];
+  Q::half_t4(r, h, a, DBG && lr < rows ? dbg : nullptr, t);
+
+  // 3. the row sums along the lanes
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < LPR; s++) {
+    float v = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xF, 0xF,
+                                                         true));  // wave_shr:1
+    v += t[0];
+    v += t[1];
+    v += t[2];
+    v += t[3];
+    acc = v;
+  }
+  if (owner) S.y[row] = add ? acc + addend : acc;
 }
 
 // total = 0; total += term_s for s = 0 .. n-1 (any n), in that order
@@ -1087,6 +1274,53 @@ TilePlan plain_plan(uint32_t row_bytes, uint32_t k, uint32_t nsub, const uint32_
   return best;
 }
 
+// The row kernel (k_gemv_row) for a plain Q4_K/Q5_K launch of k = 2048 or
+// 4096: waves per workgroup W, R = W * 64 / (2k/256) rows a tile. The
+// largest W of 16, 12, 8, 4, 2, 1 that leaves at least 7/8 of PLAIN_TILES
+// tiles, else W = 1. Measured on MI355X at config 1 (11008 x 2048, 360
+// graph-captured launches over 36 matrices): W = 12 (230 tiles of 48 rows)
+// 4.45 us, W = 4 (688 of 16) 4.46, W = 11 (251 of 44) 4.51; the
+// per-workgroup row-sum kernel (k_gemv_reg) took 5.78.
+struct RowPlan {
+  uint32_t W, R, tiles;
+};
+RowPlan row_plan(uint32_t k, const uint32_t* rows, int nseg) {
+  RowPlan p{};
+  if (k != 2048 && k != 4096) return p;
+  const uint32_t rpw = 64 / (2 * (k / 256));
+  for (uint32_t W : {16u, 12u, 8u, 4u, 2u, 1u}) {
+    uint32_t tiles = 0;
+    for (int i = 0; i < nseg; i++) tiles += (rows[i] + rpw * W - 1) / (rpw * W);
+    p = RowPlan{W, rpw * W, tiles};
+    if (tiles >= PLAIN_TILES * 7 / 8) break;
+  }
+  return p;
+}
+
+template <int T, bool MULTI, bool DBG>
+int launch_row_k(GemvParams& P, const RowPlan& rp, hipStream_t s);
+
+template <int T, bool DBG>
+int launch_row(GemvParams& P, const uint32_t* rows, const RowPlan& rp, hipStream_t s) {
+  P.R = rp.R;
+  uint32_t acc = 0;
+  for (int i = 0; i < P.nseg; i++) {
+    acc += (rows[i] + rp.R - 1) / rp.R;
+    P.tile_end[i] = acc;
+  }
+  if (P.nseg > 1) return launch_row_k<T, true, DBG>(P, rp, s);
+  return launch_row_k<T, false, DBG>(P, rp, s);
+}
+
+template <int T, bool MULTI, bool DBG>
+int launch_row_k(GemvParams& P, const RowPlan& rp, hipStream_t s) {
+  const dim3 g(rp.tiles), b(64 * rp.W);
+  if (P.k == 2048) hipLaunchKernelGGL((k_gemv_row<T, 8, MULTI, DBG>), g, b, 0, s, P);
+  else hipLaunchKernelGGL((k_gemv_row<T, 16, MULTI, DBG>), g, b, 0, s, P);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
 template <int T, bool NORM>
 int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   using Q = KQ<T>;
@@ -1103,6 +1337,10 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   //    two tiles per CU;
   //  - otherwise plain_plan's: the largest R <= 16 that leaves about a
   //    tile per CU (at least 224 tiles).
+  if constexpr (REG) {
+    const RowPlan rp = row_plan(P.k, rows, P.nseg);
+    if (rp.R) return P.dbg ? launch_row<T, true>(P, rows, rp, s) : launch_row<T, false>(P, rows, rp, s);
+  }
   uint32_t total_rows = 0;
   for (int i = 0; i < P.nseg; i++) total_rows += rows[i];
   TilePlan best{};
@@ -1384,6 +1622,11 @@ bool cx_gemv_prefetch_plan(int type, const uint8_t* w, uint32_t n, uint32_t k, c
   }
   if ((type != CX_Q4_K && type != CX_Q5_K) || k % 256 || !n) return false;
   const uint32_t rb = k / 256 * (uint32_t)cx_bpb(type), rows[1] = {n};
+  const RowPlan rp = row_plan(k, rows, 1);
+  if (rp.R) {
+    *job = cx_l2_job{w, nullptr, (size_t)n * rb, rp.R * rb, rp.tiles};
+    return true;
+  }
   const TilePlan t = type == CX_Q4_K ? plain_plan<CX_Q4_K>(rb, k, k / 32, rows, 1)
                                      : plain_plan<CX_Q5_K>(rb, k, k / 32, rows, 1);
   if (!t.R) return false;
