@@ -830,6 +830,63 @@ __global__ __launch_bounds__(1024) void k_gemv_row(GemvParams P) {
   if (owner) S.y[row] = add ? acc + addend : acc;
 }
 
+// k_gemv_reg with one (row, super-block, half) item a lane: the launch has
+// 2 * R * nb lanes rounded up to a wave (at most 1024), and every lane's
+// loads are issued at the start. Used where that fits (the 3B down
+// projection: 8 rows of 43 super-blocks, 688 items, 11 waves): k_gemv_reg's
+// two-slot ring loads a lane's third item only once its first is computed,
+// and the launch waits for that round trip (7.68 -> 7.12 us at 2048 x 11008).
+template <int T>
+__global__ __launch_bounds__(1024) void k_gemv_reg1(GemvParams P) {
+  using Q = KQ<T>;
+  constexpr int SPB = 256 / Q::SUB;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t tile = blockIdx.x;
+  int sg = 0;
+  while (tile >= P.tile_end[sg]) sg++;
+  if (sg) tile -= P.tile_end[sg - 1];
+  const cx_seg S = P.seg[sg];
+  const uint32_t row0 = tile * P.R;
+  const uint32_t rows = min(P.R, S.rows - row0);
+  const float addend = epi_addend(P, S, row0, rows, tid);
+  int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
+  float* se = reinterpret_cast<float*>(lds + P.lds_scale);
+  float* ss = se + P.nsub;
+  float* terms = reinterpret_cast<float*>(lds + P.lds_terms);
+  // the activation into LDS by waves 0-3 (the copies' wave strides assume
+  // four waves), then each lane's item
+  if (wave < 4) {
+    copy_act_padded(P.act.xq, sq, P.nb, wave, lane);
+    copy_to_lds(P.act.xe, se, P.nsub / 4, wave, lane);
+    copy_to_lds(P.act.xs, ss, P.nsub / 4, wave, lane);
+  }
+  const uint32_t items = 2 * rows * P.nb;
+  const uint32_t it = (uint32_t)tid;
+  const uint32_t q = it >> 1, r = q / P.nb, blk = q - r * P.nb;
+  typename Q::Regs buf;
+  if (it < items)
+    Q::load(S.w + (size_t)(row0 + r) * P.row_bytes + (size_t)blk * Q::BPB, (int)(it & 1), buf);
+  // a wave's loads complete in order: waiting for all but its item's loads
+  // waits for its activation loads (a wave with no item: all of them)
+  if ((uint32_t)(tid & ~63) < items) cx_wait_vm<Q::NLOAD>();
+  else cx_wait_vm<0>();
+  cx_barrier();
+  if (it < items) {
+    int32_t* dbg = P.dbg ? P.dbg + (size_t)(row0 + r) * P.nsub + blk * SPB : nullptr;
+    Q::half_regs(buf, (int)(it & 1), sq + blk * ACT_LDS_BLOCK, se + blk * SPB, ss + blk * SPB, dbg,
+                 terms + r * P.tstride + blk * SPB);
+  }
+  __syncthreads();
+
+  // the row's sum in the scalar spec's order (src/kernels/scalar.rs:141-167)
+  if ((uint32_t)tid < rows) {
+    const float acc = row_sum(terms + tid * P.tstride, P.nsub);
+    const uint32_t row = row0 + tid;
+    S.y[row] = (P.epi == CX_EPI_ACCUM || S.bias) ? acc + addend : acc;
+  }
+}
+
 // total = 0; total += term_s for s = 0 .. n-1 (any n), in that order
 __device__ inline float row_sum_any(const float* terms, uint32_t n) {
   float acc = row_sum(terms, n & ~3u);
@@ -1365,8 +1422,16 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
     acc += (rows[i] + best.R - 1) / best.R;
     P.tile_end[i] = acc;
   }
-  if constexpr (REG)
-    hipLaunchKernelGGL((k_gemv_reg<T>), dim3(best.tiles), dim3(256), best.lds, s, P);
+  if constexpr (REG) {
+    // one item a lane where the tile's items fit 1024 lanes (halving the
+    // tile to fit measured slower: config 5's 4096 x 14336 Q5_K down in
+    // 512 tiles of 8 rows took 15.1 us against 13.1 in 256 of 16)
+    const uint32_t th = (2 * best.R * P.nb + 63) / 64 * 64;
+    if (th > 256 && th <= 1024)
+      hipLaunchKernelGGL((k_gemv_reg1<T>), dim3(best.tiles), dim3(th), best.lds, s, P);
+    else
+      hipLaunchKernelGGL((k_gemv_reg<T>), dim3(best.tiles), dim3(256), best.lds, s, P);
+  }
   else
     hipLaunchKernelGGL((k_gemv<T, NORM>), dim3(best.tiles), dim3(256), best.lds, s, P);
   CX_HIP(hipGetLastError());
