@@ -830,6 +830,136 @@ __global__ __launch_bounds__(1024) void k_gemv_row(GemvParams P) {
   if (owner) S.y[row] = add ? acc + addend : acc;
 }
 
+// The row kernel with the rmsnorm prologue (the q/k/v launch): every
+// workgroup makes the normalized, quantized activation itself from the f32
+// residual x and the norm weight w while its weights are in flight. The
+// f64 sum of squares is the same fixed tree as k_gemv's prologue, so the
+// activation is bit for bit that of the other launches: 256 virtual lanes,
+// lane v holding x[8v + 2048j + e]^2 summed over j, then e, in order; each
+// virtual wave's butterfly (cx_wave_sum_d); ((r0 + r1) + r2) + r3. With W < 4
+// waves a thread holds 4/W virtual lanes (virtual wave w + W m), with W > 4
+// only waves 0-3 take part. The normalization and quantization
+// (src/kernels/scalar.rs:40-53, then ops::cuantizar_i8_en) use the same
+// groups of 8 values, into LDS.
+template <int T, int NB, int W, bool MULTI>
+__global__ __launch_bounds__(64 * W) void k_gemv_row_norm(GemvParams P) {
+  using Q = KQ<T>;
+  constexpr int LPR = 2 * NB;     // lanes per row
+  constexpr int RPW = 64 / LPR;   // rows per wave
+  constexpr int NT = 64 * W;
+  constexpr int VT = NT >= 256 ? 1 : 256 / NT;  // virtual lanes a thread
+  constexpr int GJ = NB / 8;                    // 8-value groups a virtual lane (k / 2048)
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16, "power-of-two waves");
+  __shared__ __align__(16) int8_t sq[NB * ACT_LDS_BLOCK];
+  __shared__ __align__(16) float se[8 * NB], ss[8 * NB];
+  __shared__ double red[4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t xb = (uint64_t)P.nx, wb = (uint64_t)P.nw;
+  uint32_t tile = blockIdx.x;
+  int sg = 0;
+  if constexpr (MULTI) {
+    while (tile >= P.tile_end[sg]) sg++;
+    if (sg) tile -= P.tile_end[sg - 1];
+  }
+  const cx_seg S = P.seg[sg];
+  uint64_t wbase = (uint64_t)S.w;
+  uint32_t R = P.R, rb = P.row_bytes, srows = S.rows;
+  asm volatile("" : "+s"(xb), "+s"(wb), "+s"(wbase), "+s"(R), "+s"(rb), "+s"(srows));
+  const uint32_t row0 = tile * R;
+  const uint32_t rows = min(R, srows - row0);
+  const uint32_t lr = (uint32_t)(wave * RPW + lane / LPR);
+  const int b = (lane % LPR) >> 1, h = lane & 1;
+  const bool owner = lr < rows && lane % LPR == LPR - 1;
+
+  // 1. x and w of the thread's groups (L2 hits; threads past 256 reload
+  //    the last virtual lane's), then the weights
+  const float4* const xg = (const float4*)reinterpret_cast<const __attribute__((address_space(1))) float4*>(xb);
+  const float4* const wg = (const float4*)reinterpret_cast<const __attribute__((address_space(1))) float4*>(wb);
+  float4 xv[VT * GJ * 2], wv[VT * GJ * 2];
+#pragma unroll
+  for (int m = 0; m < VT; m++)
+#pragma unroll
+    for (int j = 0; j < GJ; j++) {
+      const uint32_t vt = min((uint32_t)(tid + NT * m), 255u);
+      const uint32_t g = vt + 256u * (uint32_t)j;
+      xv[2 * (m * GJ + j)] = xg[2 * g];
+      xv[2 * (m * GJ + j) + 1] = xg[2 * g + 1];
+      wv[2 * (m * GJ + j)] = wg[2 * g];
+      wv[2 * (m * GJ + j) + 1] = wg[2 * g + 1];
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  typename Q::Regs r;
+  const uint32_t row = row0 + (lr < rows ? lr : rows - 1);
+  Q::load((const uint8_t*)reinterpret_cast<const __attribute__((address_space(1))) uint8_t*>(wbase) +
+              (size_t)row * rb + (size_t)b * Q::BPB, h, r);
+  const bool add = P.epi == CX_EPI_ACCUM || S.bias;
+  const float* addp = P.epi == CX_EPI_ACCUM ? S.y : S.bias;
+  const float addend = add ? addp[row] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. the f64 sum of squares, the tree of k_gemv's prologue
+  const bool in_tree = NT <= 256 || tid < 256;
+#pragma unroll
+  for (int m = 0; m < VT; m++) {
+    double sum = 0.0;
+#pragma unroll
+    for (int j = 0; j < GJ; j++) {
+      const float4 a0 = xv[2 * (m * GJ + j)], a1 = xv[2 * (m * GJ + j) + 1];
+      const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) sum += (double)a[e] * (double)a[e];
+    }
+    sum = cx_wave_sum_d(sum);
+    if (in_tree && lane == 0) red[wave + W * m] = sum;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  cx_wait_lds();
+  cx_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  const double tot = ((red[0] + red[1]) + red[2]) + red[3];
+  const double scale = 1.0 / sqrt(tot / (double)(NB * 256) + (double)P.eps);
+  // 3. v = (x as f64 * scale) as f32 * w, quantized into LDS
+  if (in_tree) {
+#pragma unroll
+    for (int m = 0; m < VT; m++)
+#pragma unroll
+      for (int j = 0; j < GJ; j++) {
+        const float4 a0 = xv[2 * (m * GJ + j)], a1 = xv[2 * (m * GJ + j) + 1];
+        const float4 b0 = wv[2 * (m * GJ + j)], b1 = wv[2 * (m * GJ + j) + 1];
+        const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (float)((double)a[e] * scale) * bw[e];
+        const uint32_t g = (uint32_t)(tid + NT * m) + 256u * (uint32_t)j;
+        cx_quant8_padded<Q::SUB>(v, 8 * g, sq, se, ss);
+      }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  cx_wait_lds();
+  cx_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. the lane's four terms and the row sums along the lanes (k_gemv_row)
+  Pre4 a;
+  pre4(h, sq + b * ACT_LDS_BLOCK, se + 8 * b, ss + 8 * b, a);
+  float t[4];
+  Q::half_t4(r, h, a, nullptr, t);
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < LPR; s++) {
+    float v = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xF, 0xF,
+                                                         true));  // wave_shr:1
+    v += t[0];
+    v += t[1];
+    v += t[2];
+    v += t[3];
+    acc = v;
+  }
+  if (owner) S.y[row] = add ? acc + addend : acc;
+}
+
 // k_gemv_reg with one (row, super-block, half) item a lane: the launch has
 // 2 * R * nb lanes rounded up to a wave (at most 1024), and every lane's
 // loads are issued at the start. Used where that fits (the 3B down
@@ -1378,6 +1508,53 @@ int launch_row_k(GemvParams& P, const RowPlan& rp, hipStream_t s) {
   return CX_OK;
 }
 
+// The q/k/v launch's row kernel: W waves a tile (R = W * 64 / (2k/256)
+// rows), the largest W of 16, 8, 4, 2, 1 that leaves ROW_NORM_TILES tiles.
+// Every workgroup repeats the prologue, so fewer, larger tiles pay:
+// measured on MI355X (graph-captured launches over rotating matrices, q/k/v
+// shapes of 2048 + 256 + 256 rows at k = 2048 and ~6144 rows at k = 4096):
+// 3B 320 tiles of 2 waves 5.10 us, 160 of 4 waves 3.50, 80 of 8 waves 4.49
+// (the LDS-tile k_gemv prologue kernel: 5.92); k = 4096 192 tiles of 16
+// waves 7.83 us, 384 of 8 waves 7.79 (k_gemv: 13.5).
+constexpr uint32_t ROW_NORM_TILES = 128;
+template <int T, int NB, bool MULTI>
+void launch_row_norm_w(uint32_t W, const GemvParams& P, dim3 g, hipStream_t s) {
+  switch (W) {
+    case 16: hipLaunchKernelGGL((k_gemv_row_norm<T, NB, 16, MULTI>), g, dim3(1024), 0, s, P); break;
+    case 8: hipLaunchKernelGGL((k_gemv_row_norm<T, NB, 8, MULTI>), g, dim3(512), 0, s, P); break;
+    case 4: hipLaunchKernelGGL((k_gemv_row_norm<T, NB, 4, MULTI>), g, dim3(256), 0, s, P); break;
+    case 2: hipLaunchKernelGGL((k_gemv_row_norm<T, NB, 2, MULTI>), g, dim3(128), 0, s, P); break;
+    default: hipLaunchKernelGGL((k_gemv_row_norm<T, NB, 1, MULTI>), g, dim3(64), 0, s, P); break;
+  }
+}
+template <int T>
+int launch_row_norm(GemvParams& P, const uint32_t* rows, hipStream_t s) {
+  const uint32_t rpw = 64 / (2 * (P.k / 256));
+  uint32_t W = 1, tiles = 0;
+  for (uint32_t w : {16u, 8u, 4u, 2u, 1u}) {
+    tiles = 0;
+    for (int i = 0; i < P.nseg; i++) tiles += (rows[i] + rpw * w - 1) / (rpw * w);
+    W = w;
+    if (tiles >= ROW_NORM_TILES) break;
+  }
+  P.R = rpw * W;
+  uint32_t acc = 0;
+  for (int i = 0; i < P.nseg; i++) {
+    acc += (rows[i] + P.R - 1) / P.R;
+    P.tile_end[i] = acc;
+  }
+  const dim3 g(acc);
+  if (P.k == 2048) {
+    if (P.nseg > 1) launch_row_norm_w<T, 8, true>(W, P, g, s);
+    else launch_row_norm_w<T, 8, false>(W, P, g, s);
+  } else {
+    if (P.nseg > 1) launch_row_norm_w<T, 16, true>(W, P, g, s);
+    else launch_row_norm_w<T, 16, false>(W, P, g, s);
+  }
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
 template <int T, bool NORM>
 int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   using Q = KQ<T>;
@@ -1397,6 +1574,9 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   if constexpr (REG) {
     const RowPlan rp = row_plan(P.k, rows, P.nseg);
     if (rp.R) return P.dbg ? launch_row<T, true>(P, rows, rp, s) : launch_row<T, false>(P, rows, rp, s);
+  }
+  if constexpr (NORM && (T == CX_Q4_K || T == CX_Q5_K)) {
+    if (P.k == 2048 || P.k == 4096) return launch_row_norm<T>(P, rows, s);
   }
   uint32_t total_rows = 0;
   for (int i = 0; i < P.nseg; i++) total_rows += rows[i];
