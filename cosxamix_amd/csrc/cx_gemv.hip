@@ -1155,6 +1155,138 @@ __global__ __launch_bounds__(256) void k_gemv_glu(GluParams P) {
   }
 }
 
+// The gate/up/SwiGLU launch on the row kernel's layout (Q4_K or Q5_K; the
+// launcher uses it at k = 2048, the template also builds k = 4096): tile t is still gate rows [32t, 32t+32) and the same rows
+// of up, but a lane holds one half super-block of a gate row AND the same
+// half of the same up row, so its activation registers (pre4) serve both.
+// A row's 2·NB lanes sit in one wave (k_gemv_row), the 32 rows fill
+// 32·2·NB/64 waves, every weight load is issued at the start, and the
+// normalized, quantized activation is made per workgroup from the f64 tree
+// of k_gemv_row_norm while the weights are in flight. The gate and up row
+// sums run as two interleaved DPP chains along the row's lanes (the
+// reference's order, from 0), the row's last lane forms silu(g)·u
+// (src/forward.rs:483-487), and four lanes quantize the tile's 32 values
+// for the down projection (sub-blocks of SUB) — the bytes k_gemv_glu writes.
+template <int T, int NB, int SUB>
+__global__ __launch_bounds__(64 * NB) void k_gemv_row_glu(GluParams P) {
+  using Q = KQ<T>;
+  constexpr int LPR = 2 * NB;   // lanes per row
+  constexpr int RPW = 64 / LPR; // rows per wave
+  constexpr int GJ = NB / 8;    // 8-value groups a virtual lane of the f64 tree
+  static_assert(NB == 8 || NB == 16, "k = 2048 or 4096");
+  static_assert(GLU_ROWS * LPR == 64 * NB, "the tile's rows fill the NB waves");
+  __shared__ __align__(16) int8_t sq[NB * ACT_LDS_BLOCK];
+  __shared__ __align__(16) float se[8 * NB], ss[8 * NB];
+  __shared__ double red[4];
+  __shared__ __align__(16) float act[GLU_ROWS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t xb = (uint64_t)P.nx, wb = (uint64_t)P.nw, gb = (uint64_t)P.wg, ub = (uint64_t)P.wu;
+  uint32_t rb = P.row_bytes;
+  asm volatile("" : "+s"(xb), "+s"(wb), "+s"(gb), "+s"(ub), "+s"(rb));
+  const uint32_t row0 = blockIdx.x * GLU_ROWS;
+  const uint32_t lr = (uint32_t)(wave * RPW + lane / LPR);  // the lane's row in the tile
+  const int b = (lane % LPR) >> 1, h = lane & 1;
+  const bool owner = lane % LPR == LPR - 1;
+
+  // 1. waves 0-3 (the tree's 256 virtual lanes) load x and w (L2 hits),
+  //    then every lane its gate and up halves
+  const float4* const xg = (const float4*)reinterpret_cast<const __attribute__((address_space(1))) float4*>(xb);
+  const float4* const wg = (const float4*)reinterpret_cast<const __attribute__((address_space(1))) float4*>(wb);
+  float4 xv[GJ * 2], wv[GJ * 2];
+  if (wave < 4) {
+#pragma unroll
+    for (int j = 0; j < GJ; j++) {
+      const uint32_t g = (uint32_t)tid + 256u * (uint32_t)j;
+      xv[2 * j] = xg[2 * g];
+      xv[2 * j + 1] = xg[2 * g + 1];
+      wv[2 * j] = wg[2 * g];
+      wv[2 * j + 1] = wg[2 * g + 1];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  typename Q::Regs rg, ru;
+  const size_t off = (size_t)(row0 + lr) * rb + (size_t)b * Q::BPB;
+  Q::load((const uint8_t*)reinterpret_cast<const __attribute__((address_space(1))) uint8_t*>(gb) + off, h, rg);
+  Q::load((const uint8_t*)reinterpret_cast<const __attribute__((address_space(1))) uint8_t*>(ub) + off, h, ru);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. the f64 sum of squares (the tree of k_gemv's prologue)
+  if (wave < 4) {
+    double sum = 0.0;
+#pragma unroll
+    for (int j = 0; j < GJ; j++) {
+      const float4 a0 = xv[2 * j], a1 = xv[2 * j + 1];
+      const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) sum += (double)a[e] * (double)a[e];
+    }
+    sum = cx_wave_sum_d(sum);
+    if (lane == 0) red[wave] = sum;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  cx_wait_lds();
+  cx_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  const double tot = ((red[0] + red[1]) + red[2]) + red[3];
+  const double scale = 1.0 / sqrt(tot / (double)(NB * 256) + (double)P.eps);
+  // 3. v = (x as f64 * scale) as f32 * w, quantized into LDS
+  if (wave < 4) {
+#pragma unroll
+    for (int j = 0; j < GJ; j++) {
+      const float4 a0 = xv[2 * j], a1 = xv[2 * j + 1];
+      const float4 b0 = wv[2 * j], b1 = wv[2 * j + 1];
+      const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const float bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = (float)((double)a[e] * scale) * bw[e];
+      const uint32_t g = (uint32_t)tid + 256u * (uint32_t)j;
+      cx_quant8_padded<Q::SUB>(v, 8 * g, sq, se, ss);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  cx_wait_lds();
+  cx_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. the lane's four gate and four up terms, one activation read for both
+  Pre4 a;
+  pre4(h, sq + b * ACT_LDS_BLOCK, se + 8 * b, ss + 8 * b, a);
+  float tg[4], tu[4];
+  Q::half_t4(rg, h, a, nullptr, tg);
+  Q::half_t4(ru, h, a, nullptr, tu);
+  // 5. both row sums along the lanes, then SwiGLU on the row's last lane
+  float accg = 0.0f, accu = 0.0f;
+#pragma unroll
+  for (int s = 0; s < LPR; s++) {
+    float vg = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(accg), 0x138, 0xF, 0xF,
+                                                          true));  // wave_shr:1
+    float vu = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(accu), 0x138, 0xF, 0xF,
+                                                          true));
+    vg += tg[0];
+    vu += tu[0];
+    vg += tg[1];
+    vu += tu[1];
+    vg += tg[2];
+    vu += tu[2];
+    vg += tg[3];
+    vu += tu[3];
+    accg = vg;
+    accu = vu;
+  }
+  if (owner) act[lr] = cx_swiglu(accg, accu);
+  cx_wait_lds();
+  cx_barrier();
+  // 6. the down projection's quantization of the tile's 32 values
+  if (tid < (int)(GLU_ROWS / 8)) {
+    const float4 v0 = reinterpret_cast<const float4*>(act)[2 * tid];
+    const float4 v1 = reinterpret_cast<const float4*>(act)[2 * tid + 1];
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    cx_quant8<SUB>(v, row0 + 8 * tid, P.xq, P.xe, P.xs);
+  }
+}
+
 // ------------------------------------------- 32-value blocks (Q8_0, Q5_0)
 // The buffer path of the reference for these formats (ops::matmul_i8_directo
 // and matmul_varias_una_fila, src/ops.rs:310-414, 968-993): the row unpacked
@@ -1821,6 +1953,23 @@ int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t 
   P.xq = xq;
   P.xe = xe;
   P.xs = xs;
+  if (k == 2048) {
+    // the row layout: 32 rows of gate and up in 8 waves (the 3B shape:
+    // 8.71 -> 7.75 us a launch, weights in L2). At k = 4096 (16 waves a
+    // tile, 448 tiles: config 5's 14336 x 4096, 66 MB past L2) it measured
+    // 20.4 us against k_gemv_glu's 16.3, which keeps that shape.
+    const dim3 grid(I / GLU_ROWS), block(64 * (k / 256));
+#define CX_ROW_GLU(TT, NB)                                                              \
+  do {                                                                                  \
+    if (sub == 32) hipLaunchKernelGGL((k_gemv_row_glu<TT, NB, 32>), grid, block, 0, s, P); \
+    else hipLaunchKernelGGL((k_gemv_row_glu<TT, NB, 16>), grid, block, 0, s, P);          \
+  } while (0)
+    if (type == CX_Q4_K) CX_ROW_GLU(CX_Q4_K, 8);
+    else CX_ROW_GLU(CX_Q5_K, 8);
+#undef CX_ROW_GLU
+    CX_HIP(hipGetLastError());
+    return CX_OK;
+  }
   // LDS: [xq, 272 bytes per 256][xe, xs][norm input (2k floats), then the
   // terms (64 x (nsub + 4))][64 row sums]
   P.lds_scale = P.nb * ACT_LDS_BLOCK;

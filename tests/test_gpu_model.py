@@ -53,6 +53,10 @@ CASES = [
                               contexto=200, rope=10000.0), O.Q5_K, O.Q3_K),
     ("mini-q4k-q2kdown", dict(capas=2, dim=768, cabezas=6, cabezas_kv=2, ffn=2304, vocab=900,
                               contexto=200, rope=10000.0), O.Q4_K, O.Q2_K),
+    # k = 2048: the row-layout gate/up/SwiGLU launch for Q5_K, quantizing for
+    # a down of 16-value sub-blocks
+    ("2048-q5k-q3kdown", dict(capas=1, dim=2048, cabezas=16, cabezas_kv=2, ffn=1024, vocab=1000,
+                              contexto=200, rope=1e6), O.Q5_K, O.Q3_K),
 ]
 
 
