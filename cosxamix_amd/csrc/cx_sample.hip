@@ -43,7 +43,7 @@ namespace {
 constexpr uint32_t ZB = 256;         // threads of the grid kernels
 constexpr uint32_t ZV = 8;           // values per thread of the grid kernels
 constexpr uint32_t CW = 1024;        // threads of the single-workgroup kernels
-constexpr uint32_t SEG = 2048;       // floats per chain stage (8 KiB: one KiB per loader wave)
+constexpr uint32_t SEG = 4096;       // floats per chain stage (16 KiB: two KiB per loader wave)
 constexpr uint32_t NST = 8;          // chain stages in the LDS ring
 constexpr uint32_t CAND = 1024;      // CANDIDATOS (src/sampler.rs): the first nucleus
 constexpr uint32_t RS_T = 256;       // threads of a radix-sort workgroup
@@ -115,9 +115,10 @@ __global__ __launch_bounds__(ZB) void k_samp_p(float* pb, uint32_t n, const cx_s
 }
 
 // ---------------------------------------------------------- ordered sums
-// A ring of NST stages of SEG floats: loader waves 1..8 each load one KiB of
-// every stage; stage s sits in slot s % NST. Wave 0 walks the stages in
+// A ring of NST stages of SEG floats: loader waves 1..8 each load SEG / 8
+// floats of every stage (1 KiB DMA loads); stage s sits in slot s % NST. Wave 0 walks the stages in
 // order; after each stage every wave learns whether it stopped.
+static_assert(SEG % 2048 == 0, "whole 1 KiB loads for each of the 8 loader waves");
 struct Ring {
   float* lds;
   const float* src;
@@ -125,32 +126,38 @@ struct Ring {
   uint32_t wave, lane;
   __device__ void issue(uint32_t s) {
     if (wave < 1 || wave > 8) return;
-    const uint32_t i = s * SEG + (wave - 1) * 256 + 4 * lane;
-    cx_dma16_async(src + (i < n ? i : 0), lds + (s % NST) * SEG + (wave - 1) * 256);
+#pragma unroll
+    for (uint32_t h = 0; h < SEG / 2048; h++) {
+      const uint32_t o = (wave - 1) * (SEG / 8) + 256 * h, i = s * SEG + o + 4 * lane;
+      cx_dma16_async(src + (i < n ? i : 0), lds + (s % NST) * SEG + o);
+    }
     issued++;
   }
-  // loader waves: this wave's loads up to stage s have landed (one a stage)
+  // loader waves: this wave's loads up to stage s have landed (SEG / 2048 a
+  // stage, NST - 1 stages at most after it)
   __device__ void wait(uint32_t s) {
     if (wave < 1 || wave > 8) return;
+    constexpr uint32_t L = SEG / 2048;
     const uint32_t after = issued - (s + 1);
     switch (after) {
       case 0: cx_wait_vm<0>(); break;
-      case 1: cx_wait_vm<1>(); break;
-      case 2: cx_wait_vm<2>(); break;
-      case 3: cx_wait_vm<3>(); break;
-      case 4: cx_wait_vm<4>(); break;
-      case 5: cx_wait_vm<5>(); break;
-      case 6: cx_wait_vm<6>(); break;
-      default: cx_wait_vm<7>(); break;
+      case 1: cx_wait_vm<L>(); break;
+      case 2: cx_wait_vm<2 * L>(); break;
+      case 3: cx_wait_vm<3 * L>(); break;
+      case 4: cx_wait_vm<4 * L>(); break;
+      case 5: cx_wait_vm<5 * L>(); break;
+      case 6: cx_wait_vm<6 * L>(); break;
+      default: cx_wait_vm<7 * L>(); break;
     }
   }
 };
 
 // Walks x[0..n) in order through the ring: `stage(v, m, base)` runs on wave
-// 0 for each stage (m values at LDS v, indices base..; +0.0 from m to the
-// next multiple of 16) and returns true, the same in every lane, to stop.
-// Every wave leaves with every load landed.
-template <class F>
+// 0 for each stage (with ALL, on every wave) (m values at LDS v, indices
+// base..; +0.0 from m to the next multiple of 16) and returns true, the same
+// in every lane (with ALL, in every thread), to stop. Every wave leaves with
+// every load landed.
+template <bool ALL = false, class F>
 __device__ inline void chain_walk(const float* x, uint32_t n, float* lds, F stage) {
   __shared__ uint32_t stop;
   const uint32_t tid = threadIdx.x;
@@ -163,7 +170,13 @@ __device__ inline void chain_walk(const float* x, uint32_t n, float* lds, F stag
     cx_wait_lds();
     cx_barrier();  // stage s landed; `stop` from the last stage is visible
     if (stop) break;
-    if (R.wave == 0) {
+    if (ALL) {
+      float* v = lds + (s % NST) * SEG;
+      const uint32_t m = min(SEG, n - s * SEG);
+      // (wave 0 pads what only wave 0 reads: the other waves read below m)
+      if (R.wave == 0 && R.lane < (16 - m % 16) % 16) v[m + R.lane] = 0.0f;
+      if (stage(v, m, s * SEG) && tid == 0) stop = 1;
+    } else if (R.wave == 0) {
       float* v = lds + (s % NST) * SEG;
       const uint32_t m = min(SEG, n - s * SEG);
       if (R.lane < (16 - m % 16) % 16) v[m + R.lane] = 0.0f;  // the loads past n hold x[0..]
@@ -178,6 +191,108 @@ __device__ inline void chain_walk(const float* x, uint32_t n, float* lds, F stag
   __syncthreads();
 }
 
+// One chain stage of a running sum (seq_scan's sum or search) by the whole
+// workgroup. Waves 0..MW_WIN-1 take 256-position windows in parallel, all in
+// the binade E of the running sum s where they start (unit u = 2^(E-23)): a
+// window's total N_w of rne(x/u), and whether it holds a tie or a term that
+// is not finite. While no window has such an event, the running sum reaches
+// no 2^(E+1) and, for a search, no window's last running sum passes the
+// target, every add of those windows is an exact integer add in units of u
+// (seq_scan's argument), so their sums are exactly s + u·(N_0 + N_1 + ...).
+// Wave 0 finds the first window where that fails and runs seq_scan over
+// that window alone (the event added as one f32 add, the crossing found
+// there); the windows after it start again in the new binade. The stage at
+// base 0 (the head's one-by-one adds) and a sum that is not finite go to
+// seq_scan whole. Every thread returns the sum, and *at = the crossing's
+// index in the stage or m.
+constexpr uint32_t MW_WIN = SEG / 256;
+static_assert(MW_WIN <= CW / 64 && MW_WIN <= 64, "a wave a window, a lane a window's total");
+template <int M>
+__device__ inline float stage_scan_mw(const float* v, uint32_t m, float tot, bool head,
+                                      float target, uint32_t* at) {
+  constexpr bool FIND = M != SCAN_SUM;
+  __shared__ float sN[MW_WIN];
+  __shared__ uint32_t sbad[MW_WIN];
+  __shared__ float s_tot;
+  __shared__ uint32_t s_at, s_w0;
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t nw = (m + 255) / 256;
+  float s = tot;
+  uint32_t w0 = 0, where = m;
+  for (;;) {
+    const bool whole = (head && w0 == 0) || !(s < INFINITY);
+    const int E = binade_of(s), k = 23 - E;
+    if (!whole) {
+      if (wave < MW_WIN) {
+        const uint32_t p = 256 * (w0 + wave) + 4 * lane;
+        float c = 0.0f;
+        bool bad = false;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+          const float x = p + i < m ? v[p + i] : 0.0f;
+          const float q = ldexpf(x, k), r = rintf(q);  // x / u is exact (inf past 2^128)
+          bad |= !(fabsf(q - r) < 0.5f);               // a tie, or not finite
+          c += r;
+        }
+        // the window's total: exact below 2^24, and at or above it otherwise
+        const float P = wave_scan_incl(c);
+        const uint64_t b = __builtin_amdgcn_ballot_w64(bad);
+        if (lane == 63) {
+          sN[wave] = P;
+          sbad[wave] = b != 0;
+        }
+      }
+      cx_wait_lds();
+      __syncthreads();
+    }
+    if (wave == 0) {
+      uint32_t from = 256 * w0, to = m, next = nw;
+      if (!whole) {
+        const float A0 = ldexpf(s, k);  // s / u, an integer below 2^24
+        const uint32_t cnt = min(nw - w0, MW_WIN);
+        const float N = lane < cnt ? sN[lane] : 0.0f;
+        const float P = wave_scan_incl(N);  // the sums through each window
+        const bool ev = lane < cnt && (sbad[lane] || A0 + P >= 16777216.0f ||
+                                       (FIND && scan_passes<M>(ldexpf(A0 + P, -k), target)));
+        const uint32_t j = min(first_lane(__builtin_amdgcn_ballot_w64(ev)), cnt);
+        const float before =
+            j ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(P), (int)(j - 1))) : 0.0f;
+        s = ldexpf(A0 + before, -k);  // exact: every window before j is event-free
+        if (j < cnt) {  // window w0 + j by seq_scan, the next round after it
+          from = 256 * (w0 + j);
+          to = min(m, from + 256);
+          next = w0 + j + 1;
+        } else {
+          from = to = 0;
+          next = w0 + cnt;
+        }
+      }
+      if (from < to) {
+        uint32_t kr = to - from;
+        s = seq_scan<M>(v + from, to - from, s, head && from == 0, target, FIND ? &kr : nullptr);
+        if (FIND && kr < to - from) {
+          where = from + kr;
+          next = nw;
+        }
+      }
+      if (lane == 0) {
+        s_tot = s;
+        s_at = where;
+        s_w0 = next;
+      }
+    }
+    cx_wait_lds();
+    __syncthreads();
+    s = s_tot;
+    where = s_at;
+    w0 = s_w0;
+    __syncthreads();  // every thread has read them before they are written again
+    if (w0 >= nw) break;
+  }
+  *at = where;
+  return s;
+}
+
 // The running sum of x[0..n) continued from *acc: the first index where it
 // exceeds target (M = SCAN_EXCEED) or reaches it (SCAN_REACH), or n; *acc
 // ends as the sum through that index, or through x[n - 1]. x >= 0 (or NaN).
@@ -189,11 +304,11 @@ __device__ inline uint32_t chain_find(const float* x, uint32_t n, float* lds, fl
   __syncthreads();  // every read of the last call's s_at and *acc is done
   float a = *acc;
   if (threadIdx.x == 0) s_at = n;
-  chain_walk(x, n, lds, [&](const float* v, uint32_t m, uint32_t base) {
+  chain_walk<true>(x, n, lds, [&](const float* v, uint32_t m, uint32_t base) {
     uint32_t k;
-    a = seq_scan<M>(v, m, a, base == 0, target, &k);
+    a = stage_scan_mw<M>(v, m, a, base == 0, target, &k);
     if (k < m) {
-      if ((threadIdx.x & 63) == 0) s_at = base + k;
+      if (threadIdx.x == 0) s_at = base + k;
       return true;
     }
     return false;
@@ -224,8 +339,9 @@ __global__ __launch_bounds__(CW) void k_samp_sum(const float* pb, uint32_t n, cx
   }
   if (sd->uniform) return;
   float tot = 0.0f;
-  chain_walk(pb, n, ring, [&](const float* v, uint32_t m, uint32_t base) {
-    tot = seq_sum_scan(v, m, tot, base == 0);
+  chain_walk<true>(pb, n, ring, [&](const float* v, uint32_t m, uint32_t base) {
+    uint32_t k;
+    tot = stage_scan_mw<SCAN_SUM>(v, m, tot, base == 0, 0.0f, &k);
     return false;
   });
   if (threadIdx.x == 0) sd->inv_s = 1.0f / tot;
