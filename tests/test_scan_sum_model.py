@@ -241,3 +241,102 @@ def test_scan_search_on_the_sums_and_nan():
     assert got == seq_find(x, 0.0, F(0.05), "reach")
     got = scan(x, 0.0, 256, "reach", F(0.5))
     assert got[1] == 900 and np.isnan(got[0])
+
+
+# ---------------------------------------------------------------------------
+# The sampler's workgroup version (stage_scan_mw, cosxamix_amd/csrc/
+# cx_sample.hip): stages of SEG positions; stage 0 (the head) and a sum that
+# is not finite go to scan() whole; otherwise up to 16 windows of 256 are
+# summed in parallel in units of the binade of the running sum where they
+# start, the totals combined in order, and the first window with an event
+# (a tie or a term that is not finite, the running sum reaching 2^(E+1), or
+# for a search a window-end sum that passes the target) runs through scan()
+# alone; the windows after it start again in the new binade.
+SEG, WIN = 4096, 256
+
+
+def _window_total(w, k):
+    q = np.ldexp(w.astype(np.float64), k)  # x / u exact in f64
+    r = np.rint(q)
+    bad = bool(np.any(~(np.abs(q - r) < 0.5)))
+    return r.sum(), bad  # exact integers (or inf/NaN with `bad` set)
+
+
+def stage_scan(v, tot, head, mode, target):
+    find = mode != "sum"
+    m, nw = len(v), (len(v) + WIN - 1) // WIN
+    s, w0 = F(tot), 0
+    while w0 < nw:
+        if (head and w0 == 0) or not np.isfinite(s):
+            t, at = scan(v[WIN * w0:], s, head and w0 == 0, mode, target)
+            return t, (WIN * w0 + at if at < m - WIN * w0 else m)
+        E = _binade(s)
+        k = 23 - E
+        A0 = float(np.ldexp(np.float64(s), k))
+        cnt = min(nw - w0, SEG // WIN)
+        run, j = A0, cnt
+        for i in range(cnt):
+            N, bad = _window_total(v[WIN * (w0 + i): WIN * (w0 + i + 1)], k)
+            end = run + N
+            if bad or end >= 2.0 ** 24 or (find and _passes(F(np.ldexp(end, -k)), target, mode)):
+                j = i
+                break
+            run = end
+        s = F(np.ldexp(run, -k))
+        if j == cnt:
+            w0 += cnt
+            continue
+        lo = WIN * (w0 + j)
+        t, at = scan(v[lo: lo + WIN], s, 0, mode, target)
+        if find and at < len(v[lo: lo + WIN]):
+            return t, lo + at
+        s, w0 = t, w0 + j + 1
+    return s, m
+
+
+def chain(x, tot=0.0, mode="sum", target=0.0):
+    x = np.asarray(x, F)
+    s = F(tot)
+    for b in range(0, len(x), SEG):
+        s, at = stage_scan(x[b: b + SEG], s, b == 0, mode, F(target))
+        if at < len(x[b: b + SEG]):
+            return s, b + at
+    return s, len(x)
+
+
+@pytest.mark.parametrize("mode", ["normal", "sink", "bimodal", "ties", "tiny", "wide"])
+def test_workgroup_stage_scan_equals_sequential(mode):
+    rng = np.random.default_rng(40 + ["normal", "sink", "bimodal", "ties", "tiny", "wide"].index(mode))
+    for n in (1, 300, 4096, 4097, 9000, 20000):
+        x = _exps(rng, n, mode)
+        assert _same(chain(x)[0], seq_sum(x)), (mode, n)
+        p = (x * F(F(1.0) / seq_sum(x))).astype(F)
+        for order in ("index", "descending"):
+            y = -np.sort(-p) if order == "descending" else p
+            run = np.cumsum(y, dtype=F)
+            for target in (F(rng.random()), F(0.9), run[n // 2], run[min(n - 1, 5000)],
+                           np.nextafter(run[n // 3], F(0)), F(2.0), F(np.nan)):
+                for search in ("exceed", "reach"):
+                    got, want = chain(y, 0.0, search, target), seq_find(y, 0.0, target, search)
+                    assert got[1] == want[1] and _same(got[0], want[0]), (mode, n, order, target,
+                                                                          search, got, want)
+
+
+def test_workgroup_stage_scan_events_inside_a_stage():
+    # every term 1 from 4096: the sum crosses 2^13 and 2^14 inside stages;
+    # halfway terms after the head; a NaN in the third stage
+    x = np.ones(20000, F)
+    assert chain(x)[0] == seq_sum(x)
+    u = F(np.ldexp(F(1.0), _binade(F(4096.0)) - 23))
+    y = np.ones(12000, F)
+    y[5000:5100] = u * F(0.5)
+    y[7001] = u * F(1.5)
+    assert _same(chain(y)[0], seq_sum(y))
+    y[9000] = np.nan
+    assert np.isnan(chain(y)[0]) and np.isnan(seq_sum(y))
+    run = np.cumsum(y[:8999], dtype=F)
+    # (the halfway terms at 5000.. leave the sum where it is: ties to even)
+    for j in (4096, 4097, 5050, 7001, 8191, 8192, 8998):
+        for search in ("reach", "exceed"):
+            got, want = chain(y, 0.0, search, run[j]), seq_find(y, 0.0, run[j], search)
+            assert got[1] == want[1] and _same(got[0], want[0]), (j, search)
