@@ -118,8 +118,23 @@ SIGNATURES = {
 }
 
 
+CX_OK, CX_EINVAL, CX_EHIP, CX_ENOMEM, CX_ENOTSUP = 0, -1, -2, -3, -4
+
+
 class CxError(RuntimeError):
     pass
+
+
+class CacheLlena(CxError):
+    """Generation stopped because the cache was full before it ended
+    (CX_ENOMEM). ``tokens`` holds the tokens made until then, as the C ABI
+    returns them in out/n_out, and ``tiempos`` their step times when they
+    were asked for."""
+
+    def __init__(self, msg, tokens, tiempos=None):
+        super().__init__(msg)
+        self.tokens = tokens
+        self.tiempos = tiempos
 
 
 _lib = None

@@ -28,8 +28,10 @@ static thread_local int g_device = 0;
 
 // Per-device pools of thread contexts. A thread takes a context at its first
 // call on a device and gives it back when it ends; a context is never freed,
-// so no thread can see its stream or scratch released under it. The pool
-// only grows to the largest number of threads that ran at once.
+// so no thread can see its stream released under it, and its scratch is
+// stream-ordered: the next thread's first use waits (on the device, in
+// stream order) for the work the previous holder left queued. The pool only
+// grows to the largest number of threads that ran at once.
 static std::mutex g_pool_mu;
 static std::vector<cx_lib*> g_pool[64];
 
@@ -60,33 +62,67 @@ cx_lib* cx_lib_get() {
   if (!L) {
     if (hipSetDevice(dev) != hipSuccess) return nullptr;
     hipStream_t s = nullptr;
+    hipEvent_t ev = nullptr;
     if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    L = new cx_lib{dev, s, nullptr, 0};
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+      (void)hipStreamDestroy(s);
+      return nullptr;
+    }
+    L = new cx_lib{dev, s, nullptr, 0, ev, false};
   }
   t_ctx.ctx[dev] = L;
   return L;
 }
 
-// The calling thread's scratch of at least `bytes`. Growing it waits for the
-// device (the old buffer may still be read by this thread's earlier calls on
-// any stream) before the old buffer is freed.
-int cx_scratch_reserve(size_t bytes, void** out) {
+static bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// The calling thread's scratch of at least `bytes`, for work about to be
+// enqueued on stream s. s first waits for the `used` event, which follows
+// every earlier use of the scratch on any stream (each use waited for the
+// one before it), by this thread or by the thread that held the context
+// before. Growing frees the old buffer and allocates the new one in s's
+// order (hipFreeAsync/hipMallocAsync) after those uses, so no other stream
+// or thread is waited for. Under stream capture the scratch cannot grow and
+// the captured work is not ordered after earlier uses: the caller orders its
+// graph's launches, as for any captured work.
+int cx_scratch_acquire(size_t bytes, hipStream_t s, void** out) {
   cx_lib* L = cx_lib_get();
   if (!L) {
     cx_set_error("no HIP device %d", g_device);
     return CX_EHIP;
   }
+  const bool cap = capturing(s);
+  if (!cap && L->used_valid) CX_HIP(hipStreamWaitEvent(s, L->used, 0));
   if (L->scratch_bytes < bytes) {
+    CX_REQUIRE(!cap,
+               "the calling thread's scratch must grow to %zu bytes while the stream is being "
+               "captured: make the same call once before the capture, or use "
+               "cx_matmul_auto_noalloc",
+               bytes);
     CX_HIP(hipSetDevice(L->device));
-    CX_HIP(hipDeviceSynchronize());
-    if (L->scratch) CX_HIP(hipFree(L->scratch));
+    if (L->scratch) CX_HIP(hipFreeAsync(L->scratch, s));
     L->scratch = nullptr;
     L->scratch_bytes = 0;
-    CX_HIP(hipMalloc(&L->scratch, bytes));
+    CX_HIP(hipMallocAsync(&L->scratch, bytes, s));
     L->scratch_bytes = bytes;
   }
   *out = L->scratch;
   return CX_OK;
+}
+
+void cx_scratch_release(hipStream_t s) {
+  cx_lib* L = cx_lib_get();
+  if (!L || capturing(s)) return;
+  if (hipEventRecord(L->used, s) == hipSuccess) {
+    L->used_valid = true;
+    return;
+  }
+  // without the event the next use could not be ordered: finish the work
+  (void)hipStreamSynchronize(s);
+  L->used_valid = false;
 }
 
 static int noalloc_scratch(int dev, void** out);
@@ -97,10 +133,15 @@ extern "C" int cx_init(int device) {
   CX_REQUIRE(device >= 0 && device < n && device < 64, "cx_init: device %d of %d", device, n);
   g_device = device;
   CX_HIP(hipSetDevice(device));
+  // the allocation-free entry point's array is looked up here; a failure
+  // is not cx_init's: that entry point tries again and reports it
   void* sp = nullptr;
-  int rc = noalloc_scratch(device, &sp);
-  if (rc) return rc;
-  return cx_lib_get() ? CX_OK : CX_EHIP;
+  (void)noalloc_scratch(device, &sp);
+  if (!cx_lib_get()) {
+    cx_set_error("cx_init: no stream on device %d", device);
+    return CX_EHIP;
+  }
+  return CX_OK;
 }
 
 extern "C" size_t cx_row_bytes(int type, size_t k) {
@@ -125,10 +166,11 @@ static float dot_host(int type, const uint8_t* b, const int8_t* xq, const float*
   const size_t k = nb * 256, nsub = k / cx_sub(type), rb = nb * cx_bpb(type);
   const size_t o_x = (rb + 255) / 256 * 256, o_e = o_x + k, o_s = o_e + nsub * 4,
                o_y = o_s + nsub * 4, total = o_y + 256;
-  void* sp = nullptr;
-  if (cx_scratch_reserve(total, &sp)) return NAN;
-  uint8_t* d = (uint8_t*)sp;
   hipStream_t s = L->stream;
+  void* sp = nullptr;
+  cx_scratch scr(s);
+  if (scr.get(total, &sp)) return NAN;
+  uint8_t* d = (uint8_t*)sp;
   if (hipMemcpyAsync(d, b, rb, hipMemcpyHostToDevice, s) != hipSuccess ||
       hipMemcpyAsync(d + o_x, xq, k, hipMemcpyHostToDevice, s) != hipSuccess ||
       hipMemcpyAsync(d + o_e, xe, nsub * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
@@ -188,7 +230,8 @@ extern "C" int cx_gemv(int type, const uint8_t* w, size_t n, size_t k, const int
 extern "C" int cx_gemv_subsums(int type, const uint8_t* w, size_t n, size_t k, const int8_t* xq,
                                const float* xe, const float* xs, int32_t* out, void* stream) {
   void* sp = nullptr;
-  int rc = cx_scratch_reserve(n * sizeof(float) + 256, &sp);
+  cx_scratch scr(STREAM(stream));
+  int rc = scr.get(n * sizeof(float) + 256, &sp);
   if (rc) return rc;
   return gemv_quantized(type, w, n, k, xq, xe, xs, (float*)sp, out, STREAM(stream));
 }
@@ -200,8 +243,8 @@ extern "C" int cx_quantize_blocks(int type, const float* x, size_t n, uint8_t* o
 
 // The i8 activation of `rows` rows of k values in the library's scratch:
 // xq (rows*k bytes), xe and xs (rows*k/sub floats each), for each sub-block
-// size asked for. The scratch is shared by every call on the device, so
-// these operators are stream-ordered with each other only on one stream.
+// size asked for, in the calling thread's scratch (held by `scr` for the
+// call's work).
 namespace {
 struct QuantScratch {
   int8_t* xq = nullptr;
@@ -214,12 +257,13 @@ struct QuantScratch {
 };
 }  // namespace
 
-static int quant_scratch(size_t rows, size_t k, QuantScratch* q16, QuantScratch* q32) {
+static int quant_scratch(cx_scratch& scr, size_t rows, size_t k, QuantScratch* q16,
+                         QuantScratch* q32) {
   auto up = [](size_t b) { return (b + 255) / 256 * 256; };
   const size_t xq_b = up(rows * k);
   auto part = [&](int sub) { return xq_b + 2 * up(rows * (k / sub) * 4); };
   void* sp = nullptr;
-  int rc = cx_scratch_reserve((q16 ? part(16) : 0) + (q32 ? part(32) : 0), &sp);
+  int rc = scr.get((q16 ? part(16) : 0) + (q32 ? part(32) : 0), &sp);
   if (rc) return rc;
   uint8_t* p = (uint8_t*)sp;
   auto carve = [&](QuantScratch* q, int sub) {
@@ -251,7 +295,8 @@ extern "C" int cx_dequantize_rows(int type, const uint8_t* data, size_t width, s
   }
   if (!n_rows) return CX_OK;
   void* sp = nullptr;
-  int rc = cx_scratch_reserve(n_rows * 4, &sp);
+  cx_scratch scr(STREAM(stream));
+  int rc = scr.get(n_rows * 4, &sp);
   if (rc) return rc;
   CX_HIP(hipMemcpyAsync(sp, ids.data(), n_rows * 4, hipMemcpyHostToDevice, STREAM(stream)));
   rc = cx_launch_dequantize_rows(type, data, (uint32_t)width, (const uint32_t*)sp, n_rows, y,
@@ -268,33 +313,41 @@ extern "C" int cx_unpack_i8(int type, const uint8_t* bytes, size_t n, int8_t* q,
   return rc;
 }
 
-// Scratch bytes cx_matmul_auto needs for m rows of k values of `type`: the
-// MFMA contraction's padded rows for m > 1, the rows' i8 quantization for
-// the row-by-row GEMV, nothing for F32/F16.
+// The argument checks of cx_matmul_auto and cx_matmul_auto_noalloc, made
+// before any scratch is sized or taken.
+static int matmul_auto_check(size_t k, size_t n, const float* lhs, const uint8_t* w, int type,
+                             float* dst) {
+  CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
+  // src/ops.rs:1064-1071: the unquantized formats take the f32 path
+  if (type == CX_F32 || type == CX_F16) return CX_OK;
+  CX_REQUIRE(cx_has_gemv(type), "matmul_auto: type %d has no quantized path here", type);
+  CX_REQUIRE(k % (size_t)cx_vpb(type) == 0, "matmul_auto: a row of %zu is not a multiple of the block of %d",
+             k, cx_vpb(type));
+  CX_REQUIRE(n < (1u << 31) && k < (1u << 31), "matmul_auto: shape too large");
+  return CX_OK;
+}
+
+// Scratch bytes cx_matmul_auto needs for m rows of k values of `type` (a
+// type matmul_auto_check accepts): the MFMA contraction's padded rows for
+// m > 1, the rows' i8 quantization for the row-by-row GEMV, nothing for
+// F32/F16.
 static size_t matmul_auto_scratch(size_t m, size_t k, int type) {
-  if (type == CX_F32 || type == CX_F16 || !m) return 0;
+  if (type == CX_F32 || type == CX_F16 || !m || !cx_sub(type)) return 0;
   if (m > 1 && cx_gemm_supported(type)) return cx_gemm_scratch_bytes(m, k);
   auto up = [](size_t b) { return (b + 255) / 256 * 256; };
   return up(m * k) + 2 * up(m * (k / cx_sub(type)) * 4);
 }
 
-// cx_matmul_auto on a given scratch (at least matmul_auto_scratch bytes,
-// 256-byte aligned); `reserve` when the thread's own scratch is to be used
+// cx_matmul_auto, after matmul_auto_check, on a given scratch (at least
+// matmul_auto_scratch bytes, 256-byte aligned), or on the calling thread's
+// own scratch when `scratch` is NULL
 static int matmul_auto_on(size_t m, size_t k, size_t n, const float* lhs, const uint8_t* w,
-                          int type, float* dst, void* scratch, bool reserve, hipStream_t s) {
-  // src/ops.rs:1064-1071: the unquantized formats take the f32 path
-  if (type == CX_F32 || type == CX_F16) {
-    CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
-    return cx_launch_matmul_f(type, w, n, k, lhs, m, dst, s);
-  }
-  CX_REQUIRE(cx_has_gemv(type), "matmul_auto: type %d has no quantized path here", type);
-  CX_REQUIRE(k % (size_t)cx_vpb(type) == 0, "matmul_auto: a row of %zu is not a multiple of the block of %d",
-             k, cx_vpb(type));
-  CX_REQUIRE(lhs && w && dst, "matmul_auto: null pointer");
-  CX_REQUIRE(n < (1u << 31) && k < (1u << 31), "matmul_auto: shape too large");
+                          int type, float* dst, void* scratch, hipStream_t s) {
+  if (type == CX_F32 || type == CX_F16) return cx_launch_matmul_f(type, w, n, k, lhs, m, dst, s);
   if (!m || !n) return CX_OK;
-  if (reserve) {
-    int rc = cx_scratch_reserve(matmul_auto_scratch(m, k, type), &scratch);
+  cx_scratch scr(s);
+  if (!scratch) {
+    int rc = scr.get(matmul_auto_scratch(m, k, type), &scratch);
     if (rc) return rc;
   }
   // Several rows: all at once on int8 MFMA, each output bit-identical to the
@@ -323,7 +376,9 @@ static int matmul_auto_on(size_t m, size_t k, size_t n, const float* lhs, const 
 
 extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, const uint8_t* w,
                               int type, float* dst, void* stream) {
-  return matmul_auto_on(m, k, n, lhs, w, type, dst, nullptr, true, STREAM(stream));
+  int rc = matmul_auto_check(k, n, lhs, w, type, dst);
+  if (rc) return rc;
+  return matmul_auto_on(m, k, n, lhs, w, type, dst, nullptr, STREAM(stream));
 }
 
 // ------------------------------------------- the allocation-free variant
@@ -334,26 +389,31 @@ extern "C" int cx_matmul_auto(size_t m, size_t k, size_t n, const float* lhs, co
 // quantization writes every byte the contraction reads).
 static __device__ __align__(256) uint8_t scratch[CX_NOALLOC_SCRATCH_BYTES];
 
-// The array's device address on each GPU, found once per device with that
-// device current (the host-side name is not a device address).
+// The array's device address on each GPU, looked up with that device
+// current (the host-side name is not a device address). Only a successful
+// lookup is kept; a failed one is tried again by the next call.
+static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[64];
-static hipError_t g_scratch_err[64];
-static std::once_flag g_scratch_once[64];
 
 static int noalloc_scratch(int dev, void** out) {
   CX_REQUIRE(dev >= 0 && dev < 64, "no HIP device %d", dev);
-  std::call_once(g_scratch_once[dev], [dev] {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
     int prev = 0;
+    void* p = nullptr;
     hipError_t e = hipGetDevice(&prev);
     if (e == hipSuccess) e = hipSetDevice(dev);
-    if (e == hipSuccess) e = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
-    if (e == hipSuccess) e = hipSetDevice(prev);
-    g_scratch_err[dev] = e;
-  });
-  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev]) {
-    cx_set_error("matmul_auto_noalloc: the scratch of device %d has no address: %s", dev,
-                 hipGetErrorString(g_scratch_err[dev]));
-    return CX_EHIP;
+    if (e == hipSuccess) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      const hipError_t r = hipSetDevice(prev);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess || !p) {
+      cx_set_error("matmul_auto_noalloc: the scratch of device %d has no address: %s", dev,
+                   hipGetErrorString(e));
+      return CX_EHIP;
+    }
+    g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
   return CX_OK;
@@ -361,6 +421,8 @@ static int noalloc_scratch(int dev, void** out) {
 
 extern "C" int cx_matmul_auto_noalloc(size_t m, size_t k, size_t n, const float* lhs,
                                       const uint8_t* w, int type, float* dst, void* stream) {
+  int rc = matmul_auto_check(k, n, lhs, w, type, dst);
+  if (rc) return rc;
   const size_t need = matmul_auto_scratch(m, k, type);
   CX_REQUIRE(need <= CX_NOALLOC_SCRATCH_BYTES,
              "matmul_auto_noalloc: %zu x %zu rows need %zu bytes of scratch, past its %d", m, k,
@@ -368,9 +430,8 @@ extern "C" int cx_matmul_auto_noalloc(size_t m, size_t k, size_t n, const float*
   int dev = 0;
   CX_HIP(hipGetDevice(&dev));
   void* sp = nullptr;
-  int rc = noalloc_scratch(dev, &sp);
-  if (rc) return rc;
-  return matmul_auto_on(m, k, n, lhs, w, type, dst, sp, false, STREAM(stream));
+  if ((rc = noalloc_scratch(dev, &sp))) return rc;
+  return matmul_auto_on(m, k, n, lhs, w, type, dst, sp, STREAM(stream));
 }
 
 extern "C" int cx_matmul_multi_1row(const float* x, size_t k, size_t count,
@@ -386,7 +447,8 @@ extern "C" int cx_matmul_multi_1row(const float* x, size_t k, size_t count,
     (cx_sub(types[i]) == 16 ? need16 : need32) = true;
   }
   QuantScratch q16, q32;
-  int rc = quant_scratch(1, k, need16 ? &q16 : nullptr, need32 ? &q32 : nullptr);
+  cx_scratch scr(STREAM(stream));
+  int rc = quant_scratch(scr, 1, k, need16 ? &q16 : nullptr, need32 ? &q32 : nullptr);
   if (rc) return rc;
   if (need16 && (rc = cx_launch_quantize(x, 1, k, 16, q16.xq, q16.xe, q16.xs, STREAM(stream))))
     return rc;
@@ -468,7 +530,8 @@ extern "C" int cx_attention_decode(const float* q, const float* k, const float* 
                o_cm = o_sc + up(cx_attn_score_floats(heads, cap) * 4),
                bytes = o_cm + up(cx_attn_chunk_floats(heads, cap) * 4);
   void* sp = nullptr;
-  int rc = cx_scratch_reserve(bytes, &sp);
+  cx_scratch scr(STREAM(stream));
+  int rc = scr.get(bytes, &sp);
   if (rc) return rc;
   uint8_t* b = (uint8_t*)sp;
   cx_dstate* st = (cx_dstate*)b;
@@ -536,7 +599,8 @@ extern "C" int cx_sample(const float* logits, size_t n, float temperature, float
                o_ord = o_part + up(cx_sample_parts(n) * 4), o_ordp = o_ord + up(n * 4),
                o_tok = o_ordp + up((n + 4) * 4), bytes = o_tok + 256;
   void* sp = nullptr;
-  int rc = cx_scratch_reserve(bytes, &sp);
+  cx_scratch scr(s);
+  int rc = scr.get(bytes, &sp);
   if (rc) return rc;
   uint8_t* b = (uint8_t*)sp;
   uint32_t* tok = (uint32_t*)(b + o_tok);
@@ -1723,8 +1787,10 @@ static int generate(cx_model* m, cx_cache* C, const uint32_t* prompt, size_t n, 
   }
   const hipError_t se = hipStreamSynchronize(m->stream);  // steps launched past the stop
   if (he == hipSuccess) he = se;
+  // only the steps that forwarded a returned token are timed: steps
+  // launched past the stop made tokens that are thrown away
   if (he == hipSuccess && step_ms)
-    for (size_t i = 0; i < launched && he == hipSuccess; i++)
+    for (size_t i = 0; i < forwarded && he == hipSuccess; i++)
       he = hipEventElapsedTime(&step_ms[i], ev[i], ev[i + 1]);
   for (auto& e : ev) (void)hipEventDestroy(e);
   CX_HIP(he);

@@ -260,12 +260,42 @@ __device__ inline int8_t cx_rust_i8(float r) {
 // entry points and the device scratch of the operators. Each host thread
 // holds its own (taken from a per-device pool at its first call, returned
 // when the thread ends), so calls from different threads never share a
-// stream or a scratch buffer.
+// scratch buffer at the same time: every use of a context's scratch is
+// stream-ordered after the previous one (the `used` event), whichever
+// stream or thread made it.
 struct cx_lib {
   int device;
   hipStream_t stream;   // library stream for host-pointer entry points
   void* scratch;        // device scratch of this thread's calls
   size_t scratch_bytes;
+  hipEvent_t used;      // recorded after the last enqueued work on the scratch
+  bool used_valid;
 };
 cx_lib* cx_lib_get();   // the calling thread's context on its current device
-int cx_scratch_reserve(size_t bytes, void** out);
+// The calling thread's scratch of at least `bytes` for work about to be
+// enqueued on stream s; s first waits for every earlier use of it.
+int cx_scratch_acquire(size_t bytes, hipStream_t s, void** out);
+// Marks the end of the enqueued work on s that uses the scratch.
+void cx_scratch_release(hipStream_t s);
+
+// One call's use of the calling thread's scratch on one stream: get() waits
+// (in stream order) for the earlier uses, the destructor records the end of
+// this call's work, on every return path.
+class cx_scratch {
+ public:
+  explicit cx_scratch(hipStream_t s) : s_(s) {}
+  cx_scratch(const cx_scratch&) = delete;
+  cx_scratch& operator=(const cx_scratch&) = delete;
+  int get(size_t bytes, void** out) {
+    const int rc = cx_scratch_acquire(bytes, s_, out);
+    held_ = held_ || rc == CX_OK;
+    return rc;
+  }
+  ~cx_scratch() {
+    if (held_) cx_scratch_release(s_);
+  }
+
+ private:
+  hipStream_t s_;
+  bool held_ = false;
+};

@@ -151,8 +151,9 @@ class Modelo:
                 tiempos: bool = False, muestreador=None, al_token=None, fines=None):
         """Modelo::generar (src/forward.rs:533-559): greedy, or with a
         ``sampler.Muestreador`` (its seed, temperature and top_p; the draws
-        happen on the GPU). Returns the tokens, and the per-token decode times
-        in ms if `tiempos`. ``al_token(t) -> bool`` is called with each token
+        happen on the GPU). Returns the tokens, and if `tiempos` the decode
+        time in ms of each step that forwarded a returned token (one per
+        token the cache grew by). ``al_token(t) -> bool`` is called with each token
         as it is pushed (False stops at once, src/forward.rs:549-551);
         ``fines`` is a list of stop tokens (MotorPropio stops at the end
         token and the chat's end of turn, src/engine_own.rs:259-261)."""
@@ -167,27 +168,31 @@ class Modelo:
         n = C.c_size_t()
         ms = np.zeros(max(max_nuevos, 1), np.float32) if tiempos else None
         eos = 0xFFFFFFFF if fin is None else fin
+        inicio = cache.largo()
         if muestreador is None:
-            L.check(_lib.cx_generate(self._h, cache._h, p.ctypes.data_as(L._u32p), p.size,
-                                     max_nuevos, eos, out.ctypes.data_as(L._u32p), C.byref(n),
-                                     ms.ctypes.data_as(L._f32p) if tiempos else None),
-                    "generar")
+            rc = _lib.cx_generate(self._h, cache._h, p.ctypes.data_as(L._u32p), p.size,
+                                  max_nuevos, eos, out.ctypes.data_as(L._u32p), C.byref(n),
+                                  ms.ctypes.data_as(L._f32p) if tiempos else None)
         else:
             # the sampler's generator as it stands; afterwards it is advanced
             # by the draws the reference makes: one per token, one more for
             # the end token, none past the context
-            inicio = cache.largo()
-            L.check(_lib.cx_generate_sampled(self._h, cache._h, p.ctypes.data_as(L._u32p), p.size,
-                                             max_nuevos, eos, muestreador.estado,
-                                             muestreador.temperatura, muestreador.top_p,
-                                             out.ctypes.data_as(L._u32p), C.byref(n),
-                                             ms.ctypes.data_as(L._f32p) if tiempos else None),
-                    "generar")
-            if muestreador.temperatura > 0.0:
+            rc = _lib.cx_generate_sampled(self._h, cache._h, p.ctypes.data_as(L._u32p), p.size,
+                                          max_nuevos, eos, muestreador.estado,
+                                          muestreador.temperatura, muestreador.top_p,
+                                          out.ctypes.data_as(L._u32p), C.byref(n),
+                                          ms.ctypes.data_as(L._f32p) if tiempos else None)
+            if rc == 0 and muestreador.temperatura > 0.0:
                 pasos = min(p.size + max_nuevos, self.cfg.contexto - inicio)
                 hechos = min(max_nuevos, pasos - p.size + 1)
                 muestreador.avanzar(n.value + (1 if n.value < hechos else 0))
+            elif rc == L.CX_ENOMEM and muestreador.temperatura > 0.0:
+                muestreador.avanzar(n.value)  # one draw per token made
         toks = out[: n.value].copy()
+        if tiempos:
+            # the steps that forwarded a returned token: the cache's growth
+            ms = ms[: max(0, min(cache.largo() - inicio - p.size, n.value))].copy()
+        _check_generation(rc, toks, ms)
         return (toks, ms) if tiempos else toks
 
     def _generar_stream(self, prompt, max_nuevos, cache, fines, muestreador, al_token):
@@ -216,7 +221,7 @@ class Modelo:
                                      C.byref(n))
         if estado["error"] is not None:
             raise estado["error"]
-        L.check(rc, "generar")
+        _check_generation(rc, out[: n.value].copy())
         if muestreador is not None and temp > 0.0:
             # one draw per pushed token, and one more for a stop token: the
             # loop stopped short of max_nuevos and of the context, not by al_token
@@ -224,6 +229,14 @@ class Modelo:
             fin = n.value < hechos and not estado["parado"]
             muestreador.avanzar(n.value + (1 if fin else 0))
         return out[: n.value].copy()
+
+
+def _check_generation(rc, tokens, tiempos=None):
+    """Raises for a failed generation; when the cache filled first
+    (CX_ENOMEM) the error carries the tokens made until then."""
+    if rc == L.CX_ENOMEM:
+        raise L.CacheLlena(f"generar: {L.last_error()} (status {rc})", tokens, tiempos)
+    L.check(rc, "generar")
 
 
 class Cache:

@@ -25,13 +25,18 @@
  *   - Threads. Level-1 functions are reentrant and thread-safe, like the
  *     reference's pure `type Kernel` that rayon calls from many threads at
  *     once (src/ops.rs:487-500): each host thread has its own stream and
- *     device scratch. Level-2 functions may run on several threads at once
- *     (each thread's scratch is its own); calls of ONE thread that use the
- *     scratch (cx_matmul_auto, cx_matmul_multi_1row, cx_gemv_subsums,
- *     cx_dequantize_rows, cx_attention_decode, cx_sample) on different
- *     streams must be ordered by the caller. A cx_model and its caches are
- *     used by one thread at a time; the reference serialises generation
- *     behind a Mutex (src/engine_own.rs:62,185).
+ *     device scratch. Level-2 functions may run on several threads at once.
+ *     The calls that use a thread's scratch (cx_matmul_auto,
+ *     cx_matmul_multi_1row, cx_gemv_subsums, cx_dequantize_rows,
+ *     cx_attention_decode, cx_sample) are ordered on the device after that
+ *     scratch's previous use, whatever stream it was on, also when a thread
+ *     ends with work still queued and another thread takes its scratch; the
+ *     host is not blocked, and a growing scratch is reallocated in stream
+ *     order. Under stream capture the scratch cannot grow (CX_EINVAL: make
+ *     the call once before capturing) and the caller orders the graph's
+ *     launches. A cx_model and its caches are used by one thread at a time;
+ *     the reference serialises generation behind a Mutex
+ *     (src/engine_own.rs:62,185).
  */
 #ifndef COSXAMIX_HIP_H
 #define COSXAMIX_HIP_H
@@ -165,7 +170,9 @@ int cx_matmul_auto(size_t m, size_t k, size_t n, const float *lhs,
  * needing more (about m * k bytes plus m * k / 2 for m > 1, m * k * 1.5 for
  * m = 1) fails with CX_EINVAL. Every call on a GPU shares that array, so
  * calls that overlap on one GPU (any thread, any stream) race: order them.
- * The first call on a device (or cx_init) looks the array's address up. */
+ * cx_init looks the array's address up; if that fails, every call tries
+ * again until the lookup succeeds. Arguments are checked (CX_EINVAL) before
+ * the scratch is sized. */
 #define CX_NOALLOC_SCRATCH_BYTES (32 << 20)
 int cx_matmul_auto_noalloc(size_t m, size_t k, size_t n, const float *lhs,
                            const uint8_t *w, int type, float *dst,
@@ -359,8 +366,11 @@ int cx_forward(cx_model *m, cx_cache *c, const uint32_t *toks, size_t t,
  * holds the prompt and the forwarded tokens, as the reference's. The cache
  * needs room for the positions generation reaches (CX_ENOMEM, with the
  * tokens made so far in out/n_out, when it fills first). If step_ms is not
- * NULL it gets one decode time per step run (ms, HIP events; max_new of
- * them when generation runs to max_new). */
+ * NULL (room for max_new values) it gets the decode time (ms, HIP events)
+ * of each step that forwarded a returned token, in order: their number is
+ * the cache's growth past the prompt, cx_cache_len after the call minus
+ * (cx_cache_len before it + n), at most *n_out; the rest of step_ms is
+ * left as it was. */
 int cx_generate(cx_model *m, cx_cache *c, const uint32_t *prompt, size_t n,
                 size_t max_new, uint32_t eos, uint32_t *out, size_t *n_out,
                 float *step_ms);

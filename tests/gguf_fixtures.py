@@ -58,11 +58,13 @@ def q5_0_bytes(rows, width, seed):
     return b.reshape(rows, -1)
 
 
-def mixed_model(seed=5, override=None, ctx=None, shape=None, embd=None):
+def mixed_model(seed=5, override=None, ctx=None, shape=None, embd=None, varied=False):
     """A 2-layer qwen2 GGUF: per-tensor types (k-quants by default,
     overridable), a token_embd (Q4_K by default) tied to the lm_head, q/k/v
-    biases in layer 0 only. `shape` overrides MINI's dims. Returns (file
-    bytes, host tensors by name, types by name)."""
+    biases in layer 0 only and unit norms; with `varied`, every norm
+    (output_norm too) ~ N(1, 0.1) and q/k/v biases ~ N(0, 0.3) in every
+    layer, each tensor its own draw. `shape` overrides MINI's dims. Returns
+    (file bytes, host tensors by name, types by name)."""
     c = dict(MINI, ctx=ctx or MINI["ctx"], **(shape or {}))
     D, I, V = c["dim"], c["ffn"], c["vocab"]
     kvd = c["kv_heads"] * D // c["heads"]
@@ -80,7 +82,11 @@ def mixed_model(seed=5, override=None, ctx=None, shape=None, embd=None):
         gg.append((name, [width, rows], t, b.tobytes()))
 
     def vec(name, n, ones=False):
-        v = np.ones(n, np.float32) if ones else rng.normal(0, 0.02, n).astype(np.float32)
+        if varied:
+            v = rng.normal(1.0, 0.1, n) if ones else rng.normal(0, 0.3, n)
+        else:
+            v = np.ones(n) if ones else rng.normal(0, 0.02, n)
+        v = v.astype(np.float32)
         host[name], types[name] = v, O.F32
         gg.append((name, [n], O.F32, v.tobytes()))
 
@@ -94,7 +100,7 @@ def mixed_model(seed=5, override=None, ctx=None, shape=None, embd=None):
         quant(p + "attn_q.weight", mats["attn_q"], D, D, 0.02)
         quant(p + "attn_k.weight", mats["attn_k"], kvd, D, 0.02)
         quant(p + "attn_v.weight", mats["attn_v"], kvd, D, 0.02)
-        if i == 0:  # biases in layer 0 only
+        if i == 0 or varied:  # biases in layer 0 only, unless varied
             vec(p + "attn_q.bias", D)
             vec(p + "attn_k.bias", kvd)
             vec(p + "attn_v.bias", kvd)
@@ -127,6 +133,34 @@ def oracle_of(host, types, ctx=None, shape=None):
         for b, n in (("attn_q.bias", D), ("attn_k.bias", kvd), ("attn_v.bias", kvd)):
             t.setdefault(f"blk.{i}.{b}", np.zeros(n, np.float32))
     return O.Model(c, t, ty, threads=8)
+
+
+def vary_norms_and_biases(model, seed, norm_sigma=0.1, bias_sigma=0.3):
+    """Writes into a GPU model's own device tensors: every `*_norm.weight`
+    (output_norm included) ~ N(1, norm_sigma) and every `.bias` ~ N(0,
+    bias_sigma), each tensor its own draw (an F32 cx_dequantize is a device
+    copy). Returns the names it wrote. A daiss model has unit norms and zero
+    biases by definition (src/daiss.rs:396-407); real files do not."""
+    import ctypes as C
+    import torch
+    from cosxamix_amd import _lib as L
+    lib = L.load()
+    rng = np.random.default_rng(seed)
+    done = []
+    for i, (name, t, dims, nb) in enumerate(model.tensores()):
+        if t != O.F32 or not (name.endswith("_norm.weight") or name.endswith(".bias")):
+            continue
+        n = nb // 4
+        v = rng.normal(1.0, norm_sigma, n) if name.endswith("_norm.weight") else rng.normal(0, bias_sigma, n)
+        src = torch.from_numpy(v.astype(np.float32)).cuda()
+        L.check(lib.cx_dequantize(O.F32, C.c_void_p(src.data_ptr()), n,
+                                  C.c_void_p(model.tensor_ptr(i)),
+                                  C.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                "vary_norms_and_biases")
+        torch.cuda.synchronize()
+        assert np.array_equal(model.tensor(i), v.astype(np.float32)), name
+        done.append(name)
+    return done
 
 
 def mirror(model, threads=16):

@@ -92,3 +92,18 @@ def test_argument_errors_are_reported_not_crashed(L):
     assert "quantizers" in L.last_error()
     assert lib.cx_matmul_auto(1, 100, 4, p, p, O.Q8_0, p, None) == -1
     assert "32" in L.last_error()
+
+
+def test_noalloc_checks_arguments_before_sizing_its_scratch(L):
+    """cx_matmul_auto_noalloc refuses a type with no quantized path (Q4_0,
+    an unknown id) or a ragged row with CX_EINVAL before it sizes its
+    scratch (which divides by the type's sub-block)."""
+    lib = L.load()
+    p = C.c_void_p(1)  # never dereferenced: validation fails first
+    for t in (2, 15, 99):  # Q4_0, Q8_K, not a type
+        assert lib.cx_matmul_auto_noalloc(4, 256, 8, p, p, t, p, None) == L.CX_EINVAL, t
+        assert "no quantized path" in L.last_error()
+    assert lib.cx_matmul_auto_noalloc(4, 1000, 8, p, p, O.Q4_K, p, None) == L.CX_EINVAL
+    assert "256" in L.last_error()
+    assert lib.cx_matmul_auto_noalloc(4, 256, 8, None, p, O.Q4_K, p, None) == L.CX_EINVAL
+    assert "null" in L.last_error()

@@ -133,16 +133,22 @@ MIXED_05B = {"attn_q": O.Q5_0, "attn_k": O.Q5_0, "attn_v": O.Q8_0, "attn_output"
              "ffn_gate": O.Q5_0, "ffn_up": O.Q8_0, "ffn_down": O.Q6_K}
 
 
-@pytest.mark.parametrize("over", [MIXED_05B, dict(MIXED_05B, ffn_up=O.Q5_0, ffn_down=O.Q8_0)],
-                         ids=["q4_k_m", "q5_0-gate-up"])
-def test_qwen_0_5b_style_mixed_file_matches_the_oracle(dev, tmp_path, over):
+@pytest.mark.parametrize("over,varied", [(MIXED_05B, False),
+                                         (dict(MIXED_05B, ffn_up=O.Q5_0, ffn_down=O.Q8_0), False),
+                                         (MIXED_05B, True),
+                                         (dict(MIXED_05B, ffn_up=O.Q5_0, ffn_down=O.Q8_0), True)],
+                         ids=["q4_k_m", "q5_0-gate-up", "q4_k_m-varied", "q5_0-gate-up-varied"])
+def test_qwen_0_5b_style_mixed_file_matches_the_oracle(dev, tmp_path, over, varied):
     """The layout of real Qwen2.5-0.5B Q4_K_M files: Q5_0/Q8_0 matrices of
     width 896, a k-quant ffn_down (width 4864 = 19 blocks of 256), a Q8_0
     token_embd tied to the lm_head. The second file's gate and up are both
-    Q5_0 (one fused gate/up/SwiGLU launch) and its ffn_down Q8_0."""
+    Q5_0 (one fused gate/up/SwiGLU launch) and its ffn_down Q8_0. `varied`:
+    every norm ~ N(1, 0.1), q/k/v biases ~ N(0, 0.3) in both layers (the
+    32-value block kernels' fused rmsnorm and bias epilogues)."""
     from cosxamix_amd import forward as F
     shape = dict(dim=896, heads=14, kv_heads=2, ffn=4864)
-    data, host, types = mixed_model(seed=8, override=over, shape=shape, embd=O.Q8_0)
+    data, host, types = mixed_model(seed=8, override=over, shape=shape, embd=O.Q8_0,
+                                    varied=varied)
     path = tmp_path / "qwen05.gguf"
     path.write_bytes(data)
     m = F.Modelo.abrir(path)

@@ -104,6 +104,51 @@ def test_operators_on_several_threads_do_not_share_scratch(dev):
             assert torch.equal(o.view(torch.int32), alone[i].view(torch.int32)), i
 
 
+def test_a_thread_that_exits_with_work_queued_hands_its_scratch_on_in_order(dev):
+    """Thread A queues 12 cx_matmul_auto calls on its own stream and ends
+    without waiting for them; thread B then takes A's context (and scratch)
+    from the pool and queues 12 calls on another stream, the first of them
+    growing the scratch. B's first use waits, on the device, for A's queued
+    work: every output of both threads is the bits of the same call alone."""
+    from cosxamix_amd import ops
+    n, k = 4096, 2048
+    w = torch.from_numpy(O.daiss_matrix(5, "w", n, k, 0.02, O.Q4_K)).to(dev)
+    xa = [torch.randn(64, k, generator=torch.Generator().manual_seed(100 + i)).to(dev)
+          for i in range(12)]
+    xb = [torch.randn(256 if i == 0 else 48, k, generator=torch.Generator().manual_seed(200 + i)).to(dev)
+          for i in range(12)]
+
+    def mm(x, y=None):
+        y = torch.empty(x.shape[0], n, device=dev) if y is None else y
+        ops.matmul_auto((x.shape[0], k, n), x, w, O.Q4_K, y)
+        return y
+
+    alone_a = [mm(x).cpu() for x in xa]
+    alone_b = [mm(x).cpu() for x in xb]
+    torch.cuda.synchronize()
+    outs = {}
+
+    def run(name, xs):
+        s = torch.cuda.Stream(device=dev)
+        with torch.cuda.stream(s):
+            ys = [torch.full((x.shape[0], n), float("nan"), device=dev) for x in xs]
+            for x, y in zip(xs, ys):
+                mm(x, y)
+        outs[name] = (s, ys)  # no synchronization before the thread ends
+
+    ta = threading.Thread(target=run, args=("a", xa))
+    ta.start()
+    ta.join()
+    tb = threading.Thread(target=run, args=("b", xb))
+    tb.start()
+    tb.join()
+    for name, alone in (("a", alone_a), ("b", alone_b)):
+        s, ys = outs[name]
+        s.synchronize()
+        for i, (y, want) in enumerate(zip(ys, alone)):
+            assert torch.equal(y.cpu().view(torch.int32), want.view(torch.int32)), (name, i)
+
+
 SMALL = dict(capas=2, dim=256, cabezas=4, cabezas_kv=2, ffn=768, vocab=500, contexto=128)
 
 
@@ -169,10 +214,19 @@ def test_generate_early_stop_with_a_small_cache(F):
     # the same run continues on the cache: forward the next token
     full = m.generar(p, 12, m.nueva_cache(64))
     assert np.array_equal(full, exp)
-    # a cache that fills before any stop: an error, the tokens made so far kept
+    # a cache that fills before any stop: an error that carries the tokens
+    # made so far (three forwarded, the fourth made with no room for it)
+    from cosxamix_amd import _lib as L
     small = m.nueva_cache(len(p) + 3)
-    with pytest.raises(Exception, match="full"):
+    with pytest.raises(L.CacheLlena, match="full") as err:
         m.generar(p, 12, small)
+    assert np.array_equal(err.value.tokens, exp[:4]) and small.largo() == len(p) + 3
+    # step times: one per step that forwarded a returned token, none for the
+    # steps run ahead past the stop
+    cache = m.nueva_cache(64)
+    got, ms = m.generar(p, 100, cache, fin=eos, tiempos=True)
+    assert np.array_equal(got, exp[:first]) and len(ms) == first == cache.largo() - len(p)
+    assert np.all(ms > 0), ms
 
 
 def test_generate_callback_and_stop_list(F):

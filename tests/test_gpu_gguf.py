@@ -55,14 +55,16 @@ def test_daiss_model_round_trips_through_gguf(F, tmp_path):
                           b.generar(prompt, 12, b.nueva_cache(64)))
 
 
-def test_mixed_format_file_matches_the_oracle(F, tmp_path):
-    data, host, types = mixed_model()
+@pytest.mark.parametrize("varied", [False, True], ids=["unit-norms", "varied-norms-biases"])
+def test_mixed_format_file_matches_the_oracle(F, tmp_path, varied):
+    """varied: every norm ~ N(1, 0.1) and q/k/v biases in both layers."""
+    data, host, types = mixed_model(varied=varied)
     path = tmp_path / "mixed.gguf"
     path.write_bytes(data)
     m = F.Modelo.abrir(path)
     assert (m.cfg.ffn, m.cfg.vocab) == (MINI["ffn"], MINI["vocab"])
     names = [t[0] for t in m.tensores()]
-    assert "output.weight" not in names and "blk.1.attn_q.bias" not in names
+    assert "output.weight" not in names and ("blk.1.attn_q.bias" in names) == varied
     ref = oracle_of(host, types)
     prompt = np.array([3, 600, 17, 99, 5, 250], np.uint32)
     gc, oc = m.nueva_cache(64), ref.new_cache(64)

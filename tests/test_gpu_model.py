@@ -94,6 +94,54 @@ def test_forward_logits_and_greedy_tokens_match_oracle(F, name, cfg, t, tdown):
     assert cache2.largo() == rc2.len == 48
 
 
+VARIED = [
+    # (name, config, linear type, down type, prompt length); k = 2048: the
+    # row kernels' fused rmsnorm (q/k/v, gate/up/SwiGLU); k = 4096: the LDS
+    # gate/up/SwiGLU kernel; a 300-token prompt: two prefill chunks of the
+    # MFMA contraction's fused rmsnorm; 896: the 32-value block kernels
+    ("2048-q4k", dict(capas=2, dim=2048, cabezas=16, cabezas_kv=2, ffn=11008, vocab=3000,
+                      contexto=200, rope=1e6), O.Q4_K, O.Q4_K, 24),
+    ("4096-q4k-q5kdown", dict(capas=2, dim=4096, cabezas=32, cabezas_kv=8, ffn=14336,
+                              vocab=2000, contexto=200, rope=5e5), O.Q4_K, O.Q5_K, 24),
+    ("2048-q5k-q3kdown-300", dict(capas=2, dim=2048, cabezas=16, cabezas_kv=2, ffn=1024,
+                                  vocab=1000, contexto=400, rope=1e6), O.Q5_K, O.Q3_K, 300),
+    ("512-q2k-q3kdown", dict(capas=2, dim=512, cabezas=8, cabezas_kv=2, ffn=1536, vocab=1500,
+                             contexto=200, rope=10000.0), O.Q2_K, O.Q3_K, 24),
+    ("896-q8_0", dict(capas=2, dim=896, cabezas=14, cabezas_kv=2, ffn=4864, vocab=640,
+                      contexto=200), O.Q8_0, O.Q8_0, 40),
+]
+
+
+@pytest.mark.parametrize("name,cfg,t,tdown,plen", VARIED, ids=[c[0] for c in VARIED])
+def test_varied_norms_and_biases_match_oracle(F, name, cfg, t, tdown, plen):
+    """Every norm weight ~ N(1, 0.1) (attn_norm, ffn_norm and output_norm,
+    each its own draw) and q/k/v biases ~ N(0, 0.3) in every layer, as in
+    real files (src/forward.rs:422-436, 472-474, 495-498): the fused norm
+    prologues must multiply by the right weight, and the epilogues add the
+    right bias. Prefill logits, teacher-forced steps and greedy tokens are
+    bit-identical to the oracle's."""
+    from gguf_fixtures import vary_norms_and_biases
+    c = F.Config(eps=1e-6, **cfg)
+    m = F.Modelo(c, tipo=t, semilla=17, tipo_down=tdown, tipo_salida=t)
+    names = vary_norms_and_biases(m, seed=len(name))
+    assert len(names) == 5 * c.capas + 1
+    ref = mirror(m)
+    prompt = np.random.default_rng(plen).integers(0, c.vocab, plen).astype(np.uint32)
+    cache, rc = m.nueva_cache(plen + 40), ref.new_cache(plen + 40)
+    lg, _ = m.forward(prompt, cache)
+    want = ref.forward(prompt, rc)
+    assert np.array_equal(lg.view(np.uint32), want.view(np.uint32)), name
+    tok = O.argmax(want)
+    for step in range(4):
+        lg, _ = m.forward([tok], cache)
+        want = ref.forward([tok], rc)
+        assert np.array_equal(lg.view(np.uint32), want.view(np.uint32)), (name, step)
+        tok = O.argmax(want)
+    got = m.generar(prompt, 16, m.nueva_cache(plen + 40))
+    exp = ref.generate(prompt, 16, ref.new_cache(plen + 40))
+    assert np.array_equal(got, exp), (name, got, exp)
+
+
 def test_long_cache_attention_path_bit_identical_to_oracle(F):
     """Caches above 4096 tokens stream the scores through LDS instead of
     holding them (cx_attn.hip); the arithmetic order is still the

@@ -62,6 +62,18 @@ def test_noalloc_f32_and_the_size_limit(dev):
         _call(lib, lib.cx_matmul_auto_noalloc, m, k, n, x, w, O.F32, got)
         torch.cuda.synchronize()
         assert torch.equal(got, want)
-    # 4096 rows of 14336 values need ~88 MB of scratch: refused, nothing launched
-    big = lib.cx_matmul_auto_noalloc(4096, 14336, 16, None, None, O.Q4_K, None, None)
-    assert big == -1 and b"past its" in lib.cx_last_error()
+    # 4096 rows of 14336 values need ~88 MB of scratch: refused, nothing
+    # launched (the pointers are checked for null, never dereferenced)
+    p = C.c_void_p(1)
+    big = lib.cx_matmul_auto_noalloc(4096, 14336, 16, p, p, O.Q4_K, p, None)
+    assert big == L.CX_EINVAL and b"past its" in lib.cx_last_error()
+    # a type with no quantized path (Q4_0) is refused before the scratch is
+    # sized; the next call works as before
+    assert lib.cx_matmul_auto_noalloc(4, 256, 8, p, p, 2, p, None) == L.CX_EINVAL
+    assert b"no quantized path" in lib.cx_last_error()
+    x = torch.randn(3, k, generator=torch.Generator().manual_seed(9)).to(dev)
+    want, got = torch.empty(3, n, device=dev), torch.empty(3, n, device=dev)
+    _call(lib, lib.cx_matmul_auto, 3, k, n, x, w, O.F32, want)
+    _call(lib, lib.cx_matmul_auto_noalloc, 3, k, n, x, w, O.F32, got)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
