@@ -624,17 +624,25 @@ static void block_q3k(const float *x, uint8_t *out) {
   put_f16(out + 108, dstore);
 }
 
-/* quant_kquants.rs:231-291 (bloque_q2k) -> 84 bytes */
-static void block_q2k(const float *x, uint8_t *out) {
-  int32_t l[16][16], aux[16];
-  float w[16], scales[16], mins[16], max_sc = 0.0f, max_mn = 0.0f;
+/* quant_kquants.rs:236-257: the search of each 16-value sub-block of a
+ * Q2_K block, weights |v|, absolute error */
+static void search_q2k(const float *x, float scales[16], float mins[16], int32_t l[16][16]) {
+  int32_t aux[16];
+  float w[16];
   const search_t s = {3, -0.5f, 0.1f, 15, 1};
   for (int j = 0; j < 16; j++) {
     const float *sub = x + j * 16;
     for (int i = 0; i < 16; i++) w[i] = fabsf(sub[i]);
-    float m;
-    scales[j] = quants_qkx(sub, w, 16, l[j], aux, &s, &m);
-    mins[j] = m;
+    scales[j] = quants_qkx(sub, w, 16, l[j], aux, &s, &mins[j]);
+  }
+}
+
+/* quant_kquants.rs:231-291 (bloque_q2k) -> 84 bytes */
+static void block_q2k(const float *x, uint8_t *out) {
+  int32_t l[16][16];
+  float scales[16], mins[16], max_sc = 0.0f, max_mn = 0.0f;
+  search_q2k(x, scales, mins, l);
+  for (int j = 0; j < 16; j++) {
     max_sc = fmaxf(max_sc, scales[j]);
     max_mn = fmaxf(max_mn, mins[j]);
   }
@@ -663,21 +671,29 @@ static void block_q2k(const float *x, uint8_t *out) {
   put_f16(out + 82, mstore);
 }
 
-/* quant_kquants.rs:295-348 (sub_bloques_de_32) */
-static void subblocks_32(const float *x, const search_t *b, uint16_t *dstore,
-                         uint16_t *mstore, uint8_t packed[12],
-                         int32_t l[8][32]) {
+/* quant_kquants.rs:301-313: the search of each 32-value sub-block of a
+ * Q4_K/Q5_K block, weights media + |v| (media: the block's RMS) */
+static void search_32(const float *x, const search_t *b, float scales[8], float mins[8],
+                      int32_t l[8][32]) {
   int32_t aux[32];
-  float w[32], scales[8], mins[8], max_sc = 0.0f, max_mn = 0.0f;
+  float w[32];
   float ss = 0.0f;
   for (int i = 0; i < 256; i++) ss += x[i] * x[i];
   float mean = sqrtf(ss / 256.0f);
   for (int j = 0; j < 8; j++) {
     const float *sub = x + j * 32;
     for (int i = 0; i < 32; i++) w[i] = mean + fabsf(sub[i]);
-    float m;
-    scales[j] = quants_qkx(sub, w, 32, l[j], aux, b, &m);
-    mins[j] = m;
+    scales[j] = quants_qkx(sub, w, 32, l[j], aux, b, &mins[j]);
+  }
+}
+
+/* quant_kquants.rs:295-348 (sub_bloques_de_32) */
+static void subblocks_32(const float *x, const search_t *b, uint16_t *dstore,
+                         uint16_t *mstore, uint8_t packed[12],
+                         int32_t l[8][32]) {
+  float scales[8], mins[8], max_sc = 0.0f, max_mn = 0.0f;
+  search_32(x, b, scales, mins, l);
+  for (int j = 0; j < 8; j++) {
     max_sc = fmaxf(max_sc, scales[j]);
     max_mn = fmaxf(max_mn, mins[j]);
   }
@@ -704,9 +720,13 @@ static void subblocks_32(const float *x, const search_t *b, uint16_t *dstore,
   }
 }
 
+/* quant_kquants.rs:353-359, 375-381: the searches of Q4_K and Q5_K */
+static const search_t SEARCH_Q4K = {15, -1.0f, 0.1f, 20, 0};
+static const search_t SEARCH_Q5K = {31, -0.5f, 0.1f, 15, 0};
+
 /* quant_kquants.rs:351-369 (bloque_q4k) -> 144 bytes */
 static void block_q4k(const float *x, uint8_t *out) {
-  const search_t s = {15, -1.0f, 0.1f, 20, 0};
+  const search_t s = SEARCH_Q4K;
   uint16_t d, m;
   uint8_t packed[12];
   int32_t l[8][32];
@@ -721,7 +741,7 @@ static void block_q4k(const float *x, uint8_t *out) {
 
 /* quant_kquants.rs:373-399 (bloque_q5k) -> 176 bytes */
 static void block_q5k(const float *x, uint8_t *out) {
-  const search_t s = {31, -0.5f, 0.1f, 15, 0};
+  const search_t s = SEARCH_Q5K;
   uint16_t d, m;
   uint8_t packed[12], qh[32] = {0};
   int32_t l[8][32];
@@ -739,6 +759,34 @@ static void block_q5k(const float *x, uint8_t *out) {
     for (int i = 0; i < 32; i++)
       out[48 + p * 32 + i] =
           (uint8_t)((l[2 * p][i] & 0xF) | ((l[2 * p + 1][i] & 0xF) << 4));
+}
+
+/* The per-sub-block search of one 256-value block, as the block quantizers
+ * above run it, before the scales and mins are themselves quantized:
+ * Q2_K 16 sub-blocks (scale, -min, codes 0..3), Q4_K/Q5_K 8 sub-blocks
+ * (codes 0..15 / 0..31), Q3_K 16 sub-blocks (cuantos_q3's scale, codes
+ * 0..7, mins 0). l holds 256 codes. A test hook of the oracle. */
+int orc_kquant_search(int type, const float *x, float *scales, float *neg_mins, int32_t *l) {
+  switch (type) {
+    case ORC_Q2_K:
+      search_q2k(x, scales, neg_mins, (int32_t(*)[16])l);
+      return 16;
+    case ORC_Q3_K:
+      for (int j = 0; j < 16; j++) {
+        scales[j] = quants_q3(x + j * 16, 4, l + j * 16);
+        neg_mins[j] = 0.0f;
+      }
+      return 16;
+    case ORC_Q4_K:
+      search_32(x, &SEARCH_Q4K, scales, neg_mins, (int32_t(*)[32])l);
+      return 8;
+    case ORC_Q5_K:
+      search_32(x, &SEARCH_Q5K, scales, neg_mins, (int32_t(*)[32])l);
+      return 8;
+    default:
+      set_err("kquant_search: not a k-quant with a quantizer");
+      return -1;
+  }
 }
 
 /* src/quant.rs:744-805 (cuantizar_bloques) */
@@ -1681,12 +1729,37 @@ void orc_cache_release(orc_cache *c, const orc_config *cfg) {
 /* src/forward.rs:98-110 */
 void orc_cache_truncate(orc_cache *c, size_t n) { if (n < c->len) c->len = n; }
 
+/* src/ops.rs:87-156 (ops::matmul), the path matmul_auto takes for F32 and
+ * F16 weights (src/ops.rs:1064-1071): each weight row widened to f32
+ * (descuantizar), then kernels::dot with every lhs row (spec
+ * src/kernels/scalar.rs:16-23, the sum in order from 0) */
+static int matmul_widened(size_t m, size_t k, size_t n, const float *lhs, const uint8_t *w,
+                          int type, float *dst, int threads) {
+  const size_t rowb = k * orc_bytes_per_block(type);
+  int err = 0;
+  if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(dynamic) num_threads(threads)
+  for (size_t r = 0; r < n; r++) {
+    float *col = (float *)malloc(k * 4);
+    if (!col || orc_dequantize(type, w + r * rowb, col, k) < 0) {
+      err = 1;
+    } else {
+      for (size_t f = 0; f < m; f++) dst[f * n + r] = orc_dot_f32(lhs + f * k, col, k);
+    }
+    free(col);
+  }
+  if (err) { set_err("matmul_widened: alloc or dequantize"); return -1; }
+  return 0;
+}
+
 static int proj(const orc_model *M, const float *x, size_t t, size_t k, size_t n,
                 const uint8_t *w, int type, const float *bias, float *dst) {
   orc_row_kernel kern = M->kern_override && type == ORC_Q4_K ? M->kern_override : NULL;
-  /* matmul_auto (src/ops.rs:1056-1093): the fused row kernel for the
-   * k-quants, the buffer path for Q8_0/Q5_0 */
-  if (orc_row_kernel_for(type) && k % 256 == 0) {
+  /* matmul_auto (src/ops.rs:1056-1093): the f32 path for F32/F16 weights,
+   * the fused row kernel for the k-quants, the buffer path for Q8_0/Q5_0 */
+  if (type == ORC_F32 || type == ORC_F16) {
+    if (matmul_widened(t, k, n, x, w, type, dst, M->threads)) return -1;
+  } else if (orc_row_kernel_for(type) && k % 256 == 0) {
     if (orc_matmul_fused(t, k, n, x, w, type, dst, kern, M->threads, 2)) return -1;
   } else if (orc_matmul_direct(t, k, n, x, w, type, dst, M->threads)) {
     return -1;

@@ -70,6 +70,10 @@ int orc_unpack_i8(int type, const uint8_t *src, size_t n, int8_t *q,
                   float *scales, float *offsets);
 /* src/quant.rs:744-805 + src/quant_kquants.rs. Returns bytes written or -1 */
 long orc_quantize_blocks(int type, const float *x, size_t n, uint8_t *out);
+/* Test hook: the per-sub-block search of one 256-value block of Q2_K, Q3_K,
+ * Q4_K or Q5_K as the quantizers run it (scales, -mins, 256 codes).
+ * Returns the number of sub-blocks, or -1. */
+int orc_kquant_search(int type, const float *x, float *scales, float *neg_mins, int32_t *l);
 
 /* src/daiss.rs:317-357 (Azar) and 364-379 (semilla_de) */
 typedef struct { uint64_t state; } orc_azar;

@@ -78,6 +78,7 @@ def _load():
         "orc_dequantize": (C.c_int, [C.c_int, _u8p, _f32p, C.c_size_t]),
         "orc_unpack_i8": (C.c_int, [C.c_int, _u8p, C.c_size_t, _i8p, _f32p, _f32p]),
         "orc_quantize_blocks": (C.c_long, [C.c_int, _f32p, C.c_size_t, _u8p]),
+        "orc_kquant_search": (C.c_int, [C.c_int, _f32p, _f32p, _f32p, _i32p]),
         "orc_seed_of": (C.c_uint64, [C.c_uint64, C.c_char_p, C.c_uint64]),
         "orc_daiss_row": (None, [C.c_uint64, C.c_char_p, C.c_uint64, C.c_float, _f32p, C.c_size_t]),
         "orc_daiss_matrix": (C.c_int, [C.c_uint64, C.c_char_p, C.c_size_t, C.c_size_t, C.c_float,
@@ -148,6 +149,20 @@ def quantize_blocks(t: int, x: np.ndarray) -> np.ndarray:
     if n < 0:
         raise ValueError(err())
     return out
+
+
+def kquant_search(t: int, x: np.ndarray):
+    """The per-sub-block search of one 256-value block as the quantizer runs
+    it: (scales, -mins, codes[256]) before the scales and mins are
+    themselves quantized (src/quant_kquants.rs:29-157, 236-257, 301-313)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    assert x.size == 256
+    sc, mn = np.zeros(16, np.float32), np.zeros(16, np.float32)
+    codes = np.zeros(256, np.int32)
+    n = lib.orc_kquant_search(t, _p(x, _f32p), _p(sc, _f32p), _p(mn, _f32p), _p(codes, _i32p))
+    if n < 0:
+        raise ValueError(err())
+    return sc[:n], mn[:n], codes
 
 
 def dequantize(t: int, b: np.ndarray, n: int) -> np.ndarray:
@@ -333,7 +348,10 @@ class Model:
             return _p(a, _f32p)
 
         def bp(name):
-            a = np.ascontiguousarray(tensors[name], np.uint8)
+            a = tensors[name]
+            # F32/F16 matrices travel as their bytes (ops::matmul's path)
+            a = (np.ascontiguousarray(a).view(np.uint8) if a.dtype in (np.float32, np.float16)
+                 else np.ascontiguousarray(a, np.uint8))
             self._keep.append(a)
             return _p(a, _u8p)
 

@@ -393,3 +393,123 @@ def test_q2k_quantizer_bytes_on_an_exact_grid():
         assert np.array_equal(O.dequantize(O.Q2_K, want, 256), x)
         got = O.quantize_blocks(O.Q2_K, x)
         assert np.array_equal(got, want), (np.nonzero(got != want)[0], le, c)
+
+
+# ------------------------------------------- the k-quant search on any block
+# src/quant_kquants.rs:236-243, 353-359, 375-381: the search's parameters
+# (sub-block size, nmax, first step, step, steps, absolute error)
+SEARCH = {O.Q2_K: (16, 3, -0.5, 0.1, 15, True),
+          O.Q4_K: (32, 15, -1.0, 0.1, 20, False),
+          O.Q5_K: (32, 31, -0.5, 0.1, 15, False)}
+
+
+def _round_away(v):
+    """f32::round (half away from zero) of float32 values, exactly."""
+    v = np.asarray(v, np.float64)
+    return np.where(v >= 0, np.floor(v + 0.5), np.ceil(v - 0.5))
+
+
+def _search_float64(x, w, nmax, first, step, steps, absolute):
+    """The documented search (cuantos_qkx, src/quant_kquants.rs:99-157) on
+    the sub-block x with weights w, its fits and errors in float64: start
+    from the plain rounding at nmax / (max - min) with scale 1/iscale and
+    min = min(0, min x); then for k = 0..steps form the codes at
+    (first + step k + nmax) / (max - min) from the best min so far, fit the
+    weighted least-squares scale and min (the min held at 0 when it would be
+    positive), and keep the fit if its weighted error is lower. Only the
+    codes are formed with f32 roundings, as the search forms them. Returns
+    (codes, scale, min)."""
+    f = np.float32
+    mx = x.max()
+    mn = min(f(0), x.min())
+    err = (lambda r: np.abs(r)) if absolute else (lambda r: r * r)
+    xd, wd = x.astype(np.float64), w.astype(np.float64)
+
+    def codes(isc, m):
+        return np.clip(_round_away(f(isc) * (x - f(m)).astype(f)), 0, nmax)
+
+    isc = f(f(nmax) / f(mx - mn))
+    a = codes(isc, mn)
+    s, m = float(f(1) / isc), float(mn)
+    best = float(np.sum(wd * err(s * a + m - xd)))
+    sw, sx = wd.sum(), (wd * xd).sum()
+    for k in range(steps + 1):
+        isc = f(f(f(first) + f(step) * f(k)) + f(nmax)) / f(mx - f(m))
+        c = codes(isc, m)
+        if np.all(c == c[0]):  # no fit: the search skips it (D = 0)
+            continue
+        sl, sl2, sxl = (wd * c).sum(), (wd * c * c).sum(), (wd * c * xd).sum()
+        dd = sw * sl2 - sl * sl
+        cs, cm = (sw * sxl - sx * sl) / dd, (sl2 * sx - sl * sxl) / dd
+        if cm > 0:
+            cs, cm = sxl / sl2, 0.0
+        e = float(np.sum(wd * err(cs * c + cm - xd)))
+        if e < best:
+            a, s, m, best = c, cs, cm, e
+    return a, s, m
+
+
+@pytest.mark.parametrize("t", [O.Q2_K, O.Q4_K, O.Q5_K], ids=["Q2_K", "Q4_K", "Q5_K"])
+def test_kquant_search_on_random_blocks(t):
+    """On random N(0, 0.02) blocks (the fixtures' weights, some widened),
+    each sub-block's codes, scale and min from the oracle's search equal the
+    documented search run in float64 with the reference's weights and error:
+    |v| and absolute error for Q2_K (src/quant_kquants.rs:236-249), media +
+    |v| (media the block's RMS) and squared error for Q4_K/Q5_K (301-305),
+    the steps of 353-359 and 375-381. Where an f32 near-tie takes the
+    search down another path the two may differ, but the oracle's result
+    must then not be worse: its float64 error under the reference's weights
+    is at most the documented search's (within 1e-6). A wrong weighting,
+    error or step count gives worse fits."""
+    sub, nmax, first, step, steps, absolute = SEARCH[t]
+    err = (lambda r: np.abs(r)) if absolute else (lambda r: r * r)
+    rng = np.random.default_rng(t)
+    off, worse, total = [], [], 0
+    for blk in range(150):
+        x = (rng.normal(0, 0.02, 256) * (1 + 4 * (blk % 3 == 0) * rng.random(256))).astype(np.float32)
+        scales, neg_mins, l = O.kquant_search(t, x)
+        media = math.sqrt(float(np.sum(x.astype(np.float64) ** 2)) / 256)
+        for j in range(256 // sub):
+            xs = x[j * sub:(j + 1) * sub]
+            xd = xs.astype(np.float64)
+            w = np.abs(xd) + (0.0 if t == O.Q2_K else media)
+            a, s, m = _search_float64(xs, w, nmax, first, step, steps, absolute)
+            got, gs, gm = l[j * sub:(j + 1) * sub], float(scales[j]), -float(neg_mins[j])
+            total += 1
+            if (np.array_equal(a, got) and abs(gs - s) <= 1e-4 * abs(s)
+                    and abs(gm - m) <= 1e-4 * float(np.abs(xs).max())):
+                continue
+            off.append((blk, j))
+            e_doc = float(np.sum(w * err(s * a + m - xd)))
+            e_got = float(np.sum(w * err(gs * got + gm - xd)))
+            if e_got > e_doc * (1 + 1e-6):
+                worse.append((blk, j, e_got / e_doc - 1))
+    assert total == 150 * 256 // sub
+    assert not worse, (len(worse), worse[:8])
+    assert len(off) <= total // 200, (len(off), total, off[:8])
+
+
+def test_q3k_search_scale_is_the_fit_of_its_codes():
+    """cuantos_q3 (src/quant_kquants.rs:29-84): the returned scale is the
+    x^2-weighted least-squares scale of the final codes (value - 4), and the
+    refinement never leaves the codes worse than the first rounding at
+    -nmax / (the value of largest magnitude)."""
+    rng = np.random.default_rng(33)
+    f = np.float32
+    for blk in range(100):
+        x = rng.normal(0, 0.02, 256).astype(np.float32)
+        scales, _, l = O.kquant_search(O.Q3_K, x)
+        for j in range(16):
+            xs = x[j * 16:(j + 1) * 16]
+            xd = xs.astype(np.float64)
+            w = xd * xd
+            li = l[j * 16:(j + 1) * 16].astype(np.float64) - 4
+            assert np.all((li >= -4) & (li <= 3))
+            fit = np.sum(w * xd * li) / np.sum(w * li * li)
+            assert abs(float(scales[j]) - fit) <= 1e-4 * abs(fit), (blk, j)
+            big = xs[np.argmax(np.abs(xs))]
+            l0 = np.clip(_round_away(f(f(-4) / big) * xs), -4, 3)
+
+            def e(c):
+                return np.sum(w * xd * xd) - np.sum(w * xd * c) ** 2 / np.sum(w * c * c)
+            assert e(li) <= e(l0) * (1 + 1e-9) + 1e-30, (blk, j)
