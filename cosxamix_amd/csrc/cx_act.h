@@ -86,26 +86,158 @@ __device__ inline float cx_swiglu(float g, float u) {
   return a * u;
 }
 
-// f64 sum of squares of x[0..n) over a 256-thread workgroup, then the rmsnorm
-// factor 1 / sqrt(sum / n + eps) in f64 (src/kernels/scalar.rs:46-47).
-// `red` is 4 doubles of shared memory. Deterministic: fixed tree. Every
-// square is exact in f64, so the tree differs from the sequential sum only
-// in f64 roundings (relative 1e-16), far below the f32 result's ulp.
-__device__ inline double cx_rms_scale(const float* x, uint32_t n, float eps,
-                                      double* red) {
-  const int tid = threadIdx.x;
+// ------------------------------------------------ rmsnorm's exact scale
+// The reference sums the squares in f64 in order from 0 and takes
+// scale = 1 / sqrt(sum / n + eps) (src/kernels/scalar.rs:47-48); a
+// workgroup sums them as a tree. Every square t_i = x_i^2 is exact in f64,
+// so each sum differs from the exact S only by its own roundings (u = 2^-53):
+//   in order:  |S_seq - S| <= u * (S_1 + ... + S_{n-1}) <= u * W,
+//              W = sum_i t_i * (n - i)   (S_k the partial sums);
+//   a tree:    |S_tree - S| <= D * u * S  (D its depth).
+// The scales of the two sums then differ by at most half their relative
+// difference plus the roundings of the f64 operations on each side, which
+// moves v = x * scale by a bounded number of its ulps (cx_rms_reach). Where
+// no value's f32 rounding can change within that (cx_rms_risk), the tree's
+// scale gives the reference's outputs bit for bit;
+// otherwise the workgroup sums the squares again in order (cx_rms_seq_sum).
+// About one random vector in 300 takes the second sum at n = 2048, one in
+// 80 at n = 4096.
+// A lane's share of the tree: its sum of squares s, and w >= the share of
+// W of its values, from whole groups: a group of G consecutive values from
+// index i0 adds its f64 sum times (n - i0) (>= t_i * (n - i) for each of
+// its values), kept in f32 (the bound carries the margin).
+struct cx_rms_part {
   double s = 0.0;
-  for (uint32_t i = 4 * tid; i < n; i += 4 * 256) {
-    float4 f = *reinterpret_cast<const float4*>(x + i);
-    s += (double)f.x * (double)f.x;
-    s += (double)f.y * (double)f.y;
-    s += (double)f.z * (double)f.z;
-    s += (double)f.w * (double)f.w;
+  float w = 0.0f;
+  template <int G>
+  __device__ void add(const float* a, uint32_t i0, uint32_t n) {
+    double g = 0.0;
+#pragma unroll
+    for (int e = 0; e < G; e++) g += (double)a[e] * (double)a[e];
+    s += g;
+    w = fmaf((float)g, (float)(n - i0), w);
   }
-  s = cx_wave_sum_d(s);
-  if ((tid & 63) == 0) red[tid >> 6] = s;
+};
+__device__ inline cx_rms_part cx_wave_sum_rms(cx_rms_part p) {
+  p.s = cx_wave_sum_d(p.s);
+  float w = p.w;  // only a bound: any order
+  w += __uint_as_float(cx_dpp<CX_DPP_XOR1>(__float_as_uint(w)));
+  w += __uint_as_float(cx_dpp<CX_DPP_XOR2>(__float_as_uint(w)));
+  w += __uint_as_float(cx_dpp<CX_DPP_HALF_MIRROR>(__float_as_uint(w)));
+  w += __uint_as_float(cx_dpp<CX_DPP_MIRROR>(__float_as_uint(w)));
+  w += __shfl_xor(w, 16, CX_WAVE);
+  w += __shfl_xor(w, 32, CX_WAVE);
+  p.w = w;
+  return p;
+}
+__device__ inline double cx_rms_factor(double sum, uint32_t n, float eps) {
+  return 1.0 / sqrt(sum / (double)n + (double)eps);
+}
+// The reach of the check: how far (in f64 ulps of v = x * scale) v may
+// move between the tree's sum `tot` (of depth at most `depth`, with W's
+// bound w) and the sum in order. A relative bound e moves v by at most
+// e * |v| < e * 2^53 ulps, and e * 2^53 = 0.51 (W / tot + depth) + 16 plus
+// the f32 roundings of w / tot (an approximate reciprocal, within 1 ulp),
+// covered by 0.52 and 20. 0 when the two
+// cannot differ (all zeros) or cannot matter (inf, NaN); outside
+// [1e-30, 1e30] W / tot takes its largest value, n.
+__device__ inline uint32_t cx_rms_reach(double tot, float w, uint32_t n, uint32_t depth) {
+  if (!(tot > 0.0) || !(tot < INFINITY)) return 0u;
+  float q = (float)n;
+  if (tot > 1e-30 && tot < 1e30) q = fminf(w * __builtin_amdgcn_rcpf((float)tot), q);
+  return (uint32_t)(0.52f * (q + (float)depth)) + 20u;
+}
+// Whether (float)(a * scale) may round differently when v = a * scale moves
+// by up to `reach` ulps, over all of a thread's values: for v in f32's
+// normal range its f32 rounding drops the low 29 of its 52 mantissa bits
+// and turns at 2^28 (the midpoint), so v is at risk when those bits are
+// within reach of 2^28; below 2^-126 (f32's subnormals round at a fixed
+// quantum) every nonzero v counts as at risk. The distances are kept as
+// running minima (three vector operations a test) and compared once.
+struct cx_rms_risk {
+  uint32_t mid = 0xFFFFFFFFu;  // min over values of 8 * (low 29 bits) - c, wrapping
+  uint32_t low = 0xFFFFFFFFu;  // min over values of (|v|'s high word) - 1
+  // c = 2^31 - 8 * reach: a value's 8 * (low bits) - c is at most 16 * reach
+  // exactly when its low bits are within reach of 2^28
+  __device__ void add(float a, double scale, uint32_t c) {
+    const uint64_t b = (uint64_t)__double_as_longlong((double)a * scale);
+    mid = min(mid, ((uint32_t)b << 3) - c);
+    low = min(low, ((uint32_t)(b >> 32) & 0x7FFFFFFFu) - 1u);  // zeros wrap past the test
+  }
+  __device__ bool unsure(uint32_t reach) const {
+    return mid <= 16u * reach || low < (897u << 20) - 1u;  // 0 < |v| < 2^-126
+  }
+};
+__device__ inline uint32_t cx_rms_c(uint32_t reach) { return 0x80000000u - 8u * reach; }
+// The f64 sum of squares of x[0..n) in order from 0, by one wave: lane l
+// loads x[64q + l] (coalesced), squares it, and the 64 squares are added to
+// the running sum in lane order, read across lanes; lanes past n add +0.0,
+// which leaves a sum of squares as it is. Every lane ends with the sum. x
+// may be in global memory or in LDS.
+__device__ inline double cx_rms_seq_sum(const float* x, uint32_t n) {
+  const uint32_t lane = threadIdx.x & 63;
+  double s = 0.0;
+  float nxt = lane < n ? x[lane] : 0.0f;
+  for (uint32_t q = 0; q < n; q += 64) {
+    const double t = (double)nxt * (double)nxt;
+    // the next chunk's load under this chunk's adds
+    nxt = q + 64 + lane < n ? x[q + 64 + lane] : 0.0f;
+    const uint64_t tb = (uint64_t)__double_as_longlong(t);
+    const int tlo = (int)(uint32_t)tb, thi = (int)(uint32_t)(tb >> 32);
+#pragma unroll 8
+    for (int l = 0; l < 64; l++) {
+      const uint64_t r = (uint64_t)(uint32_t)__builtin_amdgcn_readlane(tlo, l) |
+                         ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(thi, l) << 32);
+      s += __longlong_as_double((long long)r);
+    }
+  }
+  return s;
+}
+
+// The rmsnorm factor of x[0..n) (n % 4 == 0, x 16-byte aligned) over a
+// 256-thread workgroup, bit for bit the reference's: the tree (4 values a
+// lane, wave sums, ((w0 + w1) + w2) + w3), the check above, and the sum in
+// order when the check asks for it. `red` is 9 doubles and `flag` an int of
+// shared memory; every thread of the workgroup calls it.
+__device__ inline double cx_rms_scale(const float* x, uint32_t n, float eps, double* red,
+                                      int* flag) {
+  const int tid = threadIdx.x;
+  cx_rms_part p;
+  for (uint32_t i = 4 * tid; i < n; i += 4 * 256) {
+    const float4 f = *reinterpret_cast<const float4*>(x + i);
+    const float a[4] = {f.x, f.y, f.z, f.w};
+    p.add<4>(a, i, n);
+  }
+  p = cx_wave_sum_rms(p);
+  if ((tid & 63) == 0) {
+    red[tid >> 6] = p.s;
+    red[4 + (tid >> 6)] = (double)p.w;
+  }
+  if (tid == 0) *flag = 0;
   __syncthreads();
-  double tot = ((red[0] + red[1]) + red[2]) + red[3];
+  const double tot = ((red[0] + red[1]) + red[2]) + red[3];
+  const float w = (float)(((red[4] + red[5]) + red[6]) + red[7]);
+  double scale = cx_rms_factor(tot, n, eps);
+  const uint32_t reach = cx_rms_reach(tot, w, n, (n + 1023) / 1024 * 4 + 16);
+  cx_rms_risk risk;
+  const uint32_t c = cx_rms_c(reach);
+  for (uint32_t i = 4 * tid; i < n; i += 4 * 256) {
+    const float4 f = *reinterpret_cast<const float4*>(x + i);
+    risk.add(f.x, scale, c);
+    risk.add(f.y, scale, c);
+    risk.add(f.z, scale, c);
+    risk.add(f.w, scale, c);
+  }
+  if (reach && risk.unsure(reach)) *flag = 1;
   __syncthreads();
-  return 1.0 / sqrt(tot / (double)n + (double)eps);
+  if (*flag) {  // the same for every thread
+    if (tid < 64) {
+      const double seq = cx_rms_seq_sum(x, n);
+      if (tid == 0) red[8] = seq;
+    }
+    __syncthreads();
+    scale = cx_rms_factor(red[8], n, eps);
+  }
+  __syncthreads();  // red and flag are free again
+  return scale;
 }

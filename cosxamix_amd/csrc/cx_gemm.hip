@@ -692,8 +692,8 @@ __global__ __launch_bounds__(256) void k_quantize_gemm(const float* x, uint32_t 
 }
 
 // The prefill's row ops straight into that layout, for the contraction that
-// reads them: rmsnorm (k_norm_rows' arithmetic: the f64 sum of squares in
-// the same tree, then (float)(x * scale) * w; src/kernels/scalar.rs:36-54),
+// reads them: rmsnorm (k_norm_rows' arithmetic: the reference's factor by
+// cx_rms_scale, then (float)(x * scale) * w; src/kernels/scalar.rs:36-54),
 // one workgroup a row; and silu(g) * u (src/forward.rs:483-487); each
 // value is what the row kernel writes, then quantized as k_quantize_gemm
 // quantizes it. Rows [m, m_pad) are zero.
@@ -701,25 +701,13 @@ template <int SUB>
 __global__ __launch_bounds__(256) void k_norm_quant_gemm(const float* x, const float* w,
                                                          uint32_t m, uint32_t k, float eps,
                                                          uint32_t m_pad, int8_t* xq, float* xexs) {
-  __shared__ double red[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ double red[9];
+  __shared__ int flag;
+  const int tid = threadIdx.x;
   const uint32_t a = blockIdx.x;
   const float* xr = x + (size_t)a * k;
   double scale = 0.0;
-  if (a < m) {
-    double sum = 0.0;
-    for (uint32_t i = 8 * tid; i < k; i += 2048) {
-      float v[8];
-      cx_load8(xr + i, v);
-#pragma unroll
-      for (int j = 0; j < 8; j++) sum += (double)v[j] * (double)v[j];
-    }
-    sum = cx_wave_sum_d(sum);
-    if (lane == 0) red[wave] = sum;
-    __syncthreads();
-    const double tot = ((red[0] + red[1]) + red[2]) + red[3];
-    scale = 1.0 / sqrt(tot / (double)k + (double)eps);
-  }
+  if (a < m) scale = cx_rms_scale(xr, k, eps, red, &flag);  // the same for the whole workgroup
   for (uint32_t i = 8 * tid; i < k; i += 2048) {  // whole quads of lanes (k % 32 == 0)
     float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (a < m) {

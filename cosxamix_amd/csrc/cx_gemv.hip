@@ -536,7 +536,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
   using Q = KQ<T>;
   constexpr int SPB = 256 / Q::SUB;  // sub-blocks per super-block
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ double red[4];
+  __shared__ double red[9];
+  __shared__ int nflag;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t tile = blockIdx.x;
@@ -571,39 +572,69 @@ __global__ __launch_bounds__(256) void k_gemv(GemvParams P) {
     copy_act_padded(P.act.xq, sq, P.nb, wave, lane);
     copy_to_lds(P.act.xe, se, P.nsub / 4, wave, lane);
     copy_to_lds(P.act.xs, ss, P.nsub / 4, wave, lane);
-  } else {
-    // rmsnorm (src/kernels/scalar.rs:40-53) and quantization of the
-    // activation while the weights stream in: f64 sum of squares (8
-    // consecutive values a lane, fixed tree), scale = 1/sqrt(sum/k + eps),
-    // v = (x as f64 * scale) as f32 * w, then ops::cuantizar_i8_en
+  }
+  // rmsnorm (src/kernels/scalar.rs:40-53) and quantization of the
+  // activation while the weights stream in: f64 sum of squares (8
+  // consecutive values a lane, a tree), scale = 1/sqrt(sum/k + eps),
+  // v = (x as f64 * scale) as f32 * w, then ops::cuantizar_i8_en; the
+  // reference's factor bit for bit (cx_rms_reach: the sum in order when an
+  // output could round apart)
+  const float* sw = sx + P.k;
+  double scale = 0.0;
+  uint32_t reach = 0, c = 0;
+  if (NORM) {
     wait_all_but(ntile);
+    if (tid == 0) nflag = 0;
     cx_barrier();  // every wave's share of x and w has landed
-    const float* sw = sx + P.k;
-    double sum = 0.0;
+    cx_rms_part part;
     for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
       float a[8];
       cx_load8(sx + i, a);  // two 16-byte LDS reads
-#pragma unroll
-      for (int j = 0; j < 8; j++) sum += (double)a[j] * (double)a[j];
+      part.add<8>(a, i, P.k);
     }
-    sum = cx_wave_sum_d(sum);
-    if (lane == 0) red[wave] = sum;
+    part = cx_wave_sum_rms(part);
+    if (lane == 0) {
+      red[wave] = part.s;
+      red[4 + wave] = (double)part.w;
+    }
     cx_wait_lds();
     cx_barrier();
     const double tot = ((red[0] + red[1]) + red[2]) + red[3];
-    const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
-    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
-      float v[8], a[8], b[8];
-      cx_load8(sx + i, a);
-      cx_load8(sw + i, b);
-#pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = (float)((double)a[j] * scale) * b[j];
-      cx_quant8_padded<Q::SUB>(v, i, sq, se, ss);
-    }
+    const float wt = (float)(((red[4] + red[5]) + red[6]) + red[7]);
+    scale = cx_rms_factor(tot, P.k, P.eps);
+    reach = cx_rms_reach(tot, wt, P.k, P.k / 256 + 16);
+    c = cx_rms_c(reach);
   }
-  cx_wait_vm<0>();  // every direct load has landed
-  cx_wait_lds();
-  __syncthreads();
+  // the activation from the tree's factor; a second pass, when an output
+  // could round apart, from the sum in order
+#pragma unroll 1
+  for (int pass = 0;; pass++) {
+    if (NORM) {
+      cx_rms_risk risk;
+      for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+        float v[8], a[8], b[8];
+        cx_load8(sx + i, a);
+        cx_load8(sw + i, b);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          risk.add(a[j], scale, c);
+          v[j] = (float)((double)a[j] * scale) * b[j];
+        }
+        cx_quant8_padded<Q::SUB>(v, i, sq, se, ss);
+      }
+      if (pass == 0 && reach && risk.unsure(reach)) nflag = 1;
+    }
+    cx_wait_vm<0>();  // every direct load has landed
+    cx_wait_lds();
+    __syncthreads();
+    if (!NORM || pass == 1 || !nflag) break;  // the same for every thread
+    if (wave == 0) {
+      const double seq = cx_rms_seq_sum(sx, P.k);
+      if (lane == 0) red[8] = seq;
+    }
+    __syncthreads();
+    scale = cx_rms_factor(red[8], P.k, P.eps);
+  }
 
   // 2. integer dots + the reference's per-sub-block f32 terms, staged in LDS
   //    by (row, sub-block): two lanes per (row, super-block)
@@ -833,14 +864,14 @@ __global__ __launch_bounds__(1024) void k_gemv_row(GemvParams P) {
 // The row kernel with the rmsnorm prologue (the q/k/v launch): every
 // workgroup makes the normalized, quantized activation itself from the f32
 // residual x and the norm weight w while its weights are in flight. The
-// f64 sum of squares is the same fixed tree as k_gemv's prologue, so the
-// activation is bit for bit that of the other launches: 256 virtual lanes,
-// lane v holding x[8v + 2048j + e]^2 summed over j, then e, in order; each
-// virtual wave's butterfly (cx_wave_sum_d); ((r0 + r1) + r2) + r3. With W < 4
-// waves a thread holds 4/W virtual lanes (virtual wave w + W m), with W > 4
-// only waves 0-3 take part. The normalization and quantization
-// (src/kernels/scalar.rs:40-53, then ops::cuantizar_i8_en) use the same
-// groups of 8 values, into LDS.
+// f64 sum of squares is a tree over 256 virtual lanes, lane v holding
+// x[8v + 2048j + e]^2 summed over j, then e, in order; each virtual wave's
+// butterfly (cx_wave_sum_d); ((r0 + r1) + r2) + r3. With W < 4 waves a
+// thread holds 4/W virtual lanes (virtual wave w + W m), with W > 4 only
+// waves 0-3 take part. The factor is the reference's bit for bit
+// (cx_rms_reach: the sum in order when an output could round apart). The
+// normalization and quantization (src/kernels/scalar.rs:40-53, then
+// ops::cuantizar_i8_en) use the same groups of 8 values, into LDS.
 template <int T, int NB, int W, bool MULTI>
 __global__ __launch_bounds__(64 * W) void k_gemv_row_norm(GemvParams P) {
   using Q = KQ<T>;
@@ -852,7 +883,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_row_norm(GemvParams P) {
   static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16, "power-of-two waves");
   __shared__ __align__(16) int8_t sq[NB * ACT_LDS_BLOCK];
   __shared__ __align__(16) float se[8 * NB], ss[8 * NB];
-  __shared__ double red[4];
+  __shared__ double red[9];
+  __shared__ int nflag;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint64_t xb = (uint64_t)P.nx, wb = (uint64_t)P.nw;
@@ -898,52 +930,78 @@ __global__ __launch_bounds__(64 * W) void k_gemv_row_norm(GemvParams P) {
   const float addend = add ? addp[row] : 0.0f;
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. the f64 sum of squares, the tree of k_gemv's prologue
+  // 2. the f64 sum of squares over the tree, with the bound's weighted sum
+  constexpr uint32_t K = NB * 256;
   const bool in_tree = NT <= 256 || tid < 256;
+  if (tid == 0) nflag = 0;
 #pragma unroll
   for (int m = 0; m < VT; m++) {
-    double sum = 0.0;
+    cx_rms_part part;
 #pragma unroll
     for (int j = 0; j < GJ; j++) {
       const float4 a0 = xv[2 * (m * GJ + j)], a1 = xv[2 * (m * GJ + j) + 1];
       const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-      for (int e = 0; e < 8; e++) sum += (double)a[e] * (double)a[e];
+      const uint32_t g = min((uint32_t)(tid + NT * m), 255u) + 256u * (uint32_t)j;
+      part.add<8>(a, 8 * g, K);
     }
-    sum = cx_wave_sum_d(sum);
-    if (in_tree && lane == 0) red[wave + W * m] = sum;
+    part = cx_wave_sum_rms(part);
+    if (in_tree && lane == 0) {
+      red[wave + W * m] = part.s;
+      red[4 + wave + W * m] = (double)part.w;
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   cx_wait_lds();
   cx_barrier();
   __builtin_amdgcn_sched_barrier(0);
   const double tot = ((red[0] + red[1]) + red[2]) + red[3];
-  const double scale = 1.0 / sqrt(tot / (double)(NB * 256) + (double)P.eps);
-  // 3. v = (x as f64 * scale) as f32 * w, quantized into LDS
-  if (in_tree) {
-#pragma unroll
-    for (int m = 0; m < VT; m++)
-#pragma unroll
-      for (int j = 0; j < GJ; j++) {
-        const float4 a0 = xv[2 * (m * GJ + j)], a1 = xv[2 * (m * GJ + j) + 1];
-        const float4 b0 = wv[2 * (m * GJ + j)], b1 = wv[2 * (m * GJ + j) + 1];
-        const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        const float bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = (float)((double)a[e] * scale) * bw[e];
-        const uint32_t g = (uint32_t)(tid + NT * m) + 256u * (uint32_t)j;
-        cx_quant8_padded<Q::SUB>(v, 8 * g, sq, se, ss);
-      }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  cx_wait_lds();
-  cx_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 4. the lane's four terms and the row sums along the lanes (k_gemv_row)
+  const float wt = (float)(((red[4] + red[5]) + red[6]) + red[7]);
+  // 3. v = (x as f64 * scale) as f32 * w, quantized into LDS, from the
+  //    tree's factor; a second pass, when an output could round apart, from
+  //    the sum in order (x from L2). The lane's activation for step 4 is
+  //    read with the flag.
+  double scale = cx_rms_factor(tot, K, P.eps);
+  const uint32_t reach = cx_rms_reach(tot, wt, K, 8 * GJ + 16);
+  const uint32_t c = cx_rms_c(reach);
   Pre4 a;
-  pre4(h, sq + b * ACT_LDS_BLOCK, se + 8 * b, ss + 8 * b, a);
+#pragma unroll 1
+  for (int pass = 0;; pass++) {
+    cx_rms_risk risk;
+    if (in_tree) {
+#pragma unroll
+      for (int m = 0; m < VT; m++)
+#pragma unroll
+        for (int j = 0; j < GJ; j++) {
+          const float4 a0 = xv[2 * (m * GJ + j)], a1 = xv[2 * (m * GJ + j) + 1];
+          const float4 b0 = wv[2 * (m * GJ + j)], b1 = wv[2 * (m * GJ + j) + 1];
+          const float x8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+          const float bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+          float v[8];
+#pragma unroll
+          for (int q = 0; q < 8; q++) {
+            risk.add(x8[q], scale, c);
+            v[q] = (float)((double)x8[q] * scale) * bw[q];
+          }
+          const uint32_t g = (uint32_t)(tid + NT * m) + 256u * (uint32_t)j;
+          cx_quant8_padded<Q::SUB>(v, 8 * g, sq, se, ss);
+        }
+    }
+    if (pass == 0 && reach && risk.unsure(reach)) nflag = 1;
+    __builtin_amdgcn_sched_barrier(0);
+    cx_wait_lds();
+    cx_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    pre4(h, sq + b * ACT_LDS_BLOCK, se + 8 * b, ss + 8 * b, a);
+    if (pass == 1 || !nflag) break;  // the same for every thread
+    if (wave == 0) {
+      const double seq = cx_rms_seq_sum(P.nx, K);
+      if (lane == 0) red[8] = seq;
+    }
+    cx_wait_lds();
+    cx_barrier();
+    scale = cx_rms_factor(red[8], K, P.eps);
+  }
+  // 4. the lane's four terms and the row sums along the lanes (k_gemv_row)
   float t[4];
   Q::half_t4(r, h, a, nullptr, t);
   float acc = 0.0f;
@@ -1059,7 +1117,8 @@ __global__ __launch_bounds__(256) void k_gemv_glu(GluParams P) {
   using Q = KQ<T>;
   constexpr int SPB = 256 / Q::SUB;
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ double red[4];
+  __shared__ double red[9];
+  __shared__ int nflag;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t row0 = blockIdx.x * GLU_ROWS;
   int8_t* sq = reinterpret_cast<int8_t*>(lds);
@@ -1090,34 +1149,60 @@ __global__ __launch_bounds__(256) void k_gemv_glu(GluParams P) {
     }
   }
   wait_all_but(issued * Q::NLOAD);  // x and w (issued first) have landed
+  if (tid == 0) nflag = 0;
   cx_barrier();
-  // 2. rmsnorm + quantization of the activation (k_gemv's prologue)
+  // 2. rmsnorm + quantization of the activation (k_gemv's prologue, the
+  //    reference's factor bit for bit)
+  const float* sw = sx + P.k;
   {
-    const float* sw = sx + P.k;
-    double sum = 0.0;
+    cx_rms_part part;
     for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
       float a[8];
       cx_load8(sx + i, a);  // two 16-byte LDS reads
-#pragma unroll
-      for (int j = 0; j < 8; j++) sum += (double)a[j] * (double)a[j];
+      part.add<8>(a, i, P.k);
     }
-    sum = cx_wave_sum_d(sum);
-    if (lane == 0) red[wave] = sum;
+    part = cx_wave_sum_rms(part);
+    if (lane == 0) {
+      red[wave] = part.s;
+      red[4 + wave] = (double)part.w;
+    }
     cx_wait_lds();
     cx_barrier();
     const double tot = ((red[0] + red[1]) + red[2]) + red[3];
-    const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
-    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
-      float v[8], a[8], b[8];
-      cx_load8(sx + i, a);
-      cx_load8(sw + i, b);
+    const float wt = (float)(((red[4] + red[5]) + red[6]) + red[7]);
+    double scale = cx_rms_factor(tot, P.k, P.eps);
+    const uint32_t reach = cx_rms_reach(tot, wt, P.k, P.k / 256 + 16);
+    const uint32_t c = cx_rms_c(reach);
+    // a second pass, when an output could round apart, from the sum in
+    // order (x is still in LDS)
+#pragma unroll 1
+    for (int pass = 0;; pass++) {
+      cx_rms_risk risk;
+      for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+        float v[8], a[8], b[8];
+        cx_load8(sx + i, a);
+        cx_load8(sw + i, b);
 #pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = (float)((double)a[j] * scale) * b[j];
-      cx_quant8_padded<Q::SUB>(v, i, sq, se, ss);
+        for (int j = 0; j < 8; j++) {
+          risk.add(a[j], scale, c);
+          v[j] = (float)((double)a[j] * scale) * b[j];
+        }
+        cx_quant8_padded<Q::SUB>(v, i, sq, se, ss);
+      }
+      if (pass == 0 && reach && risk.unsure(reach)) nflag = 1;
+      cx_wait_lds();
+      cx_barrier();  // the activation is in LDS
+      if (pass == 1 || !nflag) break;  // the same for every thread
+      if (wave == 0) {
+        const double seq = cx_rms_seq_sum(sx, P.k);
+        if (lane == 0) red[8] = seq;
+      }
+      cx_wait_lds();
+      cx_barrier();
+      scale = cx_rms_factor(red[8], P.k, P.eps);
     }
   }
-  cx_wait_lds();
-  cx_barrier();  // the activation is in LDS; x and w are read: the region becomes the terms
+  // x and w are read: the region becomes the terms
   // 3. the 64 rows' terms; slot d of the ring holds items d, d + DEPTH, ...
   Pre4 pre;
   if (HOIST) {
@@ -1177,7 +1262,8 @@ __global__ __launch_bounds__(64 * NB) void k_gemv_row_glu(GluParams P) {
   static_assert(GLU_ROWS * LPR == 64 * NB, "the tile's rows fill the NB waves");
   __shared__ __align__(16) int8_t sq[NB * ACT_LDS_BLOCK];
   __shared__ __align__(16) float se[8 * NB], ss[8 * NB];
-  __shared__ double red[4];
+  __shared__ double red[9];
+  __shared__ int nflag;
   __shared__ __align__(16) float act[GLU_ROWS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1211,48 +1297,75 @@ __global__ __launch_bounds__(64 * NB) void k_gemv_row_glu(GluParams P) {
   Q::load((const uint8_t*)reinterpret_cast<const __attribute__((address_space(1))) uint8_t*>(ub) + off, h, ru);
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. the f64 sum of squares (the tree of k_gemv's prologue)
+  // 2. the f64 sum of squares over the tree (k_gemv_row_norm's), with the
+  //    bound's weighted sum
+  constexpr uint32_t K = NB * 256;
+  if (tid == 0) nflag = 0;
   if (wave < 4) {
-    double sum = 0.0;
+    cx_rms_part part;
 #pragma unroll
     for (int j = 0; j < GJ; j++) {
       const float4 a0 = xv[2 * j], a1 = xv[2 * j + 1];
       const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-      for (int e = 0; e < 8; e++) sum += (double)a[e] * (double)a[e];
+      const uint32_t g = (uint32_t)tid + 256u * (uint32_t)j;
+      part.add<8>(a, 8 * g, K);
     }
-    sum = cx_wave_sum_d(sum);
-    if (lane == 0) red[wave] = sum;
+    part = cx_wave_sum_rms(part);
+    if (lane == 0) {
+      red[wave] = part.s;
+      red[4 + wave] = (double)part.w;
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   cx_wait_lds();
   cx_barrier();
   __builtin_amdgcn_sched_barrier(0);
   const double tot = ((red[0] + red[1]) + red[2]) + red[3];
-  const double scale = 1.0 / sqrt(tot / (double)(NB * 256) + (double)P.eps);
-  // 3. v = (x as f64 * scale) as f32 * w, quantized into LDS
-  if (wave < 4) {
-#pragma unroll
-    for (int j = 0; j < GJ; j++) {
-      const float4 a0 = xv[2 * j], a1 = xv[2 * j + 1];
-      const float4 b0 = wv[2 * j], b1 = wv[2 * j + 1];
-      const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      const float bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = (float)((double)a[e] * scale) * bw[e];
-      const uint32_t g = (uint32_t)tid + 256u * (uint32_t)j;
-      cx_quant8_padded<Q::SUB>(v, 8 * g, sq, se, ss);
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  cx_wait_lds();
-  cx_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 4. the lane's four gate and four up terms, one activation read for both
+  const float wt = (float)(((red[4] + red[5]) + red[6]) + red[7]);
+  // 3. v = (x as f64 * scale) as f32 * w, quantized into LDS, from the
+  //    tree's factor; a second pass, when an output could round apart, from
+  //    the sum in order (x from L2). The lane's activation for step 4 is
+  //    read with the flag.
+  double scale = cx_rms_factor(tot, K, P.eps);
+  const uint32_t reach = cx_rms_reach(tot, wt, K, 8 * GJ + 16);
+  const uint32_t c = cx_rms_c(reach);
   Pre4 a;
-  pre4(h, sq + b * ACT_LDS_BLOCK, se + 8 * b, ss + 8 * b, a);
+#pragma unroll 1
+  for (int pass = 0;; pass++) {
+    cx_rms_risk risk;
+    if (wave < 4) {
+#pragma unroll
+      for (int j = 0; j < GJ; j++) {
+        const float4 a0 = xv[2 * j], a1 = xv[2 * j + 1];
+        const float4 b0 = wv[2 * j], b1 = wv[2 * j + 1];
+        const float x8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float v[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          risk.add(x8[q], scale, c);
+          v[q] = (float)((double)x8[q] * scale) * bw[q];
+        }
+        const uint32_t g = (uint32_t)tid + 256u * (uint32_t)j;
+        cx_quant8_padded<Q::SUB>(v, 8 * g, sq, se, ss);
+      }
+    }
+    if (pass == 0 && reach && risk.unsure(reach)) nflag = 1;
+    __builtin_amdgcn_sched_barrier(0);
+    cx_wait_lds();
+    cx_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    pre4(h, sq + b * ACT_LDS_BLOCK, se + 8 * b, ss + 8 * b, a);
+    if (pass == 1 || !nflag) break;  // the same for every thread
+    if (wave == 0) {
+      const double seq = cx_rms_seq_sum(P.nx, K);
+      if (lane == 0) red[8] = seq;
+    }
+    cx_wait_lds();
+    cx_barrier();
+    scale = cx_rms_factor(red[8], K, P.eps);
+  }
+  // 4. the lane's four gate and four up terms, one activation read for both
   float tg[4], tu[4];
   Q::half_t4(rg, h, a, nullptr, tg);
   Q::half_t4(ru, h, a, nullptr, tu);
@@ -1346,7 +1459,8 @@ template <int T, bool NORM>
 __global__ __launch_bounds__(256) void k_gemv32(GemvParams P) {
   using Q = B32<T>;
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ double red[4];
+  __shared__ double red[9];
+  __shared__ int nflag;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t tile = blockIdx.x;
@@ -1378,36 +1492,65 @@ __global__ __launch_bounds__(256) void k_gemv32(GemvParams P) {
   if (!NORM) {
     copy_to_lds(P.act.xq, sq, P.k / 16, wave, lane);
     for (uint32_t i = tid; i < P.nsub; i += 256) se[i] = P.act.xe[i];
-  } else {
-    // rmsnorm then quantization, as k_gemv's prologue (the same f64 tree)
+  }
+  // rmsnorm then quantization, as k_gemv's prologue (the reference's factor
+  // bit for bit)
+  const float* sw = sx + P.k;
+  double scale = 0.0;
+  uint32_t reach = 0, c = 0;
+  if (NORM) {
     wait_all_but(ntile);
+    if (tid == 0) nflag = 0;
     cx_barrier();
-    const float* sw = sx + P.k;
-    double sum = 0.0;
+    cx_rms_part part;
     for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
       float a[8];
       cx_load8(sx + i, a);  // two 16-byte LDS reads
-#pragma unroll
-      for (int j = 0; j < 8; j++) sum += (double)a[j] * (double)a[j];
+      part.add<8>(a, i, P.k);
     }
-    sum = cx_wave_sum_d(sum);
-    if (lane == 0) red[wave] = sum;
+    part = cx_wave_sum_rms(part);
+    if (lane == 0) {
+      red[wave] = part.s;
+      red[4 + wave] = (double)part.w;
+    }
     cx_wait_lds();
     cx_barrier();
     const double tot = ((red[0] + red[1]) + red[2]) + red[3];
-    const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
-    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
-      float v[8], a[8], b[8];
-      cx_load8(sx + i, a);
-      cx_load8(sw + i, b);
-#pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = (float)((double)a[j] * scale) * b[j];
-      cx_quant8<32>(v, i, sq, se, ss);
-    }
+    const float wt = (float)(((red[4] + red[5]) + red[6]) + red[7]);
+    scale = cx_rms_factor(tot, P.k, P.eps);
+    reach = cx_rms_reach(tot, wt, P.k, (P.k + 2047) / 2048 * 8 + 16);
+    c = cx_rms_c(reach);
   }
-  cx_wait_vm<0>();
-  cx_wait_lds();
-  __syncthreads();
+  // the activation from the tree's factor; a second pass, when an output
+  // could round apart, from the sum in order
+#pragma unroll 1
+  for (int pass = 0;; pass++) {
+    if (NORM) {
+      cx_rms_risk risk;
+      for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+        float v[8], a[8], b[8];
+        cx_load8(sx + i, a);
+        cx_load8(sw + i, b);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          risk.add(a[j], scale, c);
+          v[j] = (float)((double)a[j] * scale) * b[j];
+        }
+        cx_quant8<32>(v, i, sq, se, ss);
+      }
+      if (pass == 0 && reach && risk.unsure(reach)) nflag = 1;
+    }
+    cx_wait_vm<0>();
+    cx_wait_lds();
+    __syncthreads();
+    if (!NORM || pass == 1 || !nflag) break;  // the same for every thread
+    if (wave == 0) {
+      const double seq = cx_rms_seq_sum(sx, P.k);
+      if (lane == 0) red[8] = seq;
+    }
+    __syncthreads();
+    scale = cx_rms_factor(red[8], P.k, P.eps);
+  }
 
   // 2. one (row, block) a lane: E_b exactly, then (d_b * xe_b) * E_b
   float* terms = reinterpret_cast<float*>(lds + P.lds_terms);
@@ -1454,7 +1597,8 @@ template <int T, int SUB>
 __global__ __launch_bounds__(256) void k_gemv32_glu(Glu32Params P) {
   using Q = B32<T>;
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ double red[4];
+  __shared__ double red[9];
+  __shared__ int nflag;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t row0 = blockIdx.x * GLU_ROWS;
   int8_t* sq = reinterpret_cast<int8_t*>(lds + P.lds_act);
@@ -1474,36 +1618,61 @@ __global__ __launch_bounds__(256) void k_gemv32_glu(Glu32Params P) {
   uint32_t ntile = copy_to_lds(src_g - skg, lds, (skg + GLU_ROWS * P.row_bytes + 15) >> 4, wave, lane);
   ntile += copy_to_lds(src_u - sku, lds + P.lds_up, (sku + GLU_ROWS * P.row_bytes + 15) >> 4, wave,
                        lane);
-  // 2. rmsnorm then quantization, as k_gemv32's prologue (the same f64 tree)
+  // 2. rmsnorm then quantization, as k_gemv32's prologue (the reference's
+  //    factor bit for bit)
   wait_all_but(ntile);
+  if (tid == 0) nflag = 0;
   cx_barrier();
+  const float* sw = sx + P.k;
   {
-    const float* sw = sx + P.k;
-    double sum = 0.0;
+    cx_rms_part part;
     for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
       float a[8];
       cx_load8(sx + i, a);
-#pragma unroll
-      for (int j = 0; j < 8; j++) sum += (double)a[j] * (double)a[j];
+      part.add<8>(a, i, P.k);
     }
-    sum = cx_wave_sum_d(sum);
-    if (lane == 0) red[wave] = sum;
+    part = cx_wave_sum_rms(part);
+    if (lane == 0) {
+      red[wave] = part.s;
+      red[4 + wave] = (double)part.w;
+    }
     cx_wait_lds();
     cx_barrier();
     const double tot = ((red[0] + red[1]) + red[2]) + red[3];
-    const double scale = 1.0 / sqrt(tot / (double)P.k + (double)P.eps);
-    for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
-      float v[8], a[8], b[8];
-      cx_load8(sx + i, a);
-      cx_load8(sw + i, b);
+    const float wt = (float)(((red[4] + red[5]) + red[6]) + red[7]);
+    double scale = cx_rms_factor(tot, P.k, P.eps);
+    const uint32_t reach = cx_rms_reach(tot, wt, P.k, (P.k + 2047) / 2048 * 8 + 16);
+    const uint32_t c = cx_rms_c(reach);
+    // a second pass, when an output could round apart, from the sum in
+    // order (x is still in LDS)
+#pragma unroll 1
+    for (int pass = 0;; pass++) {
+      cx_rms_risk risk;
+      for (uint32_t i = 8 * tid; i < P.k; i += 2048) {
+        float v[8], a[8], b[8];
+        cx_load8(sx + i, a);
+        cx_load8(sw + i, b);
 #pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = (float)((double)a[j] * scale) * b[j];
-      cx_quant8<32>(v, i, sq, se, ss);
+        for (int j = 0; j < 8; j++) {
+          risk.add(a[j], scale, c);
+          v[j] = (float)((double)a[j] * scale) * b[j];
+        }
+        cx_quant8<32>(v, i, sq, se, ss);
+      }
+      if (pass == 0 && reach && risk.unsure(reach)) nflag = 1;
+      cx_wait_vm<0>();
+      cx_wait_lds();
+      __syncthreads();
+      if (pass == 1 || !nflag) break;  // the same for every thread
+      if (wave == 0) {
+        const double seq = cx_rms_seq_sum(sx, P.k);
+        if (lane == 0) red[8] = seq;
+      }
+      __syncthreads();
+      scale = cx_rms_factor(red[8], P.k, P.eps);
     }
   }
-  cx_wait_vm<0>();
-  cx_wait_lds();
-  __syncthreads();  // x and w are read: the region becomes the terms
+  // x and w are read: the region becomes the terms
   // 3. one (row, block) a lane: rows 0-31 are gate's, 32-63 up's
   const uint32_t items = 2 * GLU_ROWS * P.nsub;
   for (uint32_t it = tid; it < items; it += 256) {
@@ -2069,8 +2238,9 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* g, const floa
 template <int SUB>
 __global__ __launch_bounds__(256) void k_norm_quant(const float* x, const float* w, uint32_t n,
                                                     float eps, int8_t* xq, float* xe, float* xs) {
-  __shared__ double red[4];
-  const double scale = cx_rms_scale(x, n, eps, red);
+  __shared__ double red[9];
+  __shared__ int flag;
+  const double scale = cx_rms_scale(x, n, eps, red, &flag);
   for (uint32_t i = 8 * threadIdx.x; i < n; i += 8 * 256) {  // n % SUB == 0: whole groups
     float v[8], nw[8];
     cx_load8(x + i, v);
@@ -2081,29 +2251,18 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float* x, const float*
   }
 }
 
-// rmsnorm of row blockIdx.x of x[rows][k] in the tree of k_gemv's fused
-// prologue: 8 consecutive values a lane (stride 2048), f64 squares, wave
-// sums, then ((w0 + w1) + w2) + w3; v = (x as f64 * scale) as f32 * w. Rows
-// normalized here are bit for bit the values the decode step's fused GEMV
-// quantizes, so a batched prefill matches token-by-token decoding.
+// rmsnorm of row blockIdx.x of x[rows][k]: the reference's factor
+// (cx_rms_scale, bit for bit), then v = (x as f64 * scale) as f32 * w, the
+// values the decode step's fused GEMV quantizes for the same row, so a
+// batched prefill matches token-by-token decoding.
 __global__ __launch_bounds__(256) void k_norm_rows(const float* x, const float* w, uint32_t k,
                                                    float eps, float* out) {
-  __shared__ double red[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ double red[9];
+  __shared__ int flag;
+  const int tid = threadIdx.x;
   const float* xr = x + (size_t)blockIdx.x * k;
   float* yr = out + (size_t)blockIdx.x * k;
-  double sum = 0.0;
-  for (uint32_t i = 8 * tid; i < k; i += 2048) {
-    float v[8];
-    cx_load8(xr + i, v);
-#pragma unroll
-    for (int j = 0; j < 8; j++) sum += (double)v[j] * (double)v[j];
-  }
-  sum = cx_wave_sum_d(sum);
-  if (lane == 0) red[wave] = sum;
-  __syncthreads();
-  const double tot = ((red[0] + red[1]) + red[2]) + red[3];
-  const double scale = 1.0 / sqrt(tot / (double)k + (double)eps);
+  const double scale = cx_rms_scale(xr, k, eps, red, &flag);
   for (uint32_t i = 8 * tid; i < k; i += 2048) {
     float v[8], nw[8];
     cx_load8(xr + i, v);
@@ -2142,10 +2301,11 @@ __global__ __launch_bounds__(256) void k_add_rows(float* y, const float* a, uint
 
 __global__ __launch_bounds__(256) void k_rmsnorm(float* out, const float* in, const float* w,
                                                  uint32_t n, float eps) {
-  __shared__ double red[4];
+  __shared__ double red[9];
+  __shared__ int flag;
   const float* x = in + (size_t)blockIdx.x * n;
   float* y = out + (size_t)blockIdx.x * n;
-  const double scale = cx_rms_scale(x, n, eps, red);
+  const double scale = cx_rms_scale(x, n, eps, red, &flag);
   for (uint32_t i = threadIdx.x; i < n; i += 256) y[i] = (float)((double)x[i] * scale) * w[i];
 }
 }  // namespace

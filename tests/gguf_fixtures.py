@@ -163,6 +163,25 @@ def vary_norms_and_biases(model, seed, norm_sigma=0.1, bias_sigma=0.3):
     return done
 
 
+def write_tensor(model, idx, data, byte_offset=0):
+    """Writes `data` (any dtype, a whole number of 4-byte words) into a GPU
+    model's tensor `idx` at `byte_offset`, on the device (an F32
+    cx_dequantize is a device copy)."""
+    import ctypes as C
+    import torch
+    from cosxamix_amd import _lib as L
+    lib = L.load()
+    raw = np.ascontiguousarray(data).view(np.uint8).ravel()
+    assert raw.size % 4 == 0 and byte_offset % 4 == 0
+    assert byte_offset + raw.size <= model.tensores()[idx][3]
+    src = torch.from_numpy(raw.view(np.float32).copy()).cuda()
+    L.check(lib.cx_dequantize(O.F32, C.c_void_p(src.data_ptr()), raw.size // 4,
+                              C.c_void_p(model.tensor_ptr(idx) + byte_offset),
+                              C.c_void_p(torch.cuda.current_stream().cuda_stream)),
+            "write_tensor")
+    torch.cuda.synchronize()
+
+
 def mirror(model, threads=16):
     """A GPU model's tensors copied to the host, as an oracle Model."""
     tensors, types = {}, {}
