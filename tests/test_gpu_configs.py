@@ -14,7 +14,9 @@ the HIP path against the oracle (GPU).
   32 layers, an 8192-token seeded prefix prefilled through cx_forward (the
   chunked prefill and the streamed-score attention past 4096 positions at
   32/8 heads), then bit-identical teacher-forced logits and 16 identical
-  greedy tokens.
+  greedy tokens; and the whole model (all 32 layers, the bench's weights)
+  after a 4200-token prefix (positions past 4096), bit-identical logits at
+  4 teacher-forced steps and 12 identical greedy tokens.
 Bars: bit-identical logits (so max-abs 0 <= the north star's 1e-3) and
 identical greedy tokens; matmul outputs bit-identical."""
 import sys
@@ -123,4 +125,45 @@ def test_config5_8192_prefix_two_layers(F):
     assert np.array_equal(got, exp), (got, exp)
     assert cache.largo() == rc.len == 8192 + 16 + 17
     note("config 5: steps and tokens equal")
+    m.close()
+
+
+@pytest.mark.timeout(900)
+def test_config5_full_depth(F):
+    """The bench's config-5 model itself, all 32 layers (its weights:
+    semilla 8): a 4200-token prefix (the chunked prefill, then decode
+    attention past 4096 positions), 4 teacher-forced steps and 12 greedy
+    tokens, each side continuing on its own cache."""
+    c = F.LLAMA3_8B
+    m = F.Modelo(c, tipo=O.Q4_K, semilla=8, tipo_down=O.Q5_K, tipo_salida=O.Q4_K)
+    ref = mirror(m)
+    note("config 5 full depth: model on the host")
+    n0 = 4200
+    prefix = prompt_tokens(n0, c.vocab, seed=5)
+    cap = n0 + 40
+    cache, rc = m.nueva_cache(cap), ref.new_cache(cap)
+    lg, _ = m.forward(prefix, cache)
+    want = ref.forward(prefix, rc)
+    note("config 5 full depth: prefix forwarded by both")
+    assert same_bits(lg, want)
+    for step in range(4):  # teacher-forced: the oracle's token to both
+        tok = O.argmax(want)
+        lg, am = m.forward([tok], cache)
+        want = ref.forward([tok], rc)
+        assert same_bits(lg, want), step
+        assert am == O.argmax(want)
+    got, exp = [], []
+    tg = te = O.argmax(want)
+    for _ in range(12):  # greedy, each side from its own logits
+        got.append(tg)
+        exp.append(te)
+        lg, tg = m.forward([tg], cache)
+        want = ref.forward([te], rc)
+        te = O.argmax(want)
+    got.append(tg)
+    exp.append(te)
+    note("config 5 full depth: tokens generated")
+    assert got == exp, (got, exp)
+    assert same_bits(lg, want)
+    assert cache.largo() == rc.len == n0 + 4 + 12
     m.close()
