@@ -453,7 +453,7 @@ def gemv_traffic():
 BOX_CPU_SHARE = 16
 
 
-def cpu_baseline(F, L, m, prompt, decode_tokens=16, decode_tokens_1t=4):
+def cpu_baseline(F, L, m, prompt, gpu_tokens, gpu_step1, decode_tokens=16, decode_tokens_1t=4):
     """The reference's CPU decode of the same model: the 3B weights copied to
     the host; the prompt prefilled by the oracle (not timed); then decode
     tokens timed with the Q4_K row kernel the reference runs on x86 (its own
@@ -461,7 +461,13 @@ def cpu_baseline(F, L, m, prompt, decode_tokens=16, decode_tokens_1t=4):
     the reference's pool is sized (src/main.rs:578-595), and again on one
     thread. The per-token ops around the row kernel (rmsnorm, rope,
     attention, SwiGLU, argmax, the 32-row task loop) are the oracle's C
-    restatement of the reference's."""
+    restatement of the reference's.
+
+    Parity with the reference as it runs by default on x86 (its asm Q4_K
+    row kernel, which sums in AVX2 lane order, not the scalar spec's order
+    that the GPU and the oracle follow bit for bit): the CPU tokens against
+    the GPU's `gpu_tokens` (the same prompt, greedy), and the first decode
+    step's logits against the GPU's `gpu_step1`."""
     import numpy as np
     from oracle import oracle as O
     ref = O.load_ref()
@@ -487,6 +493,7 @@ def cpu_baseline(F, L, m, prompt, decode_tokens=16, decode_tokens_1t=4):
     pre = time.perf_counter() - t0
     model.set_q4k_kernel(kern)
     tok = O.argmax(lg)
+    toks, first = [tok], []
 
     def decode(n):
         per = []
@@ -495,7 +502,10 @@ def cpu_baseline(F, L, m, prompt, decode_tokens=16, decode_tokens_1t=4):
             t1 = time.perf_counter()
             lg = model.forward(np.array([tok], np.uint32), cache)
             per.append(time.perf_counter() - t1)
+            if not first:
+                first.append(lg)
             tok = O.argmax(lg)
+            toks.append(tok)
         return statistics.median(per)
 
     med = decode(decode_tokens)
@@ -504,7 +514,16 @@ def cpu_baseline(F, L, m, prompt, decode_tokens=16, decode_tokens_1t=4):
     log(f"[bench] cpu baseline: prefill {len(prompt)} tokens {pre:.1f}s (oracle kernels); decode "
         f"median {med * 1e3:.1f} ms/token on {threads} threads ({1 / med:.2f} tok/s), "
         f"{med1 * 1e3:.1f} ms/token on 1 ({1 / med1:.2f} tok/s)")
+    n = min(len(toks), len(gpu_tokens))
+    same = 0
+    while same < n and int(toks[same]) == int(gpu_tokens[same]):
+        same += 1
+    dev = float(np.max(np.abs(first[0] - gpu_step1)))
+    log(f"[bench] cpu baseline ({'asm' if ref else 'scalar'} Q4_K row kernel) against the GPU: "
+        f"first {same} of {n} greedy tokens equal, first decode step logits max-abs {dev:.3g}")
     return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads, "kind": kind,
+            "tokens_compared": n, "tokens_equal": same,
+            "first_step_logits_max_abs": round(dev, 6),
             "value_1_thread": round(1.0 / med1, 3), "cpu": name, "isa_flags": flags,
             "physical_cores": physical, "logical_cpus": logical,
             "sample": (f"same 3B Q4_K weights on the host; {len(prompt)}-token prompt prefilled "
@@ -753,7 +772,14 @@ def main():
     avg, gbps, ncopies = gemv_roofline(F, L, m)
     sustained = gemv_sustained()
     traffic, tdetail = (None, "skipped (--no-traffic)") if a.no_traffic else gemv_traffic()
-    cpu = None if a.no_cpu else cpu_baseline(F, L, m, prompt)
+    cpu = None
+    if not a.no_cpu:
+        # the GPU's logits at the first decode step, for the parity note
+        c1 = m.nueva_cache(len(prompt) + 2)
+        m.forward(prompt, c1, logits=False)
+        step1, _ = m.forward([int(toks[0])], c1)
+        c1.close()
+        cpu = cpu_baseline(F, L, m, prompt, toks, step1)
     batched = batched_bench(L, m, not a.no_cpu)
     m.close()
     config5 = None if a.no_config5 else config5_bench(F, L)

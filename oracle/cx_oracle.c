@@ -1309,6 +1309,54 @@ int orc_attention(const float *q, const float *k, const float *v, size_t tokens,
   return 0;
 }
 
+/* A test hook (not the reference's order): the attention of orc_attention
+ * with its sums split over chunks of positions, combined as a split-K kernel
+ * combines them; the scores are the same sequential dots. */
+int orc_attention_split(const float *q, const float *k, const float *v, size_t tokens,
+                        size_t total, size_t heads, size_t kvh, size_t hd, size_t chunk,
+                        float *out) {
+  if (!kvh || heads % kvh || !chunk) { set_err("attention_split: groups or chunk"); return -1; }
+  if (tokens > total) { set_err("attention_split: tokens > total"); return -1; }
+  const size_t wq = heads * hd, wkv = kvh * hd, per = heads / kvh, off = total - tokens;
+  const float scale = 1.0f / sqrtf((float)hd);
+  const size_t nch = (total + chunk - 1) / chunk;
+  int err = 0;
+#pragma omp parallel for schedule(dynamic)
+  for (size_t th = 0; th < tokens * heads; th++) {
+    const size_t t = th / heads, h = th % heads, vis = off + t + 1, base = (h / per) * hd;
+    float *sc = (float *)malloc(vis * 4), *m = (float *)malloc(nch * 4), *l = (float *)malloc(nch * 4);
+    float *o = (float *)calloc(nch * hd, 4);
+    if (!sc || !m || !l || !o) { err = 1; free(sc); free(m); free(l); free(o); continue; }
+    const float *qh = q + t * wq + h * hd;
+    for (size_t p = 0; p < vis; p++) sc[p] = orc_dot_f32(qh, k + p * wkv + base, hd) * scale;
+    size_t used = 0;
+    for (size_t c0 = 0; c0 < vis; c0 += chunk, used++) {
+      const size_t c1 = c0 + chunk < vis ? c0 + chunk : vis;
+      float mx = -INFINITY, sum = 0.0f;
+      for (size_t p = c0; p < c1; p++) mx = fmaxf(mx, sc[p]);
+      for (size_t p = c0; p < c1; p++) {
+        const float e = expf(sc[p] - mx);
+        sum += e;
+        for (size_t d = 0; d < hd; d++) o[used * hd + d] += e * v[p * wkv + base + d];
+      }
+      m[used] = mx;
+      l[used] = sum;
+    }
+    float M = -INFINITY, L = 0.0f;
+    for (size_t i = 0; i < used; i++) M = fmaxf(M, m[i]);
+    for (size_t i = 0; i < used; i++) L += l[i] * expf(m[i] - M);
+    const float inv = 1.0f / L;
+    for (size_t d = 0; d < hd; d++) {
+      float acc = 0.0f;
+      for (size_t i = 0; i < used; i++) acc += o[i * hd + d] * expf(m[i] - M);
+      out[t * wq + h * hd + d] = acc * inv;
+    }
+    free(sc); free(m); free(l); free(o);
+  }
+  if (err) { set_err("attention_split: alloc"); return -1; }
+  return 0;
+}
+
 /* ------------------------------------------------------------ matmuls */
 #define ROWS_PER_TASK 32 /* ops.rs:43 COLUMNAS_MINIMAS */
 
@@ -1807,7 +1855,11 @@ int orc_forward(const orc_model *M, const uint32_t *toks, size_t t, orc_cache *c
     if (orc_rope(kk, t, g->kv_heads, hd, M->cos_t, M->sin_t, g->ctx, c->len)) goto done;
     memcpy(c->k[li] + c->len * kvd, kk, t * kvd * 4);
     memcpy(c->v[li] + c->len * kvd, vv, t * kvd * 4);
-    if (orc_attention(qr, c->k[li], c->v[li], tr, total, g->heads, g->kv_heads, hd, att)) goto done;
+    if (M->attn_chunk
+            ? orc_attention_split(qr, c->k[li], c->v[li], tr, total, g->heads, g->kv_heads, hd,
+                                  (size_t)M->attn_chunk, att)
+            : orc_attention(qr, c->k[li], c->v[li], tr, total, g->heads, g->kv_heads, hd, att))
+      goto done;
     if (proj(M, att, tr, D, D, L->o, L->t_o, NULL, pr)) goto done;
     for (size_t i = 0; i < tr * D; i++) xr[i] += pr[i];
     for (size_t r = 0; r < tr; r++) orc_rmsnorm(xnr + r * D, xr + r * D, L->ffn_norm, D, g->eps);

@@ -173,6 +173,9 @@ typedef struct {
   float *cos_t, *sin_t;         /* ctx x head_dim/2, owned */
   orc_row_kernel kern_override; /* NULL = scalar spec */
   int threads;
+  /* 0: the reference's attention order. A test hook otherwise: the sums
+   * split over chunks of attn_chunk positions (orc_attention_split) */
+  int attn_chunk;
 } orc_model;
 
 typedef struct {
@@ -187,6 +190,13 @@ void orc_model_release(orc_model *m);
 int orc_cache_init(orc_cache *c, const orc_config *cfg, size_t cap);
 void orc_cache_release(orc_cache *c, const orc_config *cfg);
 void orc_cache_truncate(orc_cache *c, size_t n);
+/* Test hook, not the reference's order: attention whose softmax and P.V
+ * sums are split over chunks of `chunk` positions, each chunk's (max, sum of
+ * exps, unnormalized P.V) formed in order, then combined with the factors
+ * exp(m_i - M) -- the order of a split-K kernel. */
+int orc_attention_split(const float *q, const float *k, const float *v, size_t tokens,
+                        size_t total, size_t heads, size_t kvh, size_t hd, size_t chunk,
+                        float *out);
 /* logits of the last token into `logits` (vocab floats) */
 int orc_forward(const orc_model *m, const uint32_t *toks, size_t t,
                 orc_cache *c, float *logits);

@@ -60,7 +60,8 @@ class OrcLayer(C.Structure):
 class OrcModel(C.Structure):
     _fields_ = [("cfg", OrcConfig), ("embd", _f32p), ("out_norm", _f32p), ("out", _u8p),
                 ("t_out", C.c_int), ("layers", C.POINTER(OrcLayer)), ("cos_t", _f32p),
-                ("sin_t", _f32p), ("kern_override", C.c_void_p), ("threads", C.c_int)]
+                ("sin_t", _f32p), ("kern_override", C.c_void_p), ("threads", C.c_int),
+                ("attn_chunk", C.c_int)]
 
 
 class OrcCache(C.Structure):
@@ -387,6 +388,12 @@ class Model:
 
     def set_threads(self, n: int):
         self.m.threads = max(1, int(n))
+
+    def set_attention_chunk(self, n: int):
+        """0: the reference's attention order; n > 0: a test hook, the
+        softmax and P.V sums split over chunks of n positions (the order of
+        a split-K kernel, orc_attention_split)."""
+        self.m.attn_chunk = max(0, int(n))
 
     def new_cache(self, cap: int) -> "Cache":
         return Cache(self, cap)
