@@ -356,6 +356,79 @@ def gemv_sustained(iters=30, reps=5, n=151936, k=2048, copies=3):
 PROBE_COPY_BYTES = 64 << 20
 
 
+def read_peak(L, m, iters=360, reps=5):
+    """Measured read rates for the roofline (cx_stream_read: 16-byte loads
+    over a grid, no arithmetic after them), each a captured graph of
+    launches timed with HIP events, median of `reps`:
+    - 4 buffers of 256 MB in turn (1 GB, past the 256 MB Infinity Cache):
+      the read peak this chip reaches from HBM;
+    - the model's 36 ffn_gate matrices in turn, 12,681,216 B a launch, the
+      config-1 GEMV's own bytes: what a launch of that size can read with
+      nothing else to do (the launch boundary and the first bytes' latency
+      included);
+    - a 64 MiB device-to-device copy (torch), 128 MiB moved."""
+    import ctypes as C
+    import torch
+    lib = L.load()
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def timed(bufs, nbytes, n_launch):
+        def launch(i):
+            L.check(lib.cx_stream_read(C.c_void_p(bufs[i % len(bufs)]), nbytes,
+                                       C.c_void_p(sink.data_ptr()), stream()), "stream_read")
+        for i in range(len(bufs)):
+            launch(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n_launch):
+                launch(i)
+        g.replay()
+        torch.cuda.synchronize()
+        per = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            per.append(e0.elapsed_time(e1) * 1e-3 / n_launch)
+        return statistics.median(per)
+
+    big = [torch.empty(256 << 20, dtype=torch.uint8, device="cuda").random_(0, 255) for _ in range(4)]
+    t_big = timed([b.data_ptr() for b in big], 256 << 20, 40)
+    del big
+    names = [t[0] for t in m.tensores()]
+    gates = [m.tensor_ptr(i) for i, n in enumerate(names) if n.endswith("ffn_gate.weight")]
+    wbytes = 11008 * 2048 // 256 * 144
+    t_gate = timed(gates, wbytes, iters)
+    src = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e-3 / 10)
+    t_copy = statistics.median(per)
+    del src, dst
+    torch.cuda.empty_cache()
+    out = {"read_GBps": round((256 << 20) / t_big / 1e9, 1),
+           "read_12_7MB_GBps": round(wbytes / t_gate / 1e9, 1),
+           "read_12_7MB_us": round(t_gate * 1e6, 3),
+           "copy_64MiB_GBps": round(2 * PROBE_COPY_BYTES / t_copy / 1e9, 1)}
+    log(f"[bench] measured reads: {out['read_GBps']} GB/s over 1 GB; {out['read_12_7MB_GBps']} "
+        f"GB/s ({out['read_12_7MB_us']} us) a 12.7 MB launch over the 36 ffn_gate matrices; "
+        f"64 MiB copy {out['copy_64MiB_GBps']} GB/s (read + write)")
+    return out
+
+
 def gemv_probe():
     """The workload the PMC passes count: config-1 Q4_K GEMVs over 36
     rotating matrices (random bytes with finite f16 scales: traffic does not
@@ -747,10 +820,13 @@ def main():
     if a.roofline_only:
         m = F.Modelo(F.DAISS_3B, tipo=L.Q4_K, semilla=42)
         avg, gbps, ncopies = gemv_roofline(F, L, m)
+        peak = read_peak(L, m)
         m.close()
         sus = gemv_sustained()
         print(json.dumps({"us_per_launch": round(avg * 1e6, 3), "GBps": round(gbps, 1),
                           "frac": round(gbps / HBM_PEAK_GBPS, 4), "rotating_matrices": ncopies,
+                          "measured": peak, "frac_of_measured_peak": round(gbps / peak["read_GBps"], 4),
+                          "frac_of_read_at_this_size": round(gbps / peak["read_12_7MB_GBps"], 4),
                           "sustained": sus}), flush=True)
         return 0
     if a.batched_only:
@@ -770,6 +846,7 @@ def main():
     prefill = prefill_bench(m, prompt)
     sampled = sampled_bench(m, prompt)
     avg, gbps, ncopies = gemv_roofline(F, L, m)
+    measured = read_peak(L, m)
     sustained = gemv_sustained()
     traffic, tdetail = (None, "skipped (--no-traffic)") if a.no_traffic else gemv_traffic()
     cpu = None
@@ -808,6 +885,11 @@ def main():
                      "kernel": "k_gemv<Q4_K> config 1 (11008x2048)",
                      "us_per_launch": round(avg * 1e6, 3), "bytes_per_launch": CONFIG1_BYTES,
                      "rotating_matrices": ncopies,
+                     # measured on this box: the read peak (1 GB), the read rate of a
+                     # launch of the GEMV's own 12.7 MB with nothing else to do, a copy
+                     "measured_peak": measured,
+                     "frac_of_measured_peak": round(gbps / measured["read_GBps"], 4),
+                     "frac_of_read_at_this_size": round(gbps / measured["read_12_7MB_GBps"], 4),
                      # the same kernel where the launch's fixed cost is amortized
                      "sustained": sustained},
         "cpu_baseline": cpu,

@@ -74,6 +74,7 @@ SIGNATURES = {
     "cx_attention": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp]),
     "cx_attention_decode": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, C.c_int, _vp, _vp]),
     "cx_argmax": (C.c_int, [_vp, _sz, _vp, _vp]),
+    "cx_stream_read": (C.c_int, [_vp, _sz, _vp, _vp]),
     "cx_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "cx_gguf_free": (None, [_vp]),
     "cx_gguf_header": (C.c_int, [_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),

@@ -26,7 +26,7 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-ffp-contract=
          "-mllvm", "-amdgpu-mfma-vgpr-form",
          "-Wall", "-Wno-unused-function", "-I" + os.path.join(ROOT, "include")]
 SOURCES = ["cx_api.hip", "cx_gemv.hip", "cx_gemm.hip", "cx_ops.hip", "cx_attn.hip", "cx_sample.hip", "cx_gen.hip", "cx_quant.hip",
-           "cx_gguf.hip"]
+           "cx_gguf.hip", "cx_probe.hip"]
 
 
 def _run(cmd):

@@ -227,6 +227,13 @@ int cx_attention_decode(const float *q, const float *k, const float *v,
  * *out is a DEVICE uint32. */
 int cx_argmax(const float *v, size_t n, uint32_t *out, void *stream);
 
+/* A measurement probe with no counterpart in the reference: reads
+ * bytes (a multiple of 16) from the 16-byte aligned device buffer p once,
+ * with no arithmetic after the loads (sink: a device uint32 the kernel
+ * only writes for one improbable fold of the data). The bench times it to
+ * report a measured read peak beside the nominal 8 TB/s. */
+int cx_stream_read(const void *p, size_t bytes, uint32_t *sink, void *stream);
+
 /* sampler::Muestreador::elegir (src/sampler.rs:61-152) on device logits[n]:
  * temperature <= 0 is the argmax with no draw; otherwise one draw of the
  * xorshift64* generator whose state *state (HOST) holds (Azar::siguiente,

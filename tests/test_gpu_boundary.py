@@ -288,3 +288,25 @@ def test_model_freed_before_its_cache(dev):
     c2 = C.c_void_p()
     assert lib.cx_cache_new(mh, 32, C.byref(c2)) != 0  # no new cache on a freed model
     lib.cx_cache_free(ch)  # releases the model too
+
+
+def test_stream_read_probe(dev):
+    """cx_stream_read (the bench's read-peak probe) reads the whole buffer:
+    its fold reaches the sink only for the data that makes it 0x9E3779B9."""
+    import ctypes as C
+    from cosxamix_amd import _lib as L
+    lib = L.load()
+    s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for nbytes in (16, 4096, 5 << 20, (5 << 20) + 48):
+        buf = torch.zeros(nbytes // 4, dtype=torch.int32, device=dev)
+        L.check(lib.cx_stream_read(C.c_void_p(buf.data_ptr()), nbytes, C.c_void_p(sink.data_ptr()), s), "read")
+        torch.cuda.synchronize()
+        assert int(sink.item()) == 0
+        # one word anywhere -- the last one -- set to the value the fold stores
+        buf[-1] = torch.tensor(0x9E3779B9, dtype=torch.int64).to(torch.int32)
+        L.check(lib.cx_stream_read(C.c_void_p(buf.data_ptr()), nbytes, C.c_void_p(sink.data_ptr()), s), "read")
+        torch.cuda.synchronize()
+        assert int(sink.item()) & 0xFFFFFFFF == 0x9E3779B9, nbytes
+        sink.zero_()
+    assert lib.cx_stream_read(C.c_void_p(buf.data_ptr() + 4), 32, C.c_void_p(sink.data_ptr()), s) == -1
