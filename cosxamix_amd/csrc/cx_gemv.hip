@@ -1075,6 +1075,113 @@ __global__ __launch_bounds__(1024) void k_gemv_reg1(GemvParams P) {
   }
 }
 
+// The plain Q4_K/Q5_K GEMV for long rows (the down projections: k = 11008,
+// 43 super-blocks, or 14336, 56; any 16 < nb <= 64): one row a wave, lane
+// b < nb holding super-block b whole, both halves' eight terms in order. The
+// scalar spec's sum (total = 0; total += term_s, src/kernels/scalar.rs:
+// 141-167) runs along the row's lanes as in k_gemv_row: nb steps, each
+// taking the left neighbour's running sum (wave_shr:1, lane 0 reads +0.0)
+// and adding the lane's eight terms, so after step s lane s holds terms
+// 0 .. 8s + 7 summed from +0.0 in order, and lane nb - 1 ends with the row
+// total. Lanes past nb reload the last block; lanes below them never read
+// their sums. No term passes through LDS and no barrier waits for the
+// weights: a wave starts its chain once its own row has landed. With nb a
+// template argument (NB > 0) the chain is unrolled: a dependent f32 add
+// issues every ~4.5 clocks on gfx950, and a loop's branch per step cost as
+// much again. The activation (nb*20 chunks of 16 bytes: xq, then xe, then
+// xs) is loaded by every thread, ROWL_AP chunks each, and staged in LDS as
+// in k_gemv_row.
+constexpr uint32_t ROWL_NB_MAX = 64;
+template <int W>
+struct RowlShape {
+  static constexpr uint32_t AP = (ROWL_NB_MAX * 20 + 64 * W - 1) / (64 * W);
+};
+__device__ inline int4 rowl_act_load(const cx_qact& act, uint32_t nb, uint32_t c) {
+  const uint32_t nx = nb * 16, ne = nb * 2;
+  const int4* p = c < nx        ? reinterpret_cast<const int4*>(act.xq) + c
+                  : c < nx + ne ? reinterpret_cast<const int4*>(act.xe) + (c - nx)
+                                : reinterpret_cast<const int4*>(act.xs) + (c - nx - ne);
+  return *p;
+}
+__device__ inline float rowl_step(float acc, const float (&t)[8]) {
+  float v = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xF, 0xF,
+                                                       true));  // wave_shr:1
+#pragma unroll
+  for (int j = 0; j < 8; j++) v += t[j];
+  return v;
+}
+template <int T, int W, int NB>
+__global__ __launch_bounds__(64 * W) void k_gemv_rowl(GemvParams P) {
+  using Q = KQ<T>;
+  constexpr uint32_t AP = NB ? (NB * 20 + 64 * W - 1) / (64 * W) : RowlShape<W>::AP;
+  constexpr uint32_t NBL = NB ? NB : ROWL_NB_MAX;  // LDS blocks
+  __shared__ __align__(16) int8_t sq[NBL * ACT_LDS_BLOCK];
+  __shared__ __align__(16) float se[8 * NBL], ss[8 * NBL];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t tile = blockIdx.x;
+  int sg = 0;
+  while (tile >= P.tile_end[sg]) sg++;
+  if (sg) tile -= P.tile_end[sg - 1];
+  const cx_seg S = P.seg[sg];
+  const uint32_t nb = NB ? (uint32_t)NB : P.nb, nch = nb * 20;
+  const uint32_t row0 = tile * W;
+  const uint32_t rows = min((uint32_t)W, S.rows - row0);
+  const uint32_t row = row0 + min((uint32_t)wave, rows - 1);
+  const uint32_t b = min((uint32_t)lane, nb - 1);
+  // 1. the thread's activation chunks (L2 hits; past the end: the last one),
+  //    then the row's weights straight into registers
+  int4 av[AP];
+#pragma unroll
+  for (uint32_t i = 0; i < AP; i++) av[i] = rowl_act_load(P.act, nb, min(tid + 64 * W * i, nch - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  typename Q::Regs r0, r1;
+  const uint8_t* blk = S.w + (size_t)row * P.row_bytes + (size_t)b * Q::BPB;
+  Q::load(blk, 0, r0);
+  Q::load(blk, 1, r1);
+  const bool add = P.epi == CX_EPI_ACCUM || S.bias;
+  const float* addp = P.epi == CX_EPI_ACCUM ? S.y : S.bias;
+  const float addend = add ? addp[row] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (uint32_t i = 0; i < AP; i++) {
+    const uint32_t c = tid + 64 * W * i;
+    if (c >= nch) continue;
+    const uint32_t nx = nb * 16, ne = nb * 2;
+    int4* p = c < nx        ? reinterpret_cast<int4*>(sq + (c >> 4) * ACT_LDS_BLOCK + 16 * (c & 15))
+              : c < nx + ne ? reinterpret_cast<int4*>(se) + (c - nx)
+                            : reinterpret_cast<int4*>(ss) + (c - nx - ne);
+    *p = av[i];
+  }
+  // a plain barrier (__syncthreads() would also wait for the weights)
+  __builtin_amdgcn_sched_barrier(0);
+  cx_wait_lds();
+  cx_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  // 2. the lane's eight terms: half 0's sub-blocks 0-3, then half 1's 4-7
+  float t[8];
+  {
+    Pre4 a;
+    float t4[4];
+    pre4(0, sq + b * ACT_LDS_BLOCK, se + 8 * b, ss + 8 * b, a);
+    Q::half_t4(r0, 0, a, nullptr, t4);
+#pragma unroll
+    for (int j = 0; j < 4; j++) t[j] = t4[j];
+    pre4(1, sq + b * ACT_LDS_BLOCK, se + 8 * b, ss + 8 * b, a);
+    Q::half_t4(r1, 1, a, nullptr, t4);
+#pragma unroll
+    for (int j = 0; j < 4; j++) t[4 + j] = t4[j];
+  }
+  // 3. the row sum along the lanes
+  float acc = 0.0f;
+  if constexpr (NB > 0) {
+#pragma unroll
+    for (int s = 0; s < NB; s++) acc = rowl_step(acc, t);
+  } else {
+    for (uint32_t s = 0; s < nb; s++) acc = rowl_step(acc, t);
+  }
+  if ((uint32_t)wave < rows && (uint32_t)lane == nb - 1) S.y[row] = add ? acc + addend : acc;
+}
+
 // total = 0; total += term_s for s = 0 .. n-1 (any n), in that order
 __device__ inline float row_sum_any(const float* terms, uint32_t n) {
   float acc = row_sum(terms, n & ~3u);
@@ -1856,6 +1963,33 @@ int launch_row_norm(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   return CX_OK;
 }
 
+// The long-row kernel (k_gemv_rowl) for a plain Q4_K/Q5_K launch of
+// 16 < k/256 <= 64 super-blocks: W waves (W rows) a workgroup.
+// The long-row kernel (k_gemv_rowl) for a plain Q4_K/Q5_K launch of
+// 16 < k/256 <= 64 super-blocks: 4 waves (4 rows) a workgroup, the chain
+// unrolled at 43 and 56 blocks. Measured on MI355X in the 3B decode step
+// (down, 2048 x 11008, 512 tiles): 706 tok/s against 700 with 8 waves, 663
+// with 16 and 691 with k_gemv_reg1; at config 5 (4096 x 14336 Q5_K) 8 waves
+// 250.0 tok/s against 248.9 with k_gemv_reg1. A two-row ring (wave_ror:1, 32
+// lanes a row, one wave a SIMD) took 8.5 us against 7.0: a wave's chain is
+// bound by its own dependent adds, so fewer waves only delay the loads.
+template <int T>
+int launch_rowl(GemvParams& P, const uint32_t* rows, hipStream_t s) {
+  constexpr uint32_t W = 4;
+  P.R = W;
+  uint32_t acc = 0;
+  for (int i = 0; i < P.nseg; i++) {
+    acc += (rows[i] + W - 1) / W;
+    P.tile_end[i] = acc;
+  }
+  const dim3 g(acc), blk(64 * W);
+  if (P.nb == 43) hipLaunchKernelGGL((k_gemv_rowl<T, W, 43>), g, blk, 0, s, P);
+  else if (P.nb == 56) hipLaunchKernelGGL((k_gemv_rowl<T, W, 56>), g, blk, 0, s, P);
+  else hipLaunchKernelGGL((k_gemv_rowl<T, W, 0>), g, blk, 0, s, P);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
+
 template <int T, bool NORM>
 int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   using Q = KQ<T>;
@@ -1875,6 +2009,8 @@ int launch_t(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   if constexpr (REG) {
     const RowPlan rp = row_plan(P.k, rows, P.nseg);
     if (rp.R) return P.dbg ? launch_row<T, true>(P, rows, rp, s) : launch_row<T, false>(P, rows, rp, s);
+    if (!P.dbg && P.nb > 16 && P.nb <= ROWL_NB_MAX)
+      return launch_rowl<T>(P, rows, s);
   }
   if constexpr (NORM && (T == CX_Q4_K || T == CX_Q5_K)) {
     if (P.k == 2048 || P.k == 4096) return launch_row_norm<T>(P, rows, s);

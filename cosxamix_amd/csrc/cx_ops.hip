@@ -519,9 +519,10 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   //    (the same in every wave), e = exp(s - max) of the first 256
   //    positions by every thread, then of the rest by waves 1-3 while
   //    wave 0 adds the ones formed: the sum is the f32 sum in position
-  //    order from 0 (src/ops.rs:1211-1229), its first 256 adds one by one
-  //    and the rest by seq_sum_scan. The division by the sum is folded
-  //    into the products below.
+  //    order from 0 (src/ops.rs:1211-1229): one add a position when the V
+  //    slice fits the ring, else the first 256 one by one and the rest by
+  //    seq_sum_scan. The division by the sum is folded into the products
+  //    below.
   float mx = -INFINITY;
 #pragma unroll
   for (uint32_t i = 0; i < CML_MAX / 64; i++)
@@ -529,7 +530,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   mx = cx_wave_max(mx);
   const bool uniform = !isfinite(mx);  // all -inf, or a NaN (src/ops.rs:1214-1219)
   const float pu = 1.0f / (float)total;
-  const uint32_t r64 = (total + 63) / 64 * 64;  // +0.0 from total to r64 (seq_sum_dpp)
+  const uint32_t r64 = (total + 63) / 64 * 64;  // +0.0 from total to r64 (seq_add16)
   if ((uint32_t)tid < total)
     e[tid] = uniform ? pu : cx_expf_tab(e[tid] - mx, etab);
   else if ((uint32_t)tid < r64)
@@ -564,7 +565,12 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
       cx_wait_lds();
       cx_barrier();  // the rest of the exps are in LDS
       if (w != 0) issue_all();
-      if (w == 0 && !uniform) tot = seq_sum_scan(e + 256, total - 256, tot, false);
+      // one add a position (~4.5 clocks): at these lengths (at most
+      // PV_NST * PV_STP) faster than the binade scan, whose windows and
+      // events cost more than they save (1.7 us at 388 positions, against
+      // ~0.9)
+      if (w == 0 && !uniform)
+        tot = seq_add16<(PV_NST * PV_STP / 16 + 2) / 3 * 3>(e + 256, (total - 256 + 15) / 16 * 16, tot);
     }
   } else {
     // a longer cache (V streams through the ring later): stages of
@@ -596,8 +602,9 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   // 3. out[d0 + t] over the V ring, position order (wave 0)
   float* prod = ring + PV_NST * PV_STP * PV_DS;  // two buffers of PV_DS * PV_PSTR
   // helper waves: stage s's products p_j * v_j[d], p_j = e_j * (1/sum) (or
-  // 1/total when uniform), into buffer s % 2, [dim][position]; task k is
-  // dims 4 (k % DQ) .. +3 and positions 8 (k / DQ) .. +7
+  // 1/total when uniform), into buffer s % 2, [dim][position], +0.0 for
+  // positions past total; task k is dims 4 (k % DQ) .. +3 and positions
+  // 8 (k / DQ) .. +7
   auto make = [&](uint32_t s) {
     constexpr uint32_t DQ = PV_DS / 4, NT = DQ * (PV_STP / 8);
     const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS);
@@ -620,10 +627,11 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         const float4 v = vv[i];
-        r[0][i] = pp[i] * v.x;
-        r[1][i] = pp[i] * v.y;
-        r[2][i] = pp[i] * v.z;
-        r[3][i] = pp[i] * v.w;
+        const bool live = s * PV_STP + 8 * pq + i < total;
+        r[0][i] = live ? pp[i] * v.x : 0.0f;
+        r[1][i] = live ? pp[i] * v.y : 0.0f;
+        r[2][i] = live ? pp[i] * v.z : 0.0f;
+        r[3][i] = live ? pp[i] * v.w : 0.0f;
       }
 #pragma unroll
       for (int j = 0; j < 4; j++) {
@@ -651,28 +659,31 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     if (w != 0 && s + PV_NST < nstage) issue(s + PV_NST);
     if (w == 0) {
       if (t < (int)PV_DS) {
+        // 32 positions a batch, the next batch's reads ahead of the adds;
+        // the stage's last batch ends past total with products of +0.0
+        // (adding +0.0 changes no sum that starts at +0.0)
         const float* pr = prod + (s & 1) * (PV_DS * PV_PSTR) + t * PV_PSTR;
-        if ((s + 1) * PV_STP <= total) {
-          // 32 positions a batch, the next batch's reads ahead of the adds
-          const float4* p4 = reinterpret_cast<const float4*>(pr);
-          float4 a[8], b[8];
+        const uint32_t nq = min(4u, (total - s * PV_STP + 31) / 32);
+        const float4* p4 = reinterpret_cast<const float4*>(pr);
+        float4 a[8], b[8];
 #pragma unroll
-          for (int i = 0; i < 8; i++) a[i] = p4[i];
+        for (int i = 0; i < 8; i++) a[i] = p4[i];
 #pragma unroll
-          for (int i = 0; i < 8; i++) b[i] = p4[8 + i];
-          __builtin_amdgcn_sched_barrier(0);
-          add32(o, a);
+        for (int i = 0; i < 8; i++) b[i] = p4[8 + i];
+        __builtin_amdgcn_sched_barrier(0);
+        add32(o, a);
+        if (nq > 1) {
 #pragma unroll
           for (int i = 0; i < 8; i++) a[i] = p4[16 + i];
           __builtin_amdgcn_sched_barrier(0);
           add32(o, b);
+          if (nq > 2) {
 #pragma unroll
-          for (int i = 0; i < 8; i++) b[i] = p4[24 + i];
-          __builtin_amdgcn_sched_barrier(0);
-          add32(o, a);
-          add32(o, b);
-        } else {
-          for (uint32_t j = 0; s * PV_STP + j < total; j++) o += pr[j];
+            for (int i = 0; i < 8; i++) b[i] = p4[24 + i];
+            __builtin_amdgcn_sched_barrier(0);
+            add32(o, a);
+            if (nq > 3) add32(o, b);
+          }
         }
       }
       if (s + PV_NST < nstage) issue(s + PV_NST);

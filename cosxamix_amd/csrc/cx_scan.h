@@ -9,67 +9,51 @@
 
 namespace {
 
-// Sequential sum of x[0..n) from tot, with no LDS read on the chain: lanes
-// 0-15 of a wave (exactly those active) read 64 positions a batch, lane l
-// the four at 64 b + 4 l, and lane 15 adds lane l's values in position order
-// through DPP (row_shr:15-l): one v_add a position, as from registers.
-// Batches are read whole, four ahead of the adds (reads past the last batch
-// read the last batch again, so that every read is counted), and the adds
-// stop at the next multiple of 16 positions: x must hold +0.0 from n to
-// there (adding +0.0 changes no sum of non-negative terms, which is never
-// -0.0), and be readable to the next multiple of 64. The sum is valid in
-// lane 15.
-template <int S>
-__device__ inline void dpp_add(float& tot, float v) {
-  if constexpr (S == 0)
-    asm volatile("v_add_f32_e32 %0, %1, %0" : "+v"(tot) : "v"(v));
-  else
-    asm volatile("v_add_f32_dpp %0, %1, %0 row_shr:%2 row_mask:0xf bank_mask:0xf"
-                 : "+v"(tot)
-                 : "v"(v), "n"(S));
-}
-template <int L>
-__device__ inline void dpp_add4(float& tot, const float4& a) {
-  dpp_add<15 - L>(tot, a.x);
-  dpp_add<15 - L>(tot, a.y);
-  dpp_add<15 - L>(tot, a.z);
-  dpp_add<15 - L>(tot, a.w);
-}
-// one batch: `left` positions remain from its first (16 at a time)
-__device__ __forceinline__ void dpp_add64(float& tot, const float4& a, uint32_t left) {
-  // a DPP read waits 2 cycles after a VALU write of its source (copies the
-  // compiler may place between the read and the adds)
-  asm volatile("s_nop 1");
-  dpp_add4<0>(tot, a); dpp_add4<1>(tot, a); dpp_add4<2>(tot, a); dpp_add4<3>(tot, a);
-  if (left <= 16) return;
-  dpp_add4<4>(tot, a); dpp_add4<5>(tot, a); dpp_add4<6>(tot, a); dpp_add4<7>(tot, a);
-  if (left <= 32) return;
-  dpp_add4<8>(tot, a); dpp_add4<9>(tot, a); dpp_add4<10>(tot, a); dpp_add4<11>(tot, a);
-  if (left <= 48) return;
-  dpp_add4<12>(tot, a); dpp_add4<13>(tot, a); dpp_add4<14>(tot, a); dpp_add4<15>(tot, a);
-}
-__device__ __forceinline__ float seq_sum_dpp(const float* x, uint32_t n, float tot) {
-  const float4* x4 = reinterpret_cast<const float4*>(x) + (threadIdx.x & 15);
-  const uint32_t nb = (n + 63) / 64;
-  asm volatile("s_nop 4");  // a DPP read waits 5 cycles after the exec write that enabled it
-  float4 A[4], B[4];
+// tot + x[0] + x[1] + ... + x[n-1] in position order, one dependent add a
+// position (n a multiple of 16, at most 16 NB; x 16-byte aligned). Every
+// active lane forms the same sum from broadcast LDS reads: batches of 16
+// (four ds_read_b128), two batches read ahead of the adds (past the end the
+// last batch again), the batches unrolled so that the compiler's waits count
+// exactly the reads a batch needs. A dependent f32 add issues every ~4.5
+// clocks on gfx950; the sum through DPP from lanes 0-15 this replaces took
+// ~10 a position (a DPP read of an add's result stalls it).
+template <uint32_t NB>
+__device__ __forceinline__ float seq_add16(const float* x, uint32_t n, float tot) {
+  static_assert(NB % 3 == 0, "three batches an iteration");
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const uint32_t nb = n / 16;
+  if (nb == 0) return tot;
+  float4 a[4], b[4], c[4];
+  auto ld = [&](float4 (&v)[4], uint32_t k) {
+    k = min(k, nb - 1);
 #pragma unroll
-  for (uint32_t i = 0; i < 4; i++) A[i] = x4[16 * min(i, nb - 1)];
-  for (uint32_t b = 0;; b += 8) {
+    for (int i = 0; i < 4; i++) v[i] = x4[4 * k + i];
+  };
+  auto add = [&](const float4 (&v)[4]) {
 #pragma unroll
-    for (uint32_t i = 0; i < 4; i++) B[i] = x4[16 * min(b + 4 + i, nb - 1)];
+    for (int i = 0; i < 4; i++) {
+      tot += v[i].x;
+      tot += v[i].y;
+      tot += v[i].z;
+      tot += v[i].w;
+    }
+  };
+  ld(a, 0);
+  ld(b, 1);
+#pragma unroll
+  for (uint32_t k = 0; k < NB; k += 3) {
+    ld(c, k + 2);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (uint32_t i = 0; i < 4; i++)
-      if (b + i < nb) dpp_add64(tot, A[i], n - 64 * (b + i));
-    if (b + 4 >= nb) break;
-#pragma unroll
-    for (uint32_t i = 0; i < 4; i++) A[i] = x4[16 * min(b + 8 + i, nb - 1)];
+    add(a);
+    if (k + 1 >= nb) break;
+    ld(a, k + 3);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (uint32_t i = 0; i < 4; i++)
-      if (b + 4 + i < nb) dpp_add64(tot, B[i], n - 64 * (b + 4 + i));
-    if (b + 8 >= nb) break;
+    add(b);
+    if (k + 2 >= nb) break;
+    ld(b, k + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    add(c);
+    if (k + 3 >= nb) break;
   }
   return tot;
 }
@@ -131,7 +115,7 @@ constexpr uint32_t SCAN_HEAD = 256;
 // depends on s). A window is 256 positions, four a lane; after an event the
 // next window starts at the position after it, in the new binade. A sum
 // from 0 changes binade every time it doubles, so with `head` the first
-// SCAN_HEAD positions are added one by one (lanes 0-15, seq_sum_dpp). A
+// SCAN_HEAD positions are added one by one (seq_add16). A
 // sum that is not finite (a NaN term, or +inf) is continued one by one.
 //
 // The searches (M = SCAN_EXCEED, SCAN_REACH): every running sum before a
@@ -143,7 +127,8 @@ constexpr uint32_t SCAN_HEAD = 256;
 //
 // Reads x up to n + 511 (values past n are never used: the LDS there must
 // exist) and, for the head, needs +0.0 from n to the next multiple of 16
-// as seq_sum_dpp does. The result is valid in every lane.
+// (seq_add16 adds them: +0.0 changes no sum of non-negative terms, which is
+// never -0.0). The result is valid in every lane.
 template <int M>
 __device__ __forceinline__ float seq_scan(const float* x, uint32_t n, float tot, bool head,
                                           float target, uint32_t* at_out) {
@@ -171,8 +156,7 @@ __device__ __forceinline__ float seq_scan(const float* x, uint32_t n, float tot,
   if (head && n) {
     p = min(n, SCAN_HEAD);
     const float t0 = tot;
-    if (l < 16) tot = seq_sum_dpp(x, p, tot);
-    tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 15));
+    tot = seq_add16<(SCAN_HEAD / 16 + 2) / 3 * 3>(x, (p + 15) / 16 * 16, tot);
     if constexpr (FIND) {
       // the running sum never decreases (NaN aside): the head holds the
       // crossing iff its sum passes, or may if that sum is NaN

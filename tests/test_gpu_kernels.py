@@ -129,6 +129,24 @@ def test_gemv_matches_oracle_random_bytes(cx, dev, t):
         assert rel_l2(y, want) <= 1e-5, (O.NAMES[t], k, rel_l2(y, want))
 
 
+@pytest.mark.parametrize("t", (O.Q4_K, O.Q5_K))
+def test_row_kernels_bit_exact(cx, dev, t):
+    """The plain Q4_K/Q5_K row kernels: k = 2048 and 4096 (a row's lanes hold
+    half super-blocks), 17 to 64 super-blocks (a wave a row: the down
+    projections at 43 and 56): every output bit-identical to the scalar
+    spec's row sum (orc_dot_*), with row counts that leave a partial last
+    tile."""
+    ops, _ = cx
+    for k, n in ((2048, 45), (4096, 300), (4352, 37), (11008, 300), (14336, 61), (16384, 9)):
+        w = random_rows(t, n, k, seed=3 * k + t)
+        x = np.random.default_rng(k - t).normal(0, 1, k).astype(np.float32)
+        xq, xe, xs = O.quantize_act(x, O.SUB[t])
+        y = ops.gemv(t, T(w, dev), n, k, T(xq, dev), T(xe, dev), T(xs, dev)).cpu().numpy()
+        want = np.array([O.dot_row(t, w[r], xq, xe, xs) for r in range(n)], np.float32)
+        bad = np.nonzero(y.view(np.uint32) != want.view(np.uint32))[0]
+        assert bad.size == 0, (O.NAMES[t], k, bad[:5], y[bad[:3]], want[bad[:3]])
+
+
 # BASELINE config 2 shapes (rows x cols) for every type; config 1 is Q4_K gate
 SHAPES = [(2048, 2048), (256, 2048), (11008, 2048), (2048, 11008)]
 
