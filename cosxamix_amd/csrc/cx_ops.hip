@@ -234,9 +234,9 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 
 // ------------------------------------------- order-exact decode attention
 // The decode step's attention in the reference's own order, for contexts up
-// to CX_ATT_LDS_MAX, in two kernels. Both stage their cache rows in LDS
-// with direct-to-LDS loads, so a wave keeps up to 63 KiB of the cache in
-// flight instead of waiting on one row at a time.
+// to CX_ATT_LDS_MAX, in two kernels. The scores kernel stages its K rows in
+// LDS with direct-to-LDS loads, so a wave keeps up to 63 KiB of the cache
+// in flight instead of waiting on one row at a time.
 //
 // k_attn_scores, one workgroup per (64 positions, head h): the 64 K rows of
 // the head's group are copied into LDS by its four waves (rows padded by 16 bytes against bank
@@ -251,30 +251,30 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 // k_attn_seq, one workgroup per (head, 32 head dims): the head's scores are
 // copied in, then the softmax in the reference's order: exact max (from the
 // scores kernel's chunk maxima), e = exp(s - max) (glibc's expf), the sum in
-// position order from 0 (its first 256 adds one by one, the rest by binade
-// scan), p = e * (1/sum) (src/ops.rs:1211-1229). Meanwhile the V slice
-// streams through a ring of LDS stages; waves 1-3 form each stage's
-// products p * v[d] and wave 0's lane d adds them into out[d] in position
-// order (src/ops.rs:1316-1321). The output is then quantized for the
-// output projection (32 values are whole sub-blocks). Bit-identical to the
-// scalar reference.
+// position order from 0 (one add a position, or for long caches the first
+// 256 so and the rest by binade scan), p = e * (1/sum) (src/ops.rs:
+// 1211-1229). Meanwhile waves 1-3 stream the V slice into registers; they
+// form each stage's products p * v[d] and wave 0's lane d adds them into
+// out[d] in position order (src/ops.rs:1316-1321). The output is then
+// quantized for the output projection (32 values are whole sub-blocks).
+// Bit-identical to the scalar reference.
 constexpr uint32_t SC_P = 64;     // positions per scores wave
-constexpr uint32_t PV_STP = 128;  // positions per V stage
-// The softmax-V kernel's shape: DS head dims per workgroup (wave 0's lanes),
-// NST V stages of PV_STP positions in a ring of RING floats. 32 dims give
-// twice the workgroups of 64, so the softmax and chains, done once per
-// workgroup, run on more CUs at once.
-template <uint32_t DS, uint32_t RING = 32768>
-struct PvShape {
-  static constexpr uint32_t NST = RING / (PV_STP * DS);
-  static constexpr uint32_t IPS = PV_STP * DS * 4 / 1024;  // 1 KiB loads per stage
-  static constexpr uint32_t IPW = IPS / 4;                  // per wave
-  static constexpr uint32_t LPP = DS / 4;                   // lanes per position in a load
-  static_assert(IPW >= 1 && DS % 32 == 0 && NST >= 2, "whole loads per wave");
-  // A wave tracks at most 63 outstanding loads (vmcnt is 6 bits): its share
-  // of the scores (<= 4 loads for 4096 positions) plus NST - 1 stages ahead.
-  static_assert(4 + (NST - 1) * IPW <= 63, "too many loads in flight");
-};
+constexpr uint32_t PV_STP = 128;  // positions per V stage (32 head dims a workgroup:
+                                  // twice the workgroups of 64, so the softmax and
+                                  // chains, done once per workgroup, run on more CUs)
+
+// Waits until at most `later` stages' loads (IPW each) of this wave are
+// outstanding, or fewer.
+template <uint32_t IPW, uint32_t MAXL>
+__device__ inline void wait_stages(uint32_t later) {
+  if constexpr (MAXL == 0) {
+    (void)later;
+    cx_wait_vm<0>();
+  } else {
+    if (later >= MAXL) cx_wait_vm<MAXL * IPW>();
+    else wait_stages<IPW, MAXL - 1>(later);
+  }
+}
 
 
 __host__ __device__ constexpr uint32_t sc_stride(uint32_t cap) { return (cap + 3) / 4 * 4; }
@@ -397,55 +397,54 @@ __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) 
   o += t7;
 }
 
-// The products p_j * v_j[d] of a stage are formed by
-// waves 1-3 one stage ahead, into a [dim][position] buffer (rows PV_PSTR
-// floats apart, so 16 lanes' 16-byte reads fall on distinct banks), and
-// wave 0's chain reads four positions' products per LDS read: an add and a
-// quarter of a read per position, where forming them itself costs a
-// multiply, an add and three quarters of a read. The V ring is then 96 KiB,
-// to leave room for the two product buffers.
-constexpr uint32_t PV_PSTR = PV_STP + 4;
-constexpr uint32_t PV_RING_SHORT = 24576;
-// Above CX_ATT_LDS_MAX (the model's longer caches, scores from k_att_qk) the
-// ring is 80 KiB (5 stages), which leaves room for the scores of up to
-// CX_ATT_LONG_MAX positions.
-constexpr uint32_t PV_RING_LONG = 20480;
+// The P.V stage: 128 positions of a 32-dim slice, 256 blocks of 4 positions
+// x 4 dims (block b: positions 4 (b / 8) .. +3, dims 4 (b % 8) .. +3). The
+// helpers (waves 1-4) split every stage's blocks, lane l of helper h taking
+// block 64 h + l. A helper loads its
+// blocks' V rows straight into registers three stages ahead (no V passes
+// through LDS), forms the products p_j * v_j[d] (p_j = e_j * (1/sum), or
+// 1/total when uniform; +0.0 past total) and writes them transposed,
+// [dim][position], into one of two LDS buffers, while wave 0's chain adds
+// the previous stage's products from the other; one barrier a stage, and
+// wave 0 issues no load. A buffer row is 128 floats, 16-byte chunk c of
+// row d stored at chunk c ^ (d % 8), so that the helpers' writes and the
+// chain's reads (lane d: four positions of row d a read) spread over the
+// 32 banks. Measured and dropped: the ring of direct-to-LDS stages (a
+// stage's 16 loads shared by all four waves; ~2100 clocks a stage at config
+// 5 against the chain's ~1100, wave 0's refills and the stage coupling);
+// each helper a whole stage in turn, loaded into LDS slots of its own and
+// transposed in place (a helper's 16 direct-to-LDS loads took ~1450 clocks
+// to issue and its transposition ~2000: 2470 a stage); three helpers with
+// two blocks a lane (~1600 clocks a stage for a helper's share).
+constexpr uint32_t PV_BUF = PV_STP * 32;  // floats of one product buffer
+__host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap) {
+  return sc_lds(cap) + 2 * PV_BUF;
+}
+constexpr uint32_t PV_NT = 320;  // wave 0 (the chain) and four helpers
+// Softmax sums of up to SUM_PLAIN_MAX positions add one position at a time
+// (seq_add16); longer ones take the binade scan.
+constexpr uint32_t SUM_PLAIN_MAX = 768;
 constexpr uint32_t CML_MAX = 256;  // chunk maxima of one head: 16384 positions
-__host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap, uint32_t ds, uint32_t ring) {
-  return sc_lds(cap) + ring + 2 * ds * PV_PSTR;
-}
 
-// Waits until at most `later` stages' loads (IPW each) of this wave are
-// outstanding, or fewer.
-template <uint32_t IPW, uint32_t MAXL>
-__device__ inline void wait_stages(uint32_t later) {
-  if constexpr (MAXL == 0) {
-    (void)later;
-    cx_wait_vm<0>();
-  } else {
-    if (later >= MAXL) cx_wait_vm<MAXL * IPW>();
-    else wait_stages<IPW, MAXL - 1>(later);
-  }
-}
-
-// 256 threads: every wave streams its share of the V ring (4x the loads in
-// flight of one wave); wave 0's lanes run the order-exact accumulation.
-// Rows of the grid past HD / PV_DS are prefetch workgroups (pf).
-template <int HD, int SUB, uint32_t PV_DS, uint32_t RING>
-__global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* sc_all,
+// PV_NT threads: wave 0's lanes run the order-exact accumulation, waves 1-4
+// stream V. Rows of the grid past HD / 32 are prefetch workgroups (pf).
+template <int HD, int SUB>
+__global__ __launch_bounds__(PV_NT) void k_attn_seq(const float* vc, const float* sc_all,
                                                   const float* cm_all, uint32_t heads,
                                                   uint32_t kvh, const cx_dstate* st, uint32_t cap,
                                                   float* out, int8_t* xq, float* xe, float* xs,
                                                   cx_l2_prefetch pf) {
-  if (blockIdx.y >= HD / PV_DS) {
-    const uint32_t first = gridDim.x * (HD / PV_DS);
+  constexpr uint32_t DS = 32;  // head dims a workgroup
+  if (blockIdx.y >= HD / DS) {
+    const uint32_t first = gridDim.x * (HD / DS);
     cx_l2_prefetch_run(pf, blockIdx.x + gridDim.x * blockIdx.y - first, first);
     return;
   }
-  extern __shared__ __align__(16) float e[];  // sc_lds(cap) scores, then the V ring
-  float* ring = e + sc_lds(cap);
+  extern __shared__ __align__(16) float e[];  // sc_lds(cap) scores, then two product buffers
+  float* pbuf = e + sc_lds(cap);
   __shared__ uint64_t etab[32];  // exp's table in LDS: no global load after the prefetch
   __shared__ float red[4];
+  __shared__ float osum[DS];  // the output, for its quantization
   __shared__ __align__(16) float cml[CML_MAX];  // the head's chunk maxima
   // The workgroups of a (KV group, dims slice) pair
   // take linear ids i, i + 8, i + 16, ...: workgroups are dispatched to the
@@ -453,7 +452,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   // share one XCD's L2, and each V line is fetched from memory once.
   uint32_t h = blockIdx.x, y = blockIdx.y;
   {
-    constexpr uint32_t NY = HD / PV_DS;
+    constexpr uint32_t NY = HD / DS;
     const uint32_t n = heads * NY, per = heads / kvh;
     if (n % 8 == 0) {
       const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y, J = (L % 8) * (n / 8) + L / 8;
@@ -462,15 +461,11 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     }
   }
   const uint32_t total = st->pos + 1, g = h / (heads / kvh);
-  using PS = PvShape<PV_DS, RING>;
-  constexpr uint32_t PV_NST = PS::NST, PV_IPW = PS::IPW, PV_LPP = PS::LPP;
-  const uint32_t d0 = y * PV_DS, kvd = kvh * HD;
+  const uint32_t d0 = y * DS, kvd = kvh * HD;
   const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
-  // 1. the head's scores, then the first V stages, as untracked
-  //    direct-to-LDS loads; a wave's loads complete in issue order, so
-  //    waiting for all but its V loads waits for its scores only. With one
-  //    query token, wave 0 first fetches the chunk maxima the scores kernel
-  //    wrote (64 positions a chunk, at most CML_MAX chunks). Both cover the
+  // 1. the head's scores as untracked direct-to-LDS loads; with one query
+  //    token wave 0 first fetches the chunk maxima the scores kernel wrote
+  //    (64 positions a chunk, at most CML_MAX chunks). Both cover the
   //    whole cache (positions past the token's are loaded and never used),
   //    so that they are issued before the position state arrives.
   const uint32_t nckc = (cap + SC_P - 1) / SC_P;
@@ -481,7 +476,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   }
   const float* srow = sc_all + (size_t)h * sc_stride(cap);
   const uint32_t nsc = (cap + 255) / 256;  // 1 KiB per load
-  for (uint32_t c = w; c < nsc; c += 4) {
+  for (uint32_t c = w; c < nsc; c += PV_NT / 64) {
     const uint32_t i = c * 256 + 4 * t;
     cx_dma16_async(srow + (i < cap ? i : 0), e + c * 256);
   }
@@ -491,38 +486,41 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     for (int i = 0; i < 32; i++) etab[i] = tab[i];
   }
   const uint32_t nstage = (total + PV_STP - 1) / PV_STP;
-  const float* vb = vc + g * HD + d0;
-  auto issue = [&](uint32_t s) {  // wave w's loads of stage s into ring slot s % PV_NST
-    float* dst = ring + (s % PV_NST) * (PV_STP * PV_DS);
-    for (uint32_t j = 0; j < PV_IPW; j++) {
-      const uint32_t i = w + 4 * j;
-      uint32_t p = s * PV_STP + i * (64 / PV_LPP) + t / PV_LPP;  // 64/LPP positions a load
+  // a helper lane's block: position quad b0 / 8, dim quad b0 % 8
+  const uint32_t b0 = 64 * (w - 1) + t;
+  const float* vb = vc + g * HD + d0 + 4 * (b0 % 8);
+  struct Vb {
+    float4 a[4];  // the block's four positions (dims 4 (b0 % 8) .. +3)
+  };
+  auto load = [&](Vb& R, uint32_t s) {  // stage s's rows (past total: position 0's)
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      uint32_t p = s * PV_STP + 4 * (b0 / 8) + i;
       if (p >= total) p = 0;
-      cx_dma16_async(reinterpret_cast<const uint8_t*>(vb + (size_t)p * kvd) + (t % PV_LPP) * 16,
-                     dst + i * 256);
+      R.a[i] = *reinterpret_cast<const float4*>(vb + (size_t)p * kvd);
     }
   };
-  // The V loads are issued once the scores have landed: issued together,
-  // every workgroup's V burst would queue ahead of the scores that the
-  // softmax needs first (V is read only after the sum). With one query token
-  // and a V slice that fits the ring whole (early), waves 1-3 issue all of
-  // it later, while wave 0 adds the exps, so no load issue delays the
-  // softmax.
-  const bool early = nstage <= PV_NST;
+  // The scores land before the V loads are issued (issued together, every
+  // workgroup's V burst would queue ahead of the scores the softmax needs
+  // first); a helper's first three stages then load during the softmax.
   cx_wait_vm<0>();
-  if (!early)
-    for (uint32_t s = 0; s < PV_NST && s < nstage; s++) issue(s);
+  Vb r0, r1, r2;
+  if (w != 0) {  // (a stage past the last loads rows of position 0, never used)
+    load(r0, 0);
+    load(r1, 1);
+    load(r2, 2);
+  }
   cx_wait_lds();
   cx_barrier();  // every wave's scores (and chunk maxima) and the exp table are in LDS
   float o = 0.0f;
   // 2. softmax over positions [0, total): the maximum of the chunk maxima
-  //    (the same in every wave), e = exp(s - max) of the first 256
-  //    positions by every thread, then of the rest by waves 1-3 while
+  //    (the same in every wave), e = exp(s - max) of the first PV_NT
+  //    positions by every thread, then of the rest by the helpers while
   //    wave 0 adds the ones formed: the sum is the f32 sum in position
-  //    order from 0 (src/ops.rs:1211-1229): one add a position when the V
-  //    slice fits the ring, else the first 256 one by one and the rest by
-  //    seq_sum_scan. The division by the sum is folded into the products
-  //    below.
+  //    order from 0 (src/ops.rs:1211-1229): one add a position up to
+  //    SUM_PLAIN_MAX positions, else the first 256 one by one and the rest
+  //    by seq_sum_scan. The division by the sum is folded into the
+  //    products below.
   float mx = -INFINITY;
 #pragma unroll
   for (uint32_t i = 0; i < CML_MAX / 64; i++)
@@ -537,46 +535,30 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     e[tid] = 0.0f;
   cx_wait_lds();
   cx_barrier();
-  // early: the whole V slice, stage s into slot s, load i of a stage by
-  // wave 1 + i % 3
-  static_assert((PV_NST * PS::IPS + 2) / 3 <= 63, "a helper wave's share of the slice");
-  auto issue_all = [&]() {
-    for (uint32_t l = w - 1; l < nstage * PS::IPS; l += 3) {
-      const uint32_t s = l / PS::IPS, i = l % PS::IPS;
-      uint32_t p = s * PV_STP + i * (64 / PV_LPP) + t / PV_LPP;
-      if (p >= total) p = 0;
-      cx_dma16_async(reinterpret_cast<const uint8_t*>(vb + (size_t)p * kvd) + (t % PV_LPP) * 16,
-                     ring + s * (PV_STP * PV_DS) + i * 256);
-    }
-  };
   float tot = 0.0f;
-  if (early) {
-    // the V slice fits the ring: waves 1-3 form every other exp at once
-    // while wave 0 adds the first 256, then issue all of V while it adds
-    // the rest
+  if (total <= SUM_PLAIN_MAX) {
+    // the helpers form the other exps at once while wave 0 adds the first
+    // 256, then wave 0 adds the rest
     if (w != 0) {
-      for (uint32_t p = 256 + tid - 64; p < r64; p += 192)
+      for (uint32_t p = PV_NT + tid - 64; p < r64; p += PV_NT - 64)
         e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
-      if (total <= 256) issue_all();
     } else if (!uniform) {
-      tot = seq_sum_scan(e, min(total, 256u), 0.0f, true);
+      tot = seq_add16<18>(e, (min(total, 256u) + 15) / 16 * 16, 0.0f);
     }
     if (total > 256) {
       cx_wait_lds();
       cx_barrier();  // the rest of the exps are in LDS
-      if (w != 0) issue_all();
-      // one add a position (~4.5 clocks): at these lengths (at most
-      // PV_NST * PV_STP) faster than the binade scan, whose windows and
-      // events cost more than they save (1.7 us at 388 positions, against
-      // ~0.9)
+      // one add a position (~4.5 clocks): at these lengths faster than the
+      // binade scan, whose windows and events cost more than they save
+      // (1.7 us at 388 positions, against ~0.9)
       if (w == 0 && !uniform)
-        tot = seq_add16<(PV_NST * PV_STP / 16 + 2) / 3 * 3>(e + 256, (total - 256 + 15) / 16 * 16, tot);
+        tot = seq_add16<(SUM_PLAIN_MAX / 16 + 2) / 3 * 3>(e + 256, (total - 256 + 15) / 16 * 16, tot);
     }
   } else {
-    // a longer cache (V streams through the ring later): stages of
-    // SCAN_STAGE positions, the first stage's exps by every thread, then
-    // waves 1-3 forming stage s + 1's while wave 0 adds stage s's
-    for (uint32_t p = 256 + tid; p < min(SCAN_STAGE, r64); p += 256)
+    // a longer cache: stages of SCAN_STAGE positions, the first stage's
+    // exps by every thread, then the helpers forming stage s + 1's while
+    // wave 0 adds stage s's
+    for (uint32_t p = PV_NT + tid; p < min(SCAN_STAGE, r64); p += PV_NT)
       e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
     cx_wait_lds();
     cx_barrier();
@@ -584,7 +566,7 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
     for (uint32_t s = 0; s < nss; s++) {
       if (w != 0) {
         const uint32_t b = SCAN_STAGE * (s + 1), end = min(b + SCAN_STAGE, r64);
-        for (uint32_t p = b + tid - 64; p < end; p += 192)
+        for (uint32_t p = b + tid - 64; p < end; p += PV_NT - 64)
           e[p] = p >= total ? 0.0f : uniform ? pu : cx_expf_tab(e[p] - mx, etab);
       } else if (!uniform) {
         tot = seq_sum_scan(e + SCAN_STAGE * s, min(SCAN_STAGE, total - SCAN_STAGE * s), tot, s == 0);
@@ -599,110 +581,104 @@ __global__ __launch_bounds__(256) void k_attn_seq(const float* vc, const float* 
   cx_wait_lds();
   cx_barrier();
   const float inv = red[0];
-  // 3. out[d0 + t] over the V ring, position order (wave 0)
-  float* prod = ring + PV_NST * PV_STP * PV_DS;  // two buffers of PV_DS * PV_PSTR
-  // helper waves: stage s's products p_j * v_j[d], p_j = e_j * (1/sum) (or
-  // 1/total when uniform), into buffer s % 2, [dim][position], +0.0 for
-  // positions past total; task k is dims 4 (k % DQ) .. +3 and positions
-  // 8 (k / DQ) .. +7
-  auto make = [&](uint32_t s) {
-    constexpr uint32_t DQ = PV_DS / 4, NT = DQ * (PV_STP / 8);
-    const float* vs = ring + (s % PV_NST) * (PV_STP * PV_DS);
-    const float* ps = e + s * PV_STP;
-    float* pb = prod + (s & 1) * (PV_DS * PV_PSTR);
-    for (uint32_t k = tid - 64; k < NT; k += 192) {
-      const uint32_t dq = k % DQ, pq = k / DQ;
-      const float4 e0 = *reinterpret_cast<const float4*>(ps + 8 * pq);
-      const float4 e1 = *reinterpret_cast<const float4*>(ps + 8 * pq + 4);
-      float4 vv[8];
+  // 3. out[d0 + t], the sum over positions of p * v[d0 + t] in position
+  //    order (wave 0's lane t), a stage behind the helper that forms the
+  //    stage's products
+  // stage s's products into buffer s % 2, then stage s + 3 into the
+  // registers (always: past the last stage, rows of position 0)
+  auto make = [&](Vb& R, uint32_t s) {
+    float* pb = pbuf + (s & 1) * PV_BUF;
+    const uint32_t q = b0 / 8, r = b0 % 8, p0 = s * PV_STP + 4 * q;
+    const float4 e4 = *reinterpret_cast<const float4*>(e + p0);
+    float pp[4] = {e4.x, e4.y, e4.z, e4.w};
+    if (!uniform)
 #pragma unroll
-      for (int i = 0; i < 8; i++)
-        vv[i] = *reinterpret_cast<const float4*>(vs + (8 * pq + i) * PV_DS + 4 * dq);
-      __builtin_amdgcn_sched_barrier(0);  // every read in flight before the first use
-      float pp[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-      if (!uniform)
+      for (int i = 0; i < 4; i++) pp[i] = pp[i] * inv;
+    float m[4][4];  // [dim j][position i]
 #pragma unroll
-        for (int i = 0; i < 8; i++) pp[i] = pp[i] * inv;
-      float r[4][8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float4 v = vv[i];
-        const bool live = s * PV_STP + 8 * pq + i < total;
-        r[0][i] = live ? pp[i] * v.x : 0.0f;
-        r[1][i] = live ? pp[i] * v.y : 0.0f;
-        r[2][i] = live ? pp[i] * v.z : 0.0f;
-        r[3][i] = live ? pp[i] * v.w : 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        float* row = pb + (4 * dq + j) * PV_PSTR + 8 * pq;
-        *reinterpret_cast<float4*>(row) = make_float4(r[j][0], r[j][1], r[j][2], r[j][3]);
-        *reinterpret_cast<float4*>(row + 4) = make_float4(r[j][4], r[j][5], r[j][6], r[j][7]);
-      }
+    for (uint32_t i = 0; i < 4; i++) {
+      const bool live = p0 + i < total;
+      m[0][i] = live ? pp[i] * R.a[i].x : 0.0f;
+      m[1][i] = live ? pp[i] * R.a[i].y : 0.0f;
+      m[2][i] = live ? pp[i] * R.a[i].z : 0.0f;
+      m[3][i] = live ? pp[i] * R.a[i].w : 0.0f;
     }
+#pragma unroll
+    for (uint32_t j = 0; j < 4; j++) {
+      const uint32_t d = 4 * r + j;
+      *reinterpret_cast<float4*>(pb + d * PV_STP + 4 * (q ^ (d & 7))) =
+          make_float4(m[j][0], m[j][1], m[j][2], m[j][3]);
+    }
+    load(R, s + 3);
   };
-  // stages issued so far: [0, min(NST, nstage)); each iteration s issues
-  // stage s + NST into the slot of stage s, whose products are made
-  auto issued_end = [&](uint32_t s) { return min(s + PV_NST, nstage); };
-  if (early)
-    cx_wait_vm<0>();  // the whole slice has landed (wave 0 issued none)
-  else
-    wait_stages<PV_IPW, PV_NST - 1>(issued_end(0) - 1);  // stage 0 has landed
-  cx_barrier();
-  if (w != 0) make(0);
-  for (uint32_t s = 0; s < nstage; s++) {
-    if (!early && s + 1 < nstage) wait_stages<PV_IPW, PV_NST - 1>(issued_end(s) - (s + 2));
-    cx_wait_lds();
-    cx_barrier();  // stage s's products are made; stage s + 1 has landed
-    // stage s's slot is no longer read: refill it (wave 0 after its chain,
-    // which the barrier starts)
-    if (w != 0 && s + PV_NST < nstage) issue(s + PV_NST);
-    if (w == 0) {
-      if (t < (int)PV_DS) {
-        // 32 positions a batch, the next batch's reads ahead of the adds;
-        // the stage's last batch ends past total with products of +0.0
-        // (adding +0.0 changes no sum that starts at +0.0)
-        const float* pr = prod + (s & 1) * (PV_DS * PV_PSTR) + t * PV_PSTR;
-        const uint32_t nq = min(4u, (total - s * PV_STP + 31) / 32);
-        const float4* p4 = reinterpret_cast<const float4*>(pr);
-        float4 a[8], b[8];
+  // The helpers and wave 0 run loops of their own, one barrier a stage,
+  // s = 0 .. nstage. A helper forms stage s's products into buffer s % 2
+  // from the registers its loads went to three stages before, then loads
+  // stage s + 3 into them (past the last stage too: rows of position 0),
+  // every step unconditional and three stages a pass, so that r0, r1 and r2
+  // keep their registers and the compiler's wait for a stage's loads leaves
+  // the next two stages' in flight.
+  if (w != 0) {
+    for (uint32_t base = 0;; base += 3) {
+      make(r0, base);
+      cx_wait_lds();
+      cx_barrier();  // stage s's products are formed; stage s - 1's are read
+      if (base + 1 > nstage) break;
+      make(r1, base + 1);
+      cx_wait_lds();
+      cx_barrier();
+      if (base + 2 > nstage) break;
+      make(r2, base + 2);
+      cx_wait_lds();
+      cx_barrier();
+      if (base + 3 > nstage) break;
+    }
+    cx_wait_vm<0>();  // the last, unused loads
+    return;
+  }
+  for (uint32_t s = 0; s <= nstage; s++) {
+    if (s >= 1 && t < (int)DS) {
+      // stage s - 1: 32 positions a batch, the next batch's reads ahead of
+      // the adds; the stage's last batch ends past total with products of
+      // +0.0 (adding +0.0 changes no sum that starts at +0.0)
+      const uint32_t sp = s - 1;
+      const float* pr = pbuf + (sp & 1) * PV_BUF + t * PV_STP;
+      const uint32_t sw = (uint32_t)t & 7;
+      const uint32_t nq = min(4u, (total - sp * PV_STP + 31) / 32);
+      auto rd = [&](float4 (&a)[8], uint32_t b) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) a[i] = p4[i];
-#pragma unroll
-        for (int i = 0; i < 8; i++) b[i] = p4[8 + i];
+        for (uint32_t i = 0; i < 8; i++)
+          a[i] = *reinterpret_cast<const float4*>(pr + 4 * ((8 * b + i) ^ sw));
+      };
+      float4 a[8], b[8];
+      rd(a, 0);
+      rd(b, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      add32(o, a);
+      if (nq > 1) {
+        rd(a, 2);
         __builtin_amdgcn_sched_barrier(0);
-        add32(o, a);
-        if (nq > 1) {
-#pragma unroll
-          for (int i = 0; i < 8; i++) a[i] = p4[16 + i];
+        add32(o, b);
+        if (nq > 2) {
+          rd(b, 3);
           __builtin_amdgcn_sched_barrier(0);
-          add32(o, b);
-          if (nq > 2) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) b[i] = p4[24 + i];
-            __builtin_amdgcn_sched_barrier(0);
-            add32(o, a);
-            if (nq > 3) add32(o, b);
-          }
+          add32(o, a);
+          if (nq > 3) add32(o, b);
         }
       }
-      if (s + PV_NST < nstage) issue(s + PV_NST);
-    } else if (s + 1 < nstage) {
-      make(s + 1);
     }
+    cx_wait_lds();
+    cx_barrier();
   }
-  cx_wait_lds();
-  cx_barrier();  // every read of the ring and the products is done
-  if (w != 0 || t >= (int)PV_DS) return;
+  if (t >= (int)DS) return;
   out[h * HD + d0 + t] = o;
   if (!xq) return;
-  float* os = ring;  // every load has landed and every read of the ring is done
-  os[t] = o;
+  osum[t] = o;
   cx_wait_lds();
-  if (t < (int)(PV_DS / 8)) {
+  if (t < (int)(DS / 8)) {
     float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) v[j] = os[8 * t + j];
+    for (int j = 0; j < 8; j++) v[j] = osum[8 * t + j];
     cx_quant8<SUB>(v, (size_t)h * HD + d0 + 8 * t, xq, xe, xs);
   }
 }
@@ -1095,19 +1071,19 @@ size_t cx_attn_splits(size_t cap) { return (cap + ATT_P - 1) / ATT_P; }
 namespace {
 // One query token: the softmax-V kernel with helper-made products, 32 dims
 // a workgroup (a ring of RING floats), plus rows of prefetch workgroups.
-template <int HD, uint32_t RING>
+template <int HD>
 int launch_seq_one(const cx_attn_args& a, hipStream_t s) {
-  const size_t lds = pv_lds_floats(a.cap, 32, RING) * sizeof(float);
+  const size_t lds = pv_lds_floats(a.cap) * sizeof(float);
   CX_REQUIRE(lds <= 158 * 1024 && (a.cap + SC_P - 1) / SC_P <= CML_MAX,
              "attention: %u cached positions need %zu bytes of LDS", a.cap, lds);
   const uint32_t rows = HD / 32, np = cx_l2_prefetch_groups(a.pf, a.heads * rows);
   const dim3 grid(a.heads, rows + (np + a.heads - 1) / a.heads, 1);
   if (a.sub == 16)
-    hipLaunchKernelGGL((k_attn_seq<HD, 16, 32, RING>), grid, dim3(256), lds, s, a.vc, a.sc,
-                       a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+    hipLaunchKernelGGL((k_attn_seq<HD, 16>), grid, dim3(PV_NT), lds, s, a.vc, a.sc, a.cm, a.heads,
+                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   else
-    hipLaunchKernelGGL((k_attn_seq<HD, 32, 32, RING>), grid, dim3(256), lds, s, a.vc, a.sc,
-                       a.cm, a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+    hipLaunchKernelGGL((k_attn_seq<HD, 32>), grid, dim3(PV_NT), lds, s, a.vc, a.sc, a.cm, a.heads,
+                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   CX_HIP(hipGetLastError());
   return CX_OK;
 }
@@ -1135,7 +1111,7 @@ int launch_exact(const cx_attn_args& a, float scale, hipStream_t s) {
                      sc_bytes, s, a.q, a.knew, a.vnew, a.kc, a.vc, a.cos_t, a.sin_t, a.heads,
                      a.kvh, a.st, scale, a.sc, a.cm, a.cap);
   CX_HIP(hipGetLastError());
-  return launch_seq_one<HD, PV_RING_SHORT>(a, s);  // one token: 32 dims a workgroup
+  return launch_seq_one<HD>(a, s);  // one token: 32 dims a workgroup
 }
 
 // One query token over a longer cache: the scores of all heads of a KV group
@@ -1146,7 +1122,7 @@ int launch_long(const cx_attn_args& a, float scale, hipStream_t s) {
   CX_REQUIRE(a.cm, "attention: the chunk maxima buffer");
   int rc = cx_launch_att_scores(a, scale, s);
   if (rc) return rc;
-  return launch_seq_one<HD, PV_RING_LONG>(a, s);
+  return launch_seq_one<HD>(a, s);
 }
 }  // namespace
 
