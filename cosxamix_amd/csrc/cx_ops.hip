@@ -259,9 +259,6 @@ __global__ __launch_bounds__(256) void k_attention(const float* q, const float* 
 // quantized for the output projection (32 values are whole sub-blocks).
 // Bit-identical to the scalar reference.
 constexpr uint32_t SC_P = 64;     // positions per scores wave
-constexpr uint32_t PV_STP = 128;  // positions per V stage (32 head dims a workgroup:
-                                  // twice the workgroups of 64, so the softmax and
-                                  // chains, done once per workgroup, run on more CUs)
 
 // Waits until at most `later` stages' loads (IPW each) of this wave are
 // outstanding, or fewer.
@@ -397,16 +394,16 @@ __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) 
   o += t7;
 }
 
-// The P.V stage: 128 positions of a 32-dim slice, 256 blocks of 4 positions
-// x 4 dims (block b: positions 4 (b / 8) .. +3, dims 4 (b % 8) .. +3). The
-// helpers (waves 1-4) split every stage's blocks, lane l of helper h taking
-// block 64 h + l. A helper loads its
+// The P.V stage: PV_STP positions of a 32-dim slice in blocks of 4
+// positions x 4 dims (block b: positions 4 (b / 8) .. +3, dims 4 (b % 8)
+// .. +3). The helpers (waves 1-4) split every stage's blocks, lane l of
+// helper h taking blocks 256 k + 64 h + l. A helper loads its
 // blocks' V rows straight into registers three stages ahead (no V passes
 // through LDS), forms the products p_j * v_j[d] (p_j = e_j * (1/sum), or
 // 1/total when uniform; +0.0 past total) and writes them transposed,
 // [dim][position], into one of two LDS buffers, while wave 0's chain adds
 // the previous stage's products from the other; one barrier a stage, and
-// wave 0 issues no load. A buffer row is 128 floats, 16-byte chunk c of
+// wave 0 issues no load. A buffer row is PV_STP floats, 16-byte chunk c of
 // row d stored at chunk c ^ (d % 8), so that the helpers' writes and the
 // chain's reads (lane d: four positions of row d a read) spread over the
 // 32 banks. Measured and dropped: the ring of direct-to-LDS stages (a
@@ -416,11 +413,16 @@ __device__ inline void pv8(float& o, const float4 (&p)[2], const float (&v)[8]) 
 // transposed in place (a helper's 16 direct-to-LDS loads took ~1450 clocks
 // to issue and its transposition ~2000: 2470 a stage); three helpers with
 // two blocks a lane (~1600 clocks a stage for a helper's share).
-constexpr uint32_t PV_BUF = PV_STP * 32;  // floats of one product buffer
-__host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap) {
-  return sc_lds(cap) + 2 * PV_BUF;
+// The kernel's shape, PV_STP positions a stage and PV_NT threads: 128 and
+// 320 (four helpers, one block a lane) for caches up to PV_LONG_CAP
+// positions, else 256 and 576 (eight helpers): measured on MI355X, the 3B
+// decode at ~600 positions 732 tok/s with 128-position stages against 719
+// with 256 (the pipeline's fill and drain are a larger share of three
+// stages), config 5 at 8200 positions 282.9 tok/s against 273.8.
+constexpr uint32_t PV_LONG_CAP = 2048;
+__host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap, uint32_t stp) {
+  return sc_lds(cap) + 2 * stp * 32;  // the scores, then two product buffers of stp x 32
 }
-constexpr uint32_t PV_NT = 320;  // wave 0 (the chain) and four helpers
 // Softmax sums of up to SUM_PLAIN_MAX positions add one position at a time
 // (seq_add16); longer ones take the binade scan.
 constexpr uint32_t SUM_PLAIN_MAX = 768;
@@ -428,13 +430,17 @@ constexpr uint32_t CML_MAX = 256;  // chunk maxima of one head: 16384 positions
 
 // PV_NT threads: wave 0's lanes run the order-exact accumulation, waves 1-4
 // stream V. Rows of the grid past HD / 32 are prefetch workgroups (pf).
-template <int HD, int SUB>
+template <int HD, int SUB, uint32_t PV_STP, uint32_t PV_NT>
 __global__ __launch_bounds__(PV_NT) void k_attn_seq(const float* vc, const float* sc_all,
                                                   const float* cm_all, uint32_t heads,
                                                   uint32_t kvh, const cx_dstate* st, uint32_t cap,
                                                   float* out, int8_t* xq, float* xe, float* xs,
                                                   cx_l2_prefetch pf) {
-  constexpr uint32_t DS = 32;  // head dims a workgroup
+  constexpr uint32_t DS = 32;  // head dims a workgroup (32 give twice the workgroups of 64,
+                               // so the softmax and chains run on more CUs at once)
+  constexpr uint32_t PV_BUF = PV_STP * 32;                       // floats of a product buffer
+  constexpr uint32_t PV_BPL = PV_STP * 8 / 4 / (PV_NT - 64);     // blocks a helper lane a stage
+  static_assert(PV_BPL * (PV_NT - 64) * 4 == PV_STP * 8, "whole blocks a lane");
   if (blockIdx.y >= HD / DS) {
     const uint32_t first = gridDim.x * (HD / DS);
     cx_l2_prefetch_run(pf, blockIdx.x + gridDim.x * blockIdx.y - first, first);
@@ -486,19 +492,22 @@ __global__ __launch_bounds__(PV_NT) void k_attn_seq(const float* vc, const float
     for (int i = 0; i < 32; i++) etab[i] = tab[i];
   }
   const uint32_t nstage = (total + PV_STP - 1) / PV_STP;
-  // a helper lane's block: position quad b0 / 8, dim quad b0 % 8
+  // a helper lane's blocks: b = (PV_NT - 64) k + 64 (w - 1) + l, position
+  // quad b / 8, dim quad b % 8 (the same for every k)
   const uint32_t b0 = 64 * (w - 1) + t;
   const float* vb = vc + g * HD + d0 + 4 * (b0 % 8);
   struct Vb {
-    float4 a[4];  // the block's four positions (dims 4 (b0 % 8) .. +3)
+    float4 a[PV_BPL][4];  // block k's four positions (dims 4 (b0 % 8) .. +3)
   };
   auto load = [&](Vb& R, uint32_t s) {  // stage s's rows (past total: position 0's)
 #pragma unroll
-    for (uint32_t i = 0; i < 4; i++) {
-      uint32_t p = s * PV_STP + 4 * (b0 / 8) + i;
-      if (p >= total) p = 0;
-      R.a[i] = *reinterpret_cast<const float4*>(vb + (size_t)p * kvd);
-    }
+    for (uint32_t k = 0; k < PV_BPL; k++)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; i++) {
+        uint32_t p = s * PV_STP + 4 * ((b0 + (PV_NT - 64) * k) / 8) + i;
+        if (p >= total) p = 0;
+        R.a[k][i] = *reinterpret_cast<const float4*>(vb + (size_t)p * kvd);
+      }
   };
   // The scores land before the V loads are issued (issued together, every
   // workgroup's V burst would queue ahead of the scores the softmax needs
@@ -588,26 +597,29 @@ __global__ __launch_bounds__(PV_NT) void k_attn_seq(const float* vc, const float
   // registers (always: past the last stage, rows of position 0)
   auto make = [&](Vb& R, uint32_t s) {
     float* pb = pbuf + (s & 1) * PV_BUF;
-    const uint32_t q = b0 / 8, r = b0 % 8, p0 = s * PV_STP + 4 * q;
-    const float4 e4 = *reinterpret_cast<const float4*>(e + p0);
-    float pp[4] = {e4.x, e4.y, e4.z, e4.w};
-    if (!uniform)
 #pragma unroll
-      for (int i = 0; i < 4; i++) pp[i] = pp[i] * inv;
-    float m[4][4];  // [dim j][position i]
+    for (uint32_t k = 0; k < PV_BPL; k++) {
+      const uint32_t b = b0 + (PV_NT - 64) * k, q = b / 8, r = b % 8, p0 = s * PV_STP + 4 * q;
+      const float4 e4 = *reinterpret_cast<const float4*>(e + p0);
+      float pp[4] = {e4.x, e4.y, e4.z, e4.w};
+      if (!uniform)
 #pragma unroll
-    for (uint32_t i = 0; i < 4; i++) {
-      const bool live = p0 + i < total;
-      m[0][i] = live ? pp[i] * R.a[i].x : 0.0f;
-      m[1][i] = live ? pp[i] * R.a[i].y : 0.0f;
-      m[2][i] = live ? pp[i] * R.a[i].z : 0.0f;
-      m[3][i] = live ? pp[i] * R.a[i].w : 0.0f;
-    }
+        for (int i = 0; i < 4; i++) pp[i] = pp[i] * inv;
+      float m[4][4];  // [dim j][position i]
 #pragma unroll
-    for (uint32_t j = 0; j < 4; j++) {
-      const uint32_t d = 4 * r + j;
-      *reinterpret_cast<float4*>(pb + d * PV_STP + 4 * (q ^ (d & 7))) =
-          make_float4(m[j][0], m[j][1], m[j][2], m[j][3]);
+      for (uint32_t i = 0; i < 4; i++) {
+        const bool live = p0 + i < total;
+        m[0][i] = live ? pp[i] * R.a[k][i].x : 0.0f;
+        m[1][i] = live ? pp[i] * R.a[k][i].y : 0.0f;
+        m[2][i] = live ? pp[i] * R.a[k][i].z : 0.0f;
+        m[3][i] = live ? pp[i] * R.a[k][i].w : 0.0f;
+      }
+#pragma unroll
+      for (uint32_t j = 0; j < 4; j++) {
+        const uint32_t d = 4 * r + j;
+        *reinterpret_cast<float4*>(pb + d * PV_STP + 4 * (q ^ (d & 7))) =
+            make_float4(m[j][0], m[j][1], m[j][2], m[j][3]);
+      }
     }
     load(R, s + 3);
   };
@@ -644,7 +656,8 @@ __global__ __launch_bounds__(PV_NT) void k_attn_seq(const float* vc, const float
       const uint32_t sp = s - 1;
       const float* pr = pbuf + (sp & 1) * PV_BUF + t * PV_STP;
       const uint32_t sw = (uint32_t)t & 7;
-      const uint32_t nq = min(4u, (total - sp * PV_STP + 31) / 32);
+      constexpr uint32_t NQ = PV_STP / 32;  // batches a stage
+      const uint32_t nq = min(NQ, (total - sp * PV_STP + 31) / 32);
       auto rd = [&](float4 (&a)[8], uint32_t b) {
 #pragma unroll
         for (uint32_t i = 0; i < 8; i++)
@@ -653,18 +666,16 @@ __global__ __launch_bounds__(PV_NT) void k_attn_seq(const float* vc, const float
       float4 a[8], b[8];
       rd(a, 0);
       rd(b, 1);
-      __builtin_amdgcn_sched_barrier(0);
-      add32(o, a);
-      if (nq > 1) {
-        rd(a, 2);
+#pragma unroll
+      for (uint32_t k = 0; k < NQ; k += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        add32(o, a);
+        if (k + 1 >= nq) break;
+        if (k + 2 < NQ) rd(a, k + 2);
         __builtin_amdgcn_sched_barrier(0);
         add32(o, b);
-        if (nq > 2) {
-          rd(b, 3);
-          __builtin_amdgcn_sched_barrier(0);
-          add32(o, a);
-          if (nq > 3) add32(o, b);
-        }
+        if (k + 2 >= nq) break;
+        if (k + 3 < NQ) rd(b, k + 3);
       }
     }
     cx_wait_lds();
@@ -1071,21 +1082,26 @@ size_t cx_attn_splits(size_t cap) { return (cap + ATT_P - 1) / ATT_P; }
 namespace {
 // One query token: the softmax-V kernel with helper-made products, 32 dims
 // a workgroup (a ring of RING floats), plus rows of prefetch workgroups.
-template <int HD>
-int launch_seq_one(const cx_attn_args& a, hipStream_t s) {
-  const size_t lds = pv_lds_floats(a.cap) * sizeof(float);
+template <int HD, uint32_t STP, uint32_t NT>
+int launch_seq_shape(const cx_attn_args& a, hipStream_t s) {
+  const size_t lds = pv_lds_floats(a.cap, STP) * sizeof(float);
   CX_REQUIRE(lds <= 158 * 1024 && (a.cap + SC_P - 1) / SC_P <= CML_MAX,
              "attention: %u cached positions need %zu bytes of LDS", a.cap, lds);
   const uint32_t rows = HD / 32, np = cx_l2_prefetch_groups(a.pf, a.heads * rows);
   const dim3 grid(a.heads, rows + (np + a.heads - 1) / a.heads, 1);
   if (a.sub == 16)
-    hipLaunchKernelGGL((k_attn_seq<HD, 16>), grid, dim3(PV_NT), lds, s, a.vc, a.sc, a.cm, a.heads,
-                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+    hipLaunchKernelGGL((k_attn_seq<HD, 16, STP, NT>), grid, dim3(NT), lds, s, a.vc, a.sc, a.cm,
+                       a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   else
-    hipLaunchKernelGGL((k_attn_seq<HD, 32>), grid, dim3(PV_NT), lds, s, a.vc, a.sc, a.cm, a.heads,
-                       a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
+    hipLaunchKernelGGL((k_attn_seq<HD, 32, STP, NT>), grid, dim3(NT), lds, s, a.vc, a.sc, a.cm,
+                       a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   CX_HIP(hipGetLastError());
   return CX_OK;
+}
+template <int HD>
+int launch_seq_one(const cx_attn_args& a, hipStream_t s) {
+  return a.cap <= PV_LONG_CAP ? launch_seq_shape<HD, 128, 320>(a, s)
+                              : launch_seq_shape<HD, 256, 576>(a, s);
 }
 
 template <int HD>
