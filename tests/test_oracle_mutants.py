@@ -28,10 +28,10 @@ MUTANTS = {
          "float *lo = x + t * width + h * hd, *hi = lo + 1;"],
         ["test_rope_one_hot_rotation_direction"]),
     "attention_unscaled": (
-        ["float scale = 1.0f / sqrtf((float)hd);", "float scale = 1.0f;"],
+        ["tokens;\n  float scale = 1.0f / sqrtf((float)hd);", "tokens;\n  float scale = 1.0f;"],
         ["test_attention_matches_scaled_softmax_closed_form"]),
     "attention_scaled_by_dim": (
-        ["float scale = 1.0f / sqrtf((float)hd);", "float scale = 1.0f / (float)hd;"],
+        ["tokens;\n  float scale = 1.0f / sqrtf((float)hd);", "tokens;\n  float scale = 1.0f / (float)hd;"],
         ["test_attention_matches_scaled_softmax_closed_form"]),
     "box_muller_swapped": (
         ["*z0 = r * cosf(ang);\n  *z1 = r * sinf(ang);", "*z0 = r * sinf(ang);\n  *z1 = r * cosf(ang);"],
