@@ -1212,6 +1212,14 @@ struct GluParams {
   float* xs;
 };
 constexpr uint32_t GLU_ROWS = 32;
+// The row-layout gate/up launch's tile (k = 2048): 64 rows of gate and of up
+// in 16 waves when the rows divide so (172 tiles at the 3B shape, one a CU),
+// else 32 in 8. With 344 tiles of 32 on 256 CUs, 88 CUs ran two and the
+// launch ended with them (stamps: the median tile done at 4.4 us, the last
+// at 6.8).
+inline uint32_t glu_row_tile(uint32_t k, uint32_t I) {
+  return k == 2048 && I % 64 == 0 ? 64u : GLU_ROWS;
+}
 
 // Every thread keeps GLU_DEPTH items' weights in flight: all of them at
 // k = 2048 (4 items a thread), a ring refilled one item behind at larger k.
@@ -1359,25 +1367,25 @@ __global__ __launch_bounds__(256) void k_gemv_glu(GluParams P) {
 // reference's order, from 0), the row's last lane forms silu(g)·u
 // (src/forward.rs:483-487), and four lanes quantize the tile's 32 values
 // for the down projection (sub-blocks of SUB) — the bytes k_gemv_glu writes.
-template <int T, int NB, int SUB>
-__global__ __launch_bounds__(64 * NB) void k_gemv_row_glu(GluParams P) {
+template <int T, int NB, int SUB, int ROWS>
+__global__ __launch_bounds__(2 * NB * ROWS) void k_gemv_row_glu(GluParams P) {
   using Q = KQ<T>;
   constexpr int LPR = 2 * NB;   // lanes per row
   constexpr int RPW = 64 / LPR; // rows per wave
   constexpr int GJ = NB / 8;    // 8-value groups a virtual lane of the f64 tree
   static_assert(NB == 8 || NB == 16, "k = 2048 or 4096");
-  static_assert(GLU_ROWS * LPR == 64 * NB, "the tile's rows fill the NB waves");
+  static_assert(ROWS * LPR % 256 == 0 && ROWS * LPR <= 1024, "whole waves, at least the tree's four");
   __shared__ __align__(16) int8_t sq[NB * ACT_LDS_BLOCK];
   __shared__ __align__(16) float se[8 * NB], ss[8 * NB];
   __shared__ double red[9];
   __shared__ int nflag;
-  __shared__ __align__(16) float act[GLU_ROWS];
+  __shared__ __align__(16) float act[ROWS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint64_t xb = (uint64_t)P.nx, wb = (uint64_t)P.nw, gb = (uint64_t)P.wg, ub = (uint64_t)P.wu;
   uint32_t rb = P.row_bytes;
   asm volatile("" : "+s"(xb), "+s"(wb), "+s"(gb), "+s"(ub), "+s"(rb));
-  const uint32_t row0 = blockIdx.x * GLU_ROWS;
+  const uint32_t row0 = blockIdx.x * ROWS;
   const uint32_t lr = (uint32_t)(wave * RPW + lane / LPR);  // the lane's row in the tile
   const int b = (lane % LPR) >> 1, h = lane & 1;
   const bool owner = lane % LPR == LPR - 1;
@@ -1499,7 +1507,7 @@ __global__ __launch_bounds__(64 * NB) void k_gemv_row_glu(GluParams P) {
   cx_wait_lds();
   cx_barrier();
   // 6. the down projection's quantization of the tile's 32 values
-  if (tid < (int)(GLU_ROWS / 8)) {
+  if (tid < (int)(ROWS / 8)) {
     const float4 v0 = reinterpret_cast<const float4*>(act)[2 * tid];
     const float4 v1 = reinterpret_cast<const float4*>(act)[2 * tid + 1];
     const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
@@ -2263,14 +2271,20 @@ int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t 
     // 8.71 -> 7.75 us a launch, weights in L2). At k = 4096 (16 waves a
     // tile, 448 tiles: config 5's 14336 x 4096, 66 MB past L2) it measured
     // 20.4 us against k_gemv_glu's 16.3, which keeps that shape.
-    const dim3 grid(I / GLU_ROWS), block(64 * (k / 256));
-#define CX_ROW_GLU(TT, NB)                                                              \
-  do {                                                                                  \
-    if (sub == 32) hipLaunchKernelGGL((k_gemv_row_glu<TT, NB, 32>), grid, block, 0, s, P); \
-    else hipLaunchKernelGGL((k_gemv_row_glu<TT, NB, 16>), grid, block, 0, s, P);          \
+    const uint32_t rows = glu_row_tile(k, I);
+    const dim3 grid(I / rows), block(2 * (k / 256) * rows);
+#define CX_ROW_GLU(TT, NB, R)                                                              \
+  do {                                                                                     \
+    if (sub == 32) hipLaunchKernelGGL((k_gemv_row_glu<TT, NB, 32, R>), grid, block, 0, s, P); \
+    else hipLaunchKernelGGL((k_gemv_row_glu<TT, NB, 16, R>), grid, block, 0, s, P);          \
   } while (0)
-    if (type == CX_Q4_K) CX_ROW_GLU(CX_Q4_K, 8);
-    else CX_ROW_GLU(CX_Q5_K, 8);
+    if (rows == 64) {
+      if (type == CX_Q4_K) CX_ROW_GLU(CX_Q4_K, 8, 64);
+      else CX_ROW_GLU(CX_Q5_K, 8, 64);
+    } else {
+      if (type == CX_Q4_K) CX_ROW_GLU(CX_Q4_K, 8, 32);
+      else CX_ROW_GLU(CX_Q5_K, 8, 32);
+    }
 #undef CX_ROW_GLU
     CX_HIP(hipGetLastError());
     return CX_OK;
@@ -2337,7 +2351,9 @@ bool cx_glu_prefetch_plan(int type, const uint8_t* wg, const uint8_t* wu, uint32
                           cx_l2_job* job) {
   if (!cx_glu_fits(type, k) || I % GLU_ROWS) return false;
   const uint32_t rb = (cx_glu_supported(type) ? k / 256 : k / 32) * (uint32_t)cx_bpb(type);
-  *job = cx_l2_job{wg, wu, (size_t)I * rb, GLU_ROWS * rb, I / GLU_ROWS};
+  // the tiles of the launch that reads them (the row kernel's at k = 2048)
+  const uint32_t rows = cx_glu_supported(type) ? glu_row_tile(k, I) : GLU_ROWS;
+  *job = cx_l2_job{wg, wu, (size_t)I * rb, rows * rb, I / rows};
   return true;
 }
 
