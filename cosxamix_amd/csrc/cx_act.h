@@ -170,28 +170,34 @@ struct cx_rms_risk {
 };
 __device__ inline uint32_t cx_rms_c(uint32_t reach) { return 0x80000000u - 8u * reach; }
 // The f64 sum of squares of x[0..n) in order from 0, by one wave: lane l
-// loads x[64q + l] (coalesced), squares it, and the 64 squares are added to
-// the running sum in lane order, read across lanes; lanes past n add +0.0,
-// which leaves a sum of squares as it is. Every lane ends with the sum. x
-// may be in global memory or in LDS.
+// loads x[64q + l] (coalesced) and writes its square to a 64-double LDS
+// buffer, then lane 0 adds the chunk's 64 squares to the running sum in
+// order, two per 16-byte LDS read (one dependent f64 add an element; reading
+// the squares across lanes with readlane took ~41 clocks an element). Lanes
+// past n write +0.0, which leaves a sum of squares as it is. Every lane ends
+// with the sum. x may be in global memory or in LDS. The LDS writes and lane
+// 0's reads are one wave's, so LDS performs them in issue order.
 __device__ inline double cx_rms_seq_sum(const float* x, uint32_t n) {
+  __shared__ __align__(16) double sq[2][64];
   const uint32_t lane = threadIdx.x & 63;
   double s = 0.0;
   float nxt = lane < n ? x[lane] : 0.0f;
-  for (uint32_t q = 0; q < n; q += 64) {
-    const double t = (double)nxt * (double)nxt;
+  uint32_t b = 0;
+  for (uint32_t q = 0; q < n; q += 64, b ^= 1) {
+    sq[b][lane] = (double)nxt * (double)nxt;
     // the next chunk's load under this chunk's adds
     nxt = q + 64 + lane < n ? x[q + 64 + lane] : 0.0f;
-    const uint64_t tb = (uint64_t)__double_as_longlong(t);
-    const int tlo = (int)(uint32_t)tb, thi = (int)(uint32_t)(tb >> 32);
-#pragma unroll 8
-    for (int l = 0; l < 64; l++) {
-      const uint64_t r = (uint64_t)(uint32_t)__builtin_amdgcn_readlane(tlo, l) |
-                         ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(thi, l) << 32);
-      s += __longlong_as_double((long long)r);
+    if (lane == 0) {
+      const double2* p = reinterpret_cast<const double2*>(sq[b]);
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const double2 v = p[j];
+        s += v.x;
+        s += v.y;
+      }
     }
   }
-  return s;
+  return __shfl(s, 0, 64);
 }
 
 // The rmsnorm factor of x[0..n) (n % 4 == 0, x 16-byte aligned) over a
