@@ -428,10 +428,19 @@ __host__ __device__ constexpr uint32_t pv_lds_floats(uint32_t cap, uint32_t stp)
 constexpr uint32_t SUM_PLAIN_MAX = 768;
 constexpr uint32_t CML_MAX = 256;  // chunk maxima of one head: 16384 positions
 
-// PV_NT threads: wave 0's lanes run the order-exact accumulation, waves 1-4
-// stream V. Rows of the grid past HD / 32 are prefetch workgroups (pf).
+// A workgroup's waves go to the CU's four SIMDs in turn, so wave 4 of the
+// short shape (five waves) would share SIMD 0 with wave 0's chain, whose
+// adds are bound by that SIMD's issue: the short shape launches six waves
+// and wave 4 leaves at once (3B decode 741.5 -> 745.3 tok/s). The long
+// shape keeps nine (eleven with waves 4 and 8 leaving measured 282.1 ->
+// 278.4 tok/s at config 5).
+__host__ __device__ constexpr uint32_t pv_lt(uint32_t nt) { return nt == 320 ? 384 : nt; }
+
+// PV_NT active threads (of pv_lt(PV_NT) launched): wave 0's lanes run the
+// order-exact accumulation, the others stream V. Rows of the grid past
+// HD / 32 are prefetch workgroups (pf).
 template <int HD, int SUB, uint32_t PV_STP, uint32_t PV_NT>
-__global__ __launch_bounds__(PV_NT) void k_attn_seq(const float* vc, const float* sc_all,
+__global__ __launch_bounds__(pv_lt(PV_NT)) void k_attn_seq(const float* vc, const float* sc_all,
                                                   const float* cm_all, uint32_t heads,
                                                   uint32_t kvh, const cx_dstate* st, uint32_t cap,
                                                   float* out, int8_t* xq, float* xe, float* xs,
@@ -466,9 +475,12 @@ __global__ __launch_bounds__(PV_NT) void k_attn_seq(const float* vc, const float
       h = J / per / NY * per + J % per;
     }
   }
+  const int wl = threadIdx.x >> 6;  // the launched wave
+  if (pv_lt(PV_NT) != PV_NT && wl == 4) return;
   const uint32_t total = st->pos + 1, g = h / (heads / kvh);
   const uint32_t d0 = y * DS, kvd = kvh * HD;
-  const int tid = threadIdx.x, t = tid & 63, w = tid >> 6;
+  // the active wave and thread (the short shape's wave 5 is active wave 4)
+  const int t = threadIdx.x & 63, w = pv_lt(PV_NT) != PV_NT ? wl - wl / 4 : wl, tid = 64 * w + t;
   // 1. the head's scores as untracked direct-to-LDS loads; with one query
   //    token wave 0 first fetches the chunk maxima the scores kernel wrote
   //    (64 positions a chunk, at most CML_MAX chunks). Both cover the
@@ -1090,10 +1102,10 @@ int launch_seq_shape(const cx_attn_args& a, hipStream_t s) {
   const uint32_t rows = HD / 32, np = cx_l2_prefetch_groups(a.pf, a.heads * rows);
   const dim3 grid(a.heads, rows + (np + a.heads - 1) / a.heads, 1);
   if (a.sub == 16)
-    hipLaunchKernelGGL((k_attn_seq<HD, 16, STP, NT>), grid, dim3(NT), lds, s, a.vc, a.sc, a.cm,
+    hipLaunchKernelGGL((k_attn_seq<HD, 16, STP, NT>), grid, dim3(pv_lt(NT)), lds, s, a.vc, a.sc, a.cm,
                        a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   else
-    hipLaunchKernelGGL((k_attn_seq<HD, 32, STP, NT>), grid, dim3(NT), lds, s, a.vc, a.sc, a.cm,
+    hipLaunchKernelGGL((k_attn_seq<HD, 32, STP, NT>), grid, dim3(pv_lt(NT)), lds, s, a.vc, a.sc, a.cm,
                        a.heads, a.kvh, a.st, a.cap, a.out, a.xq, a.xe, a.xs, a.pf);
   CX_HIP(hipGetLastError());
   return CX_OK;
