@@ -904,22 +904,28 @@ __global__ __launch_bounds__(64 * W) void k_gemv_row_norm(GemvParams P) {
   const int b = (lane % LPR) >> 1, h = lane & 1;
   const bool owner = lr < rows && lane % LPR == LPR - 1;
 
-  // 1. x and w of the thread's groups (L2 hits; threads past 256 reload
-  //    the last virtual lane's), then the weights
+  // 1. x and w of the thread's groups (L2 hits; with more than 256 threads
+  //    only the first 256, the tree's, load them: a CU's loads pass its
+  //    address unit at a bounded rate, and at k = 4096 the other twelve
+  //    waves' copies held back the weights' issue by ~2 us), then the weights
   const float4* const xg = (const float4*)reinterpret_cast<const __attribute__((address_space(1))) float4*>(xb);
   const float4* const wg = (const float4*)reinterpret_cast<const __attribute__((address_space(1))) float4*>(wb);
   float4 xv[VT * GJ * 2], wv[VT * GJ * 2];
+  if (NT <= 256 || tid < 256) {  // whole waves
 #pragma unroll
-  for (int m = 0; m < VT; m++)
+    for (int m = 0; m < VT; m++)
 #pragma unroll
-    for (int j = 0; j < GJ; j++) {
-      const uint32_t vt = min((uint32_t)(tid + NT * m), 255u);
-      const uint32_t g = vt + 256u * (uint32_t)j;
-      xv[2 * (m * GJ + j)] = xg[2 * g];
-      xv[2 * (m * GJ + j) + 1] = xg[2 * g + 1];
-      wv[2 * (m * GJ + j)] = wg[2 * g];
-      wv[2 * (m * GJ + j) + 1] = wg[2 * g + 1];
-    }
+      for (int j = 0; j < GJ; j++) {
+        const uint32_t g = (uint32_t)(tid + NT * m) + 256u * (uint32_t)j;
+        xv[2 * (m * GJ + j)] = xg[2 * g];
+        xv[2 * (m * GJ + j) + 1] = xg[2 * g + 1];
+        wv[2 * (m * GJ + j)] = wg[2 * g];
+        wv[2 * (m * GJ + j) + 1] = wg[2 * g + 1];
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VT * GJ * 2; i++) xv[i] = wv[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
   __builtin_amdgcn_sched_barrier(0);
   typename Q::Regs r;
   const uint32_t row = row0 + (lr < rows ? lr : rows - 1);
