@@ -882,7 +882,7 @@ def main():
                      "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
                      "traffic": None if traffic is None else int(traffic),
                      "traffic_source": tdetail,
-                     "kernel": "k_gemv<Q4_K> config 1 (11008x2048)",
+                     "kernel": "k_gemv_row<Q4_K> config 1 (11008x2048, 48-row tiles of 12 waves)",
                      "us_per_launch": round(avg * 1e6, 3), "bytes_per_launch": CONFIG1_BYTES,
                      "rotating_matrices": ncopies,
                      # measured on this box: the read peak (1 GB), the read rate of a

@@ -1978,8 +1978,6 @@ int launch_row_norm(GemvParams& P, const uint32_t* rows, hipStream_t s) {
 }
 
 // The long-row kernel (k_gemv_rowl) for a plain Q4_K/Q5_K launch of
-// 16 < k/256 <= 64 super-blocks: W waves (W rows) a workgroup.
-// The long-row kernel (k_gemv_rowl) for a plain Q4_K/Q5_K launch of
 // 16 < k/256 <= 64 super-blocks: 4 waves (4 rows) a workgroup, the chain
 // unrolled at 43 and 56 blocks. Measured on MI355X in the 3B decode step
 // (down, 2048 x 11008, 512 tiles): 706 tok/s against 700 with 8 waves, 663

@@ -314,9 +314,13 @@ def test_softmax_silu_argmax(cx, dev):
 def test_decode_attention_paths(cx, dev, heads, kvh, hd):
     """The model's decode attention: order-exact mode bit-identical to the
     oracle (src/ops.rs:1258-1325) at any length, for 1, 2, 4, 7, 8 and 16
-    query heads per KV group; split-K mode within f32 rounding."""
+    query heads per KV group, on either side of the softmax-V kernel's
+    limits (768/769: the sum one add a position, then by binade scan;
+    2048/2049: 128-position stages, then 256); split-K mode within f32
+    rounding."""
     ops, _ = cx
-    for total in (1, 2, 37, 63, 64, 65, 100, 150, 255, 256, 257, 640, 1000, 2048, 4096, 4097, 8300):
+    for total in (1, 2, 37, 63, 64, 65, 100, 150, 255, 256, 257, 640, 768, 769, 1000, 2048, 2049,
+                  4096, 4097, 8300):
         rng = np.random.default_rng(total + heads)
         q = rng.normal(0, 1, heads * hd).astype(np.float32)
         k = rng.normal(0, 1, total * kvh * hd).astype(np.float32)
@@ -336,9 +340,9 @@ def test_decode_attention_paths(cx, dev, heads, kvh, hd):
 @pytest.mark.parametrize("heads,kvh", [(16, 2), (32, 8)])
 def test_decode_attention_long_path_limits(cx, dev, heads, kvh):
     """Order-exact decode attention on either side of the long one-token
-    path's limits: 4096/4097 (the scores from k_att_qk and an 80 KiB V ring
-    from 4097 on), 6145 (three stages of the softmax sum's 2048 positions and
-    one more), 11520/11521 (the last cache the long path holds in LDS, then
+    path's limits: 4096/4097 (the scores from k_att_qk from 4097 on), 6145
+    (three stages of the softmax sum's 2048 positions and one more),
+    11520/11521 (the last cache the long path holds in LDS, then
     k_att_sv); bit-identical to the oracle."""
     ops, _ = cx
     hd = 128
