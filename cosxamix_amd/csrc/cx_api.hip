@@ -859,7 +859,8 @@ static int model_finish(cx_model* m) {
     cx_set_error("model: rope tables");
     return CX_ENOMEM;
   }
-  const size_t parts = cx_argmax_parts(V);
+  // the argmax's pairs: its own first step's, or the lm_head epilogue's
+  const size_t parts = std::max(cx_argmax_parts(V), (size_t)cx_gemv_argmax_parts(m->t_out, V, D));
   if (hipMalloc(&m->x, D * 4) || hipMalloc(&m->q, D * 4) || hipMalloc(&m->k, kvd * 4) ||
       hipMalloc(&m->v, kvd * 4) || hipMalloc(&m->att, D * 4) || hipMalloc(&m->g, I * 4) ||
       hipMalloc(&m->u, I * 4) || hipMalloc(&m->logits, (size_t)V * 4) ||
@@ -1406,6 +1407,16 @@ static int enqueue_tail(cx_cache* C) {
                                    m->xs, s)))
       return rc;
     cx_seg lm{m->out, m->logits, nullptr, c.vocab};
+    if (!C->sampling) {
+      // the lm_head's tiles write the argmax's pairs themselves (one launch
+      // fewer: 3B 6.7 us a token) where the row kernel takes the matrix
+      uint32_t nparts = 0;
+      if ((rc = cx_launch_gemv_argmax(m->t_out, lm, D, act, m->apv, m->api, &nparts, s)))
+        return rc;
+      if (nparts)
+        return cx_launch_argmax_final(m->logits, m->apv, m->api, nparts, m->amax_out, C->st,
+                                      C->hist, C->htok_dev, s);
+    }
     if ((rc = cx_launch_gemv(m->t_out, &lm, 1, D, act, CX_EPI_STORE, nullptr, s))) return rc;
   } else {  // an unquantized (tied) lm_head: the f32 path (src/ops.rs:1064-1071)
     if ((rc = cx_launch_rmsnorm(m->att, m->x, m->out_norm, 1, D, c.eps, s))) return rc;

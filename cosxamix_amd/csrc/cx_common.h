@@ -149,6 +149,23 @@ __device__ inline float cx_wave_max(float v) {
   return v;
 }
 
+// argmax pairs (src/sampler.rs:129-137): the larger value, the lower index
+// among equal values; callers leave NaN out (a NaN never wins)
+struct VI {
+  float v;
+  uint32_t i;
+};
+__device__ inline VI vi_best(VI a, VI b) {
+  return (a.v > b.v || (a.v == b.v && a.i < b.i)) ? a : b;
+}
+__device__ inline VI vi_wave(VI a) {
+  for (int o = 1; o < 64; o <<= 1) {
+    VI b{__shfl_xor(a.v, o, 64), (uint32_t)__shfl_xor((int)a.i, o, 64)};
+    a = vi_best(a, b);
+  }
+  return a;
+}
+
 // Pipelines of direct-to-LDS loads (global_load_lds) need partial waits:
 // __syncthreads() carries a workgroup fence after which the compiler waits
 // for every outstanding vector load (vmcnt(0)), draining the pipeline. These

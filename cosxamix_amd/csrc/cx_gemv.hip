@@ -424,6 +424,8 @@ struct GemvParams {
   float eps;
   int epi;
   int32_t* dbg;
+  float* apv;     // per tile: the largest output and its index (the argmax's first step)
+  uint32_t* api;
 };
 
 // 16-byte chunks [0, n) of global `g` into LDS at `l`, 1 KiB per wave load
@@ -771,7 +773,7 @@ __device__ inline void row_act_store(int8_t* sq, float* se, float* ss, int c, co
                           : reinterpret_cast<int4*>(ss) + (c - NX - NE);
   *p = v;
 }
-template <int T, int NB, bool MULTI, bool DBG>
+template <int T, int NB, bool MULTI, bool DBG, bool AMAX = false>
 __global__ __launch_bounds__(1024) void k_gemv_row(GemvParams P) {
   using Q = KQ<T>;
   constexpr int AP = (NB * 20 + 63) / 64;  // activation chunks a lane of wave 0 loads
@@ -858,7 +860,26 @@ __global__ __launch_bounds__(1024) void k_gemv_row(GemvParams P) {
     v += t[3];
     acc = v;
   }
-  if (owner) S.y[row] = add ? acc + addend : acc;
+  const float y = add ? acc + addend : acc;
+  if (owner) S.y[row] = y;
+  if constexpr (AMAX) {
+    // the tile's (largest output, its row) for the argmax, NaN left out:
+    // every row slot's last lane, then one wave over the slots (rows past
+    // the matrix hold the empty pair)
+    static_assert(!MULTI, "one matrix");
+    __shared__ VI am[64];
+    if (lane % LPR == LPR - 1)
+      am[lr] = lr < rows && !(y != y) ? VI{y, row0 + lr} : VI{-INFINITY, 0xFFFFFFFFu};
+    __syncthreads();
+    if (wave == 0) {
+      VI best = (uint32_t)lane < R ? am[lane] : VI{-INFINITY, 0xFFFFFFFFu};
+      best = vi_wave(best);
+      if (lane == 0) {
+        P.apv[tile] = best.v;
+        P.api[tile] = best.i;
+      }
+    }
+  }
 }
 
 // The row kernel with the rmsnorm prologue (the q/k/v launch): every
@@ -2190,6 +2211,52 @@ int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k, const cx_
   if (rc || !total) return rc;
   P.act = act;
   return launch_type<false>(type, P, rows, s);
+}
+
+// The argmax's first step in the GEMV's epilogue (the lm_head): where the
+// row kernel takes the matrix (Q4_K/Q5_K, k = 2048 or 4096), the tiles it
+// would launch, each writing its (largest output, row) pair; else 0.
+uint32_t cx_gemv_argmax_parts(int type, uint32_t n, uint32_t k) {
+  if ((type != CX_Q4_K && type != CX_Q5_K) || !n) return 0;
+  return row_plan(k, &n, 1).tiles;
+}
+
+// y = W·act (CX_EPI_STORE, no bias) and the per-tile argmax pairs in
+// apv/api (cx_gemv_argmax_parts(type, n, k) of them); *nparts = 0 and
+// nothing launched where the row kernel does not take the matrix.
+int cx_launch_gemv_argmax(int type, const cx_seg& seg, uint32_t k, const cx_qact& act, float* apv,
+                          uint32_t* api, uint32_t* nparts, hipStream_t s) {
+  *nparts = 0;
+  const uint32_t parts = cx_gemv_argmax_parts(type, seg.rows, k);
+  if (!parts) return CX_OK;
+  CX_REQUIRE(apv && api && !seg.bias, "gemv argmax: the pair buffers, no bias");
+  CX_REQUIRE(act.xq && act.xe && act.xs && ((uintptr_t)act.xq & 15u) == 0 &&
+                 ((uintptr_t)act.xe & 15u) == 0 && ((uintptr_t)act.xs & 15u) == 0,
+             "gemv argmax: xq, xe and xs 16-byte aligned");
+  CX_REQUIRE(((uintptr_t)seg.w & 15u) == 0, "gemv argmax: weights 16-byte aligned");
+  GemvParams P{};
+  uint32_t rows[4], total;
+  int rc = gemv_setup(type, &seg, 1, k, CX_EPI_STORE, nullptr, P, rows, &total);
+  if (rc || !total) return rc;
+  P.act = act;
+  P.apv = apv;
+  P.api = api;
+  const RowPlan rp = row_plan(k, rows, 1);
+  CX_REQUIRE(rp.R && rp.tiles == parts && rp.R <= 64, "gemv argmax: row plan");
+  P.R = rp.R;
+  P.tile_end[0] = rp.tiles;
+  const dim3 g(rp.tiles), b(64 * rp.W);
+#define CX_ROW_AMAX(TT)                                                                   \
+  do {                                                                                    \
+    if (k == 2048) hipLaunchKernelGGL((k_gemv_row<TT, 8, false, false, true>), g, b, 0, s, P); \
+    else hipLaunchKernelGGL((k_gemv_row<TT, 16, false, false, true>), g, b, 0, s, P);          \
+  } while (0)
+  if (type == CX_Q4_K) CX_ROW_AMAX(CX_Q4_K);
+  else CX_ROW_AMAX(CX_Q5_K);
+#undef CX_ROW_AMAX
+  CX_HIP(hipGetLastError());
+  *nparts = parts;
+  return CX_OK;
 }
 
 int cx_launch_gemv_norm(int type, const cx_seg* segs, int nseg, uint32_t k, const float* x,

@@ -97,6 +97,12 @@ enum cx_epi { CX_EPI_STORE = 0, CX_EPI_ACCUM = 1 };
 // `dbg` (single segment only) receives the integer sub-block sums.
 int cx_launch_gemv(int type, const cx_seg* segs, int nseg, uint32_t k, const cx_qact& act,
                    int epi, int32_t* dbg, hipStream_t s);
+// The lm_head with the argmax's first step in its epilogue: the per-tile
+// (largest output, row) pairs in apv/api, *nparts of them (0, and nothing
+// launched, where the row kernel does not take the matrix).
+uint32_t cx_gemv_argmax_parts(int type, uint32_t n, uint32_t k);
+int cx_launch_gemv_argmax(int type, const cx_seg& seg, uint32_t k, const cx_qact& act, float* apv,
+                          uint32_t* api, uint32_t* nparts, hipStream_t s);
 // The same GEMV with its activation made by every workgroup from f32 x:
 // rmsnorm(x, w, eps) (kernels/mod.rs:511) then quantization (ops.rs:178), in
 // the shadow of the weight loads. For launches of a few hundred workgroups;

@@ -100,6 +100,9 @@ int cx_launch_attention(const float* q, const float* k, const float* v, size_t t
 int cx_launch_softmax(float* x, size_t len, size_t width, hipStream_t s);
 int cx_launch_silu(float* out, const float* in, size_t n, hipStream_t s);
 size_t cx_argmax_parts(size_t n);
+int cx_launch_argmax_final(const float* v, const float* pv, const uint32_t* pi, uint32_t nparts,
+                           uint32_t* out, cx_dstate* st, uint32_t* hist, uint32_t* hist_host,
+                           hipStream_t s);
 int cx_launch_argmax(const float* v, size_t n, float* pv, uint32_t* pi, uint32_t* out,
                      cx_dstate* st, uint32_t* hist, uint32_t* hist_host, hipStream_t s);
 

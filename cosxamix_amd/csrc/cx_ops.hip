@@ -926,17 +926,6 @@ __global__ void k_silu(float* out, const float* in, size_t n) {
 // (value, index) pairs; a beats b if larger, or equal with a lower index.
 // NaN entries never win; index 0 wins when v[0] is NaN (strict '>' scan of
 // src/sampler.rs:129-137 never leaves index 0 then).
-struct VI { float v; uint32_t i; };
-__device__ inline VI vi_best(VI a, VI b) {
-  return (a.v > b.v || (a.v == b.v && a.i < b.i)) ? a : b;
-}
-__device__ inline VI vi_wave(VI a) {
-  for (int o = 1; o < 64; o <<= 1) {
-    VI b{__shfl_xor(a.v, o, 64), (uint32_t)__shfl_xor((int)a.i, o, 64)};
-    a = vi_best(a, b);
-  }
-  return a;
-}
 constexpr uint32_t ARG_CHUNK = 4096;
 
 __global__ __launch_bounds__(256) void k_argmax_part(const float* v, uint32_t n, float* pv,
@@ -1225,6 +1214,18 @@ int cx_launch_silu(float* out, const float* in, size_t n, hipStream_t s) {
 }
 
 size_t cx_argmax_parts(size_t n) { return (n + ARG_CHUNK - 1) / ARG_CHUNK; }
+
+// The argmax's second step alone, over nparts pairs another launch wrote
+// (the lm_head's epilogue, cx_launch_gemv_argmax)
+int cx_launch_argmax_final(const float* v, const float* pv, const uint32_t* pi, uint32_t nparts,
+                           uint32_t* out, cx_dstate* st, uint32_t* hist, uint32_t* hist_host,
+                           hipStream_t s) {
+  CX_REQUIRE(v && pv && pi && nparts > 0, "argmax: bad arguments");
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, v, pv, pi, nparts, out, st, hist,
+                     hist_host);
+  CX_HIP(hipGetLastError());
+  return CX_OK;
+}
 
 int cx_launch_argmax(const float* v, size_t n, float* pv, uint32_t* pi, uint32_t* out,
                      cx_dstate* st, uint32_t* hist, uint32_t* hist_host, hipStream_t s) {

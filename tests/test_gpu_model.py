@@ -215,3 +215,44 @@ def test_generator_matches_oracle_rows(F):
     norm = m.tensor(names.index("blk.0.attn_norm.weight"))
     bias = m.tensor(names.index("blk.0.attn_q.bias"))
     assert (norm == 1.0).all() and (bias == 0.0).all()
+
+
+def test_lm_head_argmax_ties_and_nan(F):
+    """The decode step's argmax runs in the lm_head's epilogue (each row tile
+    writes its largest logit and row, one launch reduces the pairs): the
+    reference's argmax (src/sampler.rs:129-137) over the whole vocabulary,
+    the first index among equal maxima, a NaN never winning. The row with
+    the largest logit is copied into rows 70 and 2800 (other tiles of the
+    lm_head's 8-row tiles), and row 3's first block scale is set to NaN (f16
+    0x7E00); logits bit-identical to the oracle's and the token its argmax,
+    in the decode step and after a prefill."""
+    from cosxamix_amd import _lib as L
+    from gguf_fixtures import write_tensor
+    c = F.Config(capas=1, dim=2048, cabezas=16, cabezas_kv=2, ffn=1024, vocab=3000, contexto=64)
+    m = F.Modelo(c, tipo=L.Q4_K, semilla=77, tipo_salida=L.Q4_K)
+    try:
+        io = [x[0] for x in m.tensores()].index("output.weight")
+        W = m.tensor(io)
+        rb = W.shape[1]
+        lg, am = m.forward(np.array([5], np.uint32), m.nueva_cache(8))
+        j = int(np.argmax(lg))
+        assert am == j
+        for r in (70, 2800):
+            write_tensor(m, io, W[j], byte_offset=r * rb)
+        row3 = W[3].copy()
+        row3[0:2] = (0x00, 0x7E)
+        write_tensor(m, io, row3, byte_offset=3 * rb)
+        ref = mirror(m)
+        for prompt in ([5], [5, 9], [9]):
+            lg, am = m.forward(np.array(prompt, np.uint32), m.nueva_cache(8))
+            want = ref.forward(np.array(prompt, np.uint32), ref.new_cache(8))
+            assert np.isnan(lg[3]) and np.isnan(want[3])  # (NaN payloads may differ)
+            fin = np.arange(c.vocab) != 3
+            assert np.array_equal(lg[fin].view(np.uint32), want[fin].view(np.uint32)), prompt
+            top = np.nanmax(want)
+            assert am == O.argmax(want) == int(np.nonzero(want == top)[0][0]), (prompt, am)
+        # the tie itself, for the prompt the copies were made from
+        lg, am = m.forward(np.array([5], np.uint32), m.nueva_cache(8))
+        assert lg[70] == lg[2800] == lg[j] and am == min(j, 70)
+    finally:
+        m.close()
