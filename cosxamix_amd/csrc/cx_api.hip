@@ -1368,6 +1368,14 @@ static int enqueue_step(cx_cache* C) {
     // read back from the Infinity Cache (config 5: +0.6% a token; the next
     // layer's q/k/v as well gave nothing more)
     if (a.cap > CX_ATT_LDS_MAX) (void)cx_gemv_prefetch_plan(L.t_down, L.down, D, I, &a.pf.job[2]);
+    // and the next layer's K rows, which its scores kernel reads in one
+    // burst (config 5 285.1 -> 285.6 tok/s, 3B 742.6 -> 743.3)
+    if (li + 1 < c.layers) {
+      const size_t kb = C->cap * (size_t)kvd * 4;
+      const uint32_t tile = 256u << 10;
+      a.pf.job[3] = cx_l2_job{reinterpret_cast<const uint8_t*>(kc + 2 * C->cap * kvd), nullptr, kb,
+                              tile, (uint32_t)((kb + tile - 1) / tile)};
+    }
     if ((rc = cx_launch_attn_decode(a, s))) return rc;
     // src/forward.rs:466-469: output projection added to the residual
     cx_seg o{L.o, m->x, nullptr, D};
