@@ -1974,7 +1974,11 @@ template <int T>
 int launch_row_norm(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   const uint32_t rpw = 64 / (2 * (P.k / 256));
   uint32_t W = 1, tiles = 0;
+  // at k = 4096 at most 8 waves: with 16 (1024 threads, 128 VGPRs a lane)
+  // the prologue's registers spill to scratch
+  const uint32_t wmax = P.k == 4096 ? 8u : 16u;
   for (uint32_t w : {16u, 8u, 4u, 2u, 1u}) {
+    if (w > wmax) continue;
     tiles = 0;
     for (int i = 0; i < P.nseg; i++) tiles += (rows[i] + rpw * w - 1) / (rpw * w);
     W = w;
