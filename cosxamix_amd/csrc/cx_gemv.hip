@@ -1244,8 +1244,10 @@ constexpr uint32_t GLU_ROWS = 32;
 // else 32 in 8. With 344 tiles of 32 on 256 CUs, 88 CUs ran two and the
 // launch ended with them (stamps: the median tile done at 4.4 us, the last
 // at 6.8).
-inline uint32_t glu_row_tile(uint32_t k, uint32_t I) {
-  return k == 2048 && I % 64 == 0 ? 64u : GLU_ROWS;
+// Q4_K only: the Q5_K kernel's registers do not fit 1024 threads (it
+// spilled one VGPR to scratch).
+inline uint32_t glu_row_tile(int type, uint32_t k, uint32_t I) {
+  return type == CX_Q4_K && k == 2048 && I % 64 == 0 ? 64u : GLU_ROWS;
 }
 
 // Every thread keeps GLU_DEPTH items' weights in flight: all of them at
@@ -2346,7 +2348,7 @@ int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t 
     // 8.71 -> 7.75 us a launch, weights in L2). At k = 4096 (16 waves a
     // tile, 448 tiles: config 5's 14336 x 4096, 66 MB past L2) it measured
     // 20.4 us against k_gemv_glu's 16.3, which keeps that shape.
-    const uint32_t rows = glu_row_tile(k, I);
+    const uint32_t rows = glu_row_tile(type, k, I);
     const dim3 grid(I / rows), block(2 * (k / 256) * rows);
 #define CX_ROW_GLU(TT, NB, R)                                                              \
   do {                                                                                     \
@@ -2354,8 +2356,7 @@ int cx_launch_gemv_glu(int type, const uint8_t* wg, const uint8_t* wu, uint32_t 
     else hipLaunchKernelGGL((k_gemv_row_glu<TT, NB, 16, R>), grid, block, 0, s, P);          \
   } while (0)
     if (rows == 64) {
-      if (type == CX_Q4_K) CX_ROW_GLU(CX_Q4_K, 8, 64);
-      else CX_ROW_GLU(CX_Q5_K, 8, 64);
+      CX_ROW_GLU(CX_Q4_K, 8, 64);
     } else {
       if (type == CX_Q4_K) CX_ROW_GLU(CX_Q4_K, 8, 32);
       else CX_ROW_GLU(CX_Q5_K, 8, 32);
@@ -2427,7 +2428,7 @@ bool cx_glu_prefetch_plan(int type, const uint8_t* wg, const uint8_t* wu, uint32
   if (!cx_glu_fits(type, k) || I % GLU_ROWS) return false;
   const uint32_t rb = (cx_glu_supported(type) ? k / 256 : k / 32) * (uint32_t)cx_bpb(type);
   // the tiles of the launch that reads them (the row kernel's at k = 2048)
-  const uint32_t rows = cx_glu_supported(type) ? glu_row_tile(k, I) : GLU_ROWS;
+  const uint32_t rows = cx_glu_supported(type) ? glu_row_tile(type, k, I) : GLU_ROWS;
   *job = cx_l2_job{wg, wu, (size_t)I * rb, rows * rb, I / rows};
   return true;
 }
