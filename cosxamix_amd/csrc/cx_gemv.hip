@@ -1158,8 +1158,12 @@ __global__ __launch_bounds__(64 * W) void k_gemv_rowl(GemvParams P) {
   // 1. the thread's activation chunks (L2 hits; past the end: the last one),
   //    then the row's weights straight into registers
   int4 av[AP];
+  // (a local copy: handed P.act itself, the compiler picked each lane's
+  // pointer out of the kernel arguments with a vector load and waited for
+  // it before the activation's load, two round trips instead of one)
+  const cx_qact act = P.act;
 #pragma unroll
-  for (uint32_t i = 0; i < AP; i++) av[i] = rowl_act_load(P.act, nb, min(tid + 64 * W * i, nch - 1));
+  for (uint32_t i = 0; i < AP; i++) av[i] = rowl_act_load(act, nb, min(tid + 64 * W * i, nch - 1));
   __builtin_amdgcn_sched_barrier(0);
   typename Q::Regs r0, r1;
   const uint8_t* blk = S.w + (size_t)row * P.row_bytes + (size_t)b * Q::BPB;
