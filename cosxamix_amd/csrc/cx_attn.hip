@@ -104,21 +104,28 @@ __global__ __launch_bounds__(256) void k_att_qk(const float* q, const float* kne
   //    position with the rotated key from LDS and appends the key and value
   //    at the end (src/forward.rs:454-455), so no result depends on a row
   //    written here
+  //    Every load is issued before the first wait: the queries, the
+  //    tables, this step's key (with query head 0's pairs: j < half) and
+  //    the value the append stores in step 4 (each a round trip of its own
+  //    after the others when loaded where used).
   const bool rot = cos_t != nullptr, has_new = rot && pos < p0 + QK_P;
+  float vv = 0.0f;
+  if (has_new && (uint32_t)tid < (uint32_t)HD) vv = vnew[(size_t)z * kvd + g * HD + tid];
   if (rot) {
     const float* cc = cos_t + (size_t)pos * half;
     const float* ss = sin_t + (size_t)pos * half;
+    const float* kn = knew + (size_t)z * kvd + g * HD;
     for (uint32_t i = tid; i < per * half; i += 256) {
       const uint32_t hl = i / half, j = i % half;
-      const float x0 = q[hl * HD + j], x1 = q[hl * HD + j + half];
-      qr[hl * HD + j] = x0 * cc[j] - x1 * ss[j];
-      qr[hl * HD + j + half] = x0 * ss[j] + x1 * cc[j];
-    }
-    if (has_new) {
-      const float* kn = knew + (size_t)z * kvd + g * HD;
-      for (uint32_t j = tid; j < half; j += 256) {
-        const float k0 = kn[j], k1 = kn[j + half];
-        const float a = k0 * cc[j] - k1 * ss[j], b = k0 * ss[j] + k1 * cc[j];
+      const bool key = has_new && i < half;
+      float x0 = q[hl * HD + j], x1 = q[hl * HD + j + half];
+      float cj = cc[j], sj = ss[j], k0 = 0.0f, k1 = 0.0f;
+      if (key) k0 = kn[j], k1 = kn[j + half];
+      asm volatile("" : "+v"(x0), "+v"(x1), "+v"(cj), "+v"(sj), "+v"(k0), "+v"(k1));
+      qr[hl * HD + j] = x0 * cj - x1 * sj;
+      qr[hl * HD + j + half] = x0 * sj + x1 * cj;
+      if (key) {
+        const float a = k0 * cj - k1 * sj, b = k0 * sj + k1 * cj;
         kr[j] = a;
         kr[j + half] = b;
       }
@@ -144,14 +151,11 @@ __global__ __launch_bounds__(256) void k_att_qk(const float* q, const float* kne
   }
   // 4. the appended key (rotated, from LDS) and value: stored after the
   //    dots, since a wave waits for its stores as for its loads
-  if (has_new) {
-    const float* vn = vnew + (size_t)z * kvd + g * HD;
+  if (has_new && (uint32_t)tid < (uint32_t)HD) {
     float* kd = kc + (size_t)pos * kvd + g * HD;
     float* vd = vc + (size_t)pos * kvd + g * HD;
-    for (uint32_t j = tid; j < (uint32_t)HD; j += 256) {
-      kd[j] = kr[j];
-      vd[j] = vn[j];
-    }
+    kd[tid] = kr[tid];
+    vd[tid] = vv;
   }
 }
 

@@ -313,18 +313,31 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* q, const float
     if (r >= np || b >= ROWB) r = 0, b = 0;
     cx_dma16(reinterpret_cast<const uint8_t*>(kb + (size_t)r * kvd) + b, sm + c * 1024);
   }
-  // 2. rope while the rows arrive
+  // 2. rope while the rows arrive. Every load is issued before the first
+  //    wait: q, the tables, this step's key (loaded by every workgroup,
+  //    used by the last chunk's) and the value the append stores in step 4
+  //    (each a round trip of its own after the dots when loaded where used)
   const bool rot = cos_t != nullptr, has_new = rot && pos < p0 + SC_P;
+  const bool append = has_new && h % per == 0;
+  float vv[HD / 64];
+  if (append && w == 0) {
+#pragma unroll
+    for (int i = 0; i < HD / 64; i++) vv[i] = vnew[g * HD + t + 64 * i];
+  }
   if (rot) {
     const float* c = cos_t + (size_t)pos * half;
     const float* s = sin_t + (size_t)pos * half;
     for (uint32_t j = tid; j < half; j += 256) {
-      const float x0 = q[h * HD + j], x1 = q[h * HD + j + half];
-      qr[j] = x0 * c[j] - x1 * s[j];
-      qr[j + half] = x0 * s[j] + x1 * c[j];
+      float x0 = q[h * HD + j], x1 = q[h * HD + j + half];
+      float k0 = knew[g * HD + j], k1 = knew[g * HD + j + half];
+      float cj = c[j], sj = s[j];
+      // (one wait for all six: left alone, the compiler sinks the key's
+      // loads into the branch below, after a wait for the others)
+      asm volatile("" : "+v"(x0), "+v"(x1), "+v"(k0), "+v"(k1), "+v"(cj), "+v"(sj));
+      qr[j] = x0 * cj - x1 * sj;
+      qr[j + half] = x0 * sj + x1 * cj;
       if (has_new) {
-        const float k0 = knew[g * HD + j], k1 = knew[g * HD + j + half];
-        const float a = k0 * c[j] - k1 * s[j], b = k0 * s[j] + k1 * c[j];
+        const float a = k0 * cj - k1 * sj, b = k0 * sj + k1 * cj;
         kr[j] = a;
         kr[j + half] = b;
       }
@@ -352,12 +365,13 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* q, const float
   //    the value at st->pos for later tokens (src/forward.rs:454-455):
   //    stored after the dots, since a wave waits for its stores as for its
   //    loads, and nothing here reads them
-  if (has_new && h % per == 0) {
+  if (append) {
     float* kd = kc + (size_t)pos * kvd + g * HD;
     float* vd = vc + (size_t)pos * kvd + g * HD;
-    for (uint32_t j = t; j < (uint32_t)HD; j += 64) {
-      kd[j] = kr[j];
-      vd[j] = vnew[g * HD + j];
+#pragma unroll
+    for (int i = 0; i < HD / 64; i++) {
+      kd[t + 64 * i] = kr[t + 64 * i];
+      vd[t + 64 * i] = vv[i];
     }
   }
 }
