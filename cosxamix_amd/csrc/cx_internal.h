@@ -17,7 +17,7 @@ struct cx_l2_job {
   size_t bytes;  // of each of p0, p1
   uint32_t tile, tiles;
 };
-constexpr int CX_L2_JOBS = 4;
+constexpr int CX_L2_JOBS = 7;
 struct cx_l2_prefetch {
   cx_l2_job job[CX_L2_JOBS];
 };
