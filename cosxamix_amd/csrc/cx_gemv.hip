@@ -912,8 +912,12 @@ __global__ __launch_bounds__(64 * W) void k_gemv_row_norm(GemvParams P) {
   uint32_t tile = blockIdx.x;
   int sg = 0;
   if constexpr (MULTI) {
-    while (tile >= P.tile_end[sg]) sg++;
-    if (sg) tile -= P.tile_end[sg - 1];
+    // the tile ends and the count in one batch, then three compares (a
+    // search loop waited for one load after another)
+    const uint32_t e0 = P.tile_end[0], e1 = P.tile_end[1], e2 = P.tile_end[2];
+    const int n = P.nseg;
+    sg = (n > 1 && tile >= e0) + (n > 2 && tile >= e1) + (n > 3 && tile >= e2);
+    tile -= sg == 0 ? 0u : sg == 1 ? e0 : sg == 2 ? e1 : e2;
   }
   const cx_seg S = P.seg[sg];
   uint64_t wbase = (uint64_t)S.w;
