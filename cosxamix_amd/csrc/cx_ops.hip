@@ -968,21 +968,49 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float* v, const floa
                                                       const uint32_t* pi, uint32_t nparts,
                                                       uint32_t* out, cx_dstate* st,
                                                       uint32_t* hist, uint32_t* hist_host) {
+  constexpr uint32_t PPT = 16;  // pairs a thread a round
   __shared__ VI red[4];
+  // every load before the first wait: the token state and v[0] (thread 0's
+  // tail uses them), then a round's pairs, an index past the end reading
+  // the last pair again (a repeated pair leaves the maximum as it is). A
+  // loop of one pair a thread waited for each pair in turn.
+  float x[PPT];
+  uint32_t ix[PPT];
+  auto load = [&](uint32_t b) {
+#pragma unroll
+    for (uint32_t u = 0; u < PPT; u++) {
+      const uint32_t i = min(b + threadIdx.x + 256 * u, nparts - 1);
+      x[u] = pv[i];
+      ix[u] = pi[i];
+    }
+  };
+  load(0);
+  uint32_t pos = 0, pend = 0, cap = 0;
+  if (st) {
+    pos = st->pos;
+    pend = st->prompt_end;
+    cap = st->cap;
+  }
+  const float v0 = v[0];
   VI best{-INFINITY, 0xFFFFFFFFu};
-  for (uint32_t i = threadIdx.x; i < nparts; i += 256) best = vi_best(best, VI{pv[i], pi[i]});
+  for (uint32_t b = 0;;) {
+#pragma unroll
+    for (uint32_t u = 0; u < PPT; u++) best = vi_best(best, VI{x[u], ix[u]});
+    b += 256 * PPT;
+    if (b >= nparts) break;
+    load(b);
+  }
   best = vi_wave(best);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
   __syncthreads();
   if (threadIdx.x == 0) {
     VI r = vi_best(vi_best(red[0], red[1]), vi_best(red[2], red[3]));
     uint32_t tok = r.i;
-    const float v0 = v[0];
     if (v0 != v0 || tok == 0xFFFFFFFFu) tok = 0;
     if (out) *out = tok;
     if (st) {
-      const uint32_t nxt = st->pos + 1;
-      if (nxt >= st->prompt_end && nxt <= st->cap) {  // hist has cap+1 slots
+      const uint32_t nxt = pos + 1;
+      if (nxt >= pend && nxt <= cap) {  // hist has cap+1 slots
         hist[nxt] = tok;
         if (hist_host) hist_host[nxt] = tok;
       }
