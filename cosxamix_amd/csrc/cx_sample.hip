@@ -368,14 +368,19 @@ __global__ __launch_bounds__(RS_T) void k_rs_count(const float* pb, const uint32
   __shared__ uint32_t h[256];
   const uint32_t tid = threadIdx.x, base = blockIdx.x * RS_TILE;
   h[tid] = 0;
-  __syncthreads();
+  // every round's key loaded before the first is counted (an index past n
+  // reads element n - 1 and is not counted); a load a round waited for
+  // each in turn
+  uint32_t key[RS_R];
+#pragma unroll
   for (uint32_t r = 0; r < RS_R; r++) {
-    const uint32_t i = base + r * RS_T + tid;
-    if (i < n) {
-      const uint32_t key = D == 0 ? rs_key(pb[i]) : kin[i];
-      atomicAdd(&h[(key >> (8 * D)) & 255u], 1u);
-    }
+    const uint32_t i = min(base + r * RS_T + tid, n - 1);
+    key[r] = D == 0 ? rs_key(pb[i]) : kin[i];
   }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t r = 0; r < RS_R; r++)
+    if (base + r * RS_T + tid < n) atomicAdd(&h[(key[r] >> (8 * D)) & 255u], 1u);
   __syncthreads();
   cnt[tid * G + blockIdx.x] = h[tid];
 }
@@ -393,8 +398,15 @@ __global__ __launch_bounds__(CW) void k_rs_scan(uint32_t* cnt, uint32_t e, const
   const uint32_t tid = threadIdx.x, per = (e + CW - 1) / CW;
   const uint32_t lo = min(e, tid * per), hi = min(e, lo + per);
   uint32_t* c = LDS ? stage : cnt;
-  if (LDS) {
-    for (uint32_t i = tid; i < e; i += CW) stage[i] = cnt[i];
+  if (LDS) {  // eight loads in flight a thread (a loop of one waited for each)
+    for (uint32_t i0 = tid; i0 < e; i0 += 8 * CW) {
+      uint32_t v[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8; u++) v[u] = cnt[min(i0 + u * CW, e - 1)];
+#pragma unroll
+      for (uint32_t u = 0; u < 8; u++)
+        if (i0 + u * CW < e) stage[i0 + u * CW] = v[u];
+    }
     __syncthreads();
   }
   uint32_t sum = 0;
@@ -431,11 +443,21 @@ __global__ __launch_bounds__(RS_T) void k_rs_scatter(const float* pb, const uint
   const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6, base = blockIdx.x * RS_TILE;
   const uint64_t below = (1ull << lane) - 1;
   run[tid] = off[tid * G + blockIdx.x];
+  // every round's key and index loaded before the first round (an index
+  // past n reads element n - 1, never used)
+  uint32_t keys[RS_R], idxs[RS_R];
+#pragma unroll
+  for (uint32_t r = 0; r < RS_R; r++) {
+    const uint32_t i = min(base + r * RS_T + tid, n - 1);
+    keys[r] = D == 0 ? rs_key(pb[i]) : kin[i];
+    idxs[r] = D == 0 ? i : iin[i];
+  }
+#pragma unroll
   for (uint32_t r = 0; r < RS_R; r++) {
     const uint32_t i = base + r * RS_T + tid;
     const bool valid = i < n;
-    const uint32_t key = valid ? (D == 0 ? rs_key(pb[i]) : kin[i]) : 0u;
-    const uint32_t idx = D == 0 ? i : (valid ? iin[i] : 0u);
+    const uint32_t key = valid ? keys[r] : 0u;
+    const uint32_t idx = valid ? idxs[r] : 0u;
     const uint32_t dig = (key >> (8 * D)) & 255u;
     // the lanes of this wave with the same digit
     uint64_t m = __ballot(valid);
