@@ -43,8 +43,8 @@ namespace {
 constexpr uint32_t ZB = 256;         // threads of the grid kernels
 constexpr uint32_t ZV = 8;           // values per thread of the grid kernels
 constexpr uint32_t CW = 1024;        // threads of the single-workgroup kernels
-constexpr uint32_t SEG = 4096;       // floats per chain stage (16 KiB: two KiB per loader wave)
-constexpr uint32_t NST = 8;          // chain stages in the LDS ring
+constexpr uint32_t SEG = 8192;       // floats per chain stage (32 KiB: four KiB per loader wave)
+constexpr uint32_t NST = 4;          // chain stages in the LDS ring
 constexpr uint32_t CAND = 1024;      // CANDIDATOS (src/sampler.rs): the first nucleus
 constexpr uint32_t RS_T = 256;       // threads of a radix-sort workgroup
 constexpr uint32_t RS_R = 8;         // rounds of RS_T elements a tile
@@ -144,10 +144,7 @@ struct Ring {
       case 1: cx_wait_vm<L>(); break;
       case 2: cx_wait_vm<2 * L>(); break;
       case 3: cx_wait_vm<3 * L>(); break;
-      case 4: cx_wait_vm<4 * L>(); break;
-      case 5: cx_wait_vm<5 * L>(); break;
-      case 6: cx_wait_vm<6 * L>(); break;
-      default: cx_wait_vm<7 * L>(); break;
+      default: cx_wait_vm<3 * L>(); break;
     }
   }
 };
@@ -192,7 +189,8 @@ __device__ inline void chain_walk(const float* x, uint32_t n, float* lds, F stag
 }
 
 // One chain stage of a running sum (seq_scan's sum or search) by the whole
-// workgroup. Waves 0..MW_WIN-1 take 256-position windows in parallel, all in
+// workgroup. The waves take the MW_WIN 256-position windows in parallel (two
+// a wave: a stage of twice the positions halves the barriers a position), all in
 // the binade E of the running sum s where they start (unit u = 2^(E-23)): a
 // window's total N_w of rne(x/u), and whether it holds a tie or a term that
 // is not finite. While no window has such an event, the running sum reaches
@@ -206,7 +204,7 @@ __device__ inline void chain_walk(const float* x, uint32_t n, float* lds, F stag
 // seq_scan whole. Every thread returns the sum, and *at = the crossing's
 // index in the stage or m.
 constexpr uint32_t MW_WIN = SEG / 256;
-static_assert(MW_WIN <= CW / 64 && MW_WIN <= 64, "a wave a window, a lane a window's total");
+static_assert(MW_WIN % (CW / 64) == 0 && MW_WIN <= 64, "whole windows a wave, a lane a window's total");
 template <int M>
 __device__ inline float stage_scan_mw(const float* v, uint32_t m, float tot, bool head,
                                       float target, uint32_t* at) {
@@ -223,8 +221,9 @@ __device__ inline float stage_scan_mw(const float* v, uint32_t m, float tot, boo
     const bool whole = (head && w0 == 0) || !(s < INFINITY);
     const int E = binade_of(s), k = 23 - E;
     if (!whole) {
-      if (wave < MW_WIN) {
-        const uint32_t p = 256 * (w0 + wave) + 4 * lane;
+#pragma unroll
+      for (uint32_t wi = wave; wi < MW_WIN; wi += CW / 64) {
+        const uint32_t p = 256 * (w0 + wi) + 4 * lane;
         float c = 0.0f;
         bool bad = false;
 #pragma unroll
@@ -238,8 +237,8 @@ __device__ inline float stage_scan_mw(const float* v, uint32_t m, float tot, boo
         const float P = wave_scan_incl(c);
         const uint64_t b = __builtin_amdgcn_ballot_w64(bad);
         if (lane == 63) {
-          sN[wave] = P;
-          sbad[wave] = b != 0;
+          sN[wi] = P;
+          sbad[wi] = b != 0;
         }
       }
       cx_wait_lds();
