@@ -1387,6 +1387,14 @@ static int enqueue_step(cx_cache* C) {
         }
       }
     }
+    // At long caches the jobs stream far more than L2 holds: the o-proj's
+    // tiles go last, so that they are still in L2 when the o-proj launch,
+    // the next one, reads them
+    if (a.cap > CX_ATT_LDS_MAX) {
+      const cx_l2_job o = a.pf.job[0];
+      for (int j = 0; j + 1 < CX_L2_JOBS; j++) a.pf.job[j] = a.pf.job[j + 1];
+      a.pf.job[CX_L2_JOBS - 1] = o;
+    }
     if ((rc = cx_launch_attn_decode(a, s))) return rc;
     // src/forward.rs:466-469: output projection added to the residual
     cx_seg o{L.o, m->x, nullptr, D};
