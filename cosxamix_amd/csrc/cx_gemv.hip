@@ -1968,7 +1968,10 @@ int launch_row_k(GemvParams& P, const RowPlan& rp, hipStream_t s) {
 // shapes of 2048 + 256 + 256 rows at k = 2048 and ~6144 rows at k = 4096):
 // 3B 320 tiles of 2 waves 5.10 us, 160 of 4 waves 3.50, 80 of 8 waves 4.49
 // (the LDS-tile k_gemv prologue kernel: 5.92); k = 4096 192 tiles of 16
-// waves 7.83 us, 384 of 8 waves 7.79 (k_gemv: 13.5).
+// waves 7.83 us, 384 of 8 waves 7.79 (k_gemv: 13.5). In the config-5 decode
+// step (k = 4096), 768 tiles of 4 waves: 298.4 tok/s against 293.5 with 384
+// of 8 (whose tree waves, their x loads in a branch, waited for x before
+// issuing their weights) and 279.7 with 1536 of 2.
 constexpr uint32_t ROW_NORM_TILES = 128;
 template <int T, int NB, bool MULTI>
 void launch_row_norm_w(uint32_t W, const GemvParams& P, dim3 g, hipStream_t s) {
@@ -1984,9 +1987,9 @@ template <int T>
 int launch_row_norm(GemvParams& P, const uint32_t* rows, hipStream_t s) {
   const uint32_t rpw = 64 / (2 * (P.k / 256));
   uint32_t W = 1, tiles = 0;
-  // at k = 4096 at most 8 waves: with 16 (1024 threads, 128 VGPRs a lane)
-  // the prologue's registers spill to scratch
-  const uint32_t wmax = P.k == 4096 ? 8u : 16u;
+  // at k = 4096 at most 4 waves (with 16, 1024 threads and 128 VGPRs a
+  // lane, the prologue's registers spill to scratch; 8 measured slower)
+  const uint32_t wmax = P.k == 4096 ? 4u : 16u;
   for (uint32_t w : {16u, 8u, 4u, 2u, 1u}) {
     if (w > wmax) continue;
     tiles = 0;
